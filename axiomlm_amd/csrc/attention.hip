@@ -1,0 +1,508 @@
+// KV-cache writes (fp16 / FP8-E4M3FN / INT4, group 64 scales) and split-KV
+// decode / tree-verification attention for gfx950.
+//
+// Cache layouts are the reference StaticKVCache ones (axiomlm/engine/paged_cache.py:158-198):
+//   fp16 : [B][Hkv][S][hd]            f16
+//   fp8  : [B][Hkv][S][hd]            u8  + scales [B][Hkv][S][hd/64] f16
+//   int4 : [B][Hkv][S][hd/2]          u8  + scales [B][Hkv][S][hd/64] f16
+//
+// Attention mapping: one workgroup (4 waves) per (batch, kv head, key split)
+// and up to QR query rows that share the kv head (GQA replicas and/or tree
+// nodes).  A key row is spread over hd/8 lanes (8 elements = 16 B of fp16,
+// 8 B of fp8, 4 B of int4 per lane), so a wave walks 512/hd keys at once and
+// every key/value byte is read exactly once per workgroup.  Softmax is online
+// in the exp2 domain with fp32 state; partial (m, l, o) per split are merged by
+// a second kernel (or written directly when there is a single split).
+#include "kernels.h"
+
+namespace {
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1e30f;
+
+// ---------------------------------------------------------------------------
+// KV quantization + write.  One wave per (token, kv head, 64-group, k|v).
+// CPU semantics of quantize_kv_fp8 / quantize_kv_int4 (quant.py:692-807):
+//   scale = fp16(amax / 448 | 7)            (clamp(min=1e-8) is a no-op in fp16)
+//   xs    = fp16(x / scale)                 (fp16 division)
+//   fp8   = e4m3fn(float(xs));   int4 = clamp(rne(xs), -8, 7)
+// ---------------------------------------------------------------------------
+__global__ void kv_write_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld,
+                                int write_pos, const int* __restrict__ write_pos_dev) {
+  const int lane = threadIdx.x;  // 64 lanes
+  const int G = kv.hd / 64;
+  int idx = blockIdx.x;
+  const int g = idx % G;
+  idx /= G;
+  const int h = idx % kv.Hkv;
+  idx /= kv.Hkv;
+  const int which = idx % 2;  // 0 = k, 1 = v
+  const int t = idx / 2;
+  const int wp0 = write_pos_dev ? write_pos_dev[0] : write_pos;
+  const int slot = (wp0 + t) % kv.S;
+  const f16* src = (which == 0 ? k_rows : v_rows) + (size_t)t * ld + h * kv.hd + g * 64;
+  const f16 x = src[lane];
+  const size_t row = (size_t)h * kv.S + slot;  // batch 0
+  if (kv.kv_dtype == AXM_KV_FP16) {
+    f16* dst = (f16*)(which == 0 ? kv.k : kv.v);
+    dst[row * kv.hd + g * 64 + lane] = x;
+    return;
+  }
+  const float ax = fabsf(h2f(x));
+  const float amax = wave_max(ax);
+  const float div = kv.kv_dtype == AXM_KV_FP8 ? 448.0f : 7.0f;
+  const f16 sc = f2h(__fdiv_rn(amax, div));
+  const float scf = h2f(sc);
+  f16* sdst = which == 0 ? kv.ks : kv.vs;
+  if (lane == 0) sdst[row * G + g] = sc;
+  // fp16 division of x by the scale; 0/0 follows x86 (negative quiet NaN).
+  float q;
+  if (scf == 0.f) {
+    q = (h2f(x) == 0.f) ? __builtin_bit_cast(float, 0xFFC00000u) : h2f(x) / scf;
+  } else {
+    q = h2f(f2h(__fdiv_rn(h2f(x), scf)));
+  }
+  uint8_t* dst = (uint8_t*)(which == 0 ? kv.k : kv.v);
+  if (kv.kv_dtype == AXM_KV_FP8) {
+    dst[row * kv.hd + g * 64 + lane] = fp8e4m3fn_from_f32(q);
+  } else {
+    int qi;
+    if (q != q) {
+      qi = 0;  // NaN -> int8 conversion yields 0 on the reference CPU path
+    } else {
+      float r = __builtin_rintf(q);
+      r = fminf(fmaxf(r, -8.f), 7.f);
+      qi = (int)r;
+    }
+    const int partner = __shfl_xor(qi, 1, 64);
+    if ((lane & 1) == 0) {
+      dst[row * (kv.hd / 2) + g * 32 + lane / 2] = (uint8_t)((qi & 0xF) | ((partner & 0xF) << 4));
+    }
+  }
+}
+
+// Dequantized key/value chunk: 8 consecutive elements starting at e0 of slot `slot`.
+// Values are rounded to fp16 exactly as the reference CPU dequantizers do
+// (fp8 -> fp16 exact, then fp16 * fp16 scale rounded; int4 q * scale rounded).
+template <int KVT>
+__device__ __forceinline__ void load_kv8(const void* base, const f16* scales, size_t row, int hd, int e0,
+                                         float out[8]) {
+  if (KVT == AXM_KV_FP16) {
+    const f16x8 v = *reinterpret_cast<const f16x8*>((const f16*)base + row * hd + e0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = h2f(v[i]);
+  } else if (KVT == AXM_KV_FP8) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>((const uint8_t*)base + row * hd + e0);
+    const float sc = h2f(scales[row * (hd / 64) + e0 / 64]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t b = (v[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      out[i] = h2f(f2h(fp8e4m3fn_to_f32(b) * sc));
+    }
+  } else {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>((const uint8_t*)base + row * (hd / 2) + e0 / 2);
+    const float sc = h2f(scales[row * (hd / 64) + e0 / 64]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = (int)(((v >> (4 * i)) & 0xFu) ^ 0x8u) - 8;
+      out[i] = h2f(f2h((float)q * sc));
+    }
+  }
+}
+
+struct AttnParams {
+  const f16* q;           // query rows, row r at q + r_off(r)
+  KvView kv;
+  f16* out;
+  float* ws;              // partials [n_rows_total][n_splits][2 + hd]
+  int Hq, n_rep;
+  int n_splits;
+  int prefix_len;         // keys [0, prefix_len) (decode: active_len)
+  const int* prefix_dev;  // overrides prefix_len when non-null
+  int T;                  // tree nodes (0 for decode)
+  int write_pos;          // slot of tree node 0
+  const uint64_t* masks;  // [T] ancestor bitmasks (tree mode)
+  float scale_log2;       // log2(e) / sqrt(hd)
+};
+
+// Rows of one workgroup: decode -> (b, kv head, replica r) with r < n_rep;
+// tree -> (node u, kv head, replica) flattened, QR rows per workgroup.
+template <int KVT, int QR, bool TREE>
+__global__ void __launch_bounds__(kAttnThreads) attn_split_kernel(AttnParams p) {
+  const int hd = p.kv.hd;
+  const int LPT = hd / 8;        // lanes per key
+  const int KPW = 64 / LPT;      // keys per wave step
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane / LPT;    // key sub-slot within the wave
+  const int e0 = (lane % LPT) * 8;
+
+  // Work decomposition.
+  const int split = blockIdx.y;
+  const int kvh_all = blockIdx.x;  // (b, kv head) or (row chunk, kv head) in tree mode
+  int b, kvh, row_base, n_rows;
+  if (!TREE) {
+    b = kvh_all / p.kv.Hkv;
+    kvh = kvh_all % p.kv.Hkv;
+    row_base = blockIdx.z * QR;  // replica chunk
+    n_rows = min(QR, p.n_rep - row_base);
+  } else {
+    b = 0;
+    kvh = kvh_all % p.kv.Hkv;
+    const int chunk = kvh_all / p.kv.Hkv;  // chunk over (node, replica) pairs
+    row_base = chunk * QR;
+    n_rows = min(QR, p.T * p.n_rep - row_base);
+  }
+  if (n_rows <= 0) return;
+
+  // Global query-row index and query pointers.
+  float q[QR][8];
+  int qrow[QR];
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    int hq, tok;
+    if (!TREE) {
+      tok = b;
+      hq = kvh * p.n_rep + row_base + r;
+    } else {
+      const int rr = row_base + r;
+      tok = rr / p.n_rep;
+      hq = kvh * p.n_rep + rr % p.n_rep;
+    }
+    qrow[r] = tok * p.Hq + hq;
+    if (r < n_rows) {
+      const f16x8 v = *reinterpret_cast<const f16x8*>(p.q + (size_t)qrow[r] * hd + e0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[r][i] = h2f(v[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[r][i] = 0.f;
+    }
+  }
+
+  const int prefix = p.prefix_dev ? p.prefix_dev[0] : p.prefix_len;
+  const int n_keys = prefix + (TREE ? p.T : 0);
+  const int per = (n_keys + p.n_splits - 1) / p.n_splits;
+  const int k_begin = min(split * per, n_keys);
+  const int k_end = min(k_begin + per, n_keys);
+
+  float m[QR], l[QR], o[QR][8];
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    m[r] = kNegBig;
+    l[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[r][i] = 0.f;
+  }
+
+  const size_t head_row0 = ((size_t)b * p.kv.Hkv + kvh) * p.kv.S;
+  uint64_t node_mask[QR];
+  if (TREE) {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) node_mask[r] = r < n_rows ? p.masks[(row_base + r) / p.n_rep] : 0ull;
+  }
+
+  for (int kb = k_begin + wave * KPW; kb < k_end; kb += kAttnWaves * KPW) {
+    const int key = kb + sub;
+    const bool valid = key < k_end;
+    int slot = key;
+    if (TREE && key >= prefix) slot = (p.write_pos + (key - prefix)) % p.kv.S;
+    float kf[8], vf[8];
+    if (valid) {
+      load_kv8<KVT>(p.kv.k, p.kv.ks, head_row0 + slot, hd, e0, kf);
+      load_kv8<KVT>(p.kv.v, p.kv.vs, head_row0 + slot, hd, e0, vf);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kf[i] = vf[i] = 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[r][i], kf[i], d);
+      for (int off = LPT / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+      bool vis = valid && r < n_rows;
+      if (TREE && key >= prefix) vis = vis && ((node_mask[r] >> (key - prefix)) & 1ull);
+      const float s = vis ? d * p.scale_log2 : kNegBig;
+      const float m_new = fmaxf(m[r], s);
+      const float alpha = exp2f(m[r] - m_new);
+      const float pr = vis ? exp2f(s - m_new) : 0.f;
+      l[r] = l[r] * alpha + pr;
+      m[r] = m_new;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[r][i] = __builtin_fmaf(o[r][i], alpha, pr * vf[i]);
+    }
+  }
+
+  // Merge the KPW key sub-slots of the wave (lanes with equal e0).
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    for (int off = LPT; off < 64; off <<= 1) {
+      const float m2 = __shfl_xor(m[r], off, 64);
+      const float l2 = __shfl_xor(l[r], off, 64);
+      const float mn = fmaxf(m[r], m2);
+      const float a1 = exp2f(m[r] - mn), a2 = exp2f(m2 - mn);
+      l[r] = l[r] * a1 + l2 * a2;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float o2 = __shfl_xor(o[r][i], off, 64);
+        o[r][i] = o[r][i] * a1 + o2 * a2;
+      }
+      m[r] = mn;
+    }
+  }
+
+  // Merge the waves through LDS: [wave][r][2 + hd].
+  __shared__ float sm[kAttnWaves][QR][2 + 128];
+  if (lane < LPT) {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      if (lane == 0) {
+        sm[wave][r][0] = m[r];
+        sm[wave][r][1] = l[r];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm[wave][r][2 + e0 + i] = o[r][i];
+    }
+  }
+  __syncthreads();
+  // Thread t handles (r, e) pairs.
+  for (int idx = threadIdx.x; idx < QR * hd; idx += kAttnThreads) {
+    const int r = idx / hd, e = idx % hd;
+    if (r >= n_rows) continue;
+    float mm = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) mm = fmaxf(mm, sm[w][r][0]);
+    float ll = 0.f, oo = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float a = exp2f(sm[w][r][0] - mm);
+      ll += sm[w][r][1] * a;
+      oo += sm[w][r][2 + e] * a;
+    }
+    if (p.n_splits == 1) {
+      const int gr = (!TREE) ? (b * p.Hq + kvh * p.n_rep + row_base + r)
+                             : (((row_base + r) / p.n_rep) * p.Hq + kvh * p.n_rep + (row_base + r) % p.n_rep);
+      p.out[(size_t)gr * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+    } else {
+      const int gr = (!TREE) ? (b * p.Hq + kvh * p.n_rep + row_base + r)
+                             : (((row_base + r) / p.n_rep) * p.Hq + kvh * p.n_rep + (row_base + r) % p.n_rep);
+      float* dst = p.ws + ((size_t)gr * p.n_splits + split) * (2 + hd);
+      if (e == 0) {
+        dst[0] = mm;
+        dst[1] = ll;
+      }
+      dst[2 + e] = oo;
+    }
+  }
+}
+
+// Merge split partials: one block per query row, hd threads.
+__global__ void attn_reduce_kernel(const float* __restrict__ ws, f16* __restrict__ out, int n_splits, int hd) {
+  const int row = blockIdx.x;
+  const int e = threadIdx.x;
+  const float* base = ws + (size_t)row * n_splits * (2 + hd);
+  float mm = kNegBig;
+  for (int s = 0; s < n_splits; ++s) mm = fmaxf(mm, base[(size_t)s * (2 + hd)]);
+  float ll = 0.f, oo = 0.f;
+  for (int s = 0; s < n_splits; ++s) {
+    const float* ps = base + (size_t)s * (2 + hd);
+    const float a = exp2f(ps[0] - mm);
+    ll += ps[1] * a;
+    oo += ps[2 + e] * a;
+  }
+  if (e < hd) out[(size_t)row * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+}
+
+template <int KVT, int QR, bool TREE>
+void launch_attn_t(const AttnParams& p, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_split_kernel<KVT, QR, TREE>), grid, dim3(kAttnThreads), 0, s, p);
+}
+
+template <bool TREE>
+int launch_attn_dispatch(const AttnParams& p, int qr, dim3 grid, hipStream_t s) {
+#define AXM_ATTN_QR(KVT)                                              \
+  switch (qr) {                                                       \
+    case 1: launch_attn_t<KVT, 1, TREE>(p, grid, s); return 0;        \
+    case 2: launch_attn_t<KVT, 2, TREE>(p, grid, s); return 0;        \
+    case 4: launch_attn_t<KVT, 4, TREE>(p, grid, s); return 0;        \
+    case 8: launch_attn_t<KVT, 8, TREE>(p, grid, s); return 0;        \
+  }                                                                   \
+  break;
+  switch (p.kv.kv_dtype) {
+    case AXM_KV_FP16: AXM_ATTN_QR(AXM_KV_FP16)
+    case AXM_KV_FP8: AXM_ATTN_QR(AXM_KV_FP8)
+    case AXM_KV_INT4: AXM_ATTN_QR(AXM_KV_INT4)
+  }
+#undef AXM_ATTN_QR
+  axm_set_error("attention: unsupported kv dtype %d / rows %d", p.kv.kv_dtype, qr);
+  return -2;
+}
+
+int pick_qr(int rows) {
+  if (rows <= 1) return 1;
+  if (rows <= 2) return 2;
+  if (rows <= 4) return 4;
+  return 8;
+}
+
+}  // namespace
+
+int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int ld_rows, int T, int write_pos,
+                    const int* write_pos_dev, hipStream_t s) {
+  const int G = kv.hd / 64;
+  const unsigned blocks = (unsigned)T * 2 * kv.Hkv * G;
+  hipLaunchKernelGGL(kv_write_kernel, dim3(blocks), dim3(64), 0, s, kv, k_rows, v_rows, ld_rows, write_pos,
+                     write_pos_dev);
+  return 0;
+}
+
+size_t attn_workspace_bytes(int B, int Hq, int hd, int n_splits) {
+  return n_splits <= 1 ? 0 : (size_t)B * Hq * n_splits * (2 + hd) * sizeof(float);
+}
+
+int attn_choose_splits(int B, int Hkv, int active_len) {
+  // Aim for >= 2 workgroups per CU with >= 32 keys per split.
+  const int target_wg = 2 * axm_num_cus();
+  int splits = (target_wg + B * Hkv - 1) / (B * Hkv);
+  const int by_len = (active_len + 31) / 32;
+  if (splits > by_len) splits = by_len;
+  if (splits > 64) splits = 64;
+  if (splits < 1) splits = 1;
+  return splits;
+}
+
+int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,
+                        int n_splits, float* ws, hipStream_t s) {
+  AttnParams p{};
+  p.q = q;
+  p.kv = kv;
+  p.out = out;
+  p.ws = ws;
+  p.Hq = Hq;
+  p.n_rep = Hq / kv.Hkv;
+  p.n_splits = n_splits;
+  p.prefix_len = active_len;
+  p.prefix_dev = active_len_dev;
+  p.T = 0;
+  p.scale_log2 = kLog2e / sqrtf((float)kv.hd);
+  const int qr = pick_qr(p.n_rep);
+  dim3 grid(kv.B * kv.Hkv, n_splits, (p.n_rep + qr - 1) / qr);
+  int rc = launch_attn_dispatch<false>(p, qr, grid, s);
+  if (rc) return rc;
+  if (n_splits > 1)
+    hipLaunchKernelGGL(attn_reduce_kernel, dim3(kv.B * Hq), dim3(kv.hd), 0, s, ws, out, n_splits, kv.hd);
+  return 0;
+}
+
+size_t tree_workspace_bytes(int T, int Hq, int hd, int n_splits) {
+  return n_splits <= 1 ? 0 : (size_t)T * Hq * n_splits * (2 + hd) * sizeof(float);
+}
+
+int launch_tree_attention(const f16* q, const KvView& kv, f16* out, int Hq, int T, int prefix_len, int write_pos,
+                          const uint64_t* masks_dev, int n_splits, float* ws, hipStream_t s) {
+  AttnParams p{};
+  p.q = q;
+  p.kv = kv;
+  p.out = out;
+  p.ws = ws;
+  p.Hq = Hq;
+  p.n_rep = Hq / kv.Hkv;
+  p.n_splits = n_splits;
+  p.prefix_len = prefix_len;
+  p.T = T;
+  p.write_pos = write_pos;
+  p.masks = masks_dev;
+  p.scale_log2 = kLog2e / sqrtf((float)kv.hd);
+  const int rows = T * p.n_rep;
+  const int qr = pick_qr(rows);
+  dim3 grid(kv.Hkv * ((rows + qr - 1) / qr), n_splits, 1);
+  int rc = launch_attn_dispatch<true>(p, qr, grid, s);
+  if (rc) return rc;
+  if (n_splits > 1)
+    hipLaunchKernelGGL(attn_reduce_kernel, dim3(T * Hq), dim3(kv.hd), 0, s, ws, out, n_splits, kv.hd);
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI.
+// ---------------------------------------------------------------------------
+static int check_kv(const KvView& kv, const char* who) {
+  AXM_CHECK_ARG(kv.k && kv.v, -1, "%s: null cache pointer", who);
+  AXM_CHECK_ARG(kv.hd > 0 && kv.hd <= 128 && kv.hd % 64 == 0, -1, "%s: head_dim=%d must be 64 or 128", who, kv.hd);
+  AXM_CHECK_ARG(kv.kv_dtype >= 0 && kv.kv_dtype <= 2, -1, "%s: bad kv dtype %d", who, kv.kv_dtype);
+  AXM_CHECK_ARG(kv.kv_dtype == AXM_KV_FP16 || (kv.ks && kv.vs), -1, "%s: quantized cache needs scales", who);
+  AXM_CHECK_ARG(kv.B > 0 && kv.Hkv > 0 && kv.S > 0, -1, "%s: bad cache shape", who);
+  return 0;
+}
+
+extern "C" size_t axm_attention_workspace_bytes(int B, int n_query_rows_per_batch, int head_dim, int n_splits) {
+  return attn_workspace_bytes(B, n_query_rows_per_batch, head_dim, n_splits);
+}
+
+extern "C" int axm_attention_num_splits(int B, int n_kv_head, int active_len) {
+  return attn_choose_splits(B, n_kv_head, active_len);
+}
+
+extern "C" int axm_gqa_flash_decode(const void* q, const void* k_cache, const void* v_cache, const void* k_scales,
+                                    const void* v_scales, int kv_dtype, void* out, int B, int n_head, int n_kv_head,
+                                    int head_dim, int max_seq_len, int active_len, int num_splits, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  KvView kv{(void*)k_cache, (void*)v_cache, (f16*)k_scales, (f16*)v_scales, kv_dtype, B, n_kv_head, max_seq_len,
+            head_dim};
+  if (int rc = check_kv(kv, "gqa_flash_decode")) return rc;
+  AXM_CHECK_ARG(q && out, -1, "gqa_flash_decode: null q/out");
+  AXM_CHECK_ARG(n_head % n_kv_head == 0 && n_head / n_kv_head <= 64, -1,
+                "gqa_flash_decode: n_head=%d not a multiple of n_kv_head=%d", n_head, n_kv_head);
+  AXM_CHECK_ARG(active_len >= 1 && active_len <= max_seq_len, -1, "gqa_flash_decode: active_len=%d out of [1, %d]",
+                active_len, max_seq_len);
+  if (num_splits <= 0) num_splits = attn_choose_splits(B, n_kv_head, active_len);
+  AXM_CHECK_ARG(num_splits <= 1024, -1, "gqa_flash_decode: num_splits=%d too large", num_splits);
+  const size_t need = attn_workspace_bytes(B, n_head, head_dim, num_splits);
+  AXM_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace), -1,
+                "gqa_flash_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  int rc = launch_flash_decode((const f16*)q, kv, (f16*)out, n_head, active_len, nullptr, num_splits,
+                               (float*)workspace, (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("gqa_flash_decode");
+  return 0;
+}
+
+extern "C" int axm_gqa_tree_verify(const void* q, const void* k_cache, const void* v_cache, const void* k_scales,
+                                   const void* v_scales, int kv_dtype, void* out, int T, int n_head, int n_kv_head,
+                                   int head_dim, int max_seq_len, int prefix_len, int write_pos,
+                                   const void* masks_u64_dev, int num_splits, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  KvView kv{(void*)k_cache, (void*)v_cache, (f16*)k_scales, (f16*)v_scales, kv_dtype, 1, n_kv_head, max_seq_len,
+            head_dim};
+  if (int rc = check_kv(kv, "gqa_tree_verify")) return rc;
+  AXM_CHECK_ARG(q && out && masks_u64_dev, -1, "gqa_tree_verify: null pointer");
+  AXM_CHECK_ARG(T >= 1 && T <= 64, -1, "gqa_tree_verify: T=%d must be in [1, 64]", T);
+  AXM_CHECK_ARG(n_head % n_kv_head == 0, -1, "gqa_tree_verify: n_head %% n_kv_head != 0");
+  AXM_CHECK_ARG(prefix_len >= 0 && prefix_len <= max_seq_len, -1, "gqa_tree_verify: bad prefix_len %d", prefix_len);
+  AXM_CHECK_ARG(write_pos >= 0 && write_pos < max_seq_len, -1, "gqa_tree_verify: bad write_pos %d", write_pos);
+  if (num_splits <= 0) num_splits = attn_choose_splits(1, n_kv_head * T, prefix_len + T);
+  const size_t need = tree_workspace_bytes(T, n_head, head_dim, num_splits);
+  AXM_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace), -1,
+                "gqa_tree_verify: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  int rc = launch_tree_attention((const f16*)q, kv, (f16*)out, n_head, T, prefix_len, write_pos,
+                                 (const uint64_t*)masks_u64_dev, num_splits, (float*)workspace, (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("gqa_tree_verify");
+  return 0;
+}
+
+extern "C" int axm_kv_cache_write(const void* k_rows, const void* v_rows, int ld_rows, int T, void* k_cache,
+                                  void* v_cache, void* k_scales, void* v_scales, int kv_dtype, int n_kv_head,
+                                  int head_dim, int max_seq_len, int write_pos, void* stream) {
+  KvView kv{k_cache, v_cache, (f16*)k_scales, (f16*)v_scales, kv_dtype, 1, n_kv_head, max_seq_len, head_dim};
+  if (int rc = check_kv(kv, "kv_cache_write")) return rc;
+  AXM_CHECK_ARG(k_rows && v_rows && T >= 1, -1, "kv_cache_write: bad rows");
+  AXM_CHECK_ARG(write_pos >= 0 && write_pos < max_seq_len, -1, "kv_cache_write: write_pos %d out of range",
+                write_pos);
+  launch_kv_write(kv, (const f16*)k_rows, (const f16*)v_rows, ld_rows, T, write_pos, nullptr, (hipStream_t)stream);
+  AXM_LAUNCH_CHECK("kv_cache_write");
+  return 0;
+}

@@ -1,0 +1,58 @@
+// Internal host-side launchers shared between the C-ABI wrappers and the
+// decode runner.  All pointers are device pointers; every launcher enqueues on
+// the given stream and never synchronizes.
+#pragma once
+#include "axm_common.h"
+#include "q4_marlin.h"
+
+// ---- norms / activations (torch-CPU fp16 op semantics) ---------------------
+int launch_rmsnorm(const f16* x, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s);
+int launch_add_rmsnorm(f16* x, const f16* r, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s);
+int launch_swiglu(const f16* gu, f16* y, int rows, int H, hipStream_t s);
+// Row-wise argmax of fp16 logits; the lowest index wins ties.
+int launch_argmax(const f16* logits, int rows, int V, int64_t* out, hipStream_t s);
+
+// ---- embeddings -------------------------------------------------------------
+// tokens: int64 device array of length T (or nullptr with tok_dev pointing to
+// one int32 slot written by the runner's parameter kernel).
+// Token ids outside [0, V) produce zero rows.
+int launch_embed_f16(const f16* table, const int64_t* tokens, const int* tok_dev, f16* out, int T, int D, int V,
+                     hipStream_t s);
+int launch_embed_q8(const uint8_t* wq, const f16* sb, const int64_t* tokens, const int* tok_dev, f16* out, int T,
+                    int D, int V, hipStream_t s);
+
+// ---- Q8_G64 GEMV (affine 8-bit, group 64), optional fused fp16 RMSNorm -------
+int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
+                   const f16* ln_w, float eps, hipStream_t s);
+
+// ---- KV cache ---------------------------------------------------------------
+#include "axm.h"  // AXM_KV_* codes
+
+struct KvView {
+  void* k;        // fp16 [B][Hkv][S][hd] | u8 [B][Hkv][S][hd] | u8 [B][Hkv][S][hd/2]
+  void* v;
+  f16* ks;        // scales [B][Hkv][S][hd/64] (quantized caches)
+  f16* vs;
+  int kv_dtype;
+  int B, Hkv, S, hd;
+};
+
+// Quantize fp16 k/v rows [T][Hkv*hd] and write them at slots (write_pos+t) % S
+// (batch 0).  write_pos_dev overrides write_pos when non-null.
+int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int ld_rows, int T, int write_pos,
+                    const int* write_pos_dev, hipStream_t s);
+
+// Split-KV decode attention over slots [0, active_len) of every batch entry.
+// q: [B][Hq][hd] fp16, out: [B][Hq][hd] fp16.  ws: workspace of
+// attn_workspace_bytes(); active_len_dev overrides active_len when non-null.
+size_t attn_workspace_bytes(int B, int Hq, int hd, int n_splits);
+int attn_choose_splits(int B, int Hkv, int active_len);
+int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,
+                        int n_splits, float* ws, hipStream_t s);
+
+// Tree / multi-token verification attention (batch 0): T query tokens; prefix
+// slots [0, prefix_len) always visible; tree node j lives at slot
+// (write_pos + j) % S and is visible to node u iff bit j of mask[u] is set.
+int launch_tree_attention(const f16* q, const KvView& kv, f16* out, int Hq, int T, int prefix_len, int write_pos,
+                          const uint64_t* masks_dev, int n_splits, float* ws, hipStream_t s);
+size_t tree_workspace_bytes(int T, int Hq, int hd, int n_splits);

@@ -1,0 +1,315 @@
+// Row-wise kernels of the decode step: RMSNorm (+ residual add), SwiGLU,
+// argmax, embedding gathers and the Q8_G64 GEMV used for tied / q8 lm_heads.
+//
+// Numerics follow the reference CPU path on a half-precision model: every
+// elementwise fp16 op rounds its fp32 result to fp16 (torch CPU semantics),
+// reductions accumulate in fp32.
+#include "kernels.h"
+
+namespace {
+
+constexpr int kNormThreads = 256;
+
+__device__ float block_sum_256(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) s += red[i];
+  return s;
+}
+
+// y = half(half(x * rinv) * w)   (modules.py:41-43)
+__global__ void __launch_bounds__(kNormThreads)
+    rmsnorm_kernel(const f16* __restrict__ x, const f16* __restrict__ w, f16* __restrict__ y, int D, float eps) {
+  __shared__ float red[kNormThreads / 64];
+  const f16* xr = x + (size_t)blockIdx.x * D;
+  f16* yr = y + (size_t)blockIdx.x * D;
+  float s = 0.f;
+  for (int k = threadIdx.x; k < D; k += kNormThreads) {
+    float v = h2f(xr[k]);
+    s += h2f(f2h(v * v));
+  }
+  const float rinv = rms_inv_fp16(block_sum_256(s, red), D, eps);
+  for (int k = threadIdx.x; k < D; k += kNormThreads) {
+    f16 t = f2h(h2f(xr[k]) * rinv);
+    yr[k] = f2h(h2f(t) * h2f(w[k]));
+  }
+}
+
+// x = half(x + r);  y = rmsnorm(x)   (transformer.py:1176-1178)
+__global__ void __launch_bounds__(kNormThreads)
+    add_rmsnorm_kernel(f16* __restrict__ x, const f16* __restrict__ r, const f16* __restrict__ w,
+                       f16* __restrict__ y, int D, float eps) {
+  __shared__ float red[kNormThreads / 64];
+  f16* xr = x + (size_t)blockIdx.x * D;
+  const f16* rr = r + (size_t)blockIdx.x * D;
+  f16* yr = y + (size_t)blockIdx.x * D;
+  float s = 0.f;
+  for (int k = threadIdx.x; k < D; k += kNormThreads) {
+    f16 h = f2h(h2f(xr[k]) + h2f(rr[k]));
+    xr[k] = h;
+    float v = h2f(h);
+    s += h2f(f2h(v * v));
+  }
+  const float rinv = rms_inv_fp16(block_sum_256(s, red), D, eps);
+  for (int k = threadIdx.x; k < D; k += kNormThreads) {
+    f16 t = f2h(h2f(xr[k]) * rinv);
+    yr[k] = f2h(h2f(t) * h2f(w[k]));
+  }
+}
+
+// y = half(half(silu(g)) * u) with [g || u] rows (transformer.py:1188-1189)
+__global__ void swiglu_kernel(const f16* __restrict__ gu, f16* __restrict__ y, int rows, int H) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)rows * H) return;
+  const long r = i / H, c = i % H;
+  const float g = h2f(gu[r * 2 * H + c]);
+  const f16 sg = f2h(g / (1.0f + expf(-g)));
+  y[i] = f2h(h2f(sg) * h2f(gu[r * 2 * H + H + c]));
+}
+
+// Argmax with lowest-index tie break; NaN compares as smaller than anything.
+__global__ void __launch_bounds__(256) argmax_kernel(const f16* __restrict__ logits, int V, int64_t* __restrict__ out) {
+  __shared__ float bv[4];
+  __shared__ int bi[4];
+  const f16* lr = logits + (size_t)blockIdx.x * V;
+  float best = -INFINITY;
+  int besti = 0x7fffffff;
+  for (int k = threadIdx.x; k < V; k += 256) {
+    const float v = h2f(lr[k]);
+    if (v > best || (v == best && k < besti)) {
+      best = v;
+      besti = k;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(besti, o, 64);
+    if (ov > best || (ov == best && oi < besti)) {
+      best = ov;
+      besti = oi;
+    }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    bv[w] = best;
+    bi[w] = besti;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; ++i)
+      if (bv[i] > best || (bv[i] == best && bi[i] < besti)) {
+        best = bv[i];
+        besti = bi[i];
+      }
+    out[blockIdx.x] = besti == 0x7fffffff ? 0 : besti;
+  }
+}
+
+__device__ __forceinline__ long token_of(const int64_t* tokens, const int* tok_dev, int t) {
+  return tokens != nullptr ? (long)tokens[t] : (long)tok_dev[t];
+}
+
+// Out-of-range token ids produce a zero row instead of reading outside the table.
+__global__ void embed_f16_kernel(const f16* __restrict__ table, const int64_t* __restrict__ tokens,
+                                 const int* __restrict__ tok_dev, f16* __restrict__ out, int D, int V) {
+  const int t = blockIdx.x;
+  const long tok = token_of(tokens, tok_dev, t);
+  const bool ok = tok >= 0 && tok < V;
+  for (int k = threadIdx.x; k < D; k += blockDim.x) out[(size_t)t * D + k] = ok ? table[(size_t)tok * D + k] : f16(0);
+}
+
+// Q8_G64 row dequantization: half(q * scale + bias) in fp32 (quant.py:132-163).
+__global__ void embed_q8_kernel(const uint8_t* __restrict__ wq, const f16* __restrict__ sb,
+                                const int64_t* __restrict__ tokens, const int* __restrict__ tok_dev,
+                                f16* __restrict__ out, int D, int V) {
+  const int t = blockIdx.x;
+  const long tok = token_of(tokens, tok_dev, t);
+  const int G = D / 64;
+  if (tok < 0 || tok >= V) {
+    for (int k = threadIdx.x; k < D; k += blockDim.x) out[(size_t)t * D + k] = f16(0);
+    return;
+  }
+  for (int k = threadIdx.x; k < D; k += blockDim.x) {
+    const float q = (float)wq[(size_t)tok * D + k];
+    const f16* sbr = sb + ((size_t)tok * G + k / 64) * 2;
+    out[(size_t)t * D + k] = f2h(__fadd_rn(__fmul_rn(q, h2f(sbr[0])), h2f(sbr[1])));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_G64 GEMV:  y[n] = sum_g scale*(sum q*x) + bias*(sum x)   (quant.py:72-129)
+// One wave per output row per iteration; each lane streams 16 bytes (16 codes
+// of one group quarter).  Activations (optionally RMS-normalized) are staged
+// in LDS as fp32.
+// ---------------------------------------------------------------------------
+constexpr int kQ8Threads = 256;
+
+__global__ void __launch_bounds__(kQ8Threads)
+    q8_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ sb,
+                   const f16* __restrict__ bias, f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w,
+                   float eps) {
+  extern __shared__ __align__(16) float xs[];  // [M][K]
+  __shared__ float red[4];
+  for (int mi = 0; mi < M; ++mi) {
+    const f16* xr = x + (size_t)mi * K;
+    float rinv = 1.f;
+    if (ln_w != nullptr) {
+      float s = 0.f;
+      for (int k = threadIdx.x; k < K; k += kQ8Threads) {
+        float v = h2f(xr[k]);
+        s += h2f(f2h(v * v));
+      }
+      rinv = rms_inv_fp16(block_sum_256(s, red), K, eps);
+    }
+    for (int k = threadIdx.x; k < K; k += kQ8Threads) {
+      f16 h = xr[k];
+      if (ln_w != nullptr) h = f2h(h2f(f2h(h2f(h) * rinv)) * h2f(ln_w[k]));
+      xs[(size_t)mi * K + k] = h2f(h);
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int G = K / 64;
+  const int n_waves_total = gridDim.x * (kQ8Threads / 64);
+  for (int n = blockIdx.x * (kQ8Threads / 64) + wave; n < N; n += n_waves_total) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const uint8_t* wr = w + (size_t)n * K;
+    const f16* sbr = sb + (size_t)n * G * 2;
+    for (int k0 = lane * 16; k0 < K; k0 += 64 * 16) {
+      const u32x4 q4 = *reinterpret_cast<const u32x4*>(wr + k0);
+      const int g = k0 >> 6;
+      const float sc = h2f(sbr[2 * g]), bi = h2f(sbr[2 * g + 1]);
+      for (int mi = 0; mi < M && mi < 4; ++mi) {
+        const float* xk = xs + (size_t)mi * K + k0;
+        float d = 0.f, xsum = 0.f;
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+          const uint32_t word = q4[wi];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const float xv = xk[wi * 4 + b];
+            d = __builtin_fmaf((float)((word >> (8 * b)) & 0xFFu), xv, d);
+            xsum += xv;
+          }
+        }
+        acc[mi] = __builtin_fmaf(sc, d, __builtin_fmaf(bi, xsum, acc[mi]));
+      }
+    }
+    for (int mi = 0; mi < M && mi < 4; ++mi) {
+      const float v = wave_sum(acc[mi]);
+      if (lane == 0) {
+        f16 h = f2h(v);
+        if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[n]));
+        y[(size_t)mi * N + n] = h;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int launch_rmsnorm(const f16* x, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, w, y, D, eps);
+  return 0;
+}
+int launch_add_rmsnorm(f16* x, const f16* r, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s) {
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, r, w, y, D, eps);
+  return 0;
+}
+int launch_swiglu(const f16* gu, f16* y, int rows, int H, hipStream_t s) {
+  const long n = (long)rows * H;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gu, y, rows, H);
+  return 0;
+}
+int launch_argmax(const f16* logits, int rows, int V, int64_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, logits, V, out);
+  return 0;
+}
+int launch_embed_f16(const f16* table, const int64_t* tokens, const int* tok_dev, f16* out, int T, int D, int V,
+                     hipStream_t s) {
+  hipLaunchKernelGGL(embed_f16_kernel, dim3(T), dim3(256), 0, s, table, tokens, tok_dev, out, D, V);
+  return 0;
+}
+int launch_embed_q8(const uint8_t* wq, const f16* sb, const int64_t* tokens, const int* tok_dev, f16* out, int T,
+                    int D, int V, hipStream_t s) {
+  hipLaunchKernelGGL(embed_q8_kernel, dim3(T), dim3(256), 0, s, wq, sb, tokens, tok_dev, out, D, V);
+  return 0;
+}
+
+int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
+                   const f16* ln_w, float eps, hipStream_t s) {
+  for (int m0 = 0; m0 < M; m0 += 4) {
+    const int mc = (M - m0) < 4 ? (M - m0) : 4;
+    const size_t smem = (size_t)mc * K * sizeof(float);
+    if (smem > 160 * 1024) {
+      axm_set_error("q8 gemv: K=%d too large for LDS staging", K);
+      return -2;
+    }
+    static bool attr = false;
+    if (!attr) {
+      (void)hipFuncSetAttribute((const void*)q8_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      attr = true;
+    }
+    const int rows_per_block = kQ8Threads / 64;
+    int grid = (N + rows_per_block - 1) / rows_per_block;
+    const int cap = axm_num_cus() * 8;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(q8_gemv_kernel, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, sb, bias,
+                       y + (size_t)m0 * N, mc, K, N, ln_w, eps);
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI wrappers.
+// ---------------------------------------------------------------------------
+extern "C" int axm_rmsnorm(const void* x, const void* w, void* y, int rows, int D, float eps, void* stream) {
+  AXM_CHECK_ARG(x && w && y && rows > 0 && D > 0, -1, "rmsnorm: bad arguments");
+  launch_rmsnorm((const f16*)x, (const f16*)w, (f16*)y, rows, D, eps, (hipStream_t)stream);
+  AXM_LAUNCH_CHECK("rmsnorm");
+  return 0;
+}
+extern "C" int axm_add_rmsnorm(void* x, const void* r, const void* w, void* y, int rows, int D, float eps,
+                               void* stream) {
+  AXM_CHECK_ARG(x && r && w && y && rows > 0 && D > 0, -1, "add_rmsnorm: bad arguments");
+  launch_add_rmsnorm((f16*)x, (const f16*)r, (const f16*)w, (f16*)y, rows, D, eps, (hipStream_t)stream);
+  AXM_LAUNCH_CHECK("add_rmsnorm");
+  return 0;
+}
+extern "C" int axm_swiglu_gate_up(const void* gu, void* y, int rows, int H, void* stream) {
+  AXM_CHECK_ARG(gu && y && rows > 0 && H > 0, -1, "swiglu_gate_up: bad arguments");
+  launch_swiglu((const f16*)gu, (f16*)y, rows, H, (hipStream_t)stream);
+  AXM_LAUNCH_CHECK("swiglu_gate_up");
+  return 0;
+}
+extern "C" int axm_argmax(const void* logits, int rows, int V, void* out_i64, void* stream) {
+  AXM_CHECK_ARG(logits && out_i64 && rows > 0 && V > 0, -1, "argmax: bad arguments");
+  launch_argmax((const f16*)logits, rows, V, (int64_t*)out_i64, (hipStream_t)stream);
+  AXM_LAUNCH_CHECK("argmax");
+  return 0;
+}
+extern "C" int axm_embed_q8_g64(const void* w_packed, const void* sb, const void* tokens_i64, void* out, int T,
+                                int D, int V, void* stream) {
+  AXM_CHECK_ARG(w_packed && sb && tokens_i64 && out && T > 0 && D % 64 == 0 && V > 0, -1,
+                "embed_q8_g64: bad arguments");
+  launch_embed_q8((const uint8_t*)w_packed, (const f16*)sb, (const int64_t*)tokens_i64, nullptr, (f16*)out, T, D, V,
+                  (hipStream_t)stream);
+  AXM_LAUNCH_CHECK("embed_q8_g64");
+  return 0;
+}
+extern "C" int axm_qmv_q8_g64(const void* x, const void* w_packed, const void* sb, const void* bias, void* y, int M,
+                              int K, int N, void* stream) {
+  AXM_CHECK_ARG(x && w_packed && sb && y && M > 0 && N > 0 && K % 64 == 0, -1, "qmv_q8_g64: bad arguments");
+  int rc = launch_q8_gemv((const f16*)x, (const uint8_t*)w_packed, (const f16*)sb, (const f16*)bias, (f16*)y, M, K,
+                          N, nullptr, 0.f, (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("qmv_q8_g64");
+  return 0;
+}

@@ -1,0 +1,365 @@
+// Whole-model quantized decode runner (the MI355X counterpart of the
+// reference QuantizedDecodeGraphState, axiomlm/kernels/mps_kernels.mm:2982-3738).
+//
+// Per token and layer the step is five launches:
+//   1. QKV GEMV   : RMSNorm(x, ln1) prologue, RoPE + KV-slot write epilogue
+//   2. attention  : split-KV decode over the (fp16 | FP8 | INT4) cache (+ merge)
+//   3. O GEMV     : residual add epilogue (x += o)
+//   4. gate/up    : RMSNorm(x, ln2) prologue, SwiGLU epilogue over tile pairs
+//   5. down GEMV  : residual add epilogue (x += d)
+// followed by the lm_head GEMV with the final RMSNorm fused in.  Quantized KV
+// caches add one quantize-and-store launch after the QKV GEMV.
+//
+// Positions (rope position, write slot, active length) and the token id live
+// in a small device parameter block written by one tiny kernel before the
+// graph is replayed, so a single captured hipGraph serves every step; graphs
+// are cached per attention split count.
+#include <map>
+#include <vector>
+
+#include "axm.h"
+#include "kernels.h"
+
+namespace {
+
+enum { P_TOKEN = 0, P_ROPE = 1, P_WRITE = 2, P_ACTIVE = 3, P_COUNT = 4 };
+
+__global__ void set_params_kernel(int* params, const int64_t* idx_dev, int64_t tok_host, int rope_pos,
+                                  int write_pos, int active_len) {
+  if (threadIdx.x == 0) {
+    params[P_TOKEN] = (int)(idx_dev != nullptr ? idx_dev[0] : tok_host);
+    params[P_ROPE] = rope_pos;
+    params[P_WRITE] = write_pos;
+    params[P_ACTIVE] = active_len;
+  }
+}
+
+}  // namespace
+
+struct axm_runner {
+  axm_runner_desc d{};
+  std::vector<const void*> ln1, ln2, qkv_w, qkv_sb, qkv_b, o_w, o_sb, gu_w, gu_sb, dn_w, dn_sb;
+  std::vector<void*> kc, vc, ks, vs;
+  int q_dim = 0, kv_dim = 0, qkv_dim = 0;
+  // device buffers
+  int* params = nullptr;
+  f16* x = nullptr;
+  f16* q = nullptr;
+  f16* kvst = nullptr;
+  f16* attn_y = nullptr;
+  f16* hbuf = nullptr;
+  f16* logits = nullptr;
+  f16* norm = nullptr;
+  float* ws = nullptr;
+  size_t ws_bytes = 0;
+  int max_splits = 64;
+  bool use_graph = true;
+  hipStream_t cap_stream = nullptr;
+  std::map<int, hipGraphExec_t> graphs;
+
+  ~axm_runner() {
+    for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+    if (cap_stream) (void)hipStreamDestroy(cap_stream);
+    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws};
+    for (void* b : bufs)
+      if (b) (void)hipFree(b);
+  }
+
+  KvView kv_view(int layer) const {
+    KvView v{kc[layer], vc[layer], d.kv_dtype ? (f16*)ks[layer] : nullptr, d.kv_dtype ? (f16*)vs[layer] : nullptr,
+             d.kv_dtype, 1, d.n_kv_head, d.max_seq_len, d.head_dim};
+    return v;
+  }
+
+  // Enqueue the whole single-token step on stream s (no host synchronization).
+  int enqueue_step(int n_splits, hipStream_t s) {
+    const int D = d.d_model;
+    const int H = d.hidden_dim;
+    // Embedding gather of params[P_TOKEN].
+    if (d.wte_format == 0)
+      launch_embed_f16((const f16*)d.wte, nullptr, params + P_TOKEN, x, 1, D, d.vocab_size, s);
+    else
+      launch_embed_q8((const uint8_t*)d.wte, (const f16*)d.wte_sb, nullptr, params + P_TOKEN, x, 1, D, d.vocab_size, s);
+
+    for (int i = 0; i < d.n_layer; ++i) {
+      KvView kv = kv_view(i);
+      // 1. QKV with RMSNorm prologue and RoPE / KV-write epilogue.
+      Q4GemvArgs a{};
+      a.x = x;
+      a.ldx = D;
+      a.w = (const u32x4*)qkv_w[i];
+      a.sb = (const u32x4*)qkv_sb[i];
+      a.K = D;
+      a.KG = D / 64;
+      a.N = qkv_dim;
+      a.n_units = (qkv_dim + 7) / 8;
+      a.y = q;
+      a.ldy = q_dim;
+      a.bias = (const f16*)qkv_b[i];
+      a.ln_w = (const f16*)ln1[i];
+      a.eps = d.eps;
+      a.q_dim = q_dim;
+      a.kv_dim = kv_dim;
+      a.head_dim = d.head_dim;
+      a.freqs = d.freqs;
+      a.rope_len = d.rope_len;
+      a.rope_pos_dev = params + P_ROPE;
+      if (d.kv_dtype == AXM_KV_FP16) {
+        a.write_pos_dev = params + P_WRITE;
+        a.k_out = (f16*)kc[i];
+        a.v_out = (f16*)vc[i];
+        a.kv_stride_h = (long)d.max_seq_len * d.head_dim;
+        a.max_seq = d.max_seq_len;
+      } else {
+        // Stage fp16 k / v rows; the quantizer writes the cache slot.
+        a.write_pos = 0;
+        a.k_out = kvst;
+        a.v_out = kvst + kv_dim;
+        a.kv_stride_h = d.head_dim;
+        a.max_seq = 1;
+      }
+      int rc = q4m_gemv_launch(a, 1, Q4_EPI_QKV_ROPE, q4m_default_grid(a.n_units), s);
+      if (rc) return rc;
+      if (d.kv_dtype != AXM_KV_FP16)
+        launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
+      // 2. attention over slots [0, active_len).
+      rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
+      if (rc) return rc;
+      // 3. O projection, residual add into x.
+      Q4GemvArgs o{};
+      o.x = attn_y;
+      o.ldx = q_dim;
+      o.w = (const u32x4*)o_w[i];
+      o.sb = (const u32x4*)o_sb[i];
+      o.K = q_dim;
+      o.KG = q_dim / 64;
+      o.N = D;
+      o.n_units = (D + 7) / 8;
+      o.resid = x;
+      o.ldr = D;
+      rc = q4m_gemv_launch(o, 1, Q4_EPI_RESID, q4m_default_grid(o.n_units), s);
+      if (rc) return rc;
+      // 4. gate/up with RMSNorm prologue and SwiGLU epilogue.
+      Q4GemvArgs g{};
+      g.x = x;
+      g.ldx = D;
+      g.w = (const u32x4*)gu_w[i];
+      g.sb = (const u32x4*)gu_sb[i];
+      g.K = D;
+      g.KG = D / 64;
+      g.N = H;
+      g.n_units = (H + 7) / 8;
+      g.pair_offset = H / 8;
+      g.y = hbuf;
+      g.ldy = H;
+      g.ln_w = (const f16*)ln2[i];
+      g.eps = d.eps;
+      rc = q4m_gemv_launch(g, 1, Q4_EPI_SWIGLU, q4m_default_grid(g.n_units), s);
+      if (rc) return rc;
+      // 5. down projection, residual add.
+      Q4GemvArgs dn{};
+      dn.x = hbuf;
+      dn.ldx = H;
+      dn.w = (const u32x4*)dn_w[i];
+      dn.sb = (const u32x4*)dn_sb[i];
+      dn.K = H;
+      dn.KG = H / 64;
+      dn.N = D;
+      dn.n_units = (D + 7) / 8;
+      dn.resid = x;
+      dn.ldr = D;
+      rc = q4m_gemv_launch(dn, 1, Q4_EPI_RESID, q4m_default_grid(dn.n_units), s);
+      if (rc) return rc;
+    }
+    // Final RMSNorm + lm_head.
+    if (d.lm_head_format == 0) {
+      Q4GemvArgs l{};
+      l.x = x;
+      l.ldx = D;
+      l.w = (const u32x4*)d.lm_head_w;
+      l.sb = (const u32x4*)d.lm_head_sb;
+      l.K = D;
+      l.KG = D / 64;
+      l.N = d.vocab_size;
+      l.n_units = (d.vocab_size + 7) / 8;
+      l.y = logits;
+      l.ldy = d.vocab_size;
+      l.ln_w = (const f16*)d.lnf_w;
+      l.eps = d.eps;
+      l.x_norm_out = norm;
+      int rc = q4m_gemv_launch(l, 1, Q4_EPI_STORE, q4m_default_grid(l.n_units), s);
+      if (rc) return rc;
+    } else {
+      launch_rmsnorm(x, (const f16*)d.lnf_w, norm, 1, D, d.eps, s);
+      int rc = launch_q8_gemv(norm, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, 1, D,
+                              d.vocab_size, nullptr, 0.f, s);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+};
+
+static bool q4_shape_ok(int N, int K) { return N > 0 && K > 0 && K % 64 == 0; }
+
+extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out) {
+  AXM_CHECK_ARG(desc && out, -1, "runner_create: null argument");
+  const axm_runner_desc& d = *desc;
+  AXM_CHECK_ARG(d.n_layer >= 1 && d.n_head >= 1 && d.n_kv_head >= 1 && d.n_head % d.n_kv_head == 0, -1,
+                "runner_create: bad head configuration");
+  AXM_CHECK_ARG(d.head_dim == 64 || d.head_dim == 128, -1, "runner_create: head_dim %d must be 64 or 128",
+                d.head_dim);
+  AXM_CHECK_ARG(d.d_model == d.n_head * d.head_dim, -1, "runner_create: d_model != n_head * head_dim");
+  AXM_CHECK_ARG(q4_shape_ok(d.hidden_dim, d.d_model) && d.hidden_dim % 64 == 0 && d.hidden_dim % 8 == 0, -1,
+                "runner_create: hidden_dim %d must be a multiple of 64", d.hidden_dim);
+  AXM_CHECK_ARG(d.vocab_size > 0 && d.max_seq_len > 0 && d.rope_len > 0, -1, "runner_create: bad sizes");
+  AXM_CHECK_ARG(d.kv_dtype >= 0 && d.kv_dtype <= 2, -1, "runner_create: bad kv dtype");
+  AXM_CHECK_ARG(d.wte && d.lm_head_w && d.freqs && d.lnf_w, -1, "runner_create: null global weight");
+  AXM_CHECK_ARG(d.ln1_w && d.ln2_w && d.qkv_w && d.qkv_sb && d.o_w && d.o_sb && d.gu_w && d.gu_sb && d.down_w &&
+                    d.down_sb && d.k_cache && d.v_cache,
+                -1, "runner_create: null per-layer array");
+  AXM_CHECK_ARG(d.kv_dtype == AXM_KV_FP16 || (d.k_scales && d.v_scales), -1,
+                "runner_create: quantized KV cache needs scale arrays");
+  AXM_CHECK_ARG(d.lm_head_format == 0 || d.lm_head_format == 1, -1, "runner_create: bad lm_head format");
+  AXM_CHECK_ARG(d.lm_head_format == 1 || d.lm_head_sb, -1, "runner_create: lm_head scales missing");
+
+  axm_runner* r = new axm_runner();
+  r->d = d;
+  const int L = d.n_layer;
+  auto copy = [L](const void* const* src, std::vector<const void*>& dst, bool allow_null) {
+    dst.assign(L, nullptr);
+    if (!src) return allow_null;
+    for (int i = 0; i < L; ++i) {
+      dst[i] = src[i];
+      if (!dst[i] && !allow_null) return false;
+    }
+    return true;
+  };
+  bool ok = copy(d.ln1_w, r->ln1, false) && copy(d.ln2_w, r->ln2, false) && copy(d.qkv_w, r->qkv_w, false) &&
+            copy(d.qkv_sb, r->qkv_sb, false) && copy(d.qkv_bias, r->qkv_b, true) && copy(d.o_w, r->o_w, false) &&
+            copy(d.o_sb, r->o_sb, false) && copy(d.gu_w, r->gu_w, false) && copy(d.gu_sb, r->gu_sb, false) &&
+            copy(d.down_w, r->dn_w, false) && copy(d.down_sb, r->dn_sb, false);
+  if (!ok) {
+    delete r;
+    axm_set_error("runner_create: a per-layer weight pointer is null");
+    return -1;
+  }
+  r->kc.assign(d.k_cache, d.k_cache + L);
+  r->vc.assign(d.v_cache, d.v_cache + L);
+  if (d.kv_dtype != AXM_KV_FP16) {
+    r->ks.assign(d.k_scales, d.k_scales + L);
+    r->vs.assign(d.v_scales, d.v_scales + L);
+  } else {
+    r->ks.assign(L, nullptr);
+    r->vs.assign(L, nullptr);
+  }
+  r->d.max_tokens = d.max_tokens > 0 ? d.max_tokens : 1;
+  r->q_dim = d.n_head * d.head_dim;
+  r->kv_dim = d.n_kv_head * d.head_dim;
+  r->qkv_dim = r->q_dim + 2 * r->kv_dim;
+  const int T = r->d.max_tokens;
+  r->ws_bytes = attn_workspace_bytes(T, d.n_head, d.head_dim, r->max_splits);
+  struct {
+    void** p;
+    size_t bytes;
+  } allocs[] = {
+      {(void**)&r->params, 64 * sizeof(int)},
+      {(void**)&r->x, (size_t)T * d.d_model * sizeof(f16)},
+      {(void**)&r->q, (size_t)T * r->q_dim * sizeof(f16)},
+      {(void**)&r->kvst, (size_t)T * 2 * r->kv_dim * sizeof(f16)},
+      {(void**)&r->attn_y, (size_t)T * r->q_dim * sizeof(f16)},
+      {(void**)&r->hbuf, (size_t)T * d.hidden_dim * sizeof(f16)},
+      {(void**)&r->logits, (size_t)T * d.vocab_size * sizeof(f16)},
+      {(void**)&r->norm, (size_t)T * d.d_model * sizeof(f16)},
+      {(void**)&r->ws, r->ws_bytes > 0 ? r->ws_bytes : 256},
+  };
+  for (auto& al : allocs) {
+    if (hipMalloc(al.p, al.bytes) != hipSuccess) {
+      delete r;
+      axm_set_error("runner_create: hipMalloc of %zu bytes failed", al.bytes);
+      return -4;
+    }
+  }
+  if (hipMemset(r->params, 0, 64 * sizeof(int)) != hipSuccess ||
+      hipStreamCreateWithFlags(&r->cap_stream, hipStreamNonBlocking) != hipSuccess) {
+    delete r;
+    axm_set_error("runner_create: stream/memset setup failed");
+    return -4;
+  }
+  q4m_prepare_attributes();
+  *out = r;
+  return 0;
+}
+
+extern "C" void axm_runner_destroy(axm_runner_t r) { delete r; }
+
+extern "C" int axm_runner_set_graph(axm_runner_t r, int enable) {
+  AXM_CHECK_ARG(r, -1, "runner_set_graph: null runner");
+  r->use_graph = enable != 0;
+  return 0;
+}
+
+extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_host, int start_pos, int write_pos,
+                               int active_len, void* stream, void** logits_out) {
+  AXM_CHECK_ARG(r, -1, "runner_step: null runner");
+  const axm_runner_desc& d = r->d;
+  AXM_CHECK_ARG(write_pos >= 0 && write_pos < d.max_seq_len, -1, "runner_step: write_pos %d out of [0, %d)",
+                write_pos, d.max_seq_len);
+  AXM_CHECK_ARG(active_len >= 1 && active_len <= d.max_seq_len, -1, "runner_step: active_len %d out of [1, %d]",
+                active_len, d.max_seq_len);
+  AXM_CHECK_ARG(start_pos >= 0, -1, "runner_step: negative start_pos");
+  AXM_CHECK_ARG(idx_dev != nullptr || (tok_host >= 0 && tok_host < d.vocab_size), -1,
+                "runner_step: token id %lld out of range", (long long)tok_host);
+  hipStream_t s = (hipStream_t)stream;
+  const int rope_pos = start_pos % d.rope_len;
+  hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(64), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
+                     rope_pos, write_pos, active_len);
+  // Bucket the split count so that one graph covers a range of lengths.
+  int splits = attn_choose_splits(1, d.n_kv_head, active_len);
+  int bucket = 1;
+  while (bucket < splits) bucket <<= 1;
+  if (bucket > r->max_splits) bucket = r->max_splits;
+  if (!r->use_graph) {
+    int rc = r->enqueue_step(bucket, s);
+    if (rc) return rc;
+  } else {
+    auto it = r->graphs.find(bucket);
+    if (it == r->graphs.end()) {
+      hipGraph_t g = nullptr;
+      if (hipStreamBeginCapture(r->cap_stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        axm_set_error("runner_step: stream capture failed to start");
+        return -5;
+      }
+      int rc = r->enqueue_step(bucket, r->cap_stream);
+      hipError_t e = hipStreamEndCapture(r->cap_stream, &g);
+      if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+      }
+      if (e != hipSuccess) {
+        axm_set_error("runner_step: capture failed: %s", hipGetErrorString(e));
+        return -5;
+      }
+      hipGraphExec_t ge = nullptr;
+      e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (e != hipSuccess) {
+        axm_set_error("runner_step: graph instantiate failed: %s", hipGetErrorString(e));
+        return -5;
+      }
+      it = r->graphs.emplace(bucket, ge).first;
+    }
+    if (hipGraphLaunch(it->second, s) != hipSuccess) {
+      axm_set_error("runner_step: graph launch failed");
+      return -5;
+    }
+  }
+  AXM_LAUNCH_CHECK("runner_step");
+  if (logits_out) *logits_out = r->logits;
+  return 0;
+}
+
+extern "C" int axm_runner_last_norm(axm_runner_t r, void** norm_out) {
+  AXM_CHECK_ARG(r && norm_out, -1, "runner_last_norm: null argument");
+  *norm_out = r->norm;
+  return 0;
+}

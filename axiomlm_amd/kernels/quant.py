@@ -1,0 +1,255 @@
+"""Packed weight formats and quantized GEMV/GEMM entry points (MI355X).
+
+Drop-in mirror of ``axiomlm.kernels.quant`` (axiomlm/kernels/quant.py): same
+function names, argument meaning, packed layouts and return shapes.  Packers
+and products run as HIP kernels on the ROCm device; CPU inputs are moved to
+the current device, packed there and returned on the caller's device.  There
+is no CPU fallback: without libaxm.so every call raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+__all__ = [
+    "pack_linear_q4_marlin",
+    "dequantize_q4_marlin",
+    "qmv_q4_marlin",
+    "qmm_q4_marlin",
+    "pack_linear_q8_g64",
+    "dequantize_q8_g64",
+    "dequant_q8_rows",
+    "qmv_q8_g64",
+    "qmm_q8_g64",
+    "pack_linear_ternary",
+    "dequantize_ternary",
+    "pack_linear_q2_k",
+    "dequantize_q2_k",
+    "compute_quantization_metrics",
+]
+
+
+def _gpu_src(weight: torch.Tensor, what: str):
+    if weight.ndim != 2:
+        raise AssertionError(f"Expected 2D weight matrix, got shape {tuple(weight.shape)}")
+    N, K = weight.shape
+    if K % 64 != 0:
+        raise AssertionError(f"K ({K}) must be an exact multiple of group size 64")
+    dev = weight.device if weight.device.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
+    if not torch.cuda.is_available():
+        raise RuntimeError(f"{what}: no ROCm device available (the MI355X build has no CPU path)")
+    src = weight.detach().to(dev)
+    if src.dtype not in (torch.float16, torch.float32):
+        src = src.float()
+    return src.contiguous(), dev, int(N), int(K)
+
+
+# ---------------------------------------------------------------------------
+# MARLIN Q4  (quant.py:447-684)
+# ---------------------------------------------------------------------------
+def pack_linear_q4_marlin(
+    weight: torch.Tensor,
+    clip_search: bool = True,
+    col_importance: torch.Tensor | None = None,
+    grid_steps: int = 13,
+    min_shrink: float = 0.72,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(N, K) -> w_marlin int32 (ceil(N/8), K/64, 32, 2), sb_marlin fp16 (ceil(N/8), K/64, 8, 2).
+
+    clip_search=False and no importance: round-to-nearest (quant.py:482-494);
+    otherwise the importance-weighted MSE clip search (quant.py:495-571)."""
+    src, dev, N, K = _gpu_src(weight, "pack_linear_q4_marlin")
+    nt, KG = (N + 7) // 8, K // 64
+    w_m = torch.empty((nt, KG, 32, 2), dtype=torch.int32, device=dev)
+    sb_m = torch.empty((nt, KG, 8, 2), dtype=torch.float16, device=dev)
+    s = _lib.stream_of(dev)
+    is16 = int(src.dtype == torch.float16)
+    if not clip_search and col_importance is None:
+        _lib.check(_lib.lib().axm_pack_q4_marlin_rtn(_lib.ptr(src), is16, N, K, _lib.ptr(w_m), _lib.ptr(sb_m), s),
+                   "pack_linear_q4_marlin")
+    else:
+        imp = None
+        if col_importance is not None:
+            if col_importance.numel() != K:
+                raise AssertionError(f"Expected col_importance of length {K}, got {col_importance.numel()}")
+            imp = col_importance.detach().to(device=dev, dtype=torch.float32).reshape(K).contiguous()
+        # fp32 shrink grid exactly as torch.linspace produces it (quant.py:512)
+        alphas = torch.linspace(1.0, min_shrink, steps=max(2, grid_steps)).to(dev)
+        _lib.check(
+            _lib.lib().axm_pack_q4_marlin_mse(_lib.ptr(src), is16, N, K, _lib.ptr(imp), _lib.ptr(alphas),
+                                              int(alphas.numel()), _lib.ptr(w_m), _lib.ptr(sb_m), s),
+            "pack_linear_q4_marlin",
+        )
+    if weight.device.type != "cuda":
+        return w_m.to(weight.device), sb_m.to(weight.device)
+    return w_m, sb_m
+
+
+def dequantize_q4_marlin(w_marlin, sb_marlin, K: int, out_features: int | None = None) -> torch.Tensor:
+    """Packed MARLIN -> fp16 (N, K), quant.py:597-634."""
+    _lib.require_gpu(w_marlin, "dequantize_q4_marlin")
+    nt, KG = int(w_marlin.shape[0]), int(w_marlin.shape[1])
+    if KG * 64 != K:
+        raise AssertionError(f"Expected K={KG * 64}, got {K}")
+    N = nt * 8
+    out = torch.empty((N, K), dtype=torch.float16, device=w_marlin.device)
+    _lib.check(_lib.lib().axm_dequantize_q4_marlin(_lib.ptr(w_marlin.contiguous()), _lib.ptr(sb_marlin.contiguous()),
+                                                   _lib.ptr(out), K, N, _lib.stream_of(w_marlin.device)),
+               "dequantize_q4_marlin")
+    if out_features is not None and out_features < N:
+        out = out[:out_features]
+    return out
+
+
+def qmv_q4_marlin(x, w_marlin, sb_marlin, out_features: int | None = None, bias=None) -> torch.Tensor:
+    """y = x @ W^T (+ bias) for fp16 x (..., K); M > 1 rows are batched (quant.py:637-661)."""
+    _lib.require_gpu(x, "qmv_q4_marlin")
+    if x.dtype != torch.float16:
+        raise RuntimeError("qmv_q4_marlin: x must be float16")
+    K = x.size(-1)
+    M = x.numel() // K
+    nt, KG = int(w_marlin.shape[0]), int(w_marlin.shape[1])
+    if KG * 64 != K:
+        raise RuntimeError(f"qmv_q4_marlin: K={K} does not match packed K={KG * 64}")
+    N = nt * 8 if (out_features is None or out_features < 0) else int(out_features)
+    if N > nt * 8:
+        raise RuntimeError(f"qmv_q4_marlin: out_features={N} exceeds packed rows {nt * 8}")
+    xc = x.contiguous()
+    y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
+    b = None
+    if bias is not None:
+        b = bias.to(device=x.device, dtype=torch.float16).contiguous()
+    _lib.check(_lib.lib().axm_qmv_q4_marlin(_lib.ptr(xc), _lib.ptr(w_marlin.contiguous()),
+                                            _lib.ptr(sb_marlin.contiguous()), _lib.ptr(b), _lib.ptr(y), M, K, N,
+                                            _lib.stream_of(x.device)),
+               "qmv_q4_marlin")
+    return y
+
+
+def qmm_q4_marlin(x, w_marlin, sb_marlin, out_features: int | None = None, bias=None) -> torch.Tensor:
+    """Batched form of :func:`qmv_q4_marlin` (quant.py:664-684)."""
+    return qmv_q4_marlin(x, w_marlin, sb_marlin, out_features, bias)
+
+
+# ---------------------------------------------------------------------------
+# Q8_G64  (quant.py:72-233)
+# ---------------------------------------------------------------------------
+def pack_linear_q8_g64(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(N, K) -> packed int32 (N, K/4) (little-endian bytes), scales_biases fp16 (N, K/64, 2)."""
+    src, dev, N, K = _gpu_src(weight, "pack_linear_q8_g64")
+    packed = torch.empty((N, K // 4), dtype=torch.int32, device=dev)
+    sb = torch.empty((N, K // 64, 2), dtype=torch.float16, device=dev)
+    _lib.check(_lib.lib().axm_pack_q8_g64(_lib.ptr(src), int(src.dtype == torch.float16), N, K, _lib.ptr(packed),
+                                          _lib.ptr(sb), _lib.stream_of(dev)),
+               "pack_linear_q8_g64")
+    if weight.device.type != "cuda":
+        return packed.to(weight.device), sb.to(weight.device)
+    return packed, sb
+
+
+def dequantize_q8_g64(w_packed, scales_biases, K: int) -> torch.Tensor:
+    """fp16(q * scale + bias) in fp32 (quant.py:114-129)."""
+    N = w_packed.shape[0]
+    q = w_packed.contiguous().view(torch.uint8).view(N, K // 64, 64).float()
+    sb = scales_biases.float()
+    return (q * sb[..., 0:1] + sb[..., 1:2]).view(N, K).to(torch.float16)
+
+
+def dequant_q8_rows(indices, w_packed, scales_biases) -> torch.Tensor:
+    """Gather + dequantize token rows (quant.py:132-163) with the HIP gather kernel."""
+    _lib.require_gpu(w_packed, "dequant_q8_rows")
+    K = w_packed.shape[1] * 4
+    flat = indices.reshape(-1).to(device=w_packed.device, dtype=torch.int64).contiguous()
+    out = torch.empty((flat.numel(), K), dtype=torch.float16, device=w_packed.device)
+    _lib.check(_lib.lib().axm_embed_q8_g64(_lib.ptr(w_packed.contiguous()), _lib.ptr(scales_biases.contiguous()),
+                                           _lib.ptr(flat), _lib.ptr(out), int(flat.numel()), K,
+                                           int(w_packed.shape[0]), _lib.stream_of(w_packed.device)),
+               "dequant_q8_rows")
+    return out.view(*indices.shape, K)
+
+
+def qmv_q8_g64(x, w_packed, scales_biases) -> torch.Tensor:
+    """y = x @ W^T with Q8_G64 weights (quant.py:201-218)."""
+    _lib.require_gpu(x, "qmv_q8_g64")
+    K = x.size(-1)
+    M = x.numel() // K
+    N = w_packed.shape[0]
+    y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
+    _lib.check(_lib.lib().axm_qmv_q8_g64(_lib.ptr(x.contiguous()), _lib.ptr(w_packed.contiguous()),
+                                         _lib.ptr(scales_biases.contiguous()), None, _lib.ptr(y), M, K, N,
+                                         _lib.stream_of(x.device)),
+               "qmv_q8_g64")
+    return y
+
+
+def qmm_q8_g64(x, w_packed, scales_biases) -> torch.Tensor:
+    return qmv_q8_g64(x, w_packed, scales_biases)
+
+
+# ---------------------------------------------------------------------------
+# Ternary / reference Q2_K packers  (quant.py:236-403)
+# ---------------------------------------------------------------------------
+def pack_linear_ternary(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(N, K) -> packed uint8 (N, K/4), scales fp16 (N, K/64)."""
+    src, dev, N, K = _gpu_src(weight, "pack_linear_ternary")
+    packed = torch.empty((N, K // 4), dtype=torch.uint8, device=dev)
+    scales = torch.empty((N, K // 64), dtype=torch.float16, device=dev)
+    _lib.check(_lib.lib().axm_pack_ternary(_lib.ptr(src), int(src.dtype == torch.float16), N, K, _lib.ptr(packed),
+                                           _lib.ptr(scales), _lib.stream_of(dev)),
+               "pack_linear_ternary")
+    if weight.device.type != "cuda":
+        return packed.to(weight.device), scales.to(weight.device)
+    return packed, scales
+
+
+def dequantize_ternary(w_packed, scales, K: int | None = None) -> torch.Tensor:
+    N = w_packed.shape[0]
+    K = K or w_packed.shape[1] * 4
+    b = w_packed.unsqueeze(-1).to(torch.int32)
+    shifts = torch.arange(4, device=w_packed.device, dtype=torch.int32) * 2
+    q = ((b >> shifts) & 1) - ((b >> (shifts + 1)) & 1)
+    q = q.view(N, K // 64, 64).to(scales.dtype)
+    return (q * scales.unsqueeze(-1)).view(N, K).to(torch.float16)
+
+
+def pack_linear_q2_k(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(N, K) -> packed uint8 (N, K/4), scales_biases fp16 (N, K/64, 2)."""
+    src, dev, N, K = _gpu_src(weight, "pack_linear_q2_k")
+    packed = torch.empty((N, K // 4), dtype=torch.uint8, device=dev)
+    sb = torch.empty((N, K // 64, 2), dtype=torch.float16, device=dev)
+    _lib.check(_lib.lib().axm_pack_q2_k(_lib.ptr(src), int(src.dtype == torch.float16), N, K, _lib.ptr(packed),
+                                        _lib.ptr(sb), _lib.stream_of(dev)),
+               "pack_linear_q2_k")
+    if weight.device.type != "cuda":
+        return packed.to(weight.device), sb.to(weight.device)
+    return packed, sb
+
+
+def dequantize_q2_k(w_packed, scales_biases, K: int | None = None) -> torch.Tensor:
+    N = w_packed.shape[0]
+    K = K or w_packed.shape[1] * 4
+    b = w_packed.unsqueeze(-1).to(torch.int32)
+    shifts = torch.arange(4, device=w_packed.device, dtype=torch.int32) * 2
+    q = ((b >> shifts) & 3).view(N, K // 64, 64).to(scales_biases.dtype)
+    return (q * scales_biases[..., 0:1] + scales_biases[..., 1:2]).view(N, K).to(torch.float16)
+
+
+def compute_quantization_metrics(orig, dequant, quant_bytes: int | None = None) -> dict:
+    """SQNR / cosine / MSE / L_inf / compression ratio (quant.py:855-893)."""
+    o = orig.flatten().float()
+    d = dequant.flatten().float()
+    noise = o - d
+    sig = o.pow(2).sum()
+    npow = noise.pow(2).sum().clamp(min=1e-12)
+    ob = orig.numel() * orig.element_size()
+    return {
+        "sqnr_db": float(10.0 * torch.log10(sig / npow)),
+        "cosine_similarity": float(torch.cosine_similarity(o, d, dim=0)),
+        "mse": float(noise.pow(2).mean()),
+        "max_abs_error": float(noise.abs().max()),
+        "orig_bytes": ob,
+        "quant_bytes": quant_bytes or ob,
+        "compression_ratio": float(ob) / float(quant_bytes) if quant_bytes else 1.0,
+    }

@@ -1,0 +1,181 @@
+"""QuantizedDecodeRunner: the MPSQuantizedDecodeRunner interface on MI355X.
+
+Constructor arguments and methods follow the reference pybind class
+(axiomlm/kernels/mps_kernels.mm:4373-4461, state at :2982-3738):
+
+    QuantizedDecodeRunner(wte_emb, lmh_packed, lmh_sb, freqs_r, ln1_ws, c_attn_p, c_attn_s,
+                          c_proj_p, c_proj_s, ln2_ws, gate_up_p, gate_up_s, w_down_p, w_down_s,
+                          lnf_w, k_cs, v_cs, n_h, n_kvh, hd, use_q4, epsilon,
+                          c_attn_bs=[], vocab_sz=-1, wte_p=None, wte_s=None,
+                          k_scales=None, v_scales=None, kv_dtype="fp16")
+
+Formats are detected from the packed tensors as the reference does
+(mps_kernels.mm:3055-3068, 3149-3157): a 4-D lm_head is MARLIN Q4, a 2-D int32
+one is Q8_G64; a 2-D int32 ``wte_p`` selects the Q8 embedding gather.  The
+last three keyword arguments are this build's addition: quantized (FP8 / INT4)
+KV caches inside the captured step.
+
+The runner holds references to every tensor it was given (weights and the
+caller's KV cache views); ``step`` returns a view of a persistent logits
+buffer that is overwritten by the next call, like the reference.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .kernels.ops import KV_CODES
+
+
+def _arr(ptrs):
+    a = (ctypes.c_void_p * len(ptrs))()
+    for i, p in enumerate(ptrs):
+        a[i] = p
+    return a
+
+
+def _p(t):
+    return None if t is None or (isinstance(t, torch.Tensor) and t.numel() == 0) else t.data_ptr()
+
+
+class QuantizedDecodeRunner:
+    def __init__(self, wte_emb, lmh_packed, lmh_sb, freqs_r, ln1_ws, c_attn_p, c_attn_s, c_proj_p, c_proj_s,
+                 ln2_ws, gate_up_p, gate_up_s, w_down_p, w_down_s, lnf_w, k_cs, v_cs, n_h, n_kvh, hd, use_q4,
+                 epsilon, c_attn_bs=(), vocab_sz=-1, wte_p=None, wte_s=None, k_scales=None, v_scales=None,
+                 kv_dtype="fp16", max_tokens: int = 1):
+        L = len(ln1_ws)
+        if not use_q4 or c_attn_p[0].dim() != 4:
+            raise RuntimeError("QuantizedDecodeRunner on MI355X supports MARLIN Q4 layer weights")
+        dev = lmh_packed.device
+        _lib.require_gpu(lmh_packed, "QuantizedDecodeRunner")
+        h16 = lambda t: t.to(device=dev, dtype=torch.float16).contiguous()  # noqa: E731
+        self._keep = []  # tensors whose storage the native runner points to
+
+        def keep(t):
+            if t is not None:
+                self._keep.append(t)
+            return t
+
+        ln1 = [keep(h16(w)) for w in ln1_ws]
+        ln2 = [keep(h16(w)) for w in ln2_ws]
+        lnf = keep(h16(lnf_w))
+        freqs = keep(freqs_r.to(device=dev, dtype=torch.float32).contiguous())
+        mats = [c_attn_p, c_attn_s, c_proj_p, c_proj_s, gate_up_p, gate_up_s, w_down_p, w_down_s]
+        mats = [[keep(t.contiguous()) for t in m] for m in mats]
+        biases = [keep(h16(b)) if (b is not None and b.numel() > 0) else None for b in (c_attn_bs or [])]
+        biases = biases + [None] * (L - len(biases))
+
+        if wte_p is not None and wte_p.numel() > 0 and wte_p.dim() == 2:
+            wte_fmt, wte, wte_sb = 1, keep(wte_p.contiguous()), keep(wte_s.contiguous())
+        elif wte_emb is not None and wte_emb.dtype == torch.int32 and wte_emb.dim() == 2:
+            wte_fmt, wte, wte_sb = 1, keep(wte_emb.contiguous()), keep(lmh_sb.contiguous())
+        else:
+            wte_fmt, wte, wte_sb = 0, keep(h16(wte_emb)), None
+        lmh_fmt = 0 if lmh_packed.dim() == 4 else 1
+        lmh = keep(lmh_packed.contiguous())
+        lmh_s = keep(lmh_sb.contiguous())
+        if vocab_sz is None or vocab_sz <= 0:
+            vocab_sz = wte.shape[0] if lmh_fmt == 0 else lmh_packed.shape[0]
+        self.vocab_size = int(vocab_sz)
+        self.d_model = int(n_h * hd)
+        self.hidden_dim = int(w_down_s[0].shape[1] * 64)
+        kv_code = KV_CODES[kv_dtype]
+        self.kv_dtype = kv_dtype
+        self.max_seq_len = int(k_cs[0].shape[-2])
+
+        def first_batch(t):
+            return keep(t[0] if t.dim() == 4 else t)
+
+        kcs = [first_batch(t) for t in k_cs]
+        vcs = [first_batch(t) for t in v_cs]
+        kss = [first_batch(t) for t in k_scales] if kv_code else [None] * L
+        vss = [first_batch(t) for t in v_scales] if kv_code else [None] * L
+
+        self._arrays = [
+            _arr([_p(t) for t in ln1]), _arr([_p(t) for t in ln2]),
+            *[_arr([_p(t) for t in m]) for m in mats],
+            _arr([_p(b) for b in biases]),
+            _arr([_p(t) for t in kcs]), _arr([_p(t) for t in vcs]),
+            _arr([_p(t) for t in kss]), _arr([_p(t) for t in vss]),
+        ]
+        a = self._arrays
+        d = _lib.RunnerDesc()
+        d.n_layer, d.n_head, d.n_kv_head, d.head_dim = L, int(n_h), int(n_kvh), int(hd)
+        d.d_model, d.hidden_dim, d.vocab_size = self.d_model, self.hidden_dim, self.vocab_size
+        d.max_seq_len, d.rope_len = self.max_seq_len, int(freqs.shape[0])
+        d.eps, d.kv_dtype = float(epsilon), kv_code
+        d.wte_format, d.wte, d.wte_sb = wte_fmt, _p(wte), _p(wte_sb)
+        d.lm_head_format, d.lm_head_w, d.lm_head_sb = lmh_fmt, _p(lmh), _p(lmh_s)
+        d.freqs, d.lnf_w = _p(freqs), _p(lnf)
+        cv = ctypes.cast
+        P = ctypes.POINTER(ctypes.c_void_p)
+        d.ln1_w, d.ln2_w = cv(a[0], P), cv(a[1], P)
+        d.qkv_w, d.qkv_sb, d.o_w, d.o_sb = cv(a[2], P), cv(a[3], P), cv(a[4], P), cv(a[5], P)
+        d.gu_w, d.gu_sb, d.down_w, d.down_sb = cv(a[6], P), cv(a[7], P), cv(a[8], P), cv(a[9], P)
+        d.qkv_bias = cv(a[10], P)
+        d.k_cache, d.v_cache = cv(a[11], P), cv(a[12], P)
+        d.k_scales, d.v_scales = (cv(a[13], P), cv(a[14], P)) if kv_code else (None, None)
+        d.max_tokens = int(max_tokens)
+        self._desc = d
+        h = ctypes.c_void_p()
+        with torch.cuda.device(dev):
+            _lib.check(_lib.lib().axm_runner_create(ctypes.byref(d), ctypes.byref(h)), "QuantizedDecodeRunner")
+        self._h = h
+        self.device = dev
+        self._logits = None
+        self._norm = None
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                torch.cuda.synchronize(self.device)
+            except Exception:
+                pass
+            _lib.lib().axm_runner_destroy(h)
+            self._h = None
+
+    def set_graph(self, enable: bool) -> None:
+        _lib.check(_lib.lib().axm_runner_set_graph(self._h, int(bool(enable))), "set_graph")
+
+    def step(self, idx, start_pos: int, write_pos: int, active_len: int) -> torch.Tensor:
+        """One decode token -> logits (1, 1, V) (mps_kernels.mm:3195-3263)."""
+        out = ctypes.c_void_p()
+        if isinstance(idx, torch.Tensor) and idx.device.type == "cuda":
+            t = idx.reshape(-1)[:1].to(torch.int64)
+            rc = _lib.lib().axm_runner_step(self._h, _lib.ptr(t), 0, int(start_pos), int(write_pos),
+                                            int(active_len), _lib.stream_of(self.device), ctypes.byref(out))
+        else:
+            tok = int(idx.reshape(-1)[0]) if isinstance(idx, torch.Tensor) else int(idx)
+            rc = _lib.lib().axm_runner_step(self._h, None, tok, int(start_pos), int(write_pos), int(active_len),
+                                            _lib.stream_of(self.device), ctypes.byref(out))
+        _lib.check(rc, "QuantizedDecodeRunner.step")
+        if self._logits is None:
+            self._logits = _RawBuffer.view(out.value, self.vocab_size, self.device).view(1, 1, self.vocab_size)
+        return self._logits
+
+    def get_last_norm(self, T: int = 1) -> torch.Tensor:
+        """Clone of the final normalized hidden state (mps_kernels.mm:3732-3737)."""
+        p = ctypes.c_void_p()
+        _lib.check(_lib.lib().axm_runner_last_norm(self._h, ctypes.byref(p)), "get_last_norm")
+        return _RawBuffer.view(p.value, T * self.d_model, self.device).view(1, T, self.d_model).clone()
+
+
+class _RawBuffer:
+    """fp16 torch view of device memory owned by the native runner."""
+
+    @staticmethod
+    def view(ptr_value: int, numel: int, device) -> torch.Tensor:
+        class _Cai:
+            __cuda_array_interface__ = {
+                "shape": (numel,),
+                "typestr": "<f2",
+                "data": (ptr_value, False),
+                "version": 3,
+                "strides": None,
+            }
+
+        return torch.as_tensor(_Cai(), device=device)

@@ -1,0 +1,176 @@
+/*
+ * axm.h -- C ABI of libaxm.so, the MI355X (gfx950) implementation of the
+ * AxiomLM quantized decode step.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream); all
+ *     calls are asynchronous with respect to the host and never synchronize.
+ *   - Return value 0 = success, negative = error; axm_last_error() returns the
+ *     message of the last failure on the calling thread.
+ *   - Activations and KV values are fp16 (IEEE binary16), accumulation fp32.
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the AxiomLM source tree).
+ */
+#ifndef AXM_H_
+#define AXM_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- library ------------------------------------------------------------ */
+const char* axm_last_error(void);
+int axm_version(void);
+
+/* ---- MARLIN Q4 (group 64, fp16 scale + bias) ------------------------------
+ * w_marlin: int32 [ceil(N/8)][K/64][32][2], sb_marlin: fp16 [ceil(N/8)][K/64][8][2]
+ * x: fp16 [M][K], y: fp16 [M][N], bias: fp16 [N] or NULL.
+ * Replaces qmv_q4_marlin_mps / qmm_q4_marlin_mps
+ *   (axiomlm/kernels/mps_kernels.mm:1272-1396, bound in the pybind module at
+ *    :4302-4641; Python entry axiomlm/kernels/quant.py:637-684). */
+int axm_qmv_q4_marlin(const void* x, const void* w_marlin, const void* sb_marlin, const void* bias, void* y, int M,
+                      int K, int N, void* stream);
+/* Row-major fp16 [N][K] dequantization (axiomlm/kernels/quant.py:597-634). */
+int axm_dequantize_q4_marlin(const void* w_marlin, const void* sb_marlin, void* out, int K, int N, void* stream);
+/* Round-to-nearest packer, clip_search=False (axiomlm/kernels/quant.py:447-494, 573-593).
+ * w: fp16 (src_is_fp16=1) or fp32 [N][K]. */
+int axm_pack_q4_marlin_rtn(const void* w, int src_is_fp16, int N, int K, void* w_marlin, void* sb_marlin,
+                           void* stream);
+/* Importance-weighted MSE clip-search packer, clip_search=True (quant.py:495-571).
+ * col_importance: fp32 [K] or NULL; alphas: fp32 [n_alpha] (device) shrink grid. */
+int axm_pack_q4_marlin_mse(const void* w, int src_is_fp16, int N, int K, const float* col_importance,
+                           const float* alphas, int n_alpha, void* w_marlin, void* sb_marlin, void* stream);
+
+/* ---- Q8_G64 ------------------------------------------------------------- *
+ * w: uint8 [N][K] (the int32 [N][K/4] little-endian view), sb: fp16 [N][K/64][2].
+ * Replaces qmv_q8_g64_mps / qmm_q8_g64_mps (mps_kernels.mm:2122-2170; quant.py:201-233). */
+int axm_qmv_q8_g64(const void* x, const void* w_packed, const void* sb, const void* bias, void* y, int M, int K,
+                   int N, void* stream);
+/* Q8_G64 packer (quant.py:72-111): w fp16/fp32 [N][K] -> uint8 [N][K] + sb fp16 [N][K/64][2]. */
+int axm_pack_q8_g64(const void* w, int src_is_fp16, int N, int K, void* packed_u8, void* sb, void* stream);
+/* Token-row gather + dequantization, dequant_q8_rows (quant.py:132-163) /
+ * embed_q8_g64_gather_half_kernel (metal_kernels.metal:357-391). tokens: int64 [T]; ids outside
+ * [0, V) give zero rows. */
+int axm_embed_q8_g64(const void* w_packed, const void* sb, const void* tokens_i64, void* out, int T, int D, int V,
+                     void* stream);
+
+/* ---- BitNet 1.58 ternary and reference "Q2_K" (affine 2-bit), group 64 ----
+ * codes: uint8 [N][K/4], element 4b+j at bits 2j.  Ternary code 1 -> +1, 2 -> -1,
+ * 0 -> 0 with fp16 scales [N][K/64]; Q2 codes q in [0,3] with sb fp16 [N][K/64][2].
+ * Packers: pack_linear_ternary (quant.py:236-276), pack_linear_q2_k (quant.py:339-378). */
+int axm_pack_ternary(const void* w, int src_is_fp16, int N, int K, void* packed_u8, void* scales, void* stream);
+int axm_pack_q2_k(const void* w, int src_is_fp16, int N, int K, void* packed_u8, void* sb, void* stream);
+
+/* ---- norms / activations / argmax ---------------------------------------- */
+/* rmsnorm_infer_mps (mps_kernels.mm:247-266; math of axiomlm/models/modules.py:41-43). */
+int axm_rmsnorm(const void* x, const void* w, void* y, int rows, int D, float eps, void* stream);
+/* add_rmsnorm_infer_mps: x += r; y = rmsnorm(x) (mps_kernels.mm:405-425). */
+int axm_add_rmsnorm(void* x, const void* r, const void* w, void* y, int rows, int D, float eps, void* stream);
+/* swiglu_gate_up_mps: y = silu(g) * u over [g || u] rows (mps_kernels.mm:434-450). */
+int axm_swiglu_gate_up(const void* gu, void* y, int rows, int H, void* stream);
+/* argmax_last_token_mps / argmax_multi (mps_kernels.mm:292-366): lowest index wins ties. */
+int axm_argmax(const void* logits, int rows, int V, void* out_i64, void* stream);
+
+/* ---- KV cache and attention ---------------------------------------------- *
+ * kv_dtype: 0 = fp16, 1 = FP8 E4M3FN, 2 = INT4 (symmetric, group 64).
+ * Cache layouts: fp16/fp8 [B][Hkv][S][hd], int4 [B][Hkv][S][hd/2], scales fp16 [B][Hkv][S][hd/64]
+ * (axiomlm/engine/paged_cache.py:158-198). */
+#define AXM_KV_FP16 0
+#define AXM_KV_FP8 1
+#define AXM_KV_INT4 2
+
+/* Quantize (per 64-element group) and store T rows of k and v at slots
+ * (write_pos + t) % S of batch 0.  Replaces the cache write of
+ * rope_kv_cache_write{,_fp8,_int4}_mps (mps_kernels.mm:589-681, 817-929) with the
+ * CPU quantizer semantics of quantize_kv_fp8 / quantize_kv_int4 (quant.py:692-807). */
+int axm_kv_cache_write(const void* k_rows, const void* v_rows, int ld_rows, int T, void* k_cache, void* v_cache,
+                       void* k_scales, void* v_scales, int kv_dtype, int n_kv_head, int head_dim, int max_seq_len,
+                       int write_pos, void* stream);
+
+/* Split-KV GQA decode attention: q fp16 [B][Hq][hd] -> out fp16 [B][Hq][hd] over
+ * slots [0, active_len).  num_splits <= 0 picks a split count
+ * (axm_attention_num_splits).  workspace >= axm_attention_workspace_bytes().
+ * Replaces gqa_flash_decode{,_fp8,_int4}_mps (mps_kernels.mm:1399-1506, 1672-1906,
+ * 2040-2120; Python entry axiomlm/kernels/ops.py:552-654). */
+int axm_attention_num_splits(int B, int n_kv_head, int active_len);
+size_t axm_attention_workspace_bytes(int B, int n_query_rows_per_batch, int head_dim, int n_splits);
+int axm_gqa_flash_decode(const void* q, const void* k_cache, const void* v_cache, const void* k_scales,
+                         const void* v_scales, int kv_dtype, void* out, int B, int n_head, int n_kv_head,
+                         int head_dim, int max_seq_len, int active_len, int num_splits, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* Bitmask tree-verification attention (batch 0): q fp16 [T][Hq][hd], T <= 64,
+ * masks uint64 [T] (device) ancestor bitmasks.  Prefix slots [0, prefix_len)
+ * are visible to every node; node j lives at slot (write_pos + j) % S.
+ * workspace >= axm_attention_workspace_bytes(T, Hq, hd, num_splits).
+ * Replaces gqa_tree_verify{,_fp8,_int4}_mps (mps_kernels.mm:1508-1631, 1908-2038,
+ * 4111-4249; Python entry axiomlm/kernels/ops.py:657-797); masks are widened
+ * from uint32 (T <= 32) to uint64 (T <= 64). */
+int axm_gqa_tree_verify(const void* q, const void* k_cache, const void* v_cache, const void* k_scales,
+                        const void* v_scales, int kv_dtype, void* out, int T, int n_head, int n_kv_head,
+                        int head_dim, int max_seq_len, int prefix_len, int write_pos, const void* masks_u64_dev,
+                        int num_splits, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- whole-model decode runner ------------------------------------------- *
+ * Replaces MPSQuantizedDecodeRunner (QuantizedDecodeGraphState,
+ * mps_kernels.mm:2982-3738, bound at :4373-4461).  The runner keeps pointers to
+ * the caller's packed weights and KV cache (it never frees them), owns its
+ * activation buffers, and replays the whole step as one hipGraph. */
+typedef struct axm_runner_desc {
+  int n_layer, n_head, n_kv_head, head_dim, d_model, hidden_dim, vocab_size;
+  int max_seq_len; /* KV slots S */
+  int rope_len;    /* rows of freqs */
+  float eps;
+  int kv_dtype;       /* AXM_KV_* */
+  int wte_format;     /* 0: fp16 table [V][d]; 1: Q8_G64 (uint8 [V][d] + sb [V][d/64][2]) */
+  const void* wte;
+  const void* wte_sb;
+  int lm_head_format; /* 0: MARLIN Q4; 1: Q8_G64 */
+  const void* lm_head_w;
+  const void* lm_head_sb;
+  const float* freqs; /* [rope_len][head_dim/2][2] (cos, sin) */
+  const void* lnf_w;  /* fp16 [d] */
+  /* per-layer arrays (host arrays of device pointers), length n_layer */
+  const void* const* ln1_w;
+  const void* const* ln2_w;
+  const void* const* qkv_w;
+  const void* const* qkv_sb;
+  const void* const* qkv_bias; /* entries may be NULL; the array itself may be NULL */
+  const void* const* o_w;
+  const void* const* o_sb;
+  const void* const* gu_w; /* rows [gate; up] */
+  const void* const* gu_sb;
+  const void* const* down_w;
+  const void* const* down_sb;
+  void* const* k_cache; /* per layer, batch-1 views [Hkv][S][hd or hd/2] */
+  void* const* v_cache;
+  void* const* k_scales; /* quantized caches only */
+  void* const* v_scales;
+  int max_tokens; /* capacity of the multi-token (verify) paths, <= 64 */
+} axm_runner_desc;
+
+typedef struct axm_runner* axm_runner_t;
+
+int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out);
+void axm_runner_destroy(axm_runner_t r);
+/* One decode token.  The token id comes from idx_dev (int64, device) when
+ * non-NULL, otherwise from tok_host.  Positions follow transformer.py:1453-1462.
+ * *logits_out receives the runner's persistent fp16 [V] buffer (valid until the
+ * next call).  Replaces QuantizedDecodeGraphState::step (mps_kernels.mm:3195-3263). */
+int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_host, int start_pos, int write_pos,
+                    int active_len, void* stream, void** logits_out);
+/* Normalized final hidden state of the last call (fp16 [T][d]),
+ * get_last_norm (mps_kernels.mm:3732-3737). */
+int axm_runner_last_norm(axm_runner_t r, void** norm_out);
+/* 1 = replay the step as a captured hipGraph (default), 0 = eager launches. */
+int axm_runner_set_graph(axm_runner_t r, int enable);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AXM_H_ */

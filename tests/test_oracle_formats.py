@@ -1,0 +1,230 @@
+"""Pins the numpy oracle's formats against the reference's own known-answer tests,
+closed forms, invariants and (for torch-defined arithmetic) torch itself.
+
+CPU only.  Reference citations are paths in the AxiomLM source tree.
+"""
+
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as fm
+
+F16, F32 = np.float16, np.float32
+
+
+def test_marlin_magic_nibble_kat():
+    # tests/test_phase1_task11_disassembly.py:71-98: (n | 0x6400) - 1024 == n, ((n << 4) | 0x5400) - 64 == n
+    for n in range(16):
+        lo = struct.unpack("e", struct.pack("<H", n | 0x6400))[0] - 1024.0
+        hi = struct.unpack("e", struct.pack("<H", (n << 4) | 0x5400))[0] - 64.0
+        assert lo == n and hi == n
+
+
+def test_marlin_lane_maps_match_kernel_equations():
+    # quant.py:573-576 vs the kernel's lane decode (metal_kernels.metal:2159-2161): every (r, c0) pair
+    # with c0 in {0,2,4,6} and r in 0..7 appears exactly once over the 32 lanes.
+    r, c0 = fm.marlin_lane_maps()
+    pairs = set(zip(r.tolist(), c0.tolist()))
+    assert len(pairs) == 32
+    assert pairs == {(rr, cc) for rr in range(8) for cc in (0, 2, 4, 6)}
+    # explicit spot values
+    assert (r[0], c0[0]) == (0, 0) and (r[1], c0[1]) == (0, 2) and (r[2], c0[2]) == (1, 0)
+    assert (r[8], c0[8]) == (0, 4) and (r[16], c0[16]) == (4, 0) and (r[31], c0[31]) == (7, 6)
+
+
+def _hand_marlin_code(w_marlin, row, k):
+    """Read the code of (row, k) straight from the bit equations of the layout."""
+    r_map, c0_map = fm.marlin_lane_maps()
+    tile, c = divmod(row, 8)
+    g, kk = divmod(k, 64)
+    j, rest = divmod(kk, 32)
+    s, r = divmod(rest, 8)
+    lane = [l for l in range(32) if r_map[l] == r and c0_map[l] in (c, c - 1) and c0_map[l] % 2 == 0][0]
+    half = c - c0_map[lane]
+    word = int(w_marlin.view(np.uint32)[tile, g, lane, j])
+    return (word >> (16 * half + 4 * s)) & 0xF
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (13, 192), (8, 704)])
+def test_marlin_pack_unpack_bit_equations(N, K):
+    rng = np.random.default_rng(N * 1000 + K)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(F16)
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    assert wm.shape == ((N + 7) // 8, K // 64, 32, 2) and wm.dtype == np.int32
+    assert sb.shape == ((N + 7) // 8, K // 64, 8, 2) and sb.dtype == F16
+    codes = fm.unpack_marlin_codes(wm)
+    for _ in range(200):
+        row, k = int(rng.integers(0, N)), int(rng.integers(0, K))
+        assert codes[row, k] == _hand_marlin_code(wm, row, k)
+
+
+@pytest.mark.parametrize("src", [F16, F32])
+def test_rtn_marlin_equals_q4_g64(src):
+    # Reference invariant (quant.py:462-463): RTN MARLIN is bit-for-bit the Q4_G64 quantization.
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((40, 256)) * 0.05).astype(src)
+    wm, sbm = fm.pack_linear_q4_marlin(w, clip_search=False)
+    wq, sbq = fm.pack_linear_q4_g64(w)
+    a = fm.dequantize_q4_marlin(wm, sbm, 256, out_features=40)
+    b = fm.dequantize_q4_g64(wq, sbq, 256)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+def test_rtn_codes_are_nearest_lattice_points():
+    # Brute force: each RTN code minimizes |w - (q*s + b)| over q in 0..15 (ties resolved to even).
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((8, 64)) * 0.03).astype(F32)
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    codes = fm.unpack_marlin_codes(wm)[:8].astype(np.int64)
+    s = sb[0, 0, :, 0].astype(F32)[:, None]
+    b = sb[0, 0, :, 1].astype(F32)[:, None]
+    err = np.abs((w[..., None] - b[..., None]) / s[..., None] - np.arange(16, dtype=F32))
+    best = err.argmin(-1)
+    # where the exact quotient is not a .5 tie the brute-force minimizer must match
+    frac = np.abs(((w - b) / s) % 1.0 - 0.5)
+    ok = frac > 1e-4
+    inside = ((w - b) / s >= -0.5) & ((w - b) / s <= 15.5)
+    assert np.array_equal(codes[ok & inside], best[ok & inside])
+
+
+def test_rtn_scale_bias_closed_form():
+    # A group spanning exactly [-0.75, 0.75]: scale = fp16(1.5 / 15) = fp16(0.1), bias = -0.75, codes exact.
+    q = np.arange(64) % 16
+    w = (-0.75 + q * (1.5 / 15)).astype(F32)[None, :].repeat(8, 0)
+    w[:, 0], w[:, 1] = -0.75, 0.75
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    assert sb[0, 0, 0, 0] == F16(F32(1.5) / F32(15.0))
+    assert sb[0, 0, 0, 1] == F16(-0.75)
+    codes = fm.unpack_marlin_codes(wm)[0]
+    assert codes[0] == 0 and codes[1] == 15
+
+
+def test_mse_clip_never_worse_than_rtn():
+    # The search includes the full-range candidate (alpha = 1), so its weighted error is <= RTN's.
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((16, 128)) * 0.02).astype(F16)
+    imp = np.abs(rng.standard_normal(128)).astype(F32) + 0.1
+    wr, sr = fm.pack_linear_q4_marlin(w, clip_search=False)
+    wc, sc = fm.pack_linear_q4_marlin(w, clip_search=True, col_importance=imp)
+    ig = (imp ** 2).reshape(2, 64)
+    ig = ig / ig.mean(-1, keepdims=True)
+    ig = ig.reshape(128)
+    e_r = (ig * (w.astype(F32) - fm.dequantize_q4_marlin(wr, sr, 128).astype(F32)) ** 2).reshape(16, 2, 64).sum(-1)
+    e_c = (ig * (w.astype(F32) - fm.dequantize_q4_marlin(wc, sc, 128).astype(F32)) ** 2).reshape(16, 2, 64).sum(-1)
+    assert np.all(e_c <= e_r * (1 + 1e-3) + 1e-12)
+
+
+def test_mse_alphas_match_torch_linspace():
+    # The product passes torch.linspace(1.0, 0.72, 13) (quant.py:512); the oracle's grid must be identical.
+    for steps, lo in [(13, 0.72), (2, 0.5), (7, 0.81), (20, 0.6)]:
+        assert np.array_equal(fm.linspace_f32(1.0, lo, steps), torch.linspace(1.0, lo, steps=steps).numpy())
+
+
+def test_ternary_byte_table_and_roundtrips():
+    # tests/test_phase3_task33_bitnet_q2k.py:62-108
+    dec = fm.ternary_decode_bytes(np.arange(256, dtype=np.uint8))
+    assert set(np.unique(dec).tolist()) <= {-1, 0, 1}
+    assert dec[0b01].tolist() == [1, 0, 0, 0] and dec[0b10].tolist() == [-1, 0, 0, 0]
+    assert dec[0b11].tolist() == [0, 0, 0, 0] and dec[0b10_01_00_10].tolist() == [-1, 0, 1, -1]
+    rng = np.random.default_rng(42)
+    q = np.where(rng.standard_normal((64, 256)) > 0, 1.0, -1.0).astype(F16)
+    w = (q.astype(F32) * 0.75).astype(F16)
+    p, s = fm.pack_linear_ternary(w)
+    assert p.shape == (64, 64) and p.dtype == np.uint8 and s.shape == (64, 4)
+    assert np.array_equal(fm.dequantize_ternary(p, s, 256), w)
+    g = rng.standard_normal((64, 256)).astype(F16)
+    p, s = fm.pack_linear_ternary(g)
+    r = fm.dequantize_ternary(p, s, 256).astype(F32).reshape(64, 4, 64)
+    sg = s.astype(F32)[..., None]
+    assert np.max(np.abs(r - np.rint(r / sg) * sg)) == 0.0
+
+
+def test_q2_roundtrip_and_bytes_per_weight():
+    # tests/test_phase3_task33_bitnet_q2k.py:110-129 and :321-324
+    rng = np.random.default_rng(5)
+    q = rng.integers(0, 4, (64, 256)).astype(F32)
+    w = (q * 0.5 - 1.0).astype(F16)
+    p, sb = fm.pack_linear_q2_k(w)
+    assert p.shape == (64, 64) and sb.shape == (64, 4, 2)
+    assert np.max(np.abs(fm.dequantize_q2_k(p, sb, 256).astype(F32) - w.astype(F32))) < 1e-3
+    N, K = 4096, 11008
+    tern = N * K // 4 + N * (K // 64) * 2
+    q2 = N * K // 4 + N * (K // 64) * 4
+    assert tern / (N * K) == 0.28125 and q2 / (N * K) == 0.3125
+
+
+def test_q8_pack_closed_form():
+    rng = np.random.default_rng(9)
+    w = rng.standard_normal((4, 128)).astype(F32)
+    p, sb = fm.pack_linear_q8_g64(w)
+    d = fm.dequantize_q8_g64(p, sb, 128).astype(F32)
+    # error bounded by half a quantization step (+ fp16 rounding of the result)
+    step = sb[..., 0].astype(F32).repeat(64, axis=1)
+    assert np.all(np.abs(d - w) <= 0.5 * step + np.abs(w) * 2 ** -10 + 1e-6)
+    assert p.min() == 0 and p.max() == 255
+
+
+def test_fp8_encode_matches_torch_on_all_fp16():
+    # quant.py:719: float(fp16(x / s)).to(float8_e4m3fn) -- pin the oracle to torch's cast bitwise.
+    allh = np.arange(65536, dtype=np.uint16).view(F16).astype(F32)
+    ours = fm.fp8_e4m3fn_from_f32(allh)
+    ref = torch.from_numpy(allh).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    nan_in = np.isnan(allh)
+    assert np.array_equal(ours[~nan_in], ref[~nan_in])
+    assert np.all((ours[nan_in] & 0x7F) == 0x7F)
+
+
+def test_fp8_encode_matches_torch_random_f32():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(200000) * np.exp2(rng.integers(-12, 10, 200000))).astype(F32)
+    x = np.concatenate([x, np.array([448, 464, 464.01, 479.9, 480, -464, 2 ** -9, 1.5 * 2 ** -10], F32)])
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(fm.fp8_e4m3fn_from_f32(x), ref)
+
+
+def test_fp8_decode_matches_torch():
+    b = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(b).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    ours = fm.fp8_e4m3fn_to_f32(b)
+    finite = ~np.isnan(ref)
+    assert np.array_equal(ours[finite], ref[finite]) and np.all(np.isnan(ours[~finite]))
+
+
+def test_int4_kv_closed_form_and_lattice_roundtrip():
+    # symmetric scale amax/7 per 64 (quant.py:771-807); lattice inputs round-trip exactly
+    rng = np.random.default_rng(2)
+    q = rng.integers(-7, 8, (3, 5, 128)).astype(F32)
+    q[..., 0] = 7
+    q[..., 64] = -7
+    x = (q * 0.25).astype(F16)  # scale = 1.75 / 7 = 0.25 exactly
+    packed, sc = fm.quantize_kv_int4_single(x)
+    assert packed.shape == (3, 5, 64) and sc.shape == (3, 5, 2)
+    assert np.all(sc == F16(0.25))
+    assert np.array_equal(fm.dequantize_kv_int4(packed, sc), x)
+    # nibble order: element 2i in the low nibble, 2i+1 in the high nibble, two's complement
+    lo = (packed[..., 0] & 0xF).astype(np.int32)
+    assert np.array_equal(np.where(lo >= 8, lo - 16, lo), q[..., 0].astype(np.int32))
+
+
+def test_fp8_kv_scale_and_sqnr():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((8, 4, 128)).astype(F16)
+    codes, sc = fm.quantize_kv_fp8_single(x)
+    amax = np.abs(x.astype(F32).reshape(8, 4, 2, 64)).max(-1)
+    assert np.array_equal(sc, (amax / F32(448.0)).astype(F16))
+    d = fm.dequantize_kv_fp8(codes, sc).astype(F32)
+    sqnr = 10 * np.log10((x.astype(F32) ** 2).sum() / ((x.astype(F32) - d) ** 2).sum())
+    assert sqnr > 30.0  # tests/test_phase3_task31_kv_quantization.py:46-121
+
+
+def test_kv_zero_group_gives_nan_codes():
+    # fp16 clamp(min=1e-8) rounds the bound to 0, so an all-zero group has scale 0 and 0/0 = NaN codes.
+    x = np.zeros((1, 64), F16)
+    codes, sc = fm.quantize_kv_fp8_single(x)
+    assert sc[0, 0] == 0 and np.all(codes == 0xFF)
+    t = torch.zeros(1, 64, dtype=torch.float16)
+    s_t = torch.clamp(t.abs().amax(dim=-1, keepdim=True) / 448.0, min=1e-8).to(torch.float16)
+    assert float(s_t) == 0.0
