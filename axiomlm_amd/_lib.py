@@ -25,6 +25,9 @@ _SIGNATURES = {
     "axm_last_error": (ctypes.c_char_p, []),
     "axm_version": (c_int, []),
     "axm_qmv_q4_marlin": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "axm_qmv_q4_marlin_swiglu": (
+        c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]
+    ),
     "axm_dequantize_q4_marlin": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "axm_pack_q4_marlin_rtn": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "axm_pack_q4_marlin_mse": (

@@ -248,14 +248,21 @@ int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bia
   for (int m0 = 0; m0 < M; m0 += 4) {
     const int mc = (M - m0) < 4 ? (M - m0) : 4;
     const size_t smem = (size_t)mc * K * sizeof(float);
-    if (smem > 160 * 1024) {
+    if (smem > 150 * 1024) {
       axm_set_error("q8 gemv: K=%d too large for LDS staging", K);
       return -2;
     }
-    static bool attr = false;
-    if (!attr) {
-      (void)hipFuncSetAttribute((const void*)q8_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      attr = true;
+    static size_t attr_bytes = 0;
+    if (smem > 48 * 1024 && smem > attr_bytes) {
+      // Raise the dynamic-LDS limit to what this launch needs (the kernel also
+      // has a few bytes of static LDS, so the full 160 KiB cannot be requested).
+      if (hipFuncSetAttribute((const void*)q8_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
+          hipSuccess) {
+        (void)hipGetLastError();
+        axm_set_error("q8 gemv: cannot reserve %zu bytes of LDS", smem);
+        return -2;
+      }
+      attr_bytes = smem;
     }
     const int rows_per_block = kQ8Threads / 64;
     int grid = (N + rows_per_block - 1) / rows_per_block;

@@ -543,8 +543,9 @@ size_t q4m_gemv_smem_bytes(int M, int NT, int K) {
 
 template <int M, int NT, int EPI>
 static void set_attr_one() {
-  (void)hipFuncSetAttribute((const void*)q4m_gemv_kernel<M, NT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024);
+  if (hipFuncSetAttribute((const void*)q4m_gemv_kernel<M, NT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          160 * 1024) != hipSuccess)
+    (void)hipGetLastError();  // keep the sticky error slot clean; launches re-check sizes
 }
 
 // Raise the dynamic-LDS limit of every GEMV instantiation once per process
@@ -681,5 +682,34 @@ extern "C" int axm_pack_q4_marlin_mse(const void* w, int src_is_fp16, int N, int
     hipLaunchKernelGGL(q4m_pack_mse_kernel<false>, dim3(blocks), dim3(512), 0, (hipStream_t)stream, w, N, K,
                        col_importance, alphas, n_alpha, (uint32_t*)w_marlin, (f16x2*)sb_marlin);
   AXM_LAUNCH_CHECK("pack_q4_marlin_mse");
+  return 0;
+}
+
+// Fused RMSNorm -> gate/up MARLIN GEMV -> SwiGLU for M tokens (the MLP input
+// half of a decoder layer; transformer.py:1178-1189).  gu_w/gu_sb pack the
+// concatenated [W_gate; W_up] rows (transformer.py:959-963), H % 8 == 0.
+extern "C" int axm_qmv_q4_marlin_swiglu(const void* x, const void* ln_w, float eps, const void* gu_w,
+                                        const void* gu_sb, void* y, int M, int K, int H, void* stream) {
+  AXM_CHECK_ARG(x && gu_w && gu_sb && y, -1, "qmv_q4_marlin_swiglu: null pointer");
+  AXM_CHECK_ARG(K > 0 && K % 64 == 0 && H > 0 && H % 8 == 0, -1,
+                "qmv_q4_marlin_swiglu: K=%d must be a multiple of 64 and H=%d of 8", K, H);
+  AXM_CHECK_ARG(M >= 1 && M <= 4, -1, "qmv_q4_marlin_swiglu: M=%d must be in [1, 4]", M);
+  Q4GemvArgs a{};
+  a.x = (const f16*)x;
+  a.ldx = K;
+  a.w = (const u32x4*)gu_w;
+  a.sb = (const u32x4*)gu_sb;
+  a.K = K;
+  a.KG = K / 64;
+  a.N = H;
+  a.n_units = H / 8;
+  a.pair_offset = H / 8;
+  a.y = (f16*)y;
+  a.ldy = H;
+  a.ln_w = (const f16*)ln_w;
+  a.eps = eps;
+  int rc = q4m_gemv_launch(a, M, Q4_EPI_SWIGLU, q4m_default_grid(a.n_units), (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("qmv_q4_marlin_swiglu");
   return 0;
 }

@@ -35,6 +35,12 @@ int axm_version(void);
  *    :4302-4641; Python entry axiomlm/kernels/quant.py:637-684). */
 int axm_qmv_q4_marlin(const void* x, const void* w_marlin, const void* sb_marlin, const void* bias, void* y, int M,
                       int K, int N, void* stream);
+/* Fused RMSNorm (ln_w fp16 [K], or NULL for none) -> gate/up GEMV over the packed
+ * [W_gate; W_up] rows -> SwiGLU: y fp16 [M][H] = silu(g) * u, M <= 4.  The MLP
+ * input half of a decoder layer (transformer.py:1178-1189; runner dispatches
+ * mps_kernels.mm:3249-3253 fused into one launch). */
+int axm_qmv_q4_marlin_swiglu(const void* x, const void* ln_w, float eps, const void* gu_w, const void* gu_sb,
+                             void* y, int M, int K, int H, void* stream);
 /* Row-major fp16 [N][K] dequantization (axiomlm/kernels/quant.py:597-634). */
 int axm_dequantize_q4_marlin(const void* w_marlin, const void* sb_marlin, void* out, int K, int N, void* stream);
 /* Round-to-nearest packer, clip_search=False (axiomlm/kernels/quant.py:447-494, 573-593).

@@ -124,6 +124,9 @@ class OracleKVCache:
             self.vs = np.zeros_like(self.ks)
         self.total_seen_tokens = [0] * n_layer
         self.layer_seq_lens = [0] * n_layer
+        # When frozen, writes are skipped: the cache contents were loaded from
+        # another implementation and attention must read exactly those codes.
+        self.frozen = False
 
     def _quant(self, x16):
         if self.dtype == "fp8":
@@ -141,6 +144,8 @@ class OracleKVCache:
 
     def write(self, layer, slots, k16, v16):
         """Store rows k16/v16 [Hkv, T, hd] at the given slots."""
+        if self.frozen:
+            return
         kq, ks = self._quant(k16)
         vq, vs = self._quant(v16)
         self.k[layer][:, slots] = kq

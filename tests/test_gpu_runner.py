@@ -67,20 +67,75 @@ def _check_logits(got, ref, what):
     assert err <= TOL, f"{what}: max |logit diff| {err}"
 
 
-@pytest.mark.parametrize("kv", ["fp16", "fp8", "int4"])
-def test_runner_step_matches_oracle(dev, kv):
-    print(f"[runner_step] kv={kv}", flush=True)
+def test_runner_step_matches_oracle(dev):
+    print("[runner_step] kv=fp16", flush=True)
     cfg, ow, cos, sin = c1_model()
     model = om.OracleModel(cfg, ow, cos, sin)
     S = 128
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, kv)
-    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv)
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16")
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, "fp16")
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, cfg.vocab, 32).tolist()
     got = run_steps(runner, cache, prompt, dev)
     for i, tok in enumerate(prompt):
         ref = model.forward([tok], ocache)[-1]
         _check_logits(got[i], ref, f"prompt step {i}")
+
+
+def _load_gpu_cache(ocache, cache):
+    k = cache.cache[:, 0, 0].cpu().numpy()
+    v = cache.cache[:, 1, 0].cpu().numpy()
+    ocache.k[...] = k
+    ocache.v[...] = v
+    if cache.scales is not None:
+        ocache.ks[...] = cache.scales[:, 0, 0].cpu().numpy()
+        ocache.vs[...] = cache.scales[:, 1, 0].cpu().numpy()
+
+
+@pytest.mark.parametrize("kv", ["fp8", "int4"])
+def test_runner_quantized_kv_matches_oracle(dev, kv):
+    """Quantized KV inside the captured step.
+
+    (a) Logits: the oracle attends over exactly the codes the GPU wrote (cache
+        loaded from the device and frozen), so the comparison isolates the step
+        arithmetic: max |diff| <= 1e-2.
+    (b) Codes: an independent oracle run quantizes its own k/v; since k/v agree only
+        to fp16 rounding, a value sitting on a rounding boundary may land on the
+        neighbouring code.  Bar: >= 99% of codes identical and every difference is
+        one code step.  (Op-level bit-exactness of the quantizer on identical inputs
+        is test_gpu_kernels.py::test_kv_quantize_bit_exact.)"""
+    print(f"[runner_qkv] kv={kv}", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, kv)
+    frozen = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv)
+    frozen.frozen = True
+    indep = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv)
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, cfg.vocab, 40).tolist()
+    for i, tok in enumerate(prompt):
+        got = run_steps(runner, cache, [tok], dev)[0]
+        _load_gpu_cache(frozen, cache)
+        ref = model.forward([tok], frozen)[-1]
+        for L in range(cfg.n_layer):
+            frozen.total_seen_tokens[L] = frozen.layer_seq_lens[L] = i + 1
+        _check_logits(got, ref, f"step {i}")
+        model.forward([tok], indep)
+    n = len(prompt)
+    g_k = cache.cache[:, :, 0, :, :n].cpu().numpy()
+    o_k = np.stack([indep.k[:, :, :n], indep.v[:, :, :n]], axis=1)
+    if kv == "int4":
+        lo = lambda a: ((a.astype(np.int32) & 0xF) ^ 8) - 8  # noqa: E731
+        hi = lambda a: (((a.astype(np.int32) >> 4) & 0xF) ^ 8) - 8  # noqa: E731
+        ga, oa = np.stack([lo(g_k), hi(g_k)]), np.stack([lo(o_k), hi(o_k)])
+    else:
+        # fp8 bytes of one sign are monotone in value: adjacent codes differ by 1
+        sgn = lambda a: np.where(a & 0x80, -1, 1) * (a.astype(np.int32) & 0x7F)  # noqa: E731
+        ga, oa = sgn(g_k), sgn(o_k)
+    diff = np.abs(ga - oa)
+    assert (diff == 0).mean() >= 0.99, f"only {(diff == 0).mean():.4f} of codes identical"
+    assert diff.max() <= 1
 
 
 def test_runner_greedy_c1(dev):
