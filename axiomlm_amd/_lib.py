@@ -63,6 +63,7 @@ _SIGNATURES = {
     "axm_runner_destroy": (None, [c_void_p]),
     "axm_runner_step": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p]),
     "axm_runner_last_norm": (c_int, [c_void_p, c_void_p]),
+    "axm_runner_token_slot": (c_int, [c_void_p, c_void_p]),
     "axm_runner_set_graph": (c_int, [c_void_p, c_int]),
 }
 

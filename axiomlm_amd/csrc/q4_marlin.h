@@ -41,9 +41,13 @@ struct Q4GemvArgs {
   f16* v_out;
   long kv_stride_h;    // elements between kv heads (max_seq * head_dim)
   int max_seq;
+  int split;           // waves per unit (set by q4m_gemv_launch)
+  // Q4_EPI_STORE, M == 1: optional running argmax of the fp16 outputs as an
+  // ordered 64-bit key (value order, then lowest index), updated by atomicMax.
+  unsigned long long* argmax_key;
 };
 
 size_t q4m_gemv_smem_bytes(int M, int NT, int K);
-int q4m_gemv_launch(const Q4GemvArgs& a, int M, int epi, int grid, hipStream_t s);
-int q4m_default_grid(int n_units);
+// Picks the split-K factor and grid (a.split is overwritten).
+int q4m_gemv_launch(Q4GemvArgs a, int M, int epi, hipStream_t s);
 void q4m_prepare_attributes();

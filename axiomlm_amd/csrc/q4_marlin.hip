@@ -29,73 +29,80 @@ constexpr int kWaves = kThreads / AXM_WAVE;
 // ---------------------------------------------------------------------------
 // LDS staging of activations in the lane-permuted order.
 //   xh  : f16  [KG*8 (g,r)][8] = x[64g + 32j + 8s + r] at slot j*4+s
-//   cx  : f32x2[KG*8]          = (1024*(s even) + 64*(s odd) weighted sum, plain sum)
+//   cx  : f32x2[KG*8]          = (sum with magic weights 1024 (s even) / 64 (s odd), plain sum)
 // ---------------------------------------------------------------------------
 struct XStage {
   f16* xh;
   f32x2* cx;
 };
 
-
 template <int M>
 __device__ void stage_x(const Q4GemvArgs& a, XStage* st, float* red) {
   const int tid = threadIdx.x;
   const int K = a.K;
+  const int nv = K >> 3;  // 8-element vectors
   float rinv[M];
+#pragma unroll
+  for (int mi = 0; mi < M; ++mi) rinv[mi] = 1.f;
   if (a.ln_w != nullptr) {
-    // Pass 1: sum of fp16-rounded squares per token.
+    // Sum of fp16-rounded squares per token (vectorized loads).
+#pragma unroll
     for (int mi = 0; mi < M; ++mi) {
-      const f16* xr = a.x + (size_t)mi * a.ldx;
+      const f16x8* xr = reinterpret_cast<const f16x8*>(a.x + (size_t)mi * a.ldx);
       float s = 0.f;
-      for (int k = tid; k < K; k += kThreads) {
-        float v = h2f(xr[k]);
-        s += h2f(f2h(v * v));
+      for (int i = tid; i < nv; i += kThreads) {
+        const f16x8 v = xr[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = h2f(v[e]);
+          s += h2f(f2h(f * f));
+        }
       }
       s = wave_sum(s);
       if ((tid & 63) == 0) red[mi * kWaves + (tid >> 6)] = s;
     }
     __syncthreads();
+#pragma unroll
     for (int mi = 0; mi < M; ++mi) {
       float s = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) s += red[mi * kWaves + w];
       rinv[mi] = rms_inv_fp16(s, K, a.eps);
     }
-    __syncthreads();
   }
-  const int n_gr = a.KG * 8;
+  // Vector i holds k = 8i..8i+7: g = i>>3, j = (i>>2)&1, s = i&3, r = 0..7.
+#pragma unroll
   for (int mi = 0; mi < M; ++mi) {
-    const f16* xr = a.x + (size_t)mi * a.ldx;
+    const f16x8* xr = reinterpret_cast<const f16x8*>(a.x + (size_t)mi * a.ldx);
+    const f16x8* wr = reinterpret_cast<const f16x8*>(a.ln_w);
+    for (int i = tid; i < nv; i += kThreads) {
+      f16x8 v = xr[i];
+      if (a.ln_w != nullptr) {
+        const f16x8 w = wr[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = f2h(h2f(f2h(h2f(v[e]) * rinv[mi])) * h2f(w[e]));
+      }
+      if (a.x_norm_out != nullptr) reinterpret_cast<f16x8*>(a.x_norm_out + (size_t)mi * K)[i] = v;
+      const int g = i >> 3, js = ((i >> 2) & 1) * 4 + (i & 3);
+      f16* dst = st[mi].xh + (size_t)g * 64 + js;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) dst[r * 8] = v[r];
+    }
+  }
+  __syncthreads();
+  const int n_gr = a.KG * 8;
+#pragma unroll
+  for (int mi = 0; mi < M; ++mi) {
     for (int p = tid; p < n_gr; p += kThreads) {
-      const int g = p >> 3, r = p & 7;
-      f16x8 v;
+      const f16x8 v = *reinterpret_cast<const f16x8*>(st[mi].xh + (size_t)p * 8);
       float corr = 0.f, sum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int k = 64 * g + 32 * j + 8 * s + r;
-          f16 h = xr[k];
-          if (a.ln_w != nullptr) {
-            f16 t = f2h(h2f(h) * rinv[mi]);
-            h = f2h(h2f(t) * h2f(a.ln_w[k]));
-          }
-          v[j * 4 + s] = h;
-          float f = h2f(h);
-          sum += f;
-          corr += f * ((s & 1) ? 64.f : 1024.f);
-        }
+      for (int e = 0; e < 8; ++e) {
+        const float f = h2f(v[e]);
+        sum += f;
+        corr += f * ((e & 1) ? 64.f : 1024.f);
       }
-      *reinterpret_cast<f16x8*>(st[mi].xh + (size_t)p * 8) = v;
       st[mi].cx[p] = f32x2{corr, sum};
-      if (a.x_norm_out != nullptr) {
-        // Optional export of the normalized activations (row-major).
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            a.x_norm_out[(size_t)mi * K + 64 * g + 32 * j + 8 * s + r] = v[j * 4 + s];
-      }
     }
   }
   __syncthreads();
@@ -105,17 +112,16 @@ __device__ void stage_x(const Q4GemvArgs& a, XStage* st, float* red) {
 // wv = (A, B, C, D) words: A/B rows cb,cb+1 (j=0/1), C/D rows cb+2,cb+3.
 __device__ __forceinline__ void q4_group_fma(u32x4 wv, u32x4 sv, f16x8 xv, f32x2 cx, float acc[4]) {
   float d[4] = {0.f, 0.f, 0.f, 0.f};
-  const uint32_t words[4] = {wv[0], wv[1], wv[2], wv[3]};
 #pragma unroll
   for (int wi = 0; wi < 4; ++wi) {
-    const uint32_t w = words[wi];
-    const int j = wi & 1;         // k half
-    const int rp = (wi >> 1) * 2; // row pair offset 0 or 2
+    const uint32_t w = wv[wi];
+    const int j = wi & 1;          // k half
+    const int rp = (wi >> 1) * 2;  // row pair offset 0 or 2
     const uint32_t w8 = w >> 8;
-    f16x2 h0 = as_h2((w & 0x000F000Fu) | 0x64006400u);
-    f16x2 h1 = as_h2((w & 0x00F000F0u) | 0x54005400u);
-    f16x2 h2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u);
-    f16x2 h3 = as_h2((w8 & 0x00F000F0u) | 0x54005400u);
+    const f16x2 h0 = as_h2((w & 0x000F000Fu) | 0x64006400u);
+    const f16x2 h1 = as_h2((w & 0x00F000F0u) | 0x54005400u);
+    const f16x2 h2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u);
+    const f16x2 h3 = as_h2((w8 & 0x00F000F0u) | 0x54005400u);
     const float x0 = h2f(xv[j * 4 + 0]), x1 = h2f(xv[j * 4 + 1]);
     const float x2 = h2f(xv[j * 4 + 2]), x3 = h2f(xv[j * 4 + 3]);
     d[rp] = __builtin_fmaf(h2f(h0.x), x0, d[rp]);
@@ -127,24 +133,24 @@ __device__ __forceinline__ void q4_group_fma(u32x4 wv, u32x4 sv, f16x8 xv, f32x2
     d[rp + 1] = __builtin_fmaf(h2f(h2.y), x2, d[rp + 1]);
     d[rp + 1] = __builtin_fmaf(h2f(h3.y), x3, d[rp + 1]);
   }
-  const uint32_t sbw[4] = {sv[0], sv[1], sv[2], sv[3]};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    f16x2 sb = as_h2(sbw[i]);
+    const f16x2 sb = as_h2(sv[i]);
     acc[i] = __builtin_fmaf(h2f(sb.x), d[i] - cx.x, acc[i]);
     acc[i] = __builtin_fmaf(h2f(sb.y), cx.y, acc[i]);
   }
 }
 
-// Reduce the 4 row partials of every lane over the 32 lanes that share cb.
-// Returns, in lane L, the full sum for tile row  (L&4) + 2*(L&1) + ((L>>1)&1).
+// Reduce the 4 row partials of every lane over the lanes that share cb.
+// Returns, in lane L < 8, the full sum for tile row (L&4) + 2*(L&1) + ((L>>1)&1);
+// the rows of a RoPE pair (2i, 2i+1) sit in lanes L and L^2.
 __device__ __forceinline__ float wave_reduce_rows(const float v[4], int lane) {
   const bool b0 = lane & 1, b1 = lane & 2;
-  float s0 = b0 ? v[0] : v[2], s1 = b0 ? v[1] : v[3];
+  const float s0 = b0 ? v[0] : v[2], s1 = b0 ? v[1] : v[3];
   float k0 = b0 ? v[2] : v[0], k1 = b0 ? v[3] : v[1];
   k0 += __shfl_xor(s0, 1, 64);
   k1 += __shfl_xor(s1, 1, 64);
-  float send = b1 ? k0 : k1;
+  const float send = b1 ? k0 : k1;
   float keep = b1 ? k1 : k0;
   keep += __shfl_xor(send, 2, 64);
   keep += __shfl_xor(keep, 8, 64);
@@ -158,27 +164,119 @@ __device__ __forceinline__ int reduced_row_of_lane(int lane) {
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
-// ---------------------------------------------------------------------------
-// Main GEMV kernel.  NT = tiles per work unit (2 for the SwiGLU gate/up pair).
-// ---------------------------------------------------------------------------
+// Epilogue run by lanes 0..7 of one wave; v[t][mi] is the row sum of tile t
+// for row `row` of token mi (t = 0: the unit's tile / gate tile, t = 1: up tile).
 template <int M, int NT, int EPI>
+__device__ __forceinline__ void q4_epilogue(const Q4GemvArgs& a, int unit, int lane, const float (&v)[NT][M]) {
+  const int row = unit * 8 + reduced_row_of_lane(lane);
+  if (EPI == Q4_EPI_QKV_ROPE) {
+    // Pair partner (row ^ 1) lives in lane ^ 2; every lane of the pair needs it.
+    float pv[M];
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) pv[mi] = __shfl_xor(v[0][mi], 2, 64);
+    if (lane >= 8 || row >= a.N) return;
+    const bool even = (row & 1) == 0;
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) {
+      f16 h_self = f2h(v[0][mi]);
+      f16 h_part = f2h(pv[mi]);
+      const int row0 = row & ~1;
+      if (a.bias != nullptr) {
+        h_self = f2h(h2f(h_self) + h2f(a.bias[row]));
+        h_part = f2h(h2f(h_part) + h2f(a.bias[row ^ 1]));
+      }
+      const f16 h0 = even ? h_self : h_part;
+      const f16 h1 = even ? h_part : h_self;
+      const int hd = a.head_dim, half_hd = hd >> 1;
+      f16 out = even ? h0 : h1;
+      if (row0 < a.q_dim + a.kv_dim) {
+        const int pos = (a.rope_pos_dev ? a.rope_pos_dev[0] : a.rope_pos) + mi;
+        const int within = row0 < a.q_dim ? row0 : row0 - a.q_dim;
+        const int fi = (within % hd) >> 1;
+        const int rp = pos % a.rope_len;
+        const float c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
+        const float sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
+        const float x0 = h2f(h0), x1 = h2f(h1);
+        out = even ? f2h(x0 * c - x1 * sn) : f2h(x0 * sn + x1 * c);
+      }
+      if (row < a.q_dim) {
+        a.y[(size_t)mi * a.ldy + row] = out;
+      } else {
+        const bool is_k = row < a.q_dim + a.kv_dim;
+        const int within = is_k ? row - a.q_dim : row - a.q_dim - a.kv_dim;
+        const int kvh = within / hd, e = within % hd;
+        const int wp = (a.write_pos_dev ? a.write_pos_dev[0] : a.write_pos) + mi;
+        f16* dst = (is_k ? a.k_out : a.v_out) + ((size_t)kvh * a.kv_stride_h + (size_t)(wp % a.max_seq) * hd + e);
+        *dst = out;
+      }
+    }
+    return;
+  }
+  if (EPI == Q4_EPI_STORE && M == 1 && a.argmax_key != nullptr) {
+    // Ordered key: fp16 value (sign-folded) in the high word, ~index in the low
+    // word, so the max is the largest logit with the lowest index on ties.
+    unsigned long long key = 0ull;
+    if (lane < 8 && row < a.N) {
+      const f16 h = f2h(v[0][0]);
+      const uint32_t u = __builtin_bit_cast(uint32_t, h2f(h));
+      const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+      key = ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (uint32_t)row);
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+      const unsigned long long other = __shfl_xor(key, o, 64);
+      key = other > key ? other : key;
+    }
+    if (lane == 0) atomicMax(a.argmax_key, key);
+  }
+  if (lane >= 8 || row >= a.N) return;
+#pragma unroll
+  for (int mi = 0; mi < M; ++mi) {
+    if (EPI == Q4_EPI_SWIGLU) {
+      const f16 g = f2h(v[0][mi]);
+      const f16 u = f2h(v[NT - 1][mi]);
+      const f16 sg = f2h(silu_f(h2f(g)));
+      a.y[(size_t)mi * a.ldy + row] = f2h(h2f(sg) * h2f(u));
+    } else {
+      f16 h = f2h(v[0][mi]);
+      if (a.bias != nullptr) h = f2h(h2f(h) + h2f(a.bias[row]));
+      if (EPI == Q4_EPI_STORE) {
+        a.y[(size_t)mi * a.ldy + row] = h;
+      } else {
+        f16* xr = a.resid + (size_t)mi * a.ldr + row;
+        *xr = f2h(h2f(*xr) + h2f(h));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Main GEMV kernel.
+//   NT = tiles per work unit (2 for the SwiGLU gate/up pair).
+//   a.split (S in {1, 2, 4}) = waves that share one unit (split-K); the 4 waves of
+//   a workgroup therefore cover 4/S units at a time.  S == 1 runs a persistent
+//   loop over units; S > 1 requires one unit group per workgroup (grid covers all).
+//   P = chunk loads in flight per wave (rolling pipeline, 1 KB per chunk and tile).
+// The first P chunks of a wave are requested before the activations are staged,
+// so the staging latency hides under the weight stream.
+// ---------------------------------------------------------------------------
+template <int M, int NT, int EPI, int P>
 __global__ void __launch_bounds__(kThreads) q4m_gemv_kernel(Q4GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  // Layout: [M] xh (K halves) | [M] cx (K/8 float2) | red (kWaves*NT*M*8 f32) | fin (NT*M*8 f32)
+  // Layout: [M] xh (K halves) | [M] cx (K/8 float2) | red (kWaves*NT*M*8 f32)
   XStage st[M];
   unsigned char* p = smem;
+#pragma unroll
   for (int mi = 0; mi < M; ++mi) {
     st[mi].xh = reinterpret_cast<f16*>(p);
     p += (size_t)a.K * sizeof(f16);
   }
+#pragma unroll
   for (int mi = 0; mi < M; ++mi) {
     st[mi].cx = reinterpret_cast<f32x2*>(p);
     p += (size_t)(a.K / 8) * sizeof(f32x2);
   }
   float* red = reinterpret_cast<float*>(p);
-  float* fin = red + kWaves * NT * M * 8;
-
-  stage_x<M>(a, st, red);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -187,14 +285,34 @@ __global__ void __launch_bounds__(kThreads) q4m_gemv_kernel(Q4GemvArgs a) {
   const int m = lane & 15;
   const int r = ((m & 8) >> 1) | (m & 3);
   const int cb = m & 4;
+  const int S = a.split;
+  const int upw = kWaves / S;
+  const int sub = wave % S;
+  const int slot = wave / S;
   const int n_chunks = (a.KG + 3) >> 2;
+  const int my = (n_chunks - sub + S - 1) / S;  // chunks of this wave per unit (host keeps S <= n_chunks)
   const u32x4* __restrict__ w4 = a.w;
   const u32x4* __restrict__ sb4 = a.sb;
 
-  for (int unit = blockIdx.x; unit < a.n_units; unit += gridDim.x) {
-    int tiles[NT];
-    tiles[0] = unit;
-    if (NT == 2) tiles[NT - 1] = unit + a.pair_offset;
+  u32x4 wr[P][NT], sr[P][NT];
+  auto load = [&](int unit, int ci, int j) {
+    const int g = (sub + ci * S) * 4 + gs;
+    const bool ok = unit < a.n_units && ci < my && g < a.KG;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const size_t base = (size_t)(unit + t * a.pair_offset) * a.KG + g;
+      wr[j][t] = ok ? __builtin_nontemporal_load(w4 + base * 16 + m) : u32x4{0u, 0u, 0u, 0u};
+      sr[j][t] = ok ? sb4[base * 2 + (cb >> 2)] : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  int it = 0;
+  int unit = blockIdx.x * upw + slot;
+#pragma unroll
+  for (int j = 0; j < P; ++j) load(unit, j, j);
+  stage_x<M>(a, st, red);
+
+  while (true) {
     float acc[NT][M][4];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -203,124 +321,64 @@ __global__ void __launch_bounds__(kThreads) q4m_gemv_kernel(Q4GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][mi][i] = 0.f;
 
-    constexpr int U = (NT == 2) ? 2 : 4;  // chunks in flight per wave
-    for (int c0 = wave; c0 < n_chunks; c0 += kWaves * U) {
-      u32x4 wv[U][NT], sv[U][NT];
+    for (int ci0 = 0; ci0 < my; ci0 += P) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = c0 + u * kWaves;
-        const int g = c * 4 + gs;
-        const bool ok = (c < n_chunks) && (g < a.KG);
+      for (int j = 0; j < P; ++j) {
+        const int ci = ci0 + j;
+        if (ci < my) {
+          const int g = (sub + ci * S) * 4 + gs;
+          if (g < a.KG) {
+            const int pidx = g * 8 + r;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const size_t base = (size_t)tiles[t] * a.KG + g;
-          wv[u][t] = ok ? __builtin_nontemporal_load(w4 + base * 16 + m) : u32x4{0u, 0u, 0u, 0u};
-          sv[u][t] = ok ? sb4[base * 2 + (cb >> 2)] : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
+            for (int mi = 0; mi < M; ++mi) {
+              const f16x8 xv = *reinterpret_cast<const f16x8*>(st[mi].xh + (size_t)pidx * 8);
+              const f32x2 cx = st[mi].cx[pidx];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = c0 + u * kWaves;
-        const int g = c * 4 + gs;
-        if (c < n_chunks && g < a.KG) {
-          const int pidx = g * 8 + r;
-#pragma unroll
-          for (int mi = 0; mi < M; ++mi) {
-            const f16x8 xv = *reinterpret_cast<const f16x8*>(st[mi].xh + (size_t)pidx * 8);
-            const f32x2 cx = st[mi].cx[pidx];
-#pragma unroll
-            for (int t = 0; t < NT; ++t) q4_group_fma(wv[u][t], sv[u][t], xv, cx, acc[t][mi]);
+              for (int t = 0; t < NT; ++t) q4_group_fma(wr[j][t], sr[j][t], xv, cx, acc[t][mi]);
+            }
           }
+          if (ci + P < my) load(unit, ci + P, j);
         }
       }
     }
 
-    // Wave reduction then cross-wave reduction through LDS.
+    // Request the next unit's first chunks before the reduction / epilogue.
+    const int next_unit = (blockIdx.x + (it + 1) * gridDim.x) * upw + slot;
+    const bool more = (S == 1) && ((blockIdx.x + (it + 1) * gridDim.x) * upw < a.n_units);
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < P; ++j) load(next_unit, j, j);
+    }
+
+    float v[NT][M];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int mi = 0; mi < M; ++mi) {
-        float v = wave_reduce_rows(acc[t][mi], lane);
-        if (lane < 8) red[((wave * NT + t) * M + mi) * 8 + reduced_row_of_lane(lane)] = v;
-      }
-    __syncthreads();
-    if (tid < NT * M * 8) {
-      float s = 0.f;
+      for (int mi = 0; mi < M; ++mi) v[t][mi] = wave_reduce_rows(acc[t][mi], lane);
+    if (S > 1) {
+      // Split-K partials of the S waves of a unit meet in LDS.
+      if (lane < 8) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) s += red[w * NT * M * 8 + tid];
-      fin[tid] = s;
-    }
-    __syncthreads();
-
-    if (EPI == Q4_EPI_STORE || EPI == Q4_EPI_RESID) {
-      if (tid < M * 8) {
-        const int mi = tid >> 3, row = tiles[0] * 8 + (tid & 7);
-        if (row < a.N) {
-          float v = fin[tid];
-          f16 h = f2h(v);
-          if (a.bias != nullptr) h = f2h(h2f(h) + h2f(a.bias[row]));
-          if (EPI == Q4_EPI_STORE) {
-            a.y[(size_t)mi * a.ldy + row] = h;
-          } else {
-            f16* xr = a.resid + (size_t)mi * a.ldr + row;
-            *xr = f2h(h2f(*xr) + h2f(h));
-          }
-        }
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int mi = 0; mi < M; ++mi) red[((wave * NT + t) * M + mi) * 8 + lane] = v[t][mi];
       }
-    } else if (EPI == Q4_EPI_SWIGLU) {
-      // fin layout [t][mi][8]; t=0 gate rows, t=1 up rows.  Torch-CPU fp16
-      // semantics: gu rounded to fp16, silu(g) rounded, product rounded.
-      if (tid < M * 8) {
-        const int mi = tid >> 3, row = tiles[0] * 8 + (tid & 7);
-        if (row < a.N) {
-          f16 g = f2h(fin[(0 * M + mi) * 8 + (tid & 7)]);
-          f16 u = f2h(fin[(1 * M + mi) * 8 + (tid & 7)]);
-          f16 sg = f2h(silu_f(h2f(g)));
-          a.y[(size_t)mi * a.ldy + row] = f2h(h2f(sg) * h2f(u));
-        }
-      }
-    } else if (EPI == Q4_EPI_QKV_ROPE) {
-      // Rows [0, q_dim): rotated q -> y;  [q_dim, q_dim+kv_dim): rotated k ->
-      // k_out slot;  [q_dim+kv_dim, N): v -> v_out slot.  Pairs (2i, 2i+1)
-      // share a tile, so each thread owns one pair.
-      if (tid < M * 4) {
-        const int mi = tid >> 2, pr = tid & 3;
-        const int row0 = tiles[0] * 8 + 2 * pr;
-        if (row0 < a.N) {
-          f16 h0 = f2h(fin[mi * 8 + 2 * pr]);
-          f16 h1 = f2h(fin[mi * 8 + 2 * pr + 1]);
-          if (a.bias != nullptr) {
-            h0 = f2h(h2f(h0) + h2f(a.bias[row0]));
-            h1 = f2h(h2f(h1) + h2f(a.bias[row0 + 1]));
+      __syncthreads();
+      if (sub == 0 && lane < 8) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int mi = 0; mi < M; ++mi) {
+            float s = 0.f;
+            for (int w = wave; w < wave + S; ++w) s += red[((w * NT + t) * M + mi) * 8 + lane];
+            v[t][mi] = s;
           }
-          const int hd = a.head_dim, half_hd = hd >> 1;
-          const int pos_mi = a.rope_pos_dev ? a.rope_pos_dev[0] + mi : a.rope_pos + mi;
-          if (row0 < a.q_dim + a.kv_dim) {
-            const int within = row0 < a.q_dim ? row0 : row0 - a.q_dim;
-            const int fi = (within % hd) >> 1;
-            const int rp = pos_mi % a.rope_len;
-            const float c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
-            const float sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
-            const float x0 = h2f(h0), x1 = h2f(h1);
-            h0 = f2h(x0 * c - x1 * sn);
-            h1 = f2h(x0 * sn + x1 * c);
-          }
-          if (row0 < a.q_dim) {
-            a.y[(size_t)mi * a.ldy + row0] = h0;
-            a.y[(size_t)mi * a.ldy + row0 + 1] = h1;
-          } else {
-            const bool is_k = row0 < a.q_dim + a.kv_dim;
-            const int within = is_k ? row0 - a.q_dim : row0 - a.q_dim - a.kv_dim;
-            const int kvh = within / hd, e = within % hd;
-            const int wp = a.write_pos_dev ? a.write_pos_dev[0] + mi : a.write_pos + mi;
-            f16* dst = (is_k ? a.k_out : a.v_out) + ((size_t)kvh * a.kv_stride_h + (size_t)(wp % a.max_seq) * hd + e);
-            dst[0] = h0;
-            dst[1] = h1;
-          }
-        }
       }
     }
-    __syncthreads();
+    if (sub == 0 && unit < a.n_units) q4_epilogue<M, NT, EPI>(a, unit, lane, v);
+    if (!more) break;
+    ++it;
+    unit = next_unit;
   }
 }
 
@@ -538,13 +596,19 @@ __global__ void __launch_bounds__(512) q4m_pack_mse_kernel(const void* __restric
 // ---------------------------------------------------------------------------
 size_t q4m_gemv_smem_bytes(int M, int NT, int K) {
   return (size_t)M * K * sizeof(f16) + (size_t)M * (K / 8) * sizeof(f32x2) +
-         (size_t)kWaves * NT * M * 8 * sizeof(float) + (size_t)NT * M * 8 * sizeof(float);
+         (size_t)kWaves * NT * M * 8 * sizeof(float);
 }
+
+// Chunk loads in flight per wave: 8 KB per wave for one tile, 2 x 4 KB for pairs.
+template <int NT>
+struct PipeDepth {
+  static constexpr int value = NT == 2 ? 4 : 8;
+};
 
 template <int M, int NT, int EPI>
 static void set_attr_one() {
-  if (hipFuncSetAttribute((const void*)q4m_gemv_kernel<M, NT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          160 * 1024) != hipSuccess)
+  if (hipFuncSetAttribute((const void*)q4m_gemv_kernel<M, NT, EPI, PipeDepth<NT>::value>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
     (void)hipGetLastError();  // keep the sticky error slot clean; launches re-check sizes
 }
 
@@ -569,17 +633,41 @@ void q4m_prepare_attributes() {
 template <int M, int NT, int EPI>
 static int launch_one(const Q4GemvArgs& a, int grid, hipStream_t s) {
   const size_t smem = q4m_gemv_smem_bytes(M, NT, a.K);
-  hipLaunchKernelGGL((q4m_gemv_kernel<M, NT, EPI>), dim3(grid), dim3(kThreads), smem, s, a);
+  hipLaunchKernelGGL((q4m_gemv_kernel<M, NT, EPI, PipeDepth<NT>::value>), dim3(grid), dim3(kThreads), smem, s, a);
   return 0;
 }
 
-int q4m_gemv_launch(const Q4GemvArgs& a, int M, int epi, int grid, hipStream_t s) {
+// Work decomposition: S waves per unit (split-K inside a workgroup) so that the
+// launch has about 8 waves per CU; S == 1 launches a persistent grid.
+static void choose_split(Q4GemvArgs& a, int* grid) {
+  const int cus = axm_num_cus();
+  const int target_waves = 8 * cus;
+  const int n_chunks = (a.KG + 3) / 4;
+  int S = 1;
+  while (S < kWaves && a.n_units * S < target_waves && n_chunks >= 2 * S * 2) S *= 2;
+  a.split = S;
+  const int upw = kWaves / S;
+  int g = (a.n_units + upw - 1) / upw;
+  if (S == 1) {
+    const int cap = cus * 4;
+    if (g > cap) g = cap;
+  }
+  *grid = g;
+}
+
+int q4m_gemv_launch(Q4GemvArgs a, int M, int epi, hipStream_t s) {
   q4m_prepare_attributes();
   const int NT = (epi == Q4_EPI_SWIGLU) ? 2 : 1;
   if (q4m_gemv_smem_bytes(M, NT, a.K) > 160 * 1024) {
     axm_set_error("q4 gemv: K=%d with M=%d needs %zu B of LDS (> 160 KiB)", a.K, M, q4m_gemv_smem_bytes(M, NT, a.K));
     return -2;
   }
+  if (a.K % 64 != 0 || a.KG != a.K / 64 || a.n_units <= 0) {
+    axm_set_error("q4 gemv: bad shape K=%d units=%d", a.K, a.n_units);
+    return -2;
+  }
+  int grid = 0;
+  choose_split(a, &grid);
 #define AXM_Q4_CASE(MM)                                                              \
   case MM:                                                                           \
     switch (epi) {                                                                   \
@@ -598,11 +686,6 @@ int q4m_gemv_launch(const Q4GemvArgs& a, int M, int epi, int grid, hipStream_t s
 #undef AXM_Q4_CASE
   axm_set_error("q4 gemv: unsupported M=%d / epilogue=%d", M, epi);
   return -2;
-}
-
-int q4m_default_grid(int n_units) {
-  const int cap = axm_num_cus() * 4;
-  return n_units < cap ? n_units : cap;
 }
 
 extern "C" int axm_qmv_q4_marlin(const void* x, const void* w_marlin, const void* sb_marlin, const void* bias,
@@ -631,7 +714,7 @@ extern "C" int axm_qmv_q4_marlin(const void* x, const void* w_marlin, const void
       a.y = (f16*)y + (size_t)mm * N;
       a.ldy = N;
       a.bias = (const f16*)bias;
-      int rc = q4m_gemv_launch(a, cnt, Q4_EPI_STORE, q4m_default_grid(n_tiles), s);
+      int rc = q4m_gemv_launch(a, cnt, Q4_EPI_STORE, s);
       if (rc) return rc;
     }
   }
@@ -708,7 +791,7 @@ extern "C" int axm_qmv_q4_marlin_swiglu(const void* x, const void* ln_w, float e
   a.ldy = H;
   a.ln_w = (const f16*)ln_w;
   a.eps = eps;
-  int rc = q4m_gemv_launch(a, M, Q4_EPI_SWIGLU, q4m_default_grid(a.n_units), (hipStream_t)stream);
+  int rc = q4m_gemv_launch(a, M, Q4_EPI_SWIGLU, (hipStream_t)stream);
   if (rc) return rc;
   AXM_LAUNCH_CHECK("qmv_q4_marlin_swiglu");
   return 0;

@@ -23,11 +23,29 @@
 namespace {
 
 enum { P_TOKEN = 0, P_ROPE = 1, P_WRITE = 2, P_ACTIVE = 3, P_COUNT = 4 };
+// Byte offsets inside the parameter block: running argmax key of the lm_head
+// (u64) and the int64 token id used by the current step.
+constexpr int kArgmaxOffset = 64;
+constexpr int kTokenOffset = 72;
 
+// Token source: idx_dev[0] if non-null, else tok_host if >= 0, else the greedy
+// argmax of the previous step's logits.  Resets the argmax key for this step.
 __global__ void set_params_kernel(int* params, const int64_t* idx_dev, int64_t tok_host, int rope_pos,
                                   int write_pos, int active_len) {
   if (threadIdx.x == 0) {
-    params[P_TOKEN] = (int)(idx_dev != nullptr ? idx_dev[0] : tok_host);
+    unsigned char* base = reinterpret_cast<unsigned char*>(params);
+    unsigned long long* key = reinterpret_cast<unsigned long long*>(base + kArgmaxOffset);
+    int64_t* tok_out = reinterpret_cast<int64_t*>(base + kTokenOffset);
+    int64_t tok;
+    if (idx_dev != nullptr)
+      tok = idx_dev[0];
+    else if (tok_host >= 0)
+      tok = tok_host;
+    else
+      tok = (int64_t)(0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFull));
+    *key = 0ull;
+    *tok_out = tok;
+    params[P_TOKEN] = (int)tok;
     params[P_ROPE] = rope_pos;
     params[P_WRITE] = write_pos;
     params[P_ACTIVE] = active_len;
@@ -52,6 +70,7 @@ struct axm_runner {
   f16* norm = nullptr;
   float* ws = nullptr;
   size_t ws_bytes = 0;
+  int* counters = nullptr;  // split-merge arrival counters (self re-arming)
   int max_splits = 64;
   bool use_graph = true;
   hipStream_t cap_stream = nullptr;
@@ -60,7 +79,7 @@ struct axm_runner {
   ~axm_runner() {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
-    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws};
+    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, counters};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
   }
@@ -118,12 +137,12 @@ struct axm_runner {
         a.kv_stride_h = d.head_dim;
         a.max_seq = 1;
       }
-      int rc = q4m_gemv_launch(a, 1, Q4_EPI_QKV_ROPE, q4m_default_grid(a.n_units), s);
+      int rc = q4m_gemv_launch(a, 1, Q4_EPI_QKV_ROPE, s);
       if (rc) return rc;
       if (d.kv_dtype != AXM_KV_FP16)
         launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
       // 2. attention over slots [0, active_len).
-      rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
+      rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s, counters);
       if (rc) return rc;
       // 3. O projection, residual add into x.
       Q4GemvArgs o{};
@@ -137,7 +156,7 @@ struct axm_runner {
       o.n_units = (D + 7) / 8;
       o.resid = x;
       o.ldr = D;
-      rc = q4m_gemv_launch(o, 1, Q4_EPI_RESID, q4m_default_grid(o.n_units), s);
+      rc = q4m_gemv_launch(o, 1, Q4_EPI_RESID, s);
       if (rc) return rc;
       // 4. gate/up with RMSNorm prologue and SwiGLU epilogue.
       Q4GemvArgs g{};
@@ -154,7 +173,7 @@ struct axm_runner {
       g.ldy = H;
       g.ln_w = (const f16*)ln2[i];
       g.eps = d.eps;
-      rc = q4m_gemv_launch(g, 1, Q4_EPI_SWIGLU, q4m_default_grid(g.n_units), s);
+      rc = q4m_gemv_launch(g, 1, Q4_EPI_SWIGLU, s);
       if (rc) return rc;
       // 5. down projection, residual add.
       Q4GemvArgs dn{};
@@ -168,7 +187,7 @@ struct axm_runner {
       dn.n_units = (D + 7) / 8;
       dn.resid = x;
       dn.ldr = D;
-      rc = q4m_gemv_launch(dn, 1, Q4_EPI_RESID, q4m_default_grid(dn.n_units), s);
+      rc = q4m_gemv_launch(dn, 1, Q4_EPI_RESID, s);
       if (rc) return rc;
     }
     // Final RMSNorm + lm_head.
@@ -187,7 +206,8 @@ struct axm_runner {
       l.ln_w = (const f16*)d.lnf_w;
       l.eps = d.eps;
       l.x_norm_out = norm;
-      int rc = q4m_gemv_launch(l, 1, Q4_EPI_STORE, q4m_default_grid(l.n_units), s);
+      l.argmax_key = reinterpret_cast<unsigned long long*>(reinterpret_cast<unsigned char*>(params) + kArgmaxOffset);
+      int rc = q4m_gemv_launch(l, 1, Q4_EPI_STORE, s);
       if (rc) return rc;
     } else {
       launch_rmsnorm(x, (const f16*)d.lnf_w, norm, 1, D, d.eps, s);
@@ -271,6 +291,7 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
       {(void**)&r->logits, (size_t)T * d.vocab_size * sizeof(f16)},
       {(void**)&r->norm, (size_t)T * d.d_model * sizeof(f16)},
       {(void**)&r->ws, r->ws_bytes > 0 ? r->ws_bytes : 256},
+      {(void**)&r->counters, (size_t)T * d.n_head * sizeof(int)},
   };
   for (auto& al : allocs) {
     if (hipMalloc(al.p, al.bytes) != hipSuccess) {
@@ -280,6 +301,7 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
     }
   }
   if (hipMemset(r->params, 0, 64 * sizeof(int)) != hipSuccess ||
+      hipMemset(r->counters, 0, (size_t)T * d.n_head * sizeof(int)) != hipSuccess ||
       hipStreamCreateWithFlags(&r->cap_stream, hipStreamNonBlocking) != hipSuccess) {
     delete r;
     axm_set_error("runner_create: stream/memset setup failed");
@@ -307,8 +329,10 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
   AXM_CHECK_ARG(active_len >= 1 && active_len <= d.max_seq_len, -1, "runner_step: active_len %d out of [1, %d]",
                 active_len, d.max_seq_len);
   AXM_CHECK_ARG(start_pos >= 0, -1, "runner_step: negative start_pos");
-  AXM_CHECK_ARG(idx_dev != nullptr || (tok_host >= 0 && tok_host < d.vocab_size), -1,
-                "runner_step: token id %lld out of range", (long long)tok_host);
+  AXM_CHECK_ARG(idx_dev != nullptr || tok_host < d.vocab_size, -1, "runner_step: token id %lld out of range",
+                (long long)tok_host);
+  AXM_CHECK_ARG(idx_dev != nullptr || tok_host >= 0 || d.lm_head_format == 0, -1,
+                "runner_step: greedy feedback needs the MARLIN lm_head");
   hipStream_t s = (hipStream_t)stream;
   const int rope_pos = start_pos % d.rope_len;
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(64), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
@@ -355,6 +379,12 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
   }
   AXM_LAUNCH_CHECK("runner_step");
   if (logits_out) *logits_out = r->logits;
+  return 0;
+}
+
+extern "C" int axm_runner_token_slot(axm_runner_t r, void** tok_out) {
+  AXM_CHECK_ARG(r && tok_out, -1, "runner_token_slot: null argument");
+  *tok_out = reinterpret_cast<unsigned char*>(r->params) + kTokenOffset;
   return 0;
 }
 

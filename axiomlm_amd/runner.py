@@ -157,6 +157,23 @@ class QuantizedDecodeRunner:
             self._logits = _RawBuffer.view(out.value, self.vocab_size, self.device).view(1, 1, self.vocab_size)
         return self._logits
 
+    def step_greedy(self, start_pos: int, write_pos: int, active_len: int) -> torch.Tensor:
+        """Decode the greedy argmax of the previous step's logits without a host round trip
+        (the device loop of mps_kernels.mm:3466-3527).  Returns the logits view."""
+        out = ctypes.c_void_p()
+        rc = _lib.lib().axm_runner_step(self._h, None, -1, int(start_pos), int(write_pos), int(active_len),
+                                        _lib.stream_of(self.device), ctypes.byref(out))
+        _lib.check(rc, "QuantizedDecodeRunner.step_greedy")
+        if self._logits is None:
+            self._logits = _RawBuffer.view(out.value, self.vocab_size, self.device).view(1, 1, self.vocab_size)
+        return self._logits
+
+    def last_token(self) -> torch.Tensor:
+        """int64 device view of the token id consumed by the latest step."""
+        p = ctypes.c_void_p()
+        _lib.check(_lib.lib().axm_runner_token_slot(self._h, ctypes.byref(p)), "last_token")
+        return _RawBuffer.view(p.value, 4, self.device).view(torch.int64)
+
     def get_last_norm(self, T: int = 1) -> torch.Tensor:
         """Clone of the final normalized hidden state (mps_kernels.mm:3732-3737)."""
         p = ctypes.c_void_p()

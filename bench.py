@@ -110,15 +110,11 @@ def time_decode(runner, cache, steps, warmup, dev):
     """Greedy decode: argmax of step t (device) is the token of step t+1."""
     import torch
 
-    from axiomlm_amd.kernels import ops
-
-    tok = torch.zeros(1, dtype=torch.int64, device=dev)
     pos = CTX0
+    runner.step(torch.zeros(1, dtype=torch.int64, device=dev), pos - 1, pos - 1, pos)
 
     def one(p):
-        logits = runner.step(tok, p, p, p + 1)
-        nxt = ops.argmax_last_token(logits.view(1, -1))
-        tok.copy_(nxt.view(1))
+        runner.step_greedy(p, p, p + 1)
 
     for i in range(warmup):
         one(pos + i)

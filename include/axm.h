@@ -165,11 +165,16 @@ typedef struct axm_runner* axm_runner_t;
 int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out);
 void axm_runner_destroy(axm_runner_t r);
 /* One decode token.  The token id comes from idx_dev (int64, device) when
- * non-NULL, otherwise from tok_host.  Positions follow transformer.py:1453-1462.
+ * non-NULL, else from tok_host when >= 0, else (tok_host < 0) from the greedy
+ * argmax of the previous step's logits (lowest index on ties), computed inside
+ * the lm_head launch -- the device-side loop of speculative_decode / greedy
+ * generation (mps_kernels.mm:3466-3527).  Positions follow transformer.py:1453-1462.
  * *logits_out receives the runner's persistent fp16 [V] buffer (valid until the
  * next call).  Replaces QuantizedDecodeGraphState::step (mps_kernels.mm:3195-3263). */
 int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_host, int start_pos, int write_pos,
                     int active_len, void* stream, void** logits_out);
+/* Device int64 slot holding the token id consumed by the latest step. */
+int axm_runner_token_slot(axm_runner_t r, void** tok_out);
 /* Normalized final hidden state of the last call (fp16 [T][d]),
  * get_last_norm (mps_kernels.mm:3732-3737). */
 int axm_runner_last_norm(axm_runner_t r, void** norm_out);
