@@ -28,6 +28,9 @@ _SIGNATURES = {
     "axm_qmv_q4_marlin_swiglu": (
         c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]
     ),
+    "axm_tile16_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "axm_repack_q4_marlin_tile16": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "axm_qmv_q4_tile16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "axm_dequantize_q4_marlin": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "axm_pack_q4_marlin_rtn": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "axm_pack_q4_marlin_mse": (
@@ -86,7 +89,7 @@ class RunnerDesc(ctypes.Structure):
         ("down_w", ctypes.POINTER(c_void_p)), ("down_sb", ctypes.POINTER(c_void_p)),
         ("k_cache", ctypes.POINTER(c_void_p)), ("v_cache", ctypes.POINTER(c_void_p)),
         ("k_scales", ctypes.POINTER(c_void_p)), ("v_scales", ctypes.POINTER(c_void_p)),
-        ("max_tokens", c_int),
+        ("max_tokens", c_int), ("layout", c_int),
     ]
 
 

@@ -125,7 +125,6 @@ struct AttnParams {
   int write_pos;          // slot of tree node 0
   const uint64_t* masks;  // [T] ancestor bitmasks (tree mode)
   float scale_log2;       // log2(e) / sqrt(hd)
-  int* counters;          // optional arrival counters (zeroed, one per row group): fused split merge
 };
 
 // Rows of one workgroup: decode -> (b, kv head, replica r) with r < n_rep;
@@ -298,37 +297,6 @@ __global__ void __launch_bounds__(kAttnThreads) attn_split_kernel(AttnParams p) 
       dst[2 + e] = oo;
     }
   }
-  if (p.n_splits == 1 || p.counters == nullptr) return;
-
-  // Split merge by the last workgroup of this row group to finish (no second
-  // launch): release the partials, count arrivals, the last one acquires and
-  // merges, then re-arms the counter for the next call / graph replay.
-  __shared__ int is_last;
-  __threadfence();
-  __syncthreads();
-  const int cidx = blockIdx.x + gridDim.x * blockIdx.z;
-  if (threadIdx.x == 0) is_last = (atomicAdd(&p.counters[cidx], 1) == p.n_splits - 1);
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int idx = threadIdx.x; idx < QR * hd; idx += kAttnThreads) {
-    const int r = idx / hd, e = idx % hd;
-    if (r >= n_rows) continue;
-    const int gr = (!TREE) ? (b * p.Hq + kvh * p.n_rep + row_base + r)
-                           : (((row_base + r) / p.n_rep) * p.Hq + kvh * p.n_rep + (row_base + r) % p.n_rep);
-    const float* base = p.ws + (size_t)gr * p.n_splits * (2 + hd);
-    float mm = kNegBig;
-    for (int s = 0; s < p.n_splits; ++s) mm = fmaxf(mm, __builtin_nontemporal_load(base + (size_t)s * (2 + hd)));
-    float ll = 0.f, oo = 0.f;
-    for (int s = 0; s < p.n_splits; ++s) {
-      const float* ps = base + (size_t)s * (2 + hd);
-      const float a = exp2f(__builtin_nontemporal_load(ps) - mm);
-      ll += __builtin_nontemporal_load(ps + 1) * a;
-      oo += __builtin_nontemporal_load(ps + 2 + e) * a;
-    }
-    p.out[(size_t)gr * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
-  }
-  if (threadIdx.x == 0) atomicExch(&p.counters[cidx], 0);
 }
 
 // Merge split partials: one block per query row, hd threads.
@@ -407,7 +375,7 @@ int attn_choose_splits(int B, int Hkv, int active_len) {
 }
 
 int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,
-                        int n_splits, float* ws, hipStream_t s, int* counters) {
+                        int n_splits, float* ws, hipStream_t s) {
   AttnParams p{};
   p.q = q;
   p.kv = kv;
@@ -420,12 +388,11 @@ int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int ac
   p.prefix_dev = active_len_dev;
   p.T = 0;
   p.scale_log2 = kLog2e / sqrtf((float)kv.hd);
-  p.counters = counters;
   const int qr = pick_qr(p.n_rep);
   dim3 grid(kv.B * kv.Hkv, n_splits, (p.n_rep + qr - 1) / qr);
   int rc = launch_attn_dispatch<false>(p, qr, grid, s);
   if (rc) return rc;
-  if (n_splits > 1 && counters == nullptr)
+  if (n_splits > 1)
     hipLaunchKernelGGL(attn_reduce_kernel, dim3(kv.B * Hq), dim3(kv.hd), 0, s, ws, out, n_splits, kv.hd);
   return 0;
 }
@@ -497,7 +464,7 @@ extern "C" int axm_gqa_flash_decode(const void* q, const void* k_cache, const vo
   AXM_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace), -1,
                 "gqa_flash_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   int rc = launch_flash_decode((const f16*)q, kv, (f16*)out, n_head, active_len, nullptr, num_splits,
-                               (float*)workspace, (hipStream_t)stream, nullptr);
+                               (float*)workspace, (hipStream_t)stream);
   if (rc) return rc;
   AXM_LAUNCH_CHECK("gqa_flash_decode");
   return 0;

@@ -47,10 +47,8 @@ int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int 
 // attn_workspace_bytes(); active_len_dev overrides active_len when non-null.
 size_t attn_workspace_bytes(int B, int Hq, int hd, int n_splits);
 int attn_choose_splits(int B, int Hkv, int active_len);
-// counters: optional zero-initialised ints (>= B*Hq) that enable the in-kernel
-// split merge; they are re-armed by the kernel itself.
 int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,
-                        int n_splits, float* ws, hipStream_t s, int* counters = nullptr);
+                        int n_splits, float* ws, hipStream_t s);
 
 // Tree / multi-token verification attention (batch 0): T query tokens; prefix
 // slots [0, prefix_len) always visible; tree node j lives at slot

@@ -42,9 +42,10 @@ struct Q4GemvArgs {
   long kv_stride_h;    // elements between kv heads (max_seq * head_dim)
   int max_seq;
   int split;           // waves per unit (set by q4m_gemv_launch)
-  // Q4_EPI_STORE, M == 1: optional running argmax of the fp16 outputs as an
-  // ordered 64-bit key (value order, then lowest index), updated by atomicMax.
-  unsigned long long* argmax_key;
+  // Q4_EPI_STORE, M == 1: optional per-unit argmax of the fp16 outputs as an
+  // ordered 64-bit key (value order, then lowest index); keys[unit] is written
+  // by every launch, so the array needs no reset.
+  unsigned long long* argmax_keys;
 };
 
 size_t q4m_gemv_smem_bytes(int M, int NT, int K);

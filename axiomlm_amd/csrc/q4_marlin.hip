@@ -212,7 +212,7 @@ __device__ __forceinline__ void q4_epilogue(const Q4GemvArgs& a, int unit, int l
     }
     return;
   }
-  if (EPI == Q4_EPI_STORE && M == 1 && a.argmax_key != nullptr) {
+  if (EPI == Q4_EPI_STORE && M == 1 && a.argmax_keys != nullptr) {
     // Ordered key: fp16 value (sign-folded) in the high word, ~index in the low
     // word, so the max is the largest logit with the lowest index on ties.
     unsigned long long key = 0ull;
@@ -227,7 +227,7 @@ __device__ __forceinline__ void q4_epilogue(const Q4GemvArgs& a, int unit, int l
       const unsigned long long other = __shfl_xor(key, o, 64);
       key = other > key ? other : key;
     }
-    if (lane == 0) atomicMax(a.argmax_key, key);
+    if (lane == 0) a.argmax_keys[unit] = key;
   }
   if (lane >= 8 || row >= a.N) return;
 #pragma unroll

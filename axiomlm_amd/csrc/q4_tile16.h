@@ -1,0 +1,46 @@
+// Internal interface of the tile16 (MFMA) MARLIN Q4 GEMV used by the decode runner.
+#pragma once
+#include "axm_common.h"
+#include "q4_marlin.h"  // Q4_EPI_* epilogue codes
+
+struct T16Args {
+  const f16* x;        // [M][ldx] activations
+  int ldx;
+  const u32x4* w16;    // [N16][KB][64] x 16 B
+  const u32x2* sb16;   // [N16][KB][16] x 8 B (two groups of (scale, bias))
+  int K, KB, N;        // N = valid output rows
+  int N_rows_alloc;    // rows the w16 / sb16 arrays were packed for (2 H for gate/up)
+  size_t w16_bytes, sb16_bytes;  // set by t16_gemv_launch (buffer bounds)
+  int n_units;         // tile16 units (gate tiles for SWIGLU)
+  f16* y;
+  int ldy;
+  const f16* bias;
+  const f16* ln_w;     // optional fused RMSNorm (torch-CPU fp16 semantics)
+  float eps;
+  f16* x_norm_out;     // optional export of the normalized activations [M][K]
+  f16* resid;          // Q4_EPI_RESID
+  int ldr;
+  int pair_offset;     // Q4_EPI_SWIGLU: tile16 distance from a gate tile to its up tile
+  int q_dim, kv_dim, head_dim;  // Q4_EPI_QKV_ROPE
+  const float* freqs;
+  int rope_len;
+  int rope_pos;
+  const int* rope_pos_dev;
+  int write_pos;
+  const int* write_pos_dev;
+  f16* k_out;
+  f16* v_out;
+  long kv_stride_h;
+  int max_seq;
+  unsigned long long* argmax_keys;  // Q4_EPI_STORE, M == 1: per-unit ordered (logit, index) key
+  int split;           // waves per unit (set by t16_gemv_launch)
+  uint32_t unpack[4];  // nibble masks and fp16 magic exponents (set by t16_gemv_launch)
+};
+
+size_t t16_smem_bytes(int M, int NT, int K);
+void t16_prepare_attributes();
+// Picks split / grid (a.split is overwritten); M in [1, 4].
+int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s);
+int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16, hipStream_t s);
+size_t t16_weight_bytes(int N, int K);
+size_t t16_sb_bytes(int N, int K);

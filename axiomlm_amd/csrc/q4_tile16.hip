@@ -1,0 +1,542 @@
+// Runner-native MARLIN Q4 layout and its MFMA GEMV for gfx950.
+//
+// The reference MARLIN layout (8-row tiles, quant.py:573-593) pairs two rows in
+// every 16-bit half, which suits a SIMD-group FMA but not a matrix core.  The
+// decode runner therefore re-tiles the codes once, bit-exactly, into "tile16":
+//
+//   w16  [N16][KB][64 lanes][4 words] u32     N16 = ceil(N/16), KB = ceil(K/128)
+//        lane l, word c  ->  row j = l % 16 of the tile,
+//                            k = 128 kb + 32 c + 8 (l / 16) + i,  i = 0..7
+//        slot i sits at bits  i0:0-3  i1:16-19  i2:4-7  i3:20-23
+//                             i4:8-11 i5:24-27  i6:12-15 i7:28-31
+//   sb16 [N16][KB][16 rows][2 groups] (f16 scale, f16 bias), groups 2kb, 2kb+1
+//
+// so one dwordx4 per lane (1 KB per wave) is exactly the B operand of four
+// v_mfma_f32_16x16x32_f16 (16 rows x 128 k).  Each word expands with four
+// AND-ORs into fp16 (1024 + q | 64 + q) pairs; the magic offsets are removed
+// once per group with a precomputed sum of the activations, and the per-group
+// (scale, bias) are applied to the 16 x 16 accumulator tile after the two MFMAs
+// of that group.  Padding rows / columns carry code 0 with scale 0 and bias 0.
+//
+// The activation tile (A operand: token = lane % 16, k = 8 (lane / 16) + i)
+// is read from LDS; tokens >= M read a zero block.
+#include "kernels.h"
+#include "q4_tile16.h"
+
+namespace {
+
+constexpr int kT16Threads = 512;
+constexpr int kT16Waves = kT16Threads / 64;
+
+// Reference lane holding (r, even column c0) of an 8-row MARLIN tile
+// (inverse of quant.py:573-576).
+__device__ __forceinline__ int marlin_lane_of(int r, int c0) {
+  return ((r >> 2) << 4) | ((c0 >> 2) << 3) | ((r & 3) << 1) | ((c0 >> 1) & 1);
+}
+
+// One thread per (tile16, kb, lane): the four words of that lane.
+__global__ void repack_tile16_kernel(const uint32_t* __restrict__ wm, const f16x2* __restrict__ sbm, int N_pad8,
+                                     int K, uint32_t* __restrict__ w16, f16x2* __restrict__ sb16, int N16, int KB) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)N16 * KB * 64) return;
+  const int l = (int)(idx & 63);
+  const long tk = idx >> 6;
+  const int kb = (int)(tk % KB);
+  const int t16 = (int)(tk / KB);
+  const int KG = K / 64;
+  const int row = t16 * 16 + (l & 15);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int k = 128 * kb + 32 * c + 8 * (l >> 4) + i;
+      uint32_t q = 0;
+      if (row < N_pad8 && k < K) {
+        const int tile = row >> 3, cin = row & 7, g = k >> 6, kk = k & 63;
+        const int j = kk >> 5, s = (kk >> 3) & 3, r = kk & 7;
+        const int lane = marlin_lane_of(r, cin & ~1);
+        const uint32_t rw = wm[(((size_t)tile * KG + g) * 32 + lane) * 2 + j];
+        q = (rw >> (16 * (cin & 1) + 4 * s)) & 0xFu;
+      }
+      const int pos = (i & 1) ? 16 + 4 * (i >> 1) : 4 * (i >> 1);
+      word |= q << pos;
+    }
+    w16[idx * 4 + c] = word;
+  }
+  if (l < 16) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int g = 2 * kb + h;
+      f16x2 v = f16x2{f16(0), f16(0)};
+      if (row < N_pad8 && g < KG) v = sbm[((size_t)(row >> 3) * KG + g) * 8 + (row & 7)];
+      sb16[(((size_t)t16 * KB + kb) * 16 + l) * 2 + h] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Activation staging: xs [M][K_pad] f16 (normalized if ln_w), zero block,
+// cx [M][2 KB] float2 (magic-offset-weighted sum, plain sum) per 64-group.
+// ---------------------------------------------------------------------------
+template <int M>
+__device__ void t16_stage_x(const T16Args& a, f16* xs, f32x2* cx, float* red) {
+  const int tid = threadIdx.x;
+  const int K = a.K;
+  const int nv = K >> 3;
+  const int nv_pad = (a.KB * 128) >> 3;
+  float rinv[M];
+#pragma unroll
+  for (int mi = 0; mi < M; ++mi) rinv[mi] = 1.f;
+  if (a.ln_w != nullptr) {
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) {
+      const f16x8* xr = reinterpret_cast<const f16x8*>(a.x + (size_t)mi * a.ldx);
+      float s = 0.f;
+      for (int i = tid; i < nv; i += kT16Threads) {
+        const f16x8 v = xr[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = h2f(v[e]);
+          s += h2f(f2h(f * f));
+        }
+      }
+      s = wave_sum(s);
+      if ((tid & 63) == 0) red[mi * kT16Waves + (tid >> 6)] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < kT16Waves; ++w) s += red[mi * kT16Waves + w];
+      rinv[mi] = rms_inv_fp16(s, K, a.eps);
+    }
+  }
+  const f16x8* wr = reinterpret_cast<const f16x8*>(a.ln_w);
+#pragma unroll
+  for (int mi = 0; mi < M; ++mi) {
+    const f16x8* xr = reinterpret_cast<const f16x8*>(a.x + (size_t)mi * a.ldx);
+    // nv_pad is a multiple of 16 (KB*128/8), so the 8-lane group reduction below
+    // always runs with full wave participation.
+    for (int i0 = 0; i0 < nv_pad; i0 += kT16Threads) {
+      const int i = i0 + tid;
+      f16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = f16(0);
+      if (i < nv) {
+        v = xr[i];
+        if (a.ln_w != nullptr) {
+          const f16x8 w = wr[i];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = f2h(h2f(f2h(h2f(v[e]) * rinv[mi])) * h2f(w[e]));
+        }
+        if (a.x_norm_out != nullptr) reinterpret_cast<f16x8*>(a.x_norm_out + (size_t)mi * K)[i] = v;
+      }
+      float corr = 0.f, sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = h2f(v[e]);
+        sum += f;
+        corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
+      }
+      // 8 consecutive vectors form one 64-group.
+      corr = group_sum<8>(corr);
+      sum = group_sum<8>(sum);
+      if (i < nv_pad) {
+        reinterpret_cast<f16x8*>(xs + (size_t)mi * a.KB * 128)[i] = v;
+        if ((tid & 7) == 0) cx[(size_t)mi * 2 * a.KB + (i >> 3)] = f32x2{corr, sum};
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Nibble expansion: (w & mask) | magic as one v_and_or_b32.  gfx950 VOP3 takes
+// neither literals nor two scalar operands, so the masks live in VGPRs (loop
+// invariant) and the magic exponents in SGPRs; without the explicit instruction
+// the compiler splits every expansion into an AND plus an OR.
+struct Unpack {
+  uint32_t m_lo, m_hi, g_lo, g_hi;  // 0x000F000F, 0x00F000F0, 0x64006400, 0x54005400
+};
+
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask_v, uint32_t magic_s) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(mask_v), "s"(magic_s));
+  return r;
+}
+
+__device__ __forceinline__ f16x8 unpack_word(uint32_t w, const Unpack& u) {
+  const uint32_t w8 = w >> 8;
+  const u32x4 h = {and_or(w, u.m_lo, u.g_lo), and_or(w, u.m_hi, u.g_hi), and_or(w8, u.m_lo, u.g_lo),
+                   and_or(w8, u.m_hi, u.g_hi)};
+  return __builtin_bit_cast(f16x8, h);
+}
+
+__device__ __forceinline__ float t16_silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Epilogue for lane l: row = unit*16 + l%16, token = 4*(l/16) + v.
+template <int M, int NT, int EPI>
+__device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lane, const float (&v)[NT][4]) {
+  const int j = lane & 15;
+  const int row = unit * 16 + j;
+  if (EPI == Q4_EPI_STORE && M == 1 && a.argmax_keys != nullptr) {
+    unsigned long long key = 0ull;
+    if (lane < 16 && row < a.N) {
+      const uint32_t u = __builtin_bit_cast(uint32_t, h2f(f2h(v[0][0])));
+      const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+      key = ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (uint32_t)row);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const unsigned long long other = __shfl_xor(key, o, 64);
+      key = other > key ? other : key;
+    }
+    if (lane == 0) a.argmax_keys[unit] = key;
+  }
+#pragma unroll
+  for (int vi = 0; vi < 4; ++vi) {
+    const int tok = 4 * (lane >> 4) + vi;
+    if (EPI == Q4_EPI_QKV_ROPE) {
+      const float partner = __shfl_xor(v[0][vi], 1, 64);
+      if (tok >= M || row >= a.N) continue;
+      const bool even = (row & 1) == 0;
+      f16 h_self = f2h(v[0][vi]);
+      f16 h_part = f2h(partner);
+      if (a.bias != nullptr) {
+        h_self = f2h(h2f(h_self) + h2f(a.bias[row]));
+        h_part = f2h(h2f(h_part) + h2f(a.bias[row ^ 1]));
+      }
+      const f16 h0 = even ? h_self : h_part;
+      const f16 h1 = even ? h_part : h_self;
+      const int row0 = row & ~1;
+      const int hd = a.head_dim, half_hd = hd >> 1;
+      f16 out = h_self;
+      if (row0 < a.q_dim + a.kv_dim) {
+        const int pos = (a.rope_pos_dev ? a.rope_pos_dev[0] : a.rope_pos) + tok;
+        const int within = row0 < a.q_dim ? row0 : row0 - a.q_dim;
+        const int fi = (within % hd) >> 1;
+        const int rp = pos % a.rope_len;
+        const float c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
+        const float sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
+        const float x0 = h2f(h0), x1 = h2f(h1);
+        out = even ? f2h(x0 * c - x1 * sn) : f2h(x0 * sn + x1 * c);
+      }
+      if (row < a.q_dim) {
+        a.y[(size_t)tok * a.ldy + row] = out;
+      } else {
+        const bool is_k = row < a.q_dim + a.kv_dim;
+        const int within = is_k ? row - a.q_dim : row - a.q_dim - a.kv_dim;
+        const int kvh = within / hd, e = within % hd;
+        const int wp = (a.write_pos_dev ? a.write_pos_dev[0] : a.write_pos) + tok;
+        f16* dst = (is_k ? a.k_out : a.v_out) + ((size_t)kvh * a.kv_stride_h + (size_t)(wp % a.max_seq) * hd + e);
+        *dst = out;
+      }
+      continue;
+    }
+    if (tok >= M || row >= a.N) continue;
+    if (EPI == Q4_EPI_SWIGLU) {
+      const f16 g = f2h(v[0][vi]);
+      const f16 u = f2h(v[NT - 1][vi]);
+      const f16 sg = f2h(t16_silu(h2f(g)));
+      a.y[(size_t)tok * a.ldy + row] = f2h(h2f(sg) * h2f(u));
+    } else {
+      f16 h = f2h(v[0][vi]);
+      if (a.bias != nullptr) h = f2h(h2f(h) + h2f(a.bias[row]));
+      if (EPI == Q4_EPI_STORE) {
+        a.y[(size_t)tok * a.ldy + row] = h;
+      } else {
+        f16* xr = a.resid + (size_t)tok * a.ldr + row;
+        *xr = f2h(h2f(*xr) + h2f(h));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMV.  Unit = one tile16 (or a gate/up pair, NT = 2).  S = a.split
+// waves share a unit (split-K over kb); 8 / S units per workgroup pass.
+// S == 1 runs a persistent loop; S > 1 needs one pass (grid covers all units).
+// P kb-loads (1 KB per tile each) stay in flight per wave.
+// ---------------------------------------------------------------------------
+template <int M, int NT, int EPI, int P>
+__global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  f16* xs = reinterpret_cast<f16*>(smem);                                   // [M][KB*128]
+  f16* zero = xs + (size_t)M * a.KB * 128;                                   // 16 halves of zeros
+  f32x2* cx = reinterpret_cast<f32x2*>(zero + 16);                           // [M][2 KB]
+  float* red = reinterpret_cast<float*>(cx + (size_t)M * 2 * a.KB);          // [waves][NT][4][64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int S = a.split;
+  const int upw = kT16Waves / S;
+  const int sub = wave % S;
+  const int slot = wave / S;
+  // Contiguous kb range [kb0, kb0 + my) of this wave within a unit.
+  const int per = (a.KB + S - 1) / S;
+  const int kb0 = sub * per;
+  const int my = max(0, min(per, a.KB - kb0));
+  const int tokA = lane & 15;  // A-operand token of this lane
+  const int kq = lane >> 4;    // 8-wide k sub-block of this lane
+  const Unpack U{a.unpack[0], a.unpack[1], a.unpack[2], a.unpack[3]};
+
+  // Raw buffer descriptors: out-of-range offsets read as zero, so every chunk
+  // load is issued unconditionally and the load pipeline stays static.
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w16, (short)0, (int)a.w16_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.sb16, (short)0, (int)a.sb16_bytes, 0x00020000);
+  constexpr int kOOB = 0x7FFFFFF0;
+
+  if (tid < 8) reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
+
+  u32x4 wr[P][NT];
+  u32x2 sr[P][NT];
+  // Byte offsets of (unit, ci) for this lane, OOB when outside the wave's range.
+  auto load = [&](int unit, int ci, int j) {
+    const bool ok = unit < a.n_units && ci < my;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int base = (unit + t * a.pair_offset) * a.KB + kb0 + ci;
+      const int wo = ok ? (base * 64 + lane) * 16 : kOOB;
+      const int so = ok ? (base * 16 + (lane & 15)) * 8 : kOOB;
+      wr[j][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
+      sr[j][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+    }
+  };
+
+  int it = 0;
+  int unit = blockIdx.x * upw + slot;
+#pragma unroll
+  for (int j = 0; j < P; ++j) load(unit, j, j);
+  t16_stage_x<M>(a, xs, cx, red);
+
+  // LDS addresses: A operand of this lane and (corr, sum) of its D tokens.
+  const f16* xa = (tokA < M) ? xs + (size_t)tokA * a.KB * 128 + 8 * kq : zero;
+  const int a_kb = (tokA < M) ? 128 : 0;
+  const int a_c = (tokA < M) ? 32 : 0;
+
+  while (true) {
+    float acc[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int vi = 0; vi < 4; ++vi) acc[t][vi] = 0.f;
+
+    for (int ci0 = 0; ci0 < my; ci0 += P) {
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const int ci = ci0 + j;
+        // Chunks past the range carry zero codes and zero scales: clamp the LDS
+        // reads to a valid kb so they only ever multiply finite values by zero.
+        const int kb = kb0 + min(ci, my - 1);
+        const f16* xk = xa + kb * a_kb;
+        f16x8 A[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) A[c] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + c * a_c));
+        f32x4 cxv[4];
+#pragma unroll
+        for (int vi = 0; vi < 4; ++vi) {
+          if (vi < M) {
+            const int tok = min(4 * kq + vi, M - 1);
+            cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (size_t)tok * 2 * a.KB + 2 * kb);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+          f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], unpack_word(wr[j][t][0], U), z4, 0, 0, 0);
+          f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], unpack_word(wr[j][t][2], U), z4, 0, 0, 0);
+          d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], unpack_word(wr[j][t][1], U), d0, 0, 0, 0);
+          d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], unpack_word(wr[j][t][3], U), d1, 0, 0, 0);
+          const f16x2 sb0 = as_h2(sr[j][t][0]);
+          const f16x2 sb1 = as_h2(sr[j][t][1]);
+#pragma unroll
+          for (int vi = 0; vi < 4; ++vi) {
+            if (vi < M) {
+              float r = acc[t][vi];
+              r = __builtin_fmaf(h2f(sb0.x), d0[vi] - cxv[vi][0], r);
+              r = __builtin_fmaf(h2f(sb0.y), cxv[vi][1], r);
+              r = __builtin_fmaf(h2f(sb1.x), d1[vi] - cxv[vi][2], r);
+              r = __builtin_fmaf(h2f(sb1.y), cxv[vi][3], r);
+              acc[t][vi] = r;
+            }
+          }
+        }
+        load(unit, ci + P, j);
+      }
+    }
+
+    const int next_unit = (blockIdx.x + (it + 1) * gridDim.x) * upw + slot;
+    const bool more = (S == 1) && ((blockIdx.x + (it + 1) * gridDim.x) * upw < a.n_units);
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < P; ++j) load(next_unit, j, j);
+    }
+    if (S > 1) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int vi = 0; vi < 4; ++vi)
+          if (vi < M) red[((wave * NT + t) * 4 + vi) * 64 + lane] = acc[t][vi];
+      __syncthreads();
+      if (sub == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int vi = 0; vi < 4; ++vi)
+            if (vi < M) {
+              float s = 0.f;
+              for (int w = wave; w < wave + S; ++w) s += red[((w * NT + t) * 4 + vi) * 64 + lane];
+              acc[t][vi] = s;
+            }
+      }
+    }
+    if (sub == 0 && unit < a.n_units) t16_epilogue<M, NT, EPI>(a, unit, lane, acc);
+    if (!more) break;
+    ++it;
+    unit = next_unit;
+  }
+}
+
+template <int NT>
+struct T16Depth {
+  static constexpr int value = NT == 2 ? 4 : 8;
+};
+
+template <int M, int NT, int EPI>
+void t16_set_attr() {
+  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+    (void)hipGetLastError();
+}
+
+template <int M, int NT, int EPI>
+int t16_launch_one(const T16Args& a, int grid, size_t smem, hipStream_t s) {
+  hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value>), dim3(grid), dim3(kT16Threads), smem, s, a);
+  return 0;
+}
+
+}  // namespace
+
+size_t t16_smem_bytes(int M, int NT, int K) {
+  const int KB = (K + 127) / 128;
+  return (size_t)M * KB * 128 * sizeof(f16) + 32 + (size_t)M * 2 * KB * sizeof(f32x2) +
+         (size_t)kT16Waves * NT * 4 * 64 * sizeof(float);
+}
+
+void t16_prepare_attributes() {
+  static bool done = false;
+  if (done) return;
+  done = true;
+#define AXM_T16_ATTR(MM)                      \
+  t16_set_attr<MM, 1, Q4_EPI_STORE>();        \
+  t16_set_attr<MM, 1, Q4_EPI_RESID>();        \
+  t16_set_attr<MM, 2, Q4_EPI_SWIGLU>();       \
+  t16_set_attr<MM, 1, Q4_EPI_QKV_ROPE>();
+  AXM_T16_ATTR(1)
+  AXM_T16_ATTR(2)
+  AXM_T16_ATTR(3)
+  AXM_T16_ATTR(4)
+#undef AXM_T16_ATTR
+}
+
+int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
+  t16_prepare_attributes();
+  const int NT = (epi == Q4_EPI_SWIGLU) ? 2 : 1;
+  const size_t smem = t16_smem_bytes(M, NT, a.K);
+  if (smem > 160 * 1024 || M < 1 || M > 4) {
+    axm_set_error("tile16 gemv: M=%d K=%d needs %zu B of LDS", M, a.K, smem);
+    return -2;
+  }
+  // Waves per unit: aim for ~8 waves per CU with >= 2 kb-loads per wave.
+  const int cus = axm_num_cus();
+  int S = 1;
+  while (S < kT16Waves && a.n_units * S < 8 * cus && a.KB >= 4 * S) S *= 2;
+  a.split = S;
+  a.w16_bytes = t16_weight_bytes(a.N_rows_alloc, a.K);
+  a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K);
+  a.unpack[0] = 0x000F000Fu;
+  a.unpack[1] = 0x00F000F0u;
+  a.unpack[2] = 0x64006400u;
+  a.unpack[3] = 0x54005400u;
+  const int upw = kT16Waves / S;
+  int grid = (a.n_units + upw - 1) / upw;
+  if (S == 1 && grid > 2 * cus) grid = 2 * cus;
+#define AXM_T16_CASE(MM)                                                                 \
+  case MM:                                                                               \
+    switch (epi) {                                                                       \
+      case Q4_EPI_STORE: return t16_launch_one<MM, 1, Q4_EPI_STORE>(a, grid, smem, s);   \
+      case Q4_EPI_RESID: return t16_launch_one<MM, 1, Q4_EPI_RESID>(a, grid, smem, s);   \
+      case Q4_EPI_SWIGLU: return t16_launch_one<MM, 2, Q4_EPI_SWIGLU>(a, grid, smem, s); \
+      case Q4_EPI_QKV_ROPE: return t16_launch_one<MM, 1, Q4_EPI_QKV_ROPE>(a, grid, smem, s); \
+    }                                                                                    \
+    break;
+  switch (M) {
+    AXM_T16_CASE(1)
+    AXM_T16_CASE(2)
+    AXM_T16_CASE(3)
+    AXM_T16_CASE(4)
+  }
+#undef AXM_T16_CASE
+  axm_set_error("tile16 gemv: unsupported epilogue %d", epi);  // unreachable for valid codes
+  return -2;
+}
+
+int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16, hipStream_t s) {
+  const int n_tiles8 = (N + 7) / 8;
+  const int N16 = (N + 15) / 16;
+  const int KB = (K + 127) / 128;
+  const long total = (long)N16 * KB * 64;
+  hipLaunchKernelGGL(repack_tile16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     (const uint32_t*)w_marlin, (const f16x2*)sb_marlin, n_tiles8 * 8, K, (uint32_t*)w16,
+                     (f16x2*)sb16, N16, KB);
+  return 0;
+}
+
+size_t t16_weight_bytes(int N, int K) { return (size_t)((N + 15) / 16) * ((K + 127) / 128) * 64 * 16; }
+size_t t16_sb_bytes(int N, int K) { return (size_t)((N + 15) / 16) * ((K + 127) / 128) * 16 * 8; }
+
+// ---------------------------------------------------------------------------
+// C ABI: repack + GEMV on the tile16 layout (the runner uses the same code).
+// ---------------------------------------------------------------------------
+extern "C" size_t axm_tile16_bytes(int N, int K, int which) {
+  return which == 0 ? t16_weight_bytes(N, K) : t16_sb_bytes(N, K);
+}
+
+extern "C" int axm_repack_q4_marlin_tile16(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16,
+                                           void* sb16, void* stream) {
+  AXM_CHECK_ARG(w_marlin && sb_marlin && w16 && sb16, -1, "repack_tile16: null pointer");
+  AXM_CHECK_ARG(N > 0 && K > 0 && K % 64 == 0, -1, "repack_tile16: bad shape N=%d K=%d", N, K);
+  t16_repack(w_marlin, sb_marlin, N, K, w16, sb16, (hipStream_t)stream);
+  AXM_LAUNCH_CHECK("repack_tile16");
+  return 0;
+}
+
+extern "C" int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M,
+                                 int K, int N, void* stream) {
+  AXM_CHECK_ARG(x && w16 && sb16 && y, -1, "qmv_q4_tile16: null pointer");
+  AXM_CHECK_ARG(K > 0 && K % 64 == 0 && N > 0 && M >= 1, -1, "qmv_q4_tile16: bad shape M=%d K=%d N=%d", M, K, N);
+  for (int m0 = 0; m0 < M; m0 += 4) {
+    const int mc = (M - m0) < 4 ? (M - m0) : 4;
+    T16Args a{};
+    a.x = (const f16*)x + (size_t)m0 * K;
+    a.ldx = K;
+    a.w16 = (const u32x4*)w16;
+    a.sb16 = (const u32x2*)sb16;
+    a.K = K;
+    a.KB = (K + 127) / 128;
+    a.N = N;
+    a.n_units = (N + 15) / 16;
+    a.N_rows_alloc = N;
+    a.y = (f16*)y + (size_t)m0 * N;
+    a.ldy = N;
+    a.bias = (const f16*)bias;
+    int rc = t16_gemv_launch(a, mc, Q4_EPI_STORE, (hipStream_t)stream);
+    if (rc) return rc;
+  }
+  AXM_LAUNCH_CHECK("qmv_q4_tile16");
+  return 0;
+}

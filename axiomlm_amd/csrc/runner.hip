@@ -19,32 +19,42 @@
 
 #include "axm.h"
 #include "kernels.h"
+#include "q4_tile16.h"
 
 namespace {
 
 enum { P_TOKEN = 0, P_ROPE = 1, P_WRITE = 2, P_ACTIVE = 3, P_COUNT = 4 };
-// Byte offsets inside the parameter block: running argmax key of the lm_head
-// (u64) and the int64 token id used by the current step.
-constexpr int kArgmaxOffset = 64;
+// Byte offset inside the parameter block of the int64 token id used by the
+// current step.
 constexpr int kTokenOffset = 72;
 
 // Token source: idx_dev[0] if non-null, else tok_host if >= 0, else the greedy
-// argmax of the previous step's logits.  Resets the argmax key for this step.
-__global__ void set_params_kernel(int* params, const int64_t* idx_dev, int64_t tok_host, int rope_pos,
-                                  int write_pos, int active_len) {
+// argmax of the previous step's logits, reduced here from the per-tile keys the
+// lm_head launch wrote (largest fp16 logit, lowest index on ties).
+__global__ void __launch_bounds__(256) set_params_kernel(int* params, const int64_t* idx_dev, int64_t tok_host,
+                                                         int rope_pos, int write_pos, int active_len,
+                                                         const unsigned long long* keys, int n_keys) {
+  __shared__ unsigned long long red[4];
+  int64_t tok = 0;
+  if (idx_dev == nullptr && tok_host < 0) {
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < n_keys; i += 256) best = keys[i] > best ? keys[i] : best;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const unsigned long long other = __shfl_xor(best, o, 64);
+      best = other > best ? other : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    best = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) best = red[w] > best ? red[w] : best;
+    tok = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+  } else {
+    tok = idx_dev != nullptr ? idx_dev[0] : tok_host;
+  }
   if (threadIdx.x == 0) {
-    unsigned char* base = reinterpret_cast<unsigned char*>(params);
-    unsigned long long* key = reinterpret_cast<unsigned long long*>(base + kArgmaxOffset);
-    int64_t* tok_out = reinterpret_cast<int64_t*>(base + kTokenOffset);
-    int64_t tok;
-    if (idx_dev != nullptr)
-      tok = idx_dev[0];
-    else if (tok_host >= 0)
-      tok = tok_host;
-    else
-      tok = (int64_t)(0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFull));
-    *key = 0ull;
-    *tok_out = tok;
+    *reinterpret_cast<int64_t*>(reinterpret_cast<unsigned char*>(params) + kTokenOffset) = tok;
     params[P_TOKEN] = (int)tok;
     params[P_ROPE] = rope_pos;
     params[P_WRITE] = write_pos;
@@ -54,9 +64,100 @@ __global__ void set_params_kernel(int* params, const int64_t* idx_dev, int64_t t
 
 }  // namespace
 
+// One packed matrix: the caller's reference MARLIN tensors and, when the
+// runner re-tiled them for the matrix cores, its own tile16 copy.
+struct Mat {
+  const void* w = nullptr;
+  const void* sb = nullptr;
+  void* w16 = nullptr;
+  void* sb16 = nullptr;
+  int N = 0, K = 0;
+};
+
+// Prologue / epilogue settings shared by both GEMV paths.
+struct GemvCall {
+  const f16* x = nullptr;
+  int ldx = 0;
+  f16* y = nullptr;
+  int ldy = 0;
+  const f16* bias = nullptr;
+  const f16* ln_w = nullptr;
+  float eps = 0.f;
+  f16* x_norm_out = nullptr;
+  f16* resid = nullptr;
+  int ldr = 0;
+  int pair_rows = 0;  // SWIGLU: rows of the gate half (H)
+  int q_dim = 0, kv_dim = 0, head_dim = 0;
+  const float* freqs = nullptr;
+  int rope_len = 0;
+  const int* rope_pos_dev = nullptr;
+  int write_pos = 0;
+  const int* write_pos_dev = nullptr;
+  f16* k_out = nullptr;
+  f16* v_out = nullptr;
+  long kv_stride_h = 0;
+  int max_seq = 1;
+  unsigned long long* argmax_keys = nullptr;
+};
+
+template <class A>
+static void fill_common(A& a, const GemvCall& c, int K, int N) {
+  a.x = c.x;
+  a.ldx = c.ldx;
+  a.K = K;
+  a.N = N;
+  a.y = c.y;
+  a.ldy = c.ldy;
+  a.bias = c.bias;
+  a.ln_w = c.ln_w;
+  a.eps = c.eps;
+  a.x_norm_out = c.x_norm_out;
+  a.resid = c.resid;
+  a.ldr = c.ldr;
+  a.q_dim = c.q_dim;
+  a.kv_dim = c.kv_dim;
+  a.head_dim = c.head_dim;
+  a.freqs = c.freqs;
+  a.rope_len = c.rope_len;
+  a.rope_pos_dev = c.rope_pos_dev;
+  a.write_pos = c.write_pos;
+  a.write_pos_dev = c.write_pos_dev;
+  a.k_out = c.k_out;
+  a.v_out = c.v_out;
+  a.kv_stride_h = c.kv_stride_h;
+  a.max_seq = c.max_seq;
+  a.argmax_keys = c.argmax_keys;
+}
+
+// out_rows: valid output rows (H for the SwiGLU pair, N otherwise).
+static int run_gemv(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
+  if (m.w16 != nullptr) {
+    T16Args a{};
+    fill_common(a, c, m.K, out_rows);
+    a.w16 = (const u32x4*)m.w16;
+    a.sb16 = (const u32x2*)m.sb16;
+    a.KB = (m.K + 127) / 128;
+    a.N_rows_alloc = m.N;
+    a.n_units = (out_rows + 15) / 16;
+    a.pair_offset = c.pair_rows / 16;
+    return t16_gemv_launch(a, M, epi, s);
+  }
+  Q4GemvArgs a{};
+  fill_common(a, c, m.K, out_rows);
+  a.w = (const u32x4*)m.w;
+  a.sb = (const u32x4*)m.sb;
+  a.KG = m.K / 64;
+  a.n_units = (out_rows + 7) / 8;
+  a.pair_offset = c.pair_rows / 8;
+  return q4m_gemv_launch(a, M, epi, s);
+}
+
 struct axm_runner {
   axm_runner_desc d{};
   std::vector<const void*> ln1, ln2, qkv_w, qkv_sb, qkv_b, o_w, o_sb, gu_w, gu_sb, dn_w, dn_sb;
+  std::vector<Mat> m_qkv, m_o, m_gu, m_dn;
+  Mat m_lmh;
+  std::vector<void*> owned;  // runner-owned tile16 copies
   std::vector<void*> kc, vc, ks, vs;
   int q_dim = 0, kv_dim = 0, qkv_dim = 0;
   // device buffers
@@ -70,7 +171,7 @@ struct axm_runner {
   f16* norm = nullptr;
   float* ws = nullptr;
   size_t ws_bytes = 0;
-  int* counters = nullptr;  // split-merge arrival counters (self re-arming)
+  unsigned long long* argmax_keys = nullptr;  // per lm_head tile: ordered (logit, index) key
   int max_splits = 64;
   bool use_graph = true;
   hipStream_t cap_stream = nullptr;
@@ -79,9 +180,10 @@ struct axm_runner {
   ~axm_runner() {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
-    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, counters};
+    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
+    for (void* b : owned) (void)hipFree(b);
   }
 
   KvView kv_view(int layer) const {
@@ -98,20 +200,15 @@ struct axm_runner {
     if (d.wte_format == 0)
       launch_embed_f16((const f16*)d.wte, nullptr, params + P_TOKEN, x, 1, D, d.vocab_size, s);
     else
-      launch_embed_q8((const uint8_t*)d.wte, (const f16*)d.wte_sb, nullptr, params + P_TOKEN, x, 1, D, d.vocab_size, s);
+      launch_embed_q8((const uint8_t*)d.wte, (const f16*)d.wte_sb, nullptr, params + P_TOKEN, x, 1, D,
+                      d.vocab_size, s);
 
     for (int i = 0; i < d.n_layer; ++i) {
       KvView kv = kv_view(i);
       // 1. QKV with RMSNorm prologue and RoPE / KV-write epilogue.
-      Q4GemvArgs a{};
+      GemvCall a{};
       a.x = x;
       a.ldx = D;
-      a.w = (const u32x4*)qkv_w[i];
-      a.sb = (const u32x4*)qkv_sb[i];
-      a.K = D;
-      a.KG = D / 64;
-      a.N = qkv_dim;
-      a.n_units = (qkv_dim + 7) / 8;
       a.y = q;
       a.ldy = q_dim;
       a.bias = (const f16*)qkv_b[i];
@@ -131,83 +228,58 @@ struct axm_runner {
         a.max_seq = d.max_seq_len;
       } else {
         // Stage fp16 k / v rows; the quantizer writes the cache slot.
-        a.write_pos = 0;
         a.k_out = kvst;
         a.v_out = kvst + kv_dim;
         a.kv_stride_h = d.head_dim;
         a.max_seq = 1;
       }
-      int rc = q4m_gemv_launch(a, 1, Q4_EPI_QKV_ROPE, s);
+      int rc = run_gemv(m_qkv[i], Q4_EPI_QKV_ROPE, qkv_dim, a, 1, s);
       if (rc) return rc;
       if (d.kv_dtype != AXM_KV_FP16)
         launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
       // 2. attention over slots [0, active_len).
-      rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s, counters);
+      rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
       if (rc) return rc;
       // 3. O projection, residual add into x.
-      Q4GemvArgs o{};
+      GemvCall o{};
       o.x = attn_y;
       o.ldx = q_dim;
-      o.w = (const u32x4*)o_w[i];
-      o.sb = (const u32x4*)o_sb[i];
-      o.K = q_dim;
-      o.KG = q_dim / 64;
-      o.N = D;
-      o.n_units = (D + 7) / 8;
       o.resid = x;
       o.ldr = D;
-      rc = q4m_gemv_launch(o, 1, Q4_EPI_RESID, s);
+      rc = run_gemv(m_o[i], Q4_EPI_RESID, D, o, 1, s);
       if (rc) return rc;
       // 4. gate/up with RMSNorm prologue and SwiGLU epilogue.
-      Q4GemvArgs g{};
+      GemvCall g{};
       g.x = x;
       g.ldx = D;
-      g.w = (const u32x4*)gu_w[i];
-      g.sb = (const u32x4*)gu_sb[i];
-      g.K = D;
-      g.KG = D / 64;
-      g.N = H;
-      g.n_units = (H + 7) / 8;
-      g.pair_offset = H / 8;
       g.y = hbuf;
       g.ldy = H;
       g.ln_w = (const f16*)ln2[i];
       g.eps = d.eps;
-      rc = q4m_gemv_launch(g, 1, Q4_EPI_SWIGLU, s);
+      g.pair_rows = H;
+      rc = run_gemv(m_gu[i], Q4_EPI_SWIGLU, H, g, 1, s);
       if (rc) return rc;
       // 5. down projection, residual add.
-      Q4GemvArgs dn{};
+      GemvCall dn{};
       dn.x = hbuf;
       dn.ldx = H;
-      dn.w = (const u32x4*)dn_w[i];
-      dn.sb = (const u32x4*)dn_sb[i];
-      dn.K = H;
-      dn.KG = H / 64;
-      dn.N = D;
-      dn.n_units = (D + 7) / 8;
       dn.resid = x;
       dn.ldr = D;
-      rc = q4m_gemv_launch(dn, 1, Q4_EPI_RESID, s);
+      rc = run_gemv(m_dn[i], Q4_EPI_RESID, D, dn, 1, s);
       if (rc) return rc;
     }
-    // Final RMSNorm + lm_head.
+    // Final RMSNorm + lm_head (+ per-tile greedy argmax keys).
     if (d.lm_head_format == 0) {
-      Q4GemvArgs l{};
+      GemvCall l{};
       l.x = x;
       l.ldx = D;
-      l.w = (const u32x4*)d.lm_head_w;
-      l.sb = (const u32x4*)d.lm_head_sb;
-      l.K = D;
-      l.KG = D / 64;
-      l.N = d.vocab_size;
-      l.n_units = (d.vocab_size + 7) / 8;
       l.y = logits;
       l.ldy = d.vocab_size;
       l.ln_w = (const f16*)d.lnf_w;
       l.eps = d.eps;
       l.x_norm_out = norm;
-      l.argmax_key = reinterpret_cast<unsigned long long*>(reinterpret_cast<unsigned char*>(params) + kArgmaxOffset);
-      int rc = q4m_gemv_launch(l, 1, Q4_EPI_STORE, s);
+      l.argmax_keys = argmax_keys;
+      int rc = run_gemv(m_lmh, Q4_EPI_STORE, d.vocab_size, l, 1, s);
       if (rc) return rc;
     } else {
       launch_rmsnorm(x, (const f16*)d.lnf_w, norm, 1, D, d.eps, s);
@@ -216,6 +288,16 @@ struct axm_runner {
       if (rc) return rc;
     }
     return 0;
+  }
+
+  // Re-tile one matrix for the matrix-core GEMV (runner-owned copy).
+  int make_tile16(Mat& m) {
+    const size_t wb = t16_weight_bytes(m.N, m.K), sbb = t16_sb_bytes(m.N, m.K);
+    if (hipMalloc(&m.w16, wb) != hipSuccess) return -4;
+    owned.push_back(m.w16);
+    if (hipMalloc(&m.sb16, sbb) != hipSuccess) return -4;
+    owned.push_back(m.sb16);
+    return t16_repack(m.w, m.sb, m.N, m.K, m.w16, m.sb16, nullptr);
   }
 };
 
@@ -273,6 +355,34 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
     r->vs.assign(L, nullptr);
   }
   r->d.max_tokens = d.max_tokens > 0 ? d.max_tokens : 1;
+  {
+    const int qkv_rows = (d.n_head + 2 * d.n_kv_head) * d.head_dim;
+    for (int i = 0; i < L; ++i) {
+      r->m_qkv.push_back(Mat{r->qkv_w[i], r->qkv_sb[i], nullptr, nullptr, qkv_rows, d.d_model});
+      r->m_o.push_back(Mat{r->o_w[i], r->o_sb[i], nullptr, nullptr, d.d_model, d.n_head * d.head_dim});
+      r->m_gu.push_back(Mat{r->gu_w[i], r->gu_sb[i], nullptr, nullptr, 2 * d.hidden_dim, d.d_model});
+      r->m_dn.push_back(Mat{r->dn_w[i], r->dn_sb[i], nullptr, nullptr, d.d_model, d.hidden_dim});
+    }
+    r->m_lmh = Mat{d.lm_head_w, d.lm_head_sb, nullptr, nullptr, d.vocab_size, d.d_model};
+    // The gate/up pair shares a tile16 boundary when H % 16 == 0; otherwise keep the
+    // reference layout everywhere.
+    const bool t16 = d.hidden_dim % 16 == 0 && d.layout != 1;
+    if (t16) {
+      int rc = 0;
+      for (int i = 0; i < L && rc == 0; ++i) {
+        rc = rc ? rc : r->make_tile16(r->m_qkv[i]);
+        rc = rc ? rc : r->make_tile16(r->m_o[i]);
+        rc = rc ? rc : r->make_tile16(r->m_gu[i]);
+        rc = rc ? rc : r->make_tile16(r->m_dn[i]);
+      }
+      if (rc == 0 && d.lm_head_format == 0) rc = r->make_tile16(r->m_lmh);
+      if (rc != 0 || hipDeviceSynchronize() != hipSuccess) {
+        delete r;
+        axm_set_error("runner_create: tile16 repack failed");
+        return -4;
+      }
+    }
+  }
   r->q_dim = d.n_head * d.head_dim;
   r->kv_dim = d.n_kv_head * d.head_dim;
   r->qkv_dim = r->q_dim + 2 * r->kv_dim;
@@ -291,7 +401,7 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
       {(void**)&r->logits, (size_t)T * d.vocab_size * sizeof(f16)},
       {(void**)&r->norm, (size_t)T * d.d_model * sizeof(f16)},
       {(void**)&r->ws, r->ws_bytes > 0 ? r->ws_bytes : 256},
-      {(void**)&r->counters, (size_t)T * d.n_head * sizeof(int)},
+      {(void**)&r->argmax_keys, (size_t)((d.vocab_size + 7) / 8) * sizeof(unsigned long long)},
   };
   for (auto& al : allocs) {
     if (hipMalloc(al.p, al.bytes) != hipSuccess) {
@@ -301,7 +411,7 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
     }
   }
   if (hipMemset(r->params, 0, 64 * sizeof(int)) != hipSuccess ||
-      hipMemset(r->counters, 0, (size_t)T * d.n_head * sizeof(int)) != hipSuccess ||
+      hipMemset(r->argmax_keys, 0, (size_t)((d.vocab_size + 7) / 8) * sizeof(unsigned long long)) != hipSuccess ||
       hipStreamCreateWithFlags(&r->cap_stream, hipStreamNonBlocking) != hipSuccess) {
     delete r;
     axm_set_error("runner_create: stream/memset setup failed");
@@ -335,8 +445,8 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
                 "runner_step: greedy feedback needs the MARLIN lm_head");
   hipStream_t s = (hipStream_t)stream;
   const int rope_pos = start_pos % d.rope_len;
-  hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(64), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
-                     rope_pos, write_pos, active_len);
+  hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
+                     rope_pos, write_pos, active_len, r->argmax_keys, (d.vocab_size + 7) / 8);
   // Bucket the split count so that one graph covers a range of lengths.
   int splits = attn_choose_splits(1, d.n_kv_head, active_len);
   int bucket = 1;

@@ -32,4 +32,6 @@ from .quant import (  # noqa: F401
     qmm_q8_g64,
     qmv_q4_marlin,
     qmv_q8_g64,
+    qmv_q4_tile16,
+    repack_q4_marlin_tile16,
 )

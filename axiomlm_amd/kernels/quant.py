@@ -18,6 +18,8 @@ __all__ = [
     "dequantize_q4_marlin",
     "qmv_q4_marlin",
     "qmm_q4_marlin",
+    "repack_q4_marlin_tile16",
+    "qmv_q4_tile16",
     "pack_linear_q8_g64",
     "dequantize_q8_g64",
     "dequant_q8_rows",
@@ -131,6 +133,33 @@ def qmv_q4_marlin(x, w_marlin, sb_marlin, out_features: int | None = None, bias=
 def qmm_q4_marlin(x, w_marlin, sb_marlin, out_features: int | None = None, bias=None) -> torch.Tensor:
     """Batched form of :func:`qmv_q4_marlin` (quant.py:664-684)."""
     return qmv_q4_marlin(x, w_marlin, sb_marlin, out_features, bias)
+
+
+def repack_q4_marlin_tile16(w_marlin, sb_marlin, N: int, K: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Bit-exact re-tiling of a MARLIN matrix for the matrix-core GEMV (the layout
+    the decode runner streams); returns (w16 int32, sb16 fp16) flat buffers."""
+    _lib.require_gpu(w_marlin, "repack_q4_marlin_tile16")
+    L = _lib.lib()
+    w16 = torch.empty(L.axm_tile16_bytes(N, K, 0) // 4, dtype=torch.int32, device=w_marlin.device)
+    sb16 = torch.empty(L.axm_tile16_bytes(N, K, 1) // 2, dtype=torch.float16, device=w_marlin.device)
+    _lib.check(L.axm_repack_q4_marlin_tile16(_lib.ptr(w_marlin.contiguous()), _lib.ptr(sb_marlin.contiguous()), N, K,
+                                             _lib.ptr(w16), _lib.ptr(sb16), _lib.stream_of(w_marlin.device)),
+               "repack_q4_marlin_tile16")
+    return w16, sb16
+
+
+def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
+    """y = x @ W^T (+ bias) on a tile16 copy made by :func:`repack_q4_marlin_tile16`."""
+    _lib.require_gpu(x, "qmv_q4_tile16")
+    K = x.size(-1)
+    M = x.numel() // K
+    N = int(out_features)
+    y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
+    b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
+    _lib.check(_lib.lib().axm_qmv_q4_tile16(_lib.ptr(x.contiguous()), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b),
+                                            _lib.ptr(y), M, K, N, _lib.stream_of(x.device)),
+               "qmv_q4_tile16")
+    return y
 
 
 # ---------------------------------------------------------------------------

@@ -12,8 +12,10 @@ Constructor arguments and methods follow the reference pybind class
 Formats are detected from the packed tensors as the reference does
 (mps_kernels.mm:3055-3068, 3149-3157): a 4-D lm_head is MARLIN Q4, a 2-D int32
 one is Q8_G64; a 2-D int32 ``wte_p`` selects the Q8 embedding gather.  The
-last three keyword arguments are this build's addition: quantized (FP8 / INT4)
-KV caches inside the captured step.
+keyword arguments after ``wte_s`` are this build's additions: quantized (FP8 /
+INT4) KV caches inside the captured step, and ``layout`` -- "tile16" (default)
+re-tiles every MARLIN matrix once, bit-exactly, for the matrix-core GEMV;
+"marlin" streams the reference layout as given.
 
 The runner holds references to every tensor it was given (weights and the
 caller's KV cache views); ``step`` returns a view of a persistent logits
@@ -45,7 +47,7 @@ class QuantizedDecodeRunner:
     def __init__(self, wte_emb, lmh_packed, lmh_sb, freqs_r, ln1_ws, c_attn_p, c_attn_s, c_proj_p, c_proj_s,
                  ln2_ws, gate_up_p, gate_up_s, w_down_p, w_down_s, lnf_w, k_cs, v_cs, n_h, n_kvh, hd, use_q4,
                  epsilon, c_attn_bs=(), vocab_sz=-1, wte_p=None, wte_s=None, k_scales=None, v_scales=None,
-                 kv_dtype="fp16", max_tokens: int = 1):
+                 kv_dtype="fp16", max_tokens: int = 1, layout: str = "tile16"):
         L = len(ln1_ws)
         if not use_q4 or c_attn_p[0].dim() != 4:
             raise RuntimeError("QuantizedDecodeRunner on MI355X supports MARLIN Q4 layer weights")
@@ -119,6 +121,9 @@ class QuantizedDecodeRunner:
         d.k_cache, d.v_cache = cv(a[11], P), cv(a[12], P)
         d.k_scales, d.v_scales = (cv(a[13], P), cv(a[14], P)) if kv_code else (None, None)
         d.max_tokens = int(max_tokens)
+        if layout not in ("tile16", "marlin"):
+            raise ValueError(f"layout must be 'tile16' or 'marlin', got {layout!r}")
+        d.layout = 0 if layout == "tile16" else 1
         self._desc = d
         h = ctypes.c_void_p()
         with torch.cuda.device(dev):

@@ -41,6 +41,16 @@ int axm_qmv_q4_marlin(const void* x, const void* w_marlin, const void* sb_marlin
  * mps_kernels.mm:3249-3253 fused into one launch). */
 int axm_qmv_q4_marlin_swiglu(const void* x, const void* ln_w, float eps, const void* gu_w, const void* gu_sb,
                              void* y, int M, int K, int H, void* stream);
+/* Matrix-core ("tile16") copy of a MARLIN matrix, the layout the decode runner
+ * streams: w16 u32 [ceil(N/16)][ceil(K/128)][64][4], sb16 [ceil(N/16)][ceil(K/128)][16][2]
+ * (scale, bias).  The re-tiling is bit-exact (same codes, scales and biases).
+ * axm_tile16_bytes(N, K, 0) / (N, K, 1) give the two buffer sizes. */
+size_t axm_tile16_bytes(int N, int K, int which);
+int axm_repack_q4_marlin_tile16(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16,
+                                void* stream);
+/* y = x W^T (+ bias) on the tile16 copy, MFMA 16x16x32 f16 with fp32 accumulation. */
+int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
+                      int N, void* stream);
 /* Row-major fp16 [N][K] dequantization (axiomlm/kernels/quant.py:597-634). */
 int axm_dequantize_q4_marlin(const void* w_marlin, const void* sb_marlin, void* out, int K, int N, void* stream);
 /* Round-to-nearest packer, clip_search=False (axiomlm/kernels/quant.py:447-494, 573-593).
@@ -158,6 +168,7 @@ typedef struct axm_runner_desc {
   void* const* k_scales; /* quantized caches only */
   void* const* v_scales;
   int max_tokens; /* capacity of the multi-token (verify) paths, <= 64 */
+  int layout;     /* 0: re-tile weights for the matrix cores (default); 1: stream the reference layout */
 } axm_runner_desc;
 
 typedef struct axm_runner* axm_runner_t;

@@ -118,6 +118,87 @@ def test_q4_qmv_exact_on_lattice(dev):
     assert np.array_equal(got, ref)
 
 
+def test_mfma_16x16x32_f16_lane_layout(dev):
+    """The tile16 GEMV assumes A[i][k]: lane i%16 + 16*(k//8), B[k][j]: lane j + 16*(k//8),
+    D[i][j]: lane j + 16*(i//4), register i%4.  Checked through the GEMV itself on a one-hot
+    weight matrix: y[row] = x[k] picks exactly one activation per output row."""
+    from axiomlm_amd.kernels import qmv_q4_tile16, repack_q4_marlin_tile16
+
+    K, N_ = 256, 32
+    rng = np.random.default_rng(0)
+    q = np.zeros((N_, K), np.float32)
+    cols = rng.permutation(K)[:N_]
+    q[np.arange(N_), cols] = 15
+    w = (q * (1.0 / 15.0)).astype(F16)
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    w16, sb16 = repack_q4_marlin_tile16(T(wm, dev), T(sb, dev), N_, K)
+    x = (np.arange(K) % 61 - 30).astype(F16)[None, :]
+    got = N(qmv_q4_tile16(T(x, dev), w16, sb16, N_))[0]
+    ref = fm.qmv_q4_marlin(x, wm, sb, N_)[0]
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("N_,K", [(64, 128), (13, 192), (100, 704), (12288, 4096)])
+def test_tile16_repack_roundtrip_bit_exact(dev, N_, K):
+    """Re-tiling keeps every code / scale / bias: decode the tile16 buffers on the host
+    with the documented bit layout and compare with the oracle's unpacked codes."""
+    from axiomlm_amd.kernels import repack_q4_marlin_tile16
+
+    rng = np.random.default_rng(N_ + K)
+    w = (rng.standard_normal((N_, K)) * 0.02).astype(F16)
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    w16, sb16 = repack_q4_marlin_tile16(T(wm, dev), T(sb, dev), N_, K)
+    w16 = N(w16).view(np.uint32).reshape((N_ + 15) // 16, (K + 127) // 128, 64, 4)
+    sb16 = N(sb16).view(F16).reshape((N_ + 15) // 16, (K + 127) // 128, 16, 2, 2)
+    codes = fm.unpack_marlin_codes(wm)[:N_]
+    lane = np.arange(64)
+    pos = np.array([0, 16, 4, 20, 8, 24, 12, 28])
+    for t16 in range(w16.shape[0]):
+        for kb in range(w16.shape[1]):
+            words = w16[t16, kb]  # [64, 4]
+            nib = (words[:, :, None] >> pos) & 0xF  # [64 lanes, 4 c, 8 i]
+            rows = t16 * 16 + (lane % 16)
+            ks = 128 * kb + 32 * np.arange(4)[None, :, None] + 8 * (lane // 16)[:, None, None] + np.arange(8)
+            valid = (rows[:, None, None] < N_) & (ks < K)
+            expect = np.zeros_like(nib)
+            rr = np.broadcast_to(rows[:, None, None], ks.shape)
+            expect[valid] = codes[rr[valid], ks[valid]]
+            assert np.array_equal(nib, expect)
+    sbu = sb.transpose(0, 2, 1, 3).reshape(-1, K // 64, 2)[:N_]
+    for t16 in range(sb16.shape[0]):
+        for kb in range(sb16.shape[1]):
+            for j in range(16):
+                row = t16 * 16 + j
+                for h in range(2):
+                    g = 2 * kb + h
+                    want = sbu[row, g] if (row < N_ and g < K // 64) else np.zeros(2, F16)
+                    assert np.array_equal(sb16[t16, kb, j, h].view(np.uint16), want.view(np.uint16))
+        if t16 > 3:
+            break
+
+
+@pytest.mark.parametrize(
+    "M,N_,K,bias",
+    [(1, 256, 256, False), (1, 13, 192, True), (3, 768, 256, False), (4, 1408, 704, False), (2, 96, 704, True),
+     (1, 12288, 4096, False), (1, 4096, 11008, False), (4, 22016, 4096, False), (1, 32000, 4096, False)],
+)
+def test_tile16_qmv_matches_oracle(dev, M, N_, K, bias):
+    """Matrix-core GEMV on the re-tiled copy; same bound as the reference-layout kernel."""
+    from axiomlm_amd.kernels import qmv_q4_tile16, repack_q4_marlin_tile16
+
+    print(f"[tile16_qmv] M={M} N={N_} K={K} bias={bias}", flush=True)
+    rng = np.random.default_rng(M * 11 + N_ + K)
+    w = (rng.standard_normal((N_, K)) * 0.02).astype(F16)
+    x = rng.standard_normal((M, K)).astype(F16)
+    b = (rng.standard_normal(N_) * 0.1).astype(F16) if bias else None
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    ref = fm.qmv_q4_marlin(x, wm, sb, N_, b).astype(F32)
+    w16, sb16 = repack_q4_marlin_tile16(T(wm, dev), T(sb, dev), N_, K)
+    got = N(qmv_q4_tile16(T(x, dev), w16, sb16, N_, None if b is None else T(b, dev))).astype(F32)
+    err = np.abs(got - ref) / (1.0 + np.abs(ref))
+    assert err.max() <= 2e-3, f"max rel err {err.max()}"
+
+
 # ---------------------------------------------------------------------------
 # Q8 / ternary / Q2 packers and the Q8 GEMV / gather
 # ---------------------------------------------------------------------------

@@ -18,7 +18,7 @@ F16, F32 = np.float16, np.float32
 TOL = 1e-2
 
 
-def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False):
+def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile16"):
     from axiomlm_amd.cache import StaticKVCache
     from axiomlm_amd.runner import QuantizedDecodeRunner
 
@@ -32,7 +32,7 @@ def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False):
         [t(x) for x in ow.ln2], [t(x) for x in ow.gu_p], [t(x) for x in ow.gu_s], [t(x) for x in ow.wd_p],
         [t(x) for x in ow.wd_s], t(ow.lnf), cache.k_caches, cache.v_caches, cfg.n_head, cfg.n_kv_head,
         cfg.head_dim, True, cfg.eps, [], cfg.vocab, wte_p=t(ow.wte_p.view(np.int32).reshape(cfg.vocab, -1)),
-        wte_s=t(ow.wte_sb), k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv)
+        wte_s=t(ow.wte_sb), k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv, layout=layout)
     return r, cache
 
 
@@ -67,12 +67,13 @@ def _check_logits(got, ref, what):
     assert err <= TOL, f"{what}: max |logit diff| {err}"
 
 
-def test_runner_step_matches_oracle(dev):
-    print("[runner_step] kv=fp16", flush=True)
+@pytest.mark.parametrize("layout", ["tile16", "marlin"])
+def test_runner_step_matches_oracle(dev, layout):
+    print(f"[runner_step] kv=fp16 layout={layout}", flush=True)
     cfg, ow, cos, sin = c1_model()
     model = om.OracleModel(cfg, ow, cos, sin)
     S = 128
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16")
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16", layout=layout)
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, "fp16")
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, cfg.vocab, 32).tolist()
