@@ -153,17 +153,25 @@ __device__ void t16_stage_x(const T16Args& a, f16* xs, f32x2* cx, float* red) {
 }
 
 // Nibble expansion: (w & mask) | magic as one v_and_or_b32.  gfx950 VOP3 takes
-// neither literals nor two scalar operands, so the masks live in VGPRs (loop
-// invariant) and the magic exponents in SGPRs; without the explicit instruction
-// the compiler splits every expansion into an AND plus an OR.
+// neither literals nor two scalar operands, so the masks must sit in VGPRs and
+// the magic exponents in SGPRs for instruction selection to fuse the pair.
+// The masks are moved into VGPRs once, through an opaque move the compiler
+// cannot fold back into a constant; the AND-OR itself stays compiler-generated
+// so the MFMA hazard recognizer sees every VALU write that feeds a B operand
+// (a VALU write read by an MFMA source needs two wait states, and the
+// recognizer does not model inline-asm producers).
 struct Unpack {
   uint32_t m_lo, m_hi, g_lo, g_hi;  // 0x000F000F, 0x00F000F0, 0x64006400, 0x54005400
 };
 
+__device__ __forceinline__ uint32_t to_vgpr(uint32_t s) {
+  uint32_t v;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
+  return v;
+}
+
 __device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask_v, uint32_t magic_s) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(mask_v), "s"(magic_s));
-  return r;
+  return (w & mask_v) | magic_s;
 }
 
 __device__ __forceinline__ f16x8 unpack_word(uint32_t w, const Unpack& u) {
@@ -280,7 +288,7 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
   const int my = max(0, min(per, a.KB - kb0));
   const int tokA = lane & 15;  // A-operand token of this lane
   const int kq = lane >> 4;    // 8-wide k sub-block of this lane
-  const Unpack U{a.unpack[0], a.unpack[1], a.unpack[2], a.unpack[3]};
+  const Unpack U{to_vgpr(a.unpack[0]), to_vgpr(a.unpack[1]), a.unpack[2], a.unpack[3]};
 
   // Raw buffer descriptors: out-of-range offsets read as zero, so every chunk
   // load is issued unconditionally and the load pipeline stays static.
@@ -538,5 +546,31 @@ extern "C" int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb1
     if (rc) return rc;
   }
   AXM_LAUNCH_CHECK("qmv_q4_tile16");
+  return 0;
+}
+
+extern "C" int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const void* gu16,
+                                        const void* gusb16, void* y, int M, int K, int H, void* stream) {
+  AXM_CHECK_ARG(x && gu16 && gusb16 && y, -1, "qmv_q4_tile16_swiglu: null pointer");
+  AXM_CHECK_ARG(K > 0 && K % 64 == 0 && H > 0 && H % 16 == 0 && M >= 1 && M <= 4, -1,
+                "qmv_q4_tile16_swiglu: bad shape M=%d K=%d H=%d (H %% 16 == 0, M <= 4)", M, K, H);
+  T16Args a{};
+  a.x = (const f16*)x;
+  a.ldx = K;
+  a.w16 = (const u32x4*)gu16;
+  a.sb16 = (const u32x2*)gusb16;
+  a.K = K;
+  a.KB = (K + 127) / 128;
+  a.N = H;
+  a.n_units = H / 16;
+  a.N_rows_alloc = 2 * H;
+  a.pair_offset = H / 16;
+  a.y = (f16*)y;
+  a.ldy = H;
+  a.ln_w = (const f16*)ln_w;
+  a.eps = eps;
+  int rc = t16_gemv_launch(a, M, Q4_EPI_SWIGLU, (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("qmv_q4_tile16_swiglu");
   return 0;
 }

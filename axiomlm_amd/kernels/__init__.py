@@ -33,5 +33,7 @@ from .quant import (  # noqa: F401
     qmv_q4_marlin,
     qmv_q8_g64,
     qmv_q4_tile16,
+    qmv_q4_tile16_swiglu,
+    qmv_q4_marlin_swiglu,
     repack_q4_marlin_tile16,
 )

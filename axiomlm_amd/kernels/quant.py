@@ -20,6 +20,8 @@ __all__ = [
     "qmm_q4_marlin",
     "repack_q4_marlin_tile16",
     "qmv_q4_tile16",
+    "qmv_q4_marlin_swiglu",
+    "qmv_q4_tile16_swiglu",
     "pack_linear_q8_g64",
     "dequantize_q8_g64",
     "dequant_q8_rows",
@@ -160,6 +162,30 @@ def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
                                             _lib.ptr(y), M, K, N, _lib.stream_of(x.device)),
                "qmv_q4_tile16")
     return y
+
+
+def _swiglu_call(fn, name, x, ln_w, eps, w, sb, H):
+    _lib.require_gpu(x, name)
+    K = x.size(-1)
+    M = x.numel() // K
+    if x.dtype != torch.float16 or not 1 <= M <= 4:
+        raise RuntimeError(f"{name}: x must be float16 with 1..4 rows")
+    y = torch.empty((*x.shape[:-1], int(H)), dtype=torch.float16, device=x.device)
+    lw = None if ln_w is None else ln_w.to(device=x.device, dtype=torch.float16).contiguous()
+    _lib.check(fn(_lib.ptr(x.contiguous()), _lib.ptr(lw), float(eps), _lib.ptr(w.contiguous()),
+                  _lib.ptr(sb.contiguous()), _lib.ptr(y), M, K, int(H), _lib.stream_of(x.device)), name)
+    return y
+
+
+def qmv_q4_marlin_swiglu(x, ln_w, eps: float, gu_w, gu_sb, H: int) -> torch.Tensor:
+    """silu(g) * u of [g | u] = rmsnorm(x) @ [W_gate; W_up]^T, one launch (the MLP input of a
+    decoder layer, transformer.py:1178-1189); ``ln_w`` None skips the norm."""
+    return _swiglu_call(_lib.lib().axm_qmv_q4_marlin_swiglu, "qmv_q4_marlin_swiglu", x, ln_w, eps, gu_w, gu_sb, H)
+
+
+def qmv_q4_tile16_swiglu(x, ln_w, eps: float, gu16, gusb16, H: int) -> torch.Tensor:
+    """:func:`qmv_q4_marlin_swiglu` on the tile16 copy of the packed [W_gate; W_up] (H % 16 == 0)."""
+    return _swiglu_call(_lib.lib().axm_qmv_q4_tile16_swiglu, "qmv_q4_tile16_swiglu", x, ln_w, eps, gu16, gusb16, H)
 
 
 # ---------------------------------------------------------------------------

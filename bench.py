@@ -8,9 +8,9 @@ table, an fp16 KV cache of 4096 slots whose first CTX0 slots hold synthetic
 N(0,1) context.  One step = one greedy decode token through the captured
 whole-step hipGraph (the argmax of step t feeds step t+1 on the device).
 
-Printed JSON line: value = tokens/s; roofline = the fused RMSNorm + gate/up GEMV
-+ SwiGLU kernel (the largest per-launch weight stream, 50.7 MB) timed live with
-HIP events on its stream; cpu_baseline = the numpy oracle (the reference's CPU
+Printed JSON line: value = tokens/s; roofline = the runner's fused RMSNorm +
+gate/up GEMV + SwiGLU kernel (tile16 matrix-core layout; the largest per-launch
+weight stream, 50.7 MB) timed live with HIP events on its stream; cpu_baseline = the numpy oracle (the reference's CPU
 fallback: dequantize every weight, then matmul) on a bounded sample of the same
 step, extrapolated to tokens/s.
 """
@@ -133,26 +133,29 @@ def time_decode(runner, cache, steps, warmup, dev):
     return ms, wall, pos0
 
 
-def time_gate_up_kernel(layers, c, dev, reps=200):
-    """Average duration of the fused RMSNorm + gate/up + SwiGLU launch (7B shape), HIP events
-    recorded on the stream it is launched on."""
+def time_gate_up_kernel(layers, c, dev, reps=200, n_copies=8):
+    """Average duration of the runner's fused RMSNorm + gate/up + SwiGLU launch (tile16
+    matrix-core GEMV, 7B shape), timed with HIP events recorded on the stream it is
+    launched on.  Launches rotate over n_copies layers' weights (8 x 50.7 MB) so the
+    stream does not sit in the 256 MB last-level cache."""
     import torch
 
     from axiomlm_amd import _lib
+    from axiomlm_amd.kernels import repack_q4_marlin_tile16
 
     d, H = c["d"], c["hidden"]
     x = torch.randn(1, d, device=dev, dtype=torch.float16)
     y = torch.empty(1, H, device=dev, dtype=torch.float16)
-    L = c["n_layer"]
+    copies = [repack_q4_marlin_tile16(layers["gu_p"][i], layers["gu_s"][i], 2 * H, d) for i in range(n_copies)]
     s = torch.cuda.current_stream(dev)
     stream = _lib.stream_of(dev)
 
     def launch(i):
-        li = i % L  # rotate layers so the 50.7 MB stream does not sit in the 256 MB last-level cache
-        rc = _lib.lib().axm_qmv_q4_marlin_swiglu(_lib.ptr(x), _lib.ptr(layers["ln2"][li]), 1e-5,
-                                                 _lib.ptr(layers["gu_p"][li]), _lib.ptr(layers["gu_s"][li]),
-                                                 _lib.ptr(y), 1, d, H, stream)
-        _lib.check(rc, "qmv_q4_marlin_swiglu")
+        li = i % n_copies
+        w16, sb16 = copies[li]
+        rc = _lib.lib().axm_qmv_q4_tile16_swiglu(_lib.ptr(x), _lib.ptr(layers["ln2"][li]), 1e-5, _lib.ptr(w16),
+                                                 _lib.ptr(sb16), _lib.ptr(y), 1, d, H, stream)
+        _lib.check(rc, "qmv_q4_tile16_swiglu")
 
     for i in range(10):
         launch(i)
@@ -165,6 +168,7 @@ def time_gate_up_kernel(layers, c, dev, reps=200):
     torch.cuda.synchronize()
     avg_us = e0.elapsed_time(e1) * 1000.0 / reps
     bytes_per_launch = q4_bytes(2 * H, d) + d * 2 + d * 2 + H * 2  # weights + x + ln_w + y
+    del copies
     return avg_us, bytes_per_launch
 
 
@@ -278,7 +282,7 @@ def main():
             "step_hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": "q4m_gemv_kernel<1,2,2> (fused RMSNorm + gate/up MARLIN GEMV + SwiGLU, 22016x4096)",
+            "kernel": "t16_gemv_kernel<1,2,SWIGLU,4> (fused RMSNorm + gate/up Q4 GEMV on matrix cores + SwiGLU, 22016x4096)",
             "bound": "hbm",
             "achieved": round(ach, 1),
             "peak": HBM_PEAK_GBS,

@@ -51,6 +51,10 @@ int axm_repack_q4_marlin_tile16(const void* w_marlin, const void* sb_marlin, int
 /* y = x W^T (+ bias) on the tile16 copy, MFMA 16x16x32 f16 with fp32 accumulation. */
 int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
                       int N, void* stream);
+/* axm_qmv_q4_marlin_swiglu on the tile16 copy of the packed [W_gate; W_up] (2 H rows,
+ * H % 16 == 0): the runner's MLP-input launch (transformer.py:1178-1189). */
+int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const void* gu16, const void* gusb16,
+                             void* y, int M, int K, int H, void* stream);
 /* Row-major fp16 [N][K] dequantization (axiomlm/kernels/quant.py:597-634). */
 int axm_dequantize_q4_marlin(const void* w_marlin, const void* sb_marlin, void* out, int K, int N, void* stream);
 /* Round-to-nearest packer, clip_search=False (axiomlm/kernels/quant.py:447-494, 573-593).

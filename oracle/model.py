@@ -126,7 +126,10 @@ class OracleKVCache:
         self.layer_seq_lens = [0] * n_layer
         # When frozen, writes are skipped: the cache contents were loaded from
         # another implementation and attention must read exactly those codes.
+        # The codes a write would have stored are kept in last_write[layer] as
+        # (slots, k_codes, k_scales, v_codes, v_scales) for comparison.
         self.frozen = False
+        self.last_write = [None] * n_layer
 
     def _quant(self, x16):
         if self.dtype == "fp8":
@@ -144,10 +147,11 @@ class OracleKVCache:
 
     def write(self, layer, slots, k16, v16):
         """Store rows k16/v16 [Hkv, T, hd] at the given slots."""
-        if self.frozen:
-            return
         kq, ks = self._quant(k16)
         vq, vs = self._quant(v16)
+        if self.frozen:
+            self.last_write[layer] = (slots, kq, ks, vq, vs)
+            return
         self.k[layer][:, slots] = kq
         self.v[layer][:, slots] = vq
         if ks is not None:

@@ -199,6 +199,40 @@ def test_tile16_qmv_matches_oracle(dev, M, N_, K, bias):
     assert err.max() <= 2e-3, f"max rel err {err.max()}"
 
 
+@pytest.mark.parametrize("layout", ["marlin", "tile16"])
+@pytest.mark.parametrize("M,K,H,norm", [(1, 256, 704, True), (3, 704, 256, False), (1, 4096, 11008, True),
+                                        (4, 1024, 512, True)])
+def test_fused_gate_up_swiglu_matches_oracle(dev, layout, M, K, H, norm):
+    """RMSNorm -> [W_gate; W_up] GEMV -> silu(g) * u in one launch vs the oracle's
+    unfused sequence (transformer.py:1178-1189 with torch-CPU fp16 op semantics).
+
+    Bound: the GEMV outputs agree to fp32-accumulation order (rel 2e-3 of |g|, |u|
+    as in the plain GEMV tests); silu(g)*u is 1-Lipschitz-ish in g and linear in u,
+    so |diff| <= 4e-3 * (1 + |g|) * (1 + |u|) bounds the product."""
+    from axiomlm_amd.kernels import qmv_q4_marlin_swiglu, qmv_q4_tile16_swiglu, repack_q4_marlin_tile16
+    from oracle import model as om
+
+    print(f"[fused_swiglu] layout={layout} M={M} K={K} H={H} norm={norm}", flush=True)
+    rng = np.random.default_rng(K + H + M)
+    w = (rng.standard_normal((2 * H, K)) * 0.02).astype(F16)
+    x = rng.standard_normal((M, K)).astype(F16)
+    ln = (1.0 + 0.1 * rng.standard_normal(K)).astype(F16) if norm else None
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    h = om.rmsnorm_fp16(x, ln, 1e-5) if norm else x
+    gu = fm.qmv_q4_marlin(h, wm, sb, 2 * H).astype(F32)
+    g, u = gu[:, :H], gu[:, H:]
+    ref = (((g / (1 + np.exp(-g))).astype(F16).astype(F32)) * u).astype(F16).astype(F32)
+    ln_t = None if ln is None else T(ln, dev)
+    if layout == "marlin":
+        got = qmv_q4_marlin_swiglu(T(x, dev), ln_t, 1e-5, T(wm, dev), T(sb, dev), H)
+    else:
+        w16, sb16 = repack_q4_marlin_tile16(T(wm, dev), T(sb, dev), 2 * H, K)
+        got = qmv_q4_tile16_swiglu(T(x, dev), ln_t, 1e-5, w16, sb16, H)
+    got = N(got).astype(F32)
+    bound = 4e-3 * (1 + np.abs(g)) * (1 + np.abs(u))
+    assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) - bound)}"
+
+
 # ---------------------------------------------------------------------------
 # Q8 / ternary / Q2 packers and the Q8 GEMV / gather
 # ---------------------------------------------------------------------------
