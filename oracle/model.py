@@ -392,24 +392,42 @@ def make_float_weights(cfg: OracleConfig, seed: int = 0, std: float = 0.02):
     return W
 
 
-def pack_model_rtn(cfg: OracleConfig, W) -> OracleWeights:
-    """Round-to-nearest packing (mode 'q4_rtn', untied lm_head kept in MARLIN Q4)."""
+def pack_model(cfg: OracleConfig, W, mode: str = "q4") -> OracleWeights:
+    """``Transformer._ensure_quant_weights`` (transformer.py:822-1008) for an untied model:
+    Q8_G64 embedding, MARLIN Q4 lm_head and layer matrices (gate|up rows stacked,
+    :959-963).  mode "q4" = MSE clip search with the reference importance vectors
+    (|ln_f| for lm_head, |ln_1| for c_attn, |ln_2| for gate|up, row-norm product of
+    w_gate and w_up for w_down, none for c_proj; :876-948); "q4_rtn" = round to nearest."""
+    mse = mode == "q4"
+    if mode not in ("q4", "q4_rtn"):
+        raise ValueError(f"unsupported mode {mode!r}")
+
+    def pack(w, imp):
+        return fm.pack_linear_q4_marlin(w, clip_search=mse, col_importance=imp if mse else None)
+
+    a = lambda v: np.abs(v.astype(F32))  # noqa: E731
     wte_p, wte_sb = fm.pack_linear_q8_g64(W["wte"])
-    lmh_p, lmh_sb = fm.pack_linear_q4_marlin(W["lm_head"], clip_search=False)
+    lmh_p, lmh_sb = pack(W["lm_head"], a(W["lnf"]))
     ow = OracleWeights(wte_p, wte_sb, lmh_p, lmh_sb, [], [], W["lnf"], [], [], [], [], [], [], [], [])
     for L in W["layers"]:
         ow.ln1.append(L["ln1"])
         ow.ln2.append(L["ln2"])
-        p, s = fm.pack_linear_q4_marlin(L["c_attn"], clip_search=False)
+        p, s = pack(L["c_attn"], a(L["ln1"]))
         ow.c_attn_p.append(p)
         ow.c_attn_s.append(s)
-        p, s = fm.pack_linear_q4_marlin(L["c_proj"], clip_search=False)
+        p, s = pack(L["c_proj"], None)
         ow.c_proj_p.append(p)
         ow.c_proj_s.append(s)
-        p, s = fm.pack_linear_q4_marlin(np.concatenate([L["w_gate"], L["w_up"]], axis=0), clip_search=False)
+        p, s = pack(np.concatenate([L["w_gate"], L["w_up"]], axis=0), a(L["ln2"]))
         ow.gu_p.append(p)
         ow.gu_s.append(s)
-        p, s = fm.pack_linear_q4_marlin(L["w_down"], clip_search=False)
+        imp_sw = (np.linalg.norm(L["w_gate"].astype(F32), axis=1) * np.linalg.norm(L["w_up"].astype(F32), axis=1))
+        p, s = pack(L["w_down"], imp_sw)
         ow.wd_p.append(p)
         ow.wd_s.append(s)
     return ow
+
+
+def pack_model_rtn(cfg: OracleConfig, W) -> OracleWeights:
+    """Round-to-nearest packing (mode "q4_rtn", untied lm_head kept in MARLIN Q4)."""
+    return pack_model(cfg, W, "q4_rtn")

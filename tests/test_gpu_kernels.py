@@ -413,3 +413,45 @@ def test_tree_attention_matches_masked_sdpa(dev, T_, kind, prefix):
     got = gqa_tree_verify_mps(T(q, dev), T(kc, dev), T(vc, dev), masks, prefix, write_pos, Hq, 0,
                               None if ks is None else T(ks, dev), None if vs is None else T(vs, dev), kind)
     assert np.abs(N(got).astype(F32) - ref).max() <= 2e-3
+
+
+def test_q4_mse_pack_matches_reference_golden(dev):
+    """The GPU MSE clip-search packer on every C1 matrix against the reference's own
+    packs (tests/golden/c1_q4.npz: quant.py:495-571 with the importance vectors of
+    transformer.py:876-948).  The oracle's packs carry the reference's SHA-256
+    (test_oracle_golden.py), so they stand in for the reference arrays here.
+    Bar: a group may pick a different clip only on a near-tie of two candidates'
+    weighted errors (fp32 summation order), at most 1% of groups per matrix, and
+    where (scale, bias) agree the codes agree bit for bit."""
+    from axiomlm_amd.kernels import pack_linear_q4_marlin
+    from c1_golden import c1_config, golden, named_packs, oracle_packs, pack_digest
+
+    cfg = c1_config()
+    W = om.make_float_weights(cfg, seed=0)
+    want = dict(zip(golden()["pack_names"].tolist(), golden()["pack_sha256"].tolist()))
+    ref = named_packs(oracle_packs())
+    a = lambda v: np.abs(v.astype(F32))  # noqa: E731
+    mats = [("lmh_p", "lmh_sb", W["lm_head"], a(W["lnf"]))]
+    for i, L in enumerate(W["layers"]):
+        mats += [(f"c_attn_p{i}", f"c_attn_s{i}", L["c_attn"], a(L["ln1"])),
+                 (f"c_proj_p{i}", f"c_proj_s{i}", L["c_proj"], None),
+                 (f"gu_p{i}", f"gu_s{i}", np.concatenate([L["w_gate"], L["w_up"]]), a(L["ln2"])),
+                 (f"wd_p{i}", f"wd_s{i}", L["w_down"], np.linalg.norm(L["w_gate"].astype(F32), axis=1)
+                  * np.linalg.norm(L["w_up"].astype(F32), axis=1))]
+    exact, report = 0, []
+    for kp, ks, w, imp in mats:
+        assert pack_digest(ref[kp]) == want[kp] and pack_digest(ref[ks]) == want[ks]
+        wm, sb = pack_linear_q4_marlin(T(w, dev), clip_search=True, col_importance=None if imp is None else T(imp, dev))
+        wm, sb = N(wm), N(sb)
+        if pack_digest(wm) == want[kp] and pack_digest(sb) == want[ks]:
+            exact += 1
+            continue
+        same = np.all(sb.view(np.uint16) == ref[ks].view(np.uint16), axis=-1)  # [tile, g, row]
+        K = w.shape[1]
+        agree = same.transpose(0, 2, 1).reshape(-1, K // 64)
+        cg = fm.unpack_marlin_codes(wm).reshape(-1, K // 64, 64)
+        cr = fm.unpack_marlin_codes(ref[kp]).reshape(-1, K // 64, 64)
+        assert np.array_equal(cg[agree], cr[agree]), kp
+        report.append((kp, float(1.0 - same.mean())))
+    print(f"[mse_golden] {exact}/{len(mats)} matrices bit-identical; near-tie groups: {report}", flush=True)
+    assert all(frac <= 0.01 for _, frac in report), report

@@ -220,3 +220,30 @@ def test_runner_graph_replay_equals_eager(dev):
         outs.append(np.stack(run_steps(runner, cache, list(range(1, 20)), dev)))
         torch.cuda.synchronize()
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("layout", ["tile16", "marlin"])
+def test_runner_matches_reference_golden(dev, layout):
+    """Against the reference's own CPU path (tests/golden/c1_q4.npz): mode "q4" packs
+    (bit-identical to the reference's, test_oracle_golden.py), 32 prompt tokens through
+    step(), then 64 greedy tokens through the in-graph argmax (step_greedy).
+    Bar: logits max |diff| <= 1e-2, greedy tokens identical."""
+    from c1_golden import c1_config, golden, oracle_packs
+
+    print(f"[runner_golden] layout={layout}", flush=True)
+    g = golden()
+    cfg = c1_config()
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, cfg.rope_theta)
+    runner, cache = build_runner(cfg, oracle_packs(), cos, sin, dev, 128, layout=layout)
+    prompt = g["prompt"].tolist()
+    got = run_steps(runner, cache, prompt, dev)
+    ref = g["decode_logits"].astype(F32)
+    for i in range(len(prompt)):
+        _check_logits(got[i], ref[i], f"prompt step {i}")
+    toks = []
+    n = len(prompt)
+    for i in range(64):
+        lg = runner.step_greedy(n + i, n + i, n + i + 1)[0, 0].float().cpu().numpy()
+        toks.append(int(runner.last_token().item()))
+        _check_logits(lg, ref[n + i], f"greedy step {i}")
+    assert toks == g["greedy_tokens"].tolist()
