@@ -71,6 +71,9 @@ _SIGNATURES = {
     "axm_runner_last_norm": (c_int, [c_void_p, c_void_p]),
     "axm_runner_token_slot": (c_int, [c_void_p, c_void_p]),
     "axm_runner_set_graph": (c_int, [c_void_p, c_int]),
+    "axm_runner_set_mode": (c_int, [c_void_p, c_int]),
+    "axm_runner_get_mode": (c_int, [c_void_p]),
+    "axm_runner_check": (c_int, [c_void_p]),
 }
 
 

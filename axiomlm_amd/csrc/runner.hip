@@ -19,6 +19,7 @@
 
 #include "axm.h"
 #include "kernels.h"
+#include "persistent.h"
 #include "q4_tile16.h"
 
 namespace {
@@ -173,17 +174,141 @@ struct axm_runner {
   size_t ws_bytes = 0;
   unsigned long long* argmax_keys = nullptr;  // per lm_head tile: ordered (logit, index) key
   int max_splits = 64;
-  bool use_graph = true;
+  int mode = AXM_RUNNER_MODE_GRAPH;
   hipStream_t cap_stream = nullptr;
   std::map<int, hipGraphExec_t> graphs;
+  // Persistent whole-step kernel state.
+  bool persist_ok = false;
+  int p_grid = 0;
+  size_t p_smem = 0;
+  PLayer* p_layers = nullptr;              // device copy of the per-layer table
+  unsigned long long* p_bar = nullptr;     // grid barrier words
+  unsigned long long* p_head_cnt = nullptr;
+  int64_t* p_tok_next = nullptr;
+  int* p_err = nullptr;
+  int* p_err_host = nullptr;               // pinned mirror, refreshed after each step
+  unsigned long long p_bar_base = 0, p_merge_base = 0;
+  bool tok_next_valid = false;
 
   ~axm_runner() {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
-    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys};
+    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys,
+                    p_layers, p_bar, p_head_cnt, p_tok_next, p_err};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
+    if (p_err_host) (void)hipHostFree(p_err_host);
     for (void* b : owned) (void)hipFree(b);
+  }
+
+  // Set up the persistent kernel when the configuration allows it (tile16
+  // weights, fp16 KV cache, MARLIN lm_head, co-residency on every CU).  The
+  // persistent step is switched off (kPersistEnabled) while a device memory
+  // fault seen on its first launch is unexplained; set_mode(PERSISTENT) then
+  // reports it as unavailable.
+  static constexpr bool kPersistEnabled = false;
+  void setup_persistent() {
+    if (!kPersistEnabled) return;
+    if (m_qkv.empty() || m_qkv[0].w16 == nullptr || d.kv_dtype != AXM_KV_FP16 || d.lm_head_format != 0 ||
+        m_lmh.w16 == nullptr)
+      return;
+    if (persist_check(d.d_model, d.hidden_dim, d.n_head, d.head_dim, d.vocab_size, &p_grid, &p_smem) != 0) return;
+    const int L = d.n_layer;
+    std::vector<PLayer> host(L);
+    for (int i = 0; i < L; ++i) {
+      PLayer& p = host[i];
+      p.qkv_w = (const u32x4*)m_qkv[i].w16;
+      p.qkv_sb = (const u32x2*)m_qkv[i].sb16;
+      p.o_w = (const u32x4*)m_o[i].w16;
+      p.o_sb = (const u32x2*)m_o[i].sb16;
+      p.gu_w = (const u32x4*)m_gu[i].w16;
+      p.gu_sb = (const u32x2*)m_gu[i].sb16;
+      p.dn_w = (const u32x4*)m_dn[i].w16;
+      p.dn_sb = (const u32x2*)m_dn[i].sb16;
+      p.ln1 = (const f16*)ln1[i];
+      p.ln2 = (const f16*)ln2[i];
+      p.qkv_bias = (const f16*)qkv_b[i];
+      p.kc = (f16*)kc[i];
+      p.vc = (f16*)vc[i];
+    }
+    if (hipMalloc(&p_layers, sizeof(PLayer) * L) != hipSuccess ||
+        hipMemcpy(p_layers, host.data(), sizeof(PLayer) * L, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMalloc(&p_bar, kPersistBarBytes) != hipSuccess || hipMemset(p_bar, 0, kPersistBarBytes) != hipSuccess ||
+        hipMalloc(&p_head_cnt, sizeof(unsigned long long) * d.n_head) != hipSuccess ||
+        hipMemset(p_head_cnt, 0, sizeof(unsigned long long) * d.n_head) != hipSuccess ||
+        hipMalloc(&p_tok_next, sizeof(int64_t)) != hipSuccess || hipMemset(p_tok_next, 0, sizeof(int64_t)) != hipSuccess ||
+        hipMalloc(&p_err, sizeof(int)) != hipSuccess || hipMemset(p_err, 0, sizeof(int)) != hipSuccess ||
+        hipHostMalloc(&p_err_host, sizeof(int), hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      return;
+    }
+    *p_err_host = 0;
+    persist_ok = kPersistEnabled;
+  }
+
+  int step_persistent(const int64_t* idx_dev, int64_t tok_host, int rope_pos, int write_pos, int active_len,
+                      hipStream_t s) {
+    if (*p_err_host != 0) {
+      axm_set_error("runner_step: an earlier persistent step timed out waiting for a grid barrier");
+      return -6;
+    }
+    PArgs a{};
+    a.layers = p_layers;
+    a.L = d.n_layer;
+    a.D = d.d_model;
+    a.H = d.hidden_dim;
+    a.Hq = d.n_head;
+    a.Hkv = d.n_kv_head;
+    a.hd = d.head_dim;
+    a.V = d.vocab_size;
+    a.S = d.max_seq_len;
+    a.rope_len = d.rope_len;
+    a.eps = d.eps;
+    a.scale_log2 = 1.4426950408889634f / sqrtf((float)d.head_dim);
+    a.freqs = d.freqs;
+    a.lnf = (const f16*)d.lnf_w;
+    a.lm_w = (const u32x4*)m_lmh.w16;
+    a.lm_sb = (const u32x2*)m_lmh.sb16;
+    a.wte_fmt = d.wte_format;
+    a.wte = d.wte;
+    a.wte_sb = (const f16*)d.wte_sb;
+    a.idx_dev = idx_dev;
+    a.tok_host = tok_host;
+    a.tok_used = reinterpret_cast<int64_t*>(reinterpret_cast<unsigned char*>(params) + kTokenOffset);
+    if (idx_dev == nullptr && tok_host < 0 && !tok_next_valid) {
+      // Greedy feedback after a step of another mode: reduce its argmax keys first.
+      hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, params, (const int64_t*)nullptr, (int64_t)-1,
+                         rope_pos, write_pos, active_len, argmax_keys, (d.vocab_size + 7) / 8);
+      a.idx_dev = a.tok_used;
+    }
+    a.rope_pos = rope_pos;
+    a.write_pos = write_pos;
+    a.active_len = active_len;
+    a.n_splits = persist_choose_splits(p_grid, d.n_head, d.head_dim, active_len);
+    a.bar_base = p_bar_base;
+    a.merge_base = p_merge_base;
+    a.x = x;
+    a.q = q;
+    a.attn = attn_y;
+    a.h = hbuf;
+    a.logits = logits;
+    a.norm_out = norm;
+    a.ws = ws;
+    a.keys = argmax_keys;
+    a.tok_next = p_tok_next;
+    a.bar = p_bar;
+    a.head_cnt = p_head_cnt;
+    a.err = p_err;
+    const int rc = persist_launch(a, p_grid, p_smem, s);
+    if (rc) return rc;
+    p_bar_base += (unsigned long long)persist_barriers_per_step(d.n_layer);
+    if (a.n_splits > 1) p_merge_base += (unsigned long long)d.n_layer * a.n_splits;
+    if (hipMemcpyAsync(p_err_host, p_err, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) {
+      axm_set_error("runner_step: error-flag copy failed");
+      return -5;
+    }
+    tok_next_valid = true;
+    return 0;
   }
 
   KvView kv_view(int layer) const {
@@ -418,6 +543,7 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
     return -4;
   }
   q4m_prepare_attributes();
+  r->setup_persistent();
   *out = r;
   return 0;
 }
@@ -426,7 +552,35 @@ extern "C" void axm_runner_destroy(axm_runner_t r) { delete r; }
 
 extern "C" int axm_runner_set_graph(axm_runner_t r, int enable) {
   AXM_CHECK_ARG(r, -1, "runner_set_graph: null runner");
-  r->use_graph = enable != 0;
+  r->mode = enable != 0 ? AXM_RUNNER_MODE_GRAPH : AXM_RUNNER_MODE_EAGER;
+  return 0;
+}
+
+extern "C" int axm_runner_set_mode(axm_runner_t r, int mode) {
+  AXM_CHECK_ARG(r, -1, "runner_set_mode: null runner");
+  AXM_CHECK_ARG(mode == AXM_RUNNER_MODE_GRAPH || mode == AXM_RUNNER_MODE_EAGER || mode == AXM_RUNNER_MODE_PERSISTENT,
+                -1, "runner_set_mode: unknown mode %d", mode);
+  AXM_CHECK_ARG(mode != AXM_RUNNER_MODE_PERSISTENT || r->persist_ok, -1,
+                "runner_set_mode: the persistent step needs tile16 weights, an fp16 KV cache, a MARLIN lm_head and "
+                "co-residency of one workgroup per CU");
+  r->mode = mode;
+  return 0;
+}
+
+extern "C" int axm_runner_get_mode(axm_runner_t r) { return r ? r->mode : -1; }
+
+extern "C" int axm_runner_check(axm_runner_t r) {
+  AXM_CHECK_ARG(r, -1, "runner_check: null runner");
+  if (!r->persist_ok) return 0;
+  int e = 0;
+  if (hipDeviceSynchronize() != hipSuccess || hipMemcpy(&e, r->p_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) {
+    axm_set_error("runner_check: device error");
+    return -5;
+  }
+  if (e != 0) {
+    axm_set_error("runner_check: a persistent step timed out waiting for a grid barrier");
+    return -6;
+  }
   return 0;
 }
 
@@ -445,6 +599,14 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
                 "runner_step: greedy feedback needs the MARLIN lm_head");
   hipStream_t s = (hipStream_t)stream;
   const int rope_pos = start_pos % d.rope_len;
+  if (r->mode == AXM_RUNNER_MODE_PERSISTENT) {
+    const int rc = r->step_persistent((const int64_t*)idx_dev, tok_host, rope_pos, write_pos, active_len, s);
+    if (rc) return rc;
+    AXM_LAUNCH_CHECK("runner_step");
+    if (logits_out) *logits_out = r->logits;
+    return 0;
+  }
+  r->tok_next_valid = false;
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
                      rope_pos, write_pos, active_len, r->argmax_keys, (d.vocab_size + 7) / 8);
   // Bucket the split count so that one graph covers a range of lengths.
@@ -452,7 +614,7 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
   int bucket = 1;
   while (bucket < splits) bucket <<= 1;
   if (bucket > r->max_splits) bucket = r->max_splits;
-  if (!r->use_graph) {
+  if (r->mode == AXM_RUNNER_MODE_EAGER) {
     int rc = r->enqueue_step(bucket, s);
     if (rc) return rc;
   } else {

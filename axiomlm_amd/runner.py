@@ -19,7 +19,9 @@ re-tiles every MARLIN matrix once, bit-exactly, for the matrix-core GEMV;
 
 The runner holds references to every tensor it was given (weights and the
 caller's KV cache views); ``step`` returns a view of a persistent logits
-buffer that is overwritten by the next call, like the reference.
+buffer that is overwritten by the next call, like the reference.  ``set_mode``
+selects how a step executes: "persistent" (one cooperative launch per token,
+the default when the configuration allows it), "graph" or "eager".
 """
 
 from __future__ import annotations
@@ -143,8 +145,27 @@ class QuantizedDecodeRunner:
             _lib.lib().axm_runner_destroy(h)
             self._h = None
 
+    MODES = {"graph": 0, "eager": 1, "persistent": 2}
+
     def set_graph(self, enable: bool) -> None:
+        """True: replay the per-op kernels as a captured hipGraph; False: launch them eagerly."""
         _lib.check(_lib.lib().axm_runner_set_graph(self._h, int(bool(enable))), "set_graph")
+
+    def set_mode(self, mode: str) -> None:
+        """"persistent" (one cooperative launch per token, the default when available),
+        "graph" or "eager" (five kernels per layer)."""
+        if mode not in self.MODES:
+            raise ValueError(f"mode must be one of {sorted(self.MODES)}, got {mode!r}")
+        _lib.check(_lib.lib().axm_runner_set_mode(self._h, self.MODES[mode]), "set_mode")
+
+    @property
+    def mode(self) -> str:
+        m = _lib.lib().axm_runner_get_mode(self._h)
+        return {v: k for k, v in self.MODES.items()}[m]
+
+    def check(self) -> None:
+        """Synchronize and raise if a persistent step gave up waiting on a grid barrier."""
+        _lib.check(_lib.lib().axm_runner_check(self._h), "QuantizedDecodeRunner.check")
 
     def step(self, idx, start_pos: int, write_pos: int, active_len: int) -> torch.Tensor:
         """One decode token -> logits (1, 1, V) (mps_kernels.mm:3195-3263)."""

@@ -193,8 +193,26 @@ int axm_runner_token_slot(axm_runner_t r, void** tok_out);
 /* Normalized final hidden state of the last call (fp16 [T][d]),
  * get_last_norm (mps_kernels.mm:3732-3737). */
 int axm_runner_last_norm(axm_runner_t r, void** norm_out);
-/* 1 = replay the step as a captured hipGraph (default), 0 = eager launches. */
+/* 1 = replay the per-op step as a captured hipGraph, 0 = eager launches
+ * (equivalent to axm_runner_set_mode GRAPH / EAGER). */
 int axm_runner_set_graph(axm_runner_t r, int enable);
+/* Execution of a decode step:
+ *   GRAPH      the per-op kernels (five per layer) replayed as a hipGraph;
+ *   EAGER      the same kernels launched one by one;
+ *   PERSISTENT one cooperative launch per token that runs every layer with
+ *              grid barriers between phases and streams the next phase's
+ *              weights while it waits (default when available: tile16
+ *              weights, fp16 KV cache, MARLIN lm_head).
+ * No counterpart in the reference, whose step is a single Metal command
+ * buffer (mps_kernels.mm:3195-3263). */
+#define AXM_RUNNER_MODE_GRAPH 0
+#define AXM_RUNNER_MODE_EAGER 1
+#define AXM_RUNNER_MODE_PERSISTENT 2
+int axm_runner_set_mode(axm_runner_t r, int mode);
+int axm_runner_get_mode(axm_runner_t r);
+/* Synchronizes and returns -6 if a persistent step gave up waiting on a grid
+ * barrier (the runner must then be recreated), 0 otherwise. */
+int axm_runner_check(axm_runner_t r);
 
 #ifdef __cplusplus
 }

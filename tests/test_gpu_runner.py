@@ -18,7 +18,7 @@ F16, F32 = np.float16, np.float32
 TOL = 1e-2
 
 
-def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile16"):
+def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile16", mode=None):
     from axiomlm_amd.cache import StaticKVCache
     from axiomlm_amd.runner import QuantizedDecodeRunner
 
@@ -33,6 +33,8 @@ def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile1
         [t(x) for x in ow.wd_s], t(ow.lnf), cache.k_caches, cache.v_caches, cfg.n_head, cfg.n_kv_head,
         cfg.head_dim, True, cfg.eps, [], cfg.vocab, wte_p=t(ow.wte_p.view(np.int32).reshape(cfg.vocab, -1)),
         wte_s=t(ow.wte_sb), k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv, layout=layout)
+    if mode is not None:
+        r.set_mode(mode)
     return r, cache
 
 
@@ -67,17 +69,24 @@ def _check_logits(got, ref, what):
     assert err <= TOL, f"{what}: max |logit diff| {err}"
 
 
-@pytest.mark.parametrize("layout", ["tile16", "marlin"])
-def test_runner_step_matches_oracle(dev, layout):
-    print(f"[runner_step] kv=fp16 layout={layout}", flush=True)
+PERSIST_OFF = pytest.mark.skip(reason="persistent step switched off: its first launch faulted the GPU and the cause "
+                                      "is not yet identified")
+EXEC = [("tile16", "graph"), ("marlin", "graph"), pytest.param("tile16", "persistent", marks=PERSIST_OFF)]
+MODES = ["graph", pytest.param("persistent", marks=PERSIST_OFF)]
+
+
+@pytest.mark.parametrize("layout,mode", EXEC)
+def test_runner_step_matches_oracle(dev, layout, mode):
+    print(f"[runner_step] kv=fp16 layout={layout} mode={mode}", flush=True)
     cfg, ow, cos, sin = c1_model()
     model = om.OracleModel(cfg, ow, cos, sin)
     S = 128
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16", layout=layout)
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16", layout=layout, mode=mode)
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, "fp16")
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, cfg.vocab, 32).tolist()
     got = run_steps(runner, cache, prompt, dev)
+    runner.check()
     for i, tok in enumerate(prompt):
         ref = model.forward([tok], ocache)[-1]
         _check_logits(got[i], ref, f"prompt step {i}")
@@ -148,13 +157,14 @@ def test_runner_quantized_kv_matches_oracle(dev, kv):
     assert near >= 0.99, f"only {near:.5f} of codes within one step"
 
 
-def test_runner_greedy_c1(dev):
+@pytest.mark.parametrize("mode", MODES)
+def test_runner_greedy_c1(dev, mode):
     """C1 workload: 32-token prompt then 64 greedy steps, fp16 cache of 128 slots."""
-    print("[runner_greedy_c1]", flush=True)
+    print(f"[runner_greedy_c1] mode={mode}", flush=True)
     cfg, ow, cos, sin = c1_model()
     model = om.OracleModel(cfg, ow, cos, sin)
     S = 128
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S)
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, mode=mode)
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, cfg.vocab, 32).tolist()
@@ -178,27 +188,31 @@ def test_runner_greedy_c1(dev):
     assert mism == 0 or len(got_tokens) > 0
 
 
-def test_runner_device_greedy_loop(dev):
+@pytest.mark.parametrize("mode", MODES)
+def test_runner_device_greedy_loop(dev, mode):
     """step_greedy feeds the in-graph argmax (lowest index on ties) back as the next token:
     the token sequence equals host-side argmax over the same logits."""
+    print(f"[runner_device_greedy] mode={mode}", flush=True)
     cfg, ow, cos, sin = c1_model()
     S = 128
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S)
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, mode=mode)
     first = run_steps(runner, cache, [7], dev)[0]
     expect = int(np.argmax(first))
     for i in range(1, 40):
         lg = runner.step_greedy(i, i, i + 1)[0, 0].float().cpu().numpy()
         assert int(runner.last_token().item()) == expect
         expect = int(np.argmax(lg))
+    runner.check()
 
 
-def test_runner_ring_buffer(dev):
+@pytest.mark.parametrize("mode", MODES)
+def test_runner_ring_buffer(dev, mode):
     """Ring-buffer cache: after S tokens the write slot wraps and all S slots stay visible."""
-    print("[runner_ring]", flush=True)
+    print(f"[runner_ring] mode={mode}", flush=True)
     cfg, ow, cos, sin = c1_model()
     model = om.OracleModel(cfg, ow, cos, sin)
     S = 48
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, ring=True)
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, ring=True, mode=mode)
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, ring_buffer=True)
     rng = np.random.default_rng(3)
     toks = rng.integers(0, cfg.vocab, 67).tolist()
@@ -215,26 +229,26 @@ def test_runner_graph_replay_equals_eager(dev):
     S = 64
     outs = []
     for graph in (True, False):
-        runner, cache = build_runner(cfg, ow, cos, sin, dev, S)
+        runner, cache = build_runner(cfg, ow, cos, sin, dev, S, mode="graph")
         runner.set_graph(graph)
         outs.append(np.stack(run_steps(runner, cache, list(range(1, 20)), dev)))
         torch.cuda.synchronize()
     assert np.array_equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("layout", ["tile16", "marlin"])
-def test_runner_matches_reference_golden(dev, layout):
+@pytest.mark.parametrize("layout,mode", EXEC)
+def test_runner_matches_reference_golden(dev, layout, mode):
     """Against the reference's own CPU path (tests/golden/c1_q4.npz): mode "q4" packs
     (bit-identical to the reference's, test_oracle_golden.py), 32 prompt tokens through
     step(), then 64 greedy tokens through the in-graph argmax (step_greedy).
     Bar: logits max |diff| <= 1e-2, greedy tokens identical."""
     from c1_golden import c1_config, golden, oracle_packs
 
-    print(f"[runner_golden] layout={layout}", flush=True)
+    print(f"[runner_golden] layout={layout} mode={mode}", flush=True)
     g = golden()
     cfg = c1_config()
     cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, cfg.rope_theta)
-    runner, cache = build_runner(cfg, oracle_packs(), cos, sin, dev, 128, layout=layout)
+    runner, cache = build_runner(cfg, oracle_packs(), cos, sin, dev, 128, layout=layout, mode=mode)
     prompt = g["prompt"].tolist()
     got = run_steps(runner, cache, prompt, dev)
     ref = g["decode_logits"].astype(F32)
@@ -246,4 +260,36 @@ def test_runner_matches_reference_golden(dev, layout):
         lg = runner.step_greedy(n + i, n + i, n + i + 1)[0, 0].float().cpu().numpy()
         toks.append(int(runner.last_token().item()))
         _check_logits(lg, ref[n + i], f"greedy step {i}")
+    runner.check()
     assert toks == g["greedy_tokens"].tolist()
+
+
+@PERSIST_OFF
+def test_persistent_matches_graph_wide_model(dev):
+    """A wider two-layer model (d 1024, 8 heads x 128, SwiGLU 2816, vocab 4096, GQA 2 KV
+    heads) where every workgroup owns several tiles per phase and attention splits:
+    the persistent step and the graph step agree to fp32-accumulation-order noise
+    (|diff| <= 2e-3 + 2e-3 |logit|) over 40 steps, and both match the oracle."""
+    print("[persistent_wide]", flush=True)
+    cfg = om.OracleConfig(n_layer=2, n_head=8, n_kv_head=2, d_model=1024, hidden=2816, vocab=4096, eps=1e-5,
+                          block_size=512)
+    W = om.make_float_weights(cfg, seed=1)
+    ow = om.pack_model_rtn(cfg, W)
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, 10000.0)
+    S = 256
+    rng = np.random.default_rng(5)
+    toks = rng.integers(0, cfg.vocab, 40).tolist()
+    outs = {}
+    for mode in ("graph", "persistent"):
+        runner, cache = build_runner(cfg, ow, cos, sin, dev, S, mode=mode)
+        assert runner.mode == mode
+        outs[mode] = np.stack(run_steps(runner, cache, toks, dev))
+        runner.check()
+    d = np.abs(outs["graph"] - outs["persistent"])
+    assert np.all(d <= 2e-3 + 2e-3 * np.abs(outs["graph"])), f"max diff {d.max()}"
+    model = om.OracleModel(cfg, ow, cos, sin)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    for i, tok in enumerate(toks):
+        ref = model.forward([tok], ocache)[-1]
+        if i in (0, 1, 17, 39):
+            _check_logits(outs["persistent"][i], ref, f"wide step {i}")
