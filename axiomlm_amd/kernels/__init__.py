@@ -33,6 +33,10 @@ from .quant import (  # noqa: F401
     qmv_q4_marlin,
     qmv_q8_g64,
     qmv_q4_tile16,
+    qmv_ternary,
+    qmm_ternary,
+    qmv_q2_k,
+    qmm_q2_k,
     qmv_q4_tile16_swiglu,
     qmv_q4_marlin_swiglu,
     repack_q4_marlin_tile16,

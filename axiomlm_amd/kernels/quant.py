@@ -20,6 +20,10 @@ __all__ = [
     "qmm_q4_marlin",
     "repack_q4_marlin_tile16",
     "qmv_q4_tile16",
+    "qmv_ternary",
+    "qmm_ternary",
+    "qmv_q2_k",
+    "qmm_q2_k",
     "qmv_q4_marlin_swiglu",
     "qmv_q4_tile16_swiglu",
     "pack_linear_q8_g64",
@@ -289,6 +293,42 @@ def dequantize_q2_k(w_packed, scales_biases, K: int | None = None) -> torch.Tens
     shifts = torch.arange(4, device=w_packed.device, dtype=torch.int32) * 2
     q = ((b >> shifts) & 3).view(N, K // 64, 64).to(scales_biases.dtype)
     return (q * scales_biases[..., 0:1] + scales_biases[..., 1:2]).view(N, K).to(torch.float16)
+
+
+def _lowbit_qmv(fn, name, x, w_packed, s, bias):
+    _lib.require_gpu(x, name)
+    if x.dtype != torch.float16:
+        raise RuntimeError(f"{name}: x must be float16")
+    K = x.size(-1)
+    M = x.numel() // K
+    N = int(w_packed.shape[0])
+    if int(w_packed.shape[1]) * 4 != K:
+        raise RuntimeError(f"{name}: K={K} does not match packed K={int(w_packed.shape[1]) * 4}")
+    y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
+    b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
+    _lib.check(fn(_lib.ptr(x.contiguous()), _lib.ptr(w_packed.contiguous()), _lib.ptr(s.contiguous()), _lib.ptr(b),
+                  _lib.ptr(y), M, K, N, _lib.stream_of(x.device)), name)
+    return y
+
+
+def qmv_ternary(x, w_packed, scales, bias=None) -> torch.Tensor:
+    """y = x @ W^T (+ bias) on BitNet 1.58 ternary rows (quant.py:298-318); M > 1 rows batched."""
+    return _lowbit_qmv(_lib.lib().axm_qmv_ternary, "qmv_ternary", x, w_packed, scales, bias)
+
+
+def qmm_ternary(x, w_packed, scales, bias=None) -> torch.Tensor:
+    """Batched form of :func:`qmv_ternary` (quant.py:321-336)."""
+    return qmv_ternary(x, w_packed, scales, bias)
+
+
+def qmv_q2_k(x, w_packed, scales_biases, bias=None) -> torch.Tensor:
+    """y = x @ W^T (+ bias) on reference affine 2-bit rows (quant.py:406-426)."""
+    return _lowbit_qmv(_lib.lib().axm_qmv_q2_k, "qmv_q2_k", x, w_packed, scales_biases, bias)
+
+
+def qmm_q2_k(x, w_packed, scales_biases, bias=None) -> torch.Tensor:
+    """Batched form of :func:`qmv_q2_k` (quant.py:429-444)."""
+    return qmv_q2_k(x, w_packed, scales_biases, bias)
 
 
 def compute_quantization_metrics(orig, dequant, quant_bytes: int | None = None) -> dict:

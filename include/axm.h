@@ -85,6 +85,14 @@ int axm_embed_q8_g64(const void* w_packed, const void* sb, const void* tokens_i6
  * Packers: pack_linear_ternary (quant.py:236-276), pack_linear_q2_k (quant.py:339-378). */
 int axm_pack_ternary(const void* w, int src_is_fp16, int N, int K, void* packed_u8, void* scales, void* stream);
 int axm_pack_q2_k(const void* w, int src_is_fp16, int N, int K, void* packed_u8, void* sb, void* stream);
+/* y = x W^T (+ bias) on the packed 2-bit rows, x fp16 [M][K], y fp16 [M][N], fp32
+ * accumulation.  Replaces qmv/qmm_ternary_mps (qmv/qmm_ternary_half_kernel,
+ * metal_kernels.metal:3990-4160; Python quant.py:298-336) and qmv/qmm_q2_k_mps
+ * (metal_kernels.metal:4167-4334; quant.py:406-444). */
+int axm_qmv_ternary(const void* x, const void* w_packed, const void* scales, const void* bias, void* y, int M, int K,
+                    int N, void* stream);
+int axm_qmv_q2_k(const void* x, const void* w_packed, const void* scales_biases, const void* bias, void* y, int M,
+                 int K, int N, void* stream);
 
 /* ---- norms / activations / argmax ---------------------------------------- */
 /* rmsnorm_infer_mps (mps_kernels.mm:247-266; math of axiomlm/models/modules.py:41-43). */

@@ -236,6 +236,66 @@ def test_fused_gate_up_swiglu_matches_oracle(dev, layout, M, K, H, norm):
 # ---------------------------------------------------------------------------
 # Q8 / ternary / Q2 packers and the Q8 GEMV / gather
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("fmt", ["ternary", "q2"])
+@pytest.mark.parametrize("M,N_,K,bias", [(1, 11008, 4096, False), (1, 4096, 11008, False), (3, 704, 256, True),
+                                         (5, 96, 1024, False), (2, 13, 64, True)])
+def test_lowbit_qmv_matches_oracle(dev, fmt, M, N_, K, bias):
+    """Ternary / affine 2-bit GEMV vs the reference CPU path (dequantize to fp16, then an
+    fp32-accumulated fp16 linear, quant.py:298-318 / 406-426).  The packed bytes are
+    uniform random, so every 2-bit code (including ternary's unused code 3, which the
+    reference decodes to 0) occurs.  Ternary weights dequantize exactly (+-scale), so
+    only the summation order differs: |y - ref| <= 2e-3 (1 + |ref|).  The reference Q2
+    path rounds q*s and then +b to fp16 for every weight, which the kernel does not, so
+    Q2 is checked against the unrounded weights q*s + b (<= 1e-3 (1 + |ref|), fp32
+    accumulation and the output rounding) and against the reference CPU path with the
+    per-weight rounding noise allowed (<= 4e-3 (1 + |ref|))."""
+    from axiomlm_amd.kernels import qmv_q2_k, qmv_ternary
+
+    print(f"[lowbit_qmv] fmt={fmt} M={M} N={N_} K={K} bias={bias}", flush=True)
+    rng = np.random.default_rng(N_ + K + M)
+    packed = rng.integers(0, 256, (N_, K // 4), dtype=np.uint8)
+    x = rng.standard_normal((M, K)).astype(F16)
+    b = (rng.standard_normal(N_) * 0.1).astype(F16) if bias else None
+    if fmt == "ternary":
+        s = (np.abs(rng.standard_normal((N_, K // 64))) * 0.02 + 0.001).astype(F16)
+        w = fm.dequantize_ternary(packed, s, K)
+        got = qmv_ternary(T(x, dev), T(packed, dev), T(s, dev), None if b is None else T(b, dev))
+    else:
+        s = np.stack([np.abs(rng.standard_normal((N_, K // 64))) * 0.01,
+                      rng.standard_normal((N_, K // 64)) * 0.02], axis=-1).astype(F16)
+        w = fm.dequantize_q2_k(packed, s, K)
+        got = qmv_q2_k(T(x, dev), T(packed, dev), T(s, dev), None if b is None else T(b, dev))
+    ref = fm.linear_fp16(x, w, b).astype(F32)
+    got = N(got).astype(F32)
+    err = np.abs(got - ref) / (1.0 + np.abs(ref))
+    if fmt == "ternary":
+        assert err.max() <= 2e-3, f"max rel err {err.max()}"
+        return
+    assert err.max() <= 4e-3, f"max rel err vs the reference path {err.max()}"
+    codes = ((packed.astype(np.int64)[..., None] >> (2 * np.arange(4))) & 3).reshape(N_, K // 64, 64)
+    w_exact = (codes * s[..., 0:1].astype(np.float64) + s[..., 1:2].astype(np.float64)).reshape(N_, K)
+    ref_exact = x.astype(np.float64) @ w_exact.T
+    if b is not None:
+        ref_exact = ref_exact + b.astype(np.float64)
+    err_exact = np.abs(got - ref_exact) / (1.0 + np.abs(ref_exact))
+    assert err_exact.max() <= 1e-3, f"max rel err vs unrounded weights {err_exact.max()}"
+
+
+def test_ternary_qmv_exact_on_integers(dev):
+    """Unit scales and small-integer activations make every partial sum exact in fp32:
+    the kernel must equal the reference result bit for bit."""
+    from axiomlm_amd.kernels import qmv_ternary
+
+    rng = np.random.default_rng(3)
+    N_, K = 64, 512
+    packed = rng.integers(0, 256, (N_, K // 4), dtype=np.uint8)
+    s = np.ones((N_, K // 64), F16)
+    x = rng.integers(-3, 4, (2, K)).astype(F16)
+    ref = fm.linear_fp16(x, fm.dequantize_ternary(packed, s, K))
+    got = N(qmv_ternary(T(x, dev), T(packed, dev), T(s, dev)))
+    assert np.array_equal(got, ref)
+
+
 @pytest.mark.parametrize("src", [F16, F32])
 def test_q8_pack_and_gather_bit_exact(dev, src):
     from axiomlm_amd.kernels import dequant_q8_rows, pack_linear_q8_g64
