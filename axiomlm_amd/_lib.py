@@ -31,6 +31,9 @@ _SIGNATURES = {
     "axm_tile16_bytes": (c_size_t, [c_int, c_int, c_int]),
     "axm_repack_q4_marlin_tile16": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "axm_qmv_q4_tile16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "axm_compact_tree_kv": (
+        c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int), c_int, c_void_p]
+    ),
     "axm_qmv_ternary": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "axm_qmv_q2_k": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "axm_qmv_q4_tile16_swiglu": (

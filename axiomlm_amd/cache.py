@@ -5,11 +5,13 @@ Same constructor, tensor layout and counters as the reference:
   scales (L, 2, B, Hkv, S, hd/64)   fp16 for the quantized caches
 ``k_caches[i]`` / ``v_caches[i]`` are views of ``cache[i, 0]`` / ``cache[i, 1]``.
 Writes of new rows (``update``) quantize on the GPU with the reference CPU
-quantizer semantics; ``compact_tree_path`` moves accepted tree slots with one
-HIP copy kernel per call.
+quantizer semantics; ``compact_tree_path`` moves accepted tree slots of every
+layer with one HIP kernel per call.
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -139,18 +141,19 @@ class StaticKVCache:
 
     def compact_tree_path(self, write_pos: int, accepted_indices: list[int], new_total_seen: int | None = None):
         """Move accepted tree slots (write_pos + a[m]) % S to (write_pos + m) % S in every layer
-        (paged_cache.py:376-462)."""
+        with one race-free HIP pass (paged_cache.py:376-462)."""
         n = len(accepted_indices)
         if n > 0 and not all(int(a) == m for m, a in enumerate(accepted_indices)):
-            S = self.max_seq_len
-            src = torch.tensor([(write_pos + int(a)) % S for a in accepted_indices], dtype=torch.long,
-                               device=self.cache.device)
-            dst = torch.tensor([(write_pos + m) % S for m in range(n)], dtype=torch.long, device=self.cache.device)
-            staged = self.cache.index_select(4, src).clone()
-            self.cache.index_copy_(4, dst, staged)
-            if self.scales is not None:
-                staged_s = self.scales.index_select(4, src).clone()
-                self.scales.index_copy_(4, dst, staged_s)
+            _lib.require_gpu(self.cache, "compact_tree_path")
+            if not self.cache.is_contiguous() or (self.scales is not None and not self.scales.is_contiguous()):
+                raise RuntimeError("compact_tree_path: cache and scales must be contiguous")
+            L, two, B, H, S = self.cache.shape[:5]
+            slot_bytes = self.cache.shape[5] * self.cache.element_size()
+            halves = self.scales.shape[5] if self.scales is not None else 0
+            arr = (ctypes.c_int * n)(*[int(a) for a in accepted_indices])
+            _lib.check(_lib.lib().axm_compact_tree_kv(
+                _lib.ptr(self.cache), _lib.ptr(self.scales), L * two * B * H, S, slot_bytes, halves, int(write_pos),
+                arr, n, _lib.stream_of(self.cache.device)), "compact_tree_path")
         if new_total_seen is not None:
             active = min(new_total_seen, self.max_seq_len)
             self.total_seen_tokens[:] = [new_total_seen] * self.n_layer

@@ -506,3 +506,76 @@ extern "C" int axm_kv_cache_write(const void* k_rows, const void* v_rows, int ld
   AXM_LAUNCH_CHECK("kv_cache_write");
   return 0;
 }
+
+// ---------------------------------------------------------------------------
+// Tree-path KV compaction (compact_tree_kv_{half,fp8,int4}_kernel,
+// metal_kernels.metal:3145-3179 / :3875-3978; StaticKVCache.compact_tree_path,
+// axiomlm/engine/paged_cache.py:376-462): slot (wp + acc[m]) % S moves to
+// (wp + m) % S for every (layer, k|v, batch, head) row block.  One wave owns one
+// row block and stages all accepted source rows in LDS before it writes any
+// destination, so overlapping source / destination slots cannot race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kMaxAccepted = 64;
+
+struct Accepted {
+  int idx[kMaxAccepted];
+};
+
+// words: 32-bit words per slot row of the cache; halves: fp16 scales per slot (0 = none).
+__global__ void __launch_bounds__(64) compact_tree_kernel(uint32_t* __restrict__ cache, f16* __restrict__ scales,
+                                                          int S, int words, int halves, int write_pos, Accepted acc,
+                                                          int n) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t* stage_w = reinterpret_cast<uint32_t*>(smem);         // [n][words]
+  f16* stage_s = reinterpret_cast<f16*>(stage_w + (size_t)n * words);  // [n][halves]
+  const int lane = threadIdx.x;
+  const size_t block = blockIdx.x;
+  uint32_t* rows = cache + block * (size_t)S * words;
+  f16* srows = scales != nullptr ? scales + block * (size_t)S * halves : nullptr;
+  for (int m = 0; m < n; ++m) {
+    const int src = (write_pos + acc.idx[m]) % S;
+    for (int w = lane; w < words; w += 64) stage_w[m * words + w] = rows[(size_t)src * words + w];
+    if (srows != nullptr)
+      for (int h = lane; h < halves; h += 64) stage_s[m * halves + h] = srows[(size_t)src * halves + h];
+  }
+  __syncthreads();
+  for (int m = 0; m < n; ++m) {
+    const int dst = (write_pos + m) % S;
+    for (int w = lane; w < words; w += 64) rows[(size_t)dst * words + w] = stage_w[m * words + w];
+    if (srows != nullptr)
+      for (int h = lane; h < halves; h += 64) srows[(size_t)dst * halves + h] = stage_s[m * halves + h];
+  }
+}
+
+}  // namespace
+
+extern "C" int axm_compact_tree_kv(void* cache, void* scales, int n_blocks, int max_seq_len, int slot_bytes,
+                                   int scale_halves, int write_pos, const int* accepted_host, int n_accepted,
+                                   void* stream) {
+  AXM_CHECK_ARG(cache && n_blocks > 0 && max_seq_len > 0, -1, "compact_tree_kv: bad cache");
+  AXM_CHECK_ARG(slot_bytes > 0 && slot_bytes % 4 == 0, -1, "compact_tree_kv: slot_bytes %d must be a multiple of 4",
+                slot_bytes);
+  AXM_CHECK_ARG(scales == nullptr || scale_halves > 0, -1, "compact_tree_kv: scales need scale_halves > 0");
+  AXM_CHECK_ARG(n_accepted >= 0 && n_accepted <= kMaxAccepted, -1, "compact_tree_kv: %d accepted slots (max %d)",
+                n_accepted, kMaxAccepted);
+  AXM_CHECK_ARG(write_pos >= 0 && write_pos < max_seq_len, -1, "compact_tree_kv: write_pos %d out of range",
+                write_pos);
+  if (n_accepted == 0) return 0;
+  AXM_CHECK_ARG(accepted_host != nullptr, -1, "compact_tree_kv: null accepted list");
+  Accepted acc{};
+  for (int m = 0; m < n_accepted; ++m) {
+    AXM_CHECK_ARG(accepted_host[m] >= 0 && accepted_host[m] < max_seq_len, -1,
+                  "compact_tree_kv: accepted index %d out of range", accepted_host[m]);
+    acc.idx[m] = accepted_host[m];
+  }
+  const int words = slot_bytes / 4;
+  const int halves = scales != nullptr ? scale_halves : 0;
+  const size_t smem = (size_t)n_accepted * words * 4 + (size_t)n_accepted * halves * 2;
+  AXM_CHECK_ARG(smem <= 64 * 1024, -1, "compact_tree_kv: slot rows too large (%zu B of staging)", smem);
+  hipLaunchKernelGGL(compact_tree_kernel, dim3((unsigned)n_blocks), dim3(64), smem, (hipStream_t)stream,
+                     (uint32_t*)cache, (f16*)scales, max_seq_len, words, halves, write_pos, acc, n_accepted);
+  AXM_LAUNCH_CHECK("compact_tree_kv");
+  return 0;
+}

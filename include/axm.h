@@ -116,6 +116,15 @@ int axm_argmax(const void* logits, int rows, int V, void* out_i64, void* stream)
  * (write_pos + t) % S of batch 0.  Replaces the cache write of
  * rope_kv_cache_write{,_fp8,_int4}_mps (mps_kernels.mm:589-681, 817-929) with the
  * CPU quantizer semantics of quantize_kv_fp8 / quantize_kv_int4 (quant.py:692-807). */
+/* Tree-path compaction after tree verification: in every row block of the cache
+ * (n_blocks = L * 2 * B * Hkv blocks of max_seq_len slots of slot_bytes bytes, plus
+ * optional fp16 scales of scale_halves per slot), slot (write_pos + a[m]) % S moves
+ * to (write_pos + m) % S for m < n_accepted (<= 64; accepted_host is a host array).
+ * Replaces compact_tree_kv{,_quant}_mps (compact_tree_kv_*_kernel,
+ * metal_kernels.metal:3145-3179, :3875-3978) behind StaticKVCache.compact_tree_path
+ * (axiomlm/engine/paged_cache.py:376-462). */
+int axm_compact_tree_kv(void* cache, void* scales, int n_blocks, int max_seq_len, int slot_bytes, int scale_halves,
+                        int write_pos, const int* accepted_host, int n_accepted, void* stream);
 int axm_kv_cache_write(const void* k_rows, const void* v_rows, int ld_rows, int T, void* k_cache, void* v_cache,
                        void* k_scales, void* v_scales, int kv_dtype, int n_kv_head, int head_dim, int max_seq_len,
                        int write_pos, void* stream);

@@ -515,3 +515,40 @@ def test_q4_mse_pack_matches_reference_golden(dev):
         report.append((kp, float(1.0 - same.mean())))
     print(f"[mse_golden] {exact}/{len(mats)} matrices bit-identical; near-tie groups: {report}", flush=True)
     assert all(frac <= 0.01 for _, frac in report), report
+
+
+@pytest.mark.parametrize("kv", ["fp16", "fp8", "int4"])
+def test_compact_tree_path_bit_exact(dev, kv):
+    """Tree-path compaction (paged_cache.py:376-462) against the oracle: overlapping
+    source / destination slots, a ring wrap-around and a no-op identity list."""
+    from axiomlm_amd.cache import StaticKVCache
+
+    print(f"[compact_tree] kv={kv}", flush=True)
+    L, Hkv, S, hd = 3, 2, 40, 128
+    cache = StaticKVCache(1, S, L, Hkv, hd, device=dev, cache_dtype=kv)
+    oc = om.OracleKVCache(S, L, Hkv, hd, kv)
+    rng = np.random.default_rng(9)
+    if kv == "fp16":
+        data = rng.standard_normal(tuple(cache.cache.shape)).astype(F16)
+    else:
+        data = rng.integers(0, 256, tuple(cache.cache.shape), dtype=np.uint8)
+    cache.cache.copy_(T(data, dev))
+    oc.k[...] = data[:, 0, 0]
+    oc.v[...] = data[:, 1, 0]
+    if cache.scales is not None:
+        sc = rng.standard_normal(tuple(cache.scales.shape)).astype(F16)
+        cache.scales.copy_(T(sc, dev))
+        oc.ks[...] = sc[:, 0, 0]
+        oc.vs[...] = sc[:, 1, 0]
+    for wp, acc in ((5, [0, 2, 3, 7]), (36, [1, 3, 4, 6, 7]), (10, [0, 1, 2]), (0, [4, 1, 9, 2])):
+        cache.compact_tree_path(wp, acc, new_total_seen=wp + len(acc))
+        oc.compact_tree_path(wp, acc, new_total_seen=wp + len(acc))
+        got = N(cache.cache)
+        assert np.array_equal(got[:, 0, 0].view(np.uint8), oc.k.view(np.uint8))
+        assert np.array_equal(got[:, 1, 0].view(np.uint8), oc.v.view(np.uint8))
+        if cache.scales is not None:
+            gs = N(cache.scales)
+            assert np.array_equal(gs[:, 0, 0].view(np.uint16), oc.ks.view(np.uint16))
+            assert np.array_equal(gs[:, 1, 0].view(np.uint16), oc.vs.view(np.uint16))
+        assert cache.total_seen_tokens == oc.total_seen_tokens
+        assert cache.layer_seq_lens == oc.layer_seq_lens
