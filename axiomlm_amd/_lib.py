@@ -73,6 +73,11 @@ _SIGNATURES = {
     "axm_runner_create": (c_int, [c_void_p, c_void_p]),
     "axm_runner_destroy": (None, [c_void_p]),
     "axm_runner_step": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "axm_runner_verify_step": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "axm_runner_verify_tree_step": (
+        c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
+                ctypes.POINTER(ctypes.c_uint64), c_void_p, c_void_p]
+    ),
     "axm_runner_last_norm": (c_int, [c_void_p, c_void_p]),
     "axm_runner_token_slot": (c_int, [c_void_p, c_void_p]),
     "axm_runner_set_graph": (c_int, [c_void_p, c_int]),

@@ -63,6 +63,51 @@ __global__ void __launch_bounds__(256) set_params_kernel(int* params, const int6
   }
 }
 
+constexpr int kMaxVerify = 64;
+
+struct TreeParams {
+  int pos[kMaxVerify];               // rope position of each token
+  unsigned long long mask[kMaxVerify];
+};
+
+// Copies the per-call tree description into device memory (kernel arguments,
+// so no host-to-device copy is needed).
+__global__ void set_tree_kernel(TreeParams p, int T, int* pos_dev, unsigned long long* mask_dev) {
+  const int t = threadIdx.x;
+  if (t < T) {
+    pos_dev[t] = p.pos[t];
+    mask_dev[t] = p.mask[t];
+  }
+}
+
+// Multi-token RoPE (rope_tree_kv_cache_write_half_kernel, metal_kernels.metal:2862-2918):
+// token t of qkv [T][qkv_dim] (bias already added) is rotated at pos_dev[t]; q rows go to
+// q [T][q_dim], rotated k and raw v rows to kv [T][2 kv_dim] for the cache writer.
+__global__ void rope_tokens_kernel(const f16* __restrict__ qkv, int q_dim, int kv_dim, int hd,
+                                   const float* __restrict__ freqs, const int* __restrict__ pos_dev,
+                                   f16* __restrict__ q, f16* __restrict__ kv) {
+  const int t = blockIdx.x;
+  const int qkv_dim = q_dim + 2 * kv_dim;
+  const f16* src = qkv + (size_t)t * qkv_dim;
+  const int pos = pos_dev[t];
+  const int half = hd / 2;
+  for (int e = threadIdx.x; e < qkv_dim; e += blockDim.x) {
+    f16 out = src[e];
+    if (e < q_dim + kv_dim) {
+      const int within = e < q_dim ? e : e - q_dim;
+      const int fi = (within % hd) >> 1;
+      const float c = freqs[((size_t)pos * half + fi) * 2 + 0];
+      const float sn = freqs[((size_t)pos * half + fi) * 2 + 1];
+      const float x0 = h2f(src[e & ~1]), x1 = h2f(src[e | 1]);
+      out = (e & 1) == 0 ? f2h(x0 * c - x1 * sn) : f2h(x0 * sn + x1 * c);
+    }
+    if (e < q_dim)
+      q[(size_t)t * q_dim + e] = out;
+    else
+      kv[(size_t)t * 2 * kv_dim + (e - q_dim)] = out;
+  }
+}
+
 }  // namespace
 
 // One packed matrix: the caller's reference MARLIN tensors and, when the
@@ -170,6 +215,9 @@ struct axm_runner {
   f16* hbuf = nullptr;
   f16* logits = nullptr;
   f16* norm = nullptr;
+  f16* qkvbuf = nullptr;                 // [T][qkv_dim] (multi-token paths)
+  int* tree_pos = nullptr;               // [kMaxVerify]
+  unsigned long long* tree_mask = nullptr;  // [kMaxVerify]
   float* ws = nullptr;
   size_t ws_bytes = 0;
   unsigned long long* argmax_keys = nullptr;  // per lm_head tile: ordered (logit, index) key
@@ -194,7 +242,7 @@ struct axm_runner {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
     void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys,
-                    p_layers, p_bar, p_head_cnt, p_tok_next, p_err};
+                    qkvbuf, tree_pos, tree_mask, p_layers, p_bar, p_head_cnt, p_tok_next, p_err};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     if (p_err_host) (void)hipHostFree(p_err_host);
@@ -415,6 +463,99 @@ struct axm_runner {
     return 0;
   }
 
+  // GEMV over T token rows in launches of at most 4 rows.
+  int gemv_rows(const Mat& m, int epi, int out_rows, GemvCall c, int T, hipStream_t s) {
+    for (int t0 = 0; t0 < T; t0 += 4) {
+      const int mc = (T - t0) < 4 ? (T - t0) : 4;
+      GemvCall cc = c;
+      cc.x = c.x + (size_t)t0 * c.ldx;
+      if (c.y) cc.y = c.y + (size_t)t0 * c.ldy;
+      if (c.resid) cc.resid = c.resid + (size_t)t0 * c.ldr;
+      if (c.x_norm_out) cc.x_norm_out = c.x_norm_out + (size_t)t0 * c.ldx;
+      const int rc = run_gemv(m, epi, out_rows, cc, mc, s);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+
+  // Multi-token step (verify_step / verify_tree_step, mps_kernels.mm:3265-3464).
+  // tree: token t is rotated at start_pos + depth[t], written to slot
+  // (write_pos + t) % S and attends to [0, prefix) plus the tree slots its mask
+  // selects.  !tree (ring wrap-around): all T rows are written, then every token
+  // attends over all S slots, as the reference does in that case.
+  int enqueue_verify(const int64_t* idx_dev, int T, int write_pos, int prefix, bool tree, hipStream_t s) {
+    const int D = d.d_model, H = d.hidden_dim;
+    if (d.wte_format == 0)
+      launch_embed_f16((const f16*)d.wte, idx_dev, nullptr, x, T, D, d.vocab_size, s);
+    else
+      launch_embed_q8((const uint8_t*)d.wte, (const f16*)d.wte_sb, idx_dev, nullptr, x, T, D, d.vocab_size, s);
+    for (int i = 0; i < d.n_layer; ++i) {
+      KvView kv = kv_view(i);
+      GemvCall a{};
+      a.x = x;
+      a.ldx = D;
+      a.y = qkvbuf;
+      a.ldy = qkv_dim;
+      a.bias = (const f16*)qkv_b[i];
+      a.ln_w = (const f16*)ln1[i];
+      a.eps = d.eps;
+      int rc = gemv_rows(m_qkv[i], Q4_EPI_STORE, qkv_dim, a, T, s);
+      if (rc) return rc;
+      hipLaunchKernelGGL(rope_tokens_kernel, dim3(T), dim3(256), 0, s, qkvbuf, q_dim, kv_dim, d.head_dim, d.freqs,
+                         tree_pos, q, kvst);
+      launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, T, write_pos, nullptr, s);
+      if (tree) {
+        const int splits = attn_choose_splits(T, d.n_kv_head, prefix + T);
+        rc = launch_tree_attention(q, kv, attn_y, d.n_head, T, prefix, write_pos, (const uint64_t*)tree_mask, splits, ws,
+                                   s);
+      } else {
+        const int splits = attn_choose_splits(1, d.n_kv_head, d.max_seq_len);
+        for (int t = 0; t < T && rc == 0; ++t)
+          rc = launch_flash_decode(q + (size_t)t * q_dim, kv, attn_y + (size_t)t * q_dim, d.n_head, d.max_seq_len,
+                                   nullptr, splits, ws, s);
+      }
+      if (rc) return rc;
+      GemvCall o{};
+      o.x = attn_y;
+      o.ldx = q_dim;
+      o.resid = x;
+      o.ldr = D;
+      rc = gemv_rows(m_o[i], Q4_EPI_RESID, D, o, T, s);
+      if (rc) return rc;
+      GemvCall g{};
+      g.x = x;
+      g.ldx = D;
+      g.y = hbuf;
+      g.ldy = H;
+      g.ln_w = (const f16*)ln2[i];
+      g.eps = d.eps;
+      g.pair_rows = H;
+      rc = gemv_rows(m_gu[i], Q4_EPI_SWIGLU, H, g, T, s);
+      if (rc) return rc;
+      GemvCall dn{};
+      dn.x = hbuf;
+      dn.ldx = H;
+      dn.resid = x;
+      dn.ldr = D;
+      rc = gemv_rows(m_dn[i], Q4_EPI_RESID, D, dn, T, s);
+      if (rc) return rc;
+    }
+    if (d.lm_head_format == 0) {
+      GemvCall l{};
+      l.x = x;
+      l.ldx = D;
+      l.y = logits;
+      l.ldy = d.vocab_size;
+      l.ln_w = (const f16*)d.lnf_w;
+      l.eps = d.eps;
+      l.x_norm_out = norm;
+      return gemv_rows(m_lmh, Q4_EPI_STORE, d.vocab_size, l, T, s);
+    }
+    launch_rmsnorm(x, (const f16*)d.lnf_w, norm, T, D, d.eps, s);
+    return launch_q8_gemv(norm, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, T, D,
+                          d.vocab_size, nullptr, 0.f, s);
+  }
+
   // Re-tile one matrix for the matrix-core GEMV (runner-owned copy).
   int make_tile16(Mat& m) {
     const size_t wb = t16_weight_bytes(m.N, m.K), sbb = t16_sb_bytes(m.N, m.K);
@@ -527,6 +668,9 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
       {(void**)&r->norm, (size_t)T * d.d_model * sizeof(f16)},
       {(void**)&r->ws, r->ws_bytes > 0 ? r->ws_bytes : 256},
       {(void**)&r->argmax_keys, (size_t)((d.vocab_size + 7) / 8) * sizeof(unsigned long long)},
+      {(void**)&r->qkvbuf, (size_t)T * r->qkv_dim * sizeof(f16)},
+      {(void**)&r->tree_pos, kMaxVerify * sizeof(int)},
+      {(void**)&r->tree_mask, kMaxVerify * sizeof(unsigned long long)},
   };
   for (auto& al : allocs) {
     if (hipMalloc(al.p, al.bytes) != hipSuccess) {
@@ -664,4 +808,60 @@ extern "C" int axm_runner_last_norm(axm_runner_t r, void** norm_out) {
   AXM_CHECK_ARG(r && norm_out, -1, "runner_last_norm: null argument");
   *norm_out = r->norm;
   return 0;
+}
+
+static int verify_common(axm_runner_t r, const void* idx_dev, int T, int start_pos, int write_pos, int prefix,
+                         const int* depths, const unsigned long long* masks, bool tree, void* stream,
+                         void** logits_out) {
+  const axm_runner_desc& d = r->d;
+  TreeParams tp{};
+  for (int t = 0; t < T; ++t) {
+    AXM_CHECK_ARG(depths[t] >= 0, -1, "verify: negative tree depth at %d", t);
+    tp.pos[t] = (int)(((long long)start_pos + depths[t]) % d.rope_len);
+    tp.mask[t] = masks ? masks[t] : 0ull;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(set_tree_kernel, dim3(1), dim3(kMaxVerify), 0, s, tp, T, r->tree_pos, r->tree_mask);
+  r->tok_next_valid = false;
+  const int rc = r->enqueue_verify((const int64_t*)idx_dev, T, write_pos, prefix, tree, s);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("runner_verify");
+  if (logits_out) *logits_out = r->logits;
+  return 0;
+}
+
+extern "C" int axm_runner_verify_step(axm_runner_t r, const void* idx_dev, int T, int start_pos, int write_pos,
+                                      int active_len, void* stream, void** logits_out) {
+  AXM_CHECK_ARG(r && idx_dev, -1, "runner_verify_step: null argument");
+  const axm_runner_desc& d = r->d;
+  AXM_CHECK_ARG(T >= 1 && T <= d.max_tokens && T <= kMaxVerify, -1,
+                "runner_verify_step: T=%d outside [1, %d] (runner max_tokens)", T, d.max_tokens);
+  AXM_CHECK_ARG(write_pos >= 0 && write_pos < d.max_seq_len && start_pos >= 0, -1, "runner_verify_step: bad positions");
+  AXM_CHECK_ARG(active_len >= 1 && active_len <= d.max_seq_len, -1, "runner_verify_step: bad active_len %d",
+                active_len);
+  int depths[kMaxVerify];
+  unsigned long long masks[kMaxVerify];
+  for (int t = 0; t < T; ++t) {
+    depths[t] = t;
+    masks[t] = (t == 63) ? ~0ull : ((1ull << (t + 1)) - 1ull);
+  }
+  // A contiguous chain is a tree with causal masks over the prefix [0, write_pos)
+  // (mps_kernels.mm:3371-3378); otherwise the ring case attends over all slots.
+  const bool chain = write_pos + T <= d.max_seq_len && active_len == write_pos + T;
+  return verify_common(r, idx_dev, T, start_pos, write_pos, write_pos, depths, masks, chain, stream, logits_out);
+}
+
+extern "C" int axm_runner_verify_tree_step(axm_runner_t r, const void* idx_dev, int T, int start_pos, int write_pos,
+                                           int prefix_len, const int* depths_host, const uint64_t* masks_host,
+                                           void* stream, void** logits_out) {
+  AXM_CHECK_ARG(r && idx_dev && depths_host && masks_host, -1, "runner_verify_tree_step: null argument");
+  const axm_runner_desc& d = r->d;
+  AXM_CHECK_ARG(T >= 1 && T <= d.max_tokens && T <= kMaxVerify, -1,
+                "runner_verify_tree_step: T=%d outside [1, %d] (runner max_tokens)", T, d.max_tokens);
+  AXM_CHECK_ARG(write_pos >= 0 && write_pos < d.max_seq_len && start_pos >= 0, -1,
+                "runner_verify_tree_step: bad positions");
+  AXM_CHECK_ARG(prefix_len >= 0 && prefix_len + T <= d.max_seq_len, -1, "runner_verify_tree_step: bad prefix_len %d",
+                prefix_len);
+  return verify_common(r, idx_dev, T, start_pos, write_pos, prefix_len, depths_host,
+                       (const unsigned long long*)masks_host, true, stream, logits_out);
 }

@@ -49,7 +49,7 @@ class QuantizedDecodeRunner:
     def __init__(self, wte_emb, lmh_packed, lmh_sb, freqs_r, ln1_ws, c_attn_p, c_attn_s, c_proj_p, c_proj_s,
                  ln2_ws, gate_up_p, gate_up_s, w_down_p, w_down_s, lnf_w, k_cs, v_cs, n_h, n_kvh, hd, use_q4,
                  epsilon, c_attn_bs=(), vocab_sz=-1, wte_p=None, wte_s=None, k_scales=None, v_scales=None,
-                 kv_dtype="fp16", max_tokens: int = 1, layout: str = "tile16"):
+                 kv_dtype="fp16", max_tokens: int = 32, layout: str = "tile16"):
         L = len(ln1_ws)
         if not use_q4 or c_attn_p[0].dim() != 4:
             raise RuntimeError("QuantizedDecodeRunner on MI355X supports MARLIN Q4 layer weights")
@@ -193,6 +193,40 @@ class QuantizedDecodeRunner:
         if self._logits is None:
             self._logits = _RawBuffer.view(out.value, self.vocab_size, self.device).view(1, 1, self.vocab_size)
         return self._logits
+
+    def _tokens(self, idx) -> torch.Tensor:
+        t = idx if isinstance(idx, torch.Tensor) else torch.tensor(idx)
+        return t.reshape(-1).to(device=self.device, dtype=torch.int64).contiguous()
+
+    def verify_step(self, idx, start_pos: int, write_pos: int, active_len: int) -> torch.Tensor:
+        """T tokens in one pass -> logits (1, T, V) (mps_kernels.mm:3359-3464); T == 1 is a step."""
+        t = self._tokens(idx)
+        T = int(t.numel())
+        if T == 1:
+            return self.step(t, start_pos, write_pos, active_len)
+        out = ctypes.c_void_p()
+        rc = _lib.lib().axm_runner_verify_step(self._h, _lib.ptr(t), T, int(start_pos), int(write_pos),
+                                               int(active_len), _lib.stream_of(self.device), ctypes.byref(out))
+        _lib.check(rc, "QuantizedDecodeRunner.verify_step")
+        self._keep_tokens = t
+        return _RawBuffer.view(out.value, T * self.vocab_size, self.device).view(1, T, self.vocab_size)
+
+    def verify_tree_step(self, idx, start_pos: int, write_pos: int, prefix_len: int, depths, masks) -> torch.Tensor:
+        """Tree verification -> logits (1, T, V) (mps_kernels.mm:3265-3357).  ``masks[u]`` has bit j set
+        when tree node j is visible to node u (Python ints, up to 64 nodes)."""
+        t = self._tokens(idx)
+        T = int(t.numel())
+        if len(depths) != T or len(masks) != T:
+            raise RuntimeError("tree_depths and tree_mask must match T")
+        d = (ctypes.c_int * T)(*[int(v) for v in depths])
+        m = (ctypes.c_uint64 * T)(*[int(v) & 0xFFFFFFFFFFFFFFFF for v in masks])
+        out = ctypes.c_void_p()
+        rc = _lib.lib().axm_runner_verify_tree_step(self._h, _lib.ptr(t), T, int(start_pos), int(write_pos),
+                                                    int(prefix_len), d, m, _lib.stream_of(self.device),
+                                                    ctypes.byref(out))
+        _lib.check(rc, "QuantizedDecodeRunner.verify_tree_step")
+        self._keep_tokens = t
+        return _RawBuffer.view(out.value, T * self.vocab_size, self.device).view(1, T, self.vocab_size)
 
     def last_token(self) -> torch.Tensor:
         """int64 device view of the token id consumed by the latest step."""

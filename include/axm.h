@@ -205,6 +205,21 @@ void axm_runner_destroy(axm_runner_t r);
  * next call).  Replaces QuantizedDecodeGraphState::step (mps_kernels.mm:3195-3263). */
 int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_host, int start_pos, int write_pos,
                     int active_len, void* stream, void** logits_out);
+/* T tokens (idx_dev: device int64 [T], T <= desc.max_tokens <= 64) in one pass;
+ * *logits_out receives the runner's fp16 [T][V] buffer.  verify_step rotates token t
+ * at start_pos + t and writes slot (write_pos + t) % S; when the T slots are contiguous
+ * and active_len == write_pos + T it attends causally over [0, write_pos) + the chain,
+ * otherwise (ring wrap-around) every token attends over all S slots, as the
+ * reference does.  Replaces verify_step (mps_kernels.mm:3359-3464). */
+int axm_runner_verify_step(axm_runner_t r, const void* idx_dev, int T, int start_pos, int write_pos, int active_len,
+                           void* stream, void** logits_out);
+/* Tree verification: token t is rotated at start_pos + depths[t], written to slot
+ * (write_pos + t) % S and attends to slots [0, prefix_len) plus the tree slots whose
+ * bit is set in masks[t] (64-bit masks; host arrays).  Replaces verify_tree_step
+ * (mps_kernels.mm:3265-3357), whose masks are 32-bit. */
+int axm_runner_verify_tree_step(axm_runner_t r, const void* idx_dev, int T, int start_pos, int write_pos,
+                                int prefix_len, const int* depths_host, const uint64_t* masks_host, void* stream,
+                                void** logits_out);
 /* Device int64 slot holding the token id consumed by the latest step. */
 int axm_runner_token_slot(axm_runner_t r, void** tok_out);
 /* Normalized final hidden state of the last call (fp16 [T][d]),

@@ -346,6 +346,43 @@ class OracleModel:
         xn = rmsnorm_fp16(x, self.w.lnf, c.eps)
         return qlin(xn, self.w.lmh_p, self.w.lmh_sb, c.vocab)
 
+    def forward_verify_ring(self, idx, cache: OracleKVCache, start_pos: int, write_pos: int):
+        """verify_step of the reference runner when the T slots wrap around the ring
+        (mps_kernels.mm:3380-3464): every token is rotated at start_pos + t and written to
+        slot (write_pos + t) % S, then each token attends over all S slots, unmasked."""
+        c = self.cfg
+        idx = np.asarray(idx).reshape(-1)
+        T = idx.shape[0]
+        hd = c.head_dim
+        qd, kvd = c.n_head * hd, c.n_kv_head * hd
+        n_rep = c.n_head // c.n_kv_head
+        S = cache.S
+        pos = np.array([(start_pos + t) % self.cos.shape[0] for t in range(T)])
+        cs, sn = self.cos[pos], self.sin[pos]
+        slots = np.array([(write_pos + t) % S for t in range(T)])
+        x = fm.dequant_q8_rows(idx, self.w.wte_p, self.w.wte_sb).astype(F16)
+        for i in range(c.n_layer):
+            h1 = rmsnorm_fp16(x, self.w.ln1[i], c.eps)
+            b_i = self.w.c_attn_b[i] if self.w.c_attn_b else None
+            qkv = qlin(h1, self.w.c_attn_p[i], self.w.c_attn_s[i], qd + 2 * kvd, b_i)
+            q = qkv[:, :qd].reshape(T, c.n_head, hd).transpose(1, 0, 2)
+            k = qkv[:, qd:qd + kvd].reshape(T, c.n_kv_head, hd).transpose(1, 0, 2)
+            v = qkv[:, qd + kvd:].reshape(T, c.n_kv_head, hd).transpose(1, 0, 2)
+            q = apply_rope_fp16(q, cs, sn)
+            k = apply_rope_fp16(k, cs, sn)
+            cache.write(i, slots, k, v)
+            k_all, v_all = cache.view(i, S)
+            y = sdpa_fp16(q, repeat_kv(k_all, n_rep), repeat_kv(v_all, n_rep))
+            y = y.transpose(1, 0, 2).reshape(T, qd)
+            x = (x.astype(F32) + qlin(y, self.w.c_proj_p[i], self.w.c_proj_s[i], qd).astype(F32)).astype(F16)
+            h2 = rmsnorm_fp16(x, self.w.ln2[i], c.eps)
+            gu = qlin(h2, self.w.gu_p[i], self.w.gu_s[i], 2 * c.hidden)
+            g, u = gu[:, :c.hidden].astype(F32), gu[:, c.hidden:].astype(F32)
+            sw = _h(_h(g / (F32(1.0) + np.exp(-g))) * u).astype(F16)
+            x = (x.astype(F32) + qlin(sw, self.w.wd_p[i], self.w.wd_s[i], qd).astype(F32)).astype(F16)
+        xn = rmsnorm_fp16(x, self.w.lnf, c.eps)
+        return qlin(xn, self.w.lmh_p, self.w.lmh_sb, c.vocab)
+
     def generate_greedy(self, prompt, n_new, cache: OracleKVCache):
         """Prefill the prompt then n_new greedy steps; returns (tokens, per-step logits)."""
         logits = self.forward(prompt, cache)

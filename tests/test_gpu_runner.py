@@ -293,3 +293,81 @@ def test_persistent_matches_graph_wide_model(dev):
         ref = model.forward([tok], ocache)[-1]
         if i in (0, 1, 17, 39):
             _check_logits(outs["persistent"][i], ref, f"wide step {i}")
+
+
+def _prefill(runner, cache, ocache, model, toks, dev):
+    run_steps(runner, cache, toks, dev)
+    for t in toks:
+        model.forward([t], ocache)
+
+
+def test_runner_verify_step_chain(dev):
+    """verify_step over a contiguous chain (causal over the prefix + chain,
+    mps_kernels.mm:3371-3378) against the oracle's multi-token forward, then a
+    decode step that reads the verified slots."""
+    print("[runner_verify_chain]", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    rng = np.random.default_rng(11)
+    _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 10).tolist(), dev)
+    for T in (5, 17):
+        seen = cache.total_seen_tokens[0]
+        toks = rng.integers(0, cfg.vocab, T).tolist()
+        got = runner.verify_step(torch.tensor([toks], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
+        ref = model.forward(toks, ocache, return_all_logits=True)
+        cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
+        cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
+        for t in range(T):
+            _check_logits(got[t], ref[t], f"verify T={T} token {t}")
+    tok = int(rng.integers(0, cfg.vocab))
+    got = run_steps(runner, cache, [tok], dev)[0]
+    _check_logits(got, model.forward([tok], ocache)[-1], "step after verify")
+
+
+def test_runner_verify_tree_step(dev):
+    """A 12-node draft tree (depths and 64-bit ancestor masks) against the oracle's
+    bitmask tree attention (transformer.py:639-784 semantics)."""
+    print("[runner_verify_tree]", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    rng = np.random.default_rng(12)
+    _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 20).tolist(), dev)
+    parents = [-1, 0, 0, 1, 1, 2, 3, 3, 4, 6, 6, 9]
+    depths, masks = [], []
+    for u, p in enumerate(parents):
+        depths.append(0 if p < 0 else depths[p] + 1)
+        masks.append((0 if p < 0 else masks[p]) | (1 << u))
+    toks = rng.integers(0, cfg.vocab, len(parents)).tolist()
+    seen = cache.total_seen_tokens[0]
+    got = runner.verify_tree_step(torch.tensor([toks], device=dev), seen, seen, seen, depths, masks)
+    got = got[0].float().cpu().numpy()
+    ref = model.forward_tree(toks, ocache, depths, masks)
+    for t in range(len(toks)):
+        _check_logits(got[t], ref[t], f"tree node {t}")
+
+
+def test_runner_verify_step_ring_wrap(dev):
+    """verify_step whose slots wrap around a ring cache: every token attends over all
+    S slots (the reference runner's wrap-around branch, mps_kernels.mm:3380-3464)."""
+    print("[runner_verify_ring]", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 48
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, ring=True)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, ring_buffer=True)
+    rng = np.random.default_rng(13)
+    _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 45).tolist(), dev)
+    seen = cache.total_seen_tokens[0]
+    T = 6
+    toks = rng.integers(0, cfg.vocab, T).tolist()
+    got = runner.verify_step(torch.tensor([toks], device=dev), seen, seen % S, min(seen + T, S))
+    got = got[0].float().cpu().numpy()
+    ref = model.forward_verify_ring(toks, ocache, seen, seen % S)
+    for t in range(T):
+        _check_logits(got[t], ref[t], f"ring verify token {t}")
