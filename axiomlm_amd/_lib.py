@@ -78,6 +78,10 @@ _SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
                 ctypes.POINTER(ctypes.c_uint64), c_void_p, c_void_p]
     ),
+    "axm_runner_speculative_decode": (
+        c_int, [c_void_p, ctypes.POINTER(c_int64), c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int64), c_int,
+                ctypes.POINTER(c_int64), c_void_p]
+    ),
     "axm_runner_last_norm": (c_int, [c_void_p, c_void_p]),
     "axm_runner_token_slot": (c_int, [c_void_p, c_void_p]),
     "axm_runner_set_graph": (c_int, [c_void_p, c_int]),

@@ -14,6 +14,9 @@
 // in a small device parameter block written by one tiny kernel before the
 // graph is replayed, so a single captured hipGraph serves every step; graphs
 // are cached per attention split count.
+#include <algorithm>
+#include <chrono>
+#include <cstring>
 #include <map>
 #include <vector>
 
@@ -864,4 +867,134 @@ extern "C" int axm_runner_verify_tree_step(axm_runner_t r, const void* idx_dev, 
                 prefix_len);
   return verify_common(r, idx_dev, T, start_pos, write_pos, prefix_len, depths_host,
                        (const unsigned long long*)masks_host, true, stream, logits_out);
+}
+
+// ---------------------------------------------------------------------------
+// Prompt-lookup speculative decoding with greedy acceptance, run natively
+// (speculative_decode, mps_kernels.mm:3639-3730; find_candidate_ngram_cpp,
+// :368-396).  Each iteration either decodes one token (no n-gram match) or
+// verifies [last token, candidates...] in one multi-token pass and accepts the
+// matching prefix plus the first corrected / bonus token.
+// ---------------------------------------------------------------------------
+static std::vector<int64_t> find_candidate_ngram(const std::vector<int64_t>& ids, int64_t n, int64_t max_spec) {
+  const int64_t len = (int64_t)ids.size();
+  if (len < n + 1) return {};
+  const int64_t search_end = len - n;
+  for (int64_t i = search_end - 1; i >= 0; --i) {
+    bool match = true;
+    for (int64_t k = 0; k < n; ++k)
+      if (ids[i + k] != ids[search_end + k]) {
+        match = false;
+        break;
+      }
+    if (match) {
+      const int64_t start = i + n;
+      const int64_t end = std::min(start + max_spec, search_end);
+      if (start < end) return std::vector<int64_t>(ids.begin() + start, ids.begin() + end);
+    }
+  }
+  return {};
+}
+
+extern "C" int axm_runner_speculative_decode(axm_runner_t r, const int64_t* initial_tokens, int n_initial,
+                                             int max_new_tokens, int ngram_size, int max_spec_tokens, int start_pos,
+                                             int64_t* out_tokens, int out_capacity, int64_t* stats, void* stream) {
+  AXM_CHECK_ARG(r && initial_tokens && out_tokens && stats, -1, "speculative_decode: null argument");
+  AXM_CHECK_ARG(n_initial >= 1 && max_new_tokens >= 0 && ngram_size >= 1 && max_spec_tokens >= 0 && start_pos >= 0,
+                -1, "speculative_decode: bad arguments");
+  AXM_CHECK_ARG(out_capacity >= n_initial + max_new_tokens, -1, "speculative_decode: output capacity too small");
+  const axm_runner_desc& d = r->d;
+  AXM_CHECK_ARG(1 + max_spec_tokens <= d.max_tokens, -1, "speculative_decode: max_spec_tokens + 1 exceeds max_tokens %d",
+                d.max_tokens);
+  AXM_CHECK_ARG(d.lm_head_format == 0 || d.lm_head_format == 1, -1, "speculative_decode: bad lm_head");
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<int64_t> gen(initial_tokens, initial_tokens + n_initial);
+  const int64_t target = (int64_t)n_initial + max_new_tokens;
+  int64_t seen = start_pos, calls = 0, drafted = 0, accepted_total = 0;
+  int64_t* host = nullptr;  // pinned staging: [0, 64) tokens in, [64, 128) predictions out
+  int64_t* dev = nullptr;
+  if (hipHostMalloc((void**)&host, 128 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess ||
+      hipMalloc((void**)&dev, 128 * sizeof(int64_t)) != hipSuccess) {
+    if (host) (void)hipHostFree(host);
+    axm_set_error("speculative_decode: staging allocation failed");
+    return -4;
+  }
+  int rc = 0;
+  if (hipStreamSynchronize(s) != hipSuccess) rc = -5;
+  const auto t0 = std::chrono::high_resolution_clock::now();
+  while (rc == 0 && (int64_t)gen.size() < target) {
+    const std::vector<int64_t> cand = find_candidate_ngram(gen, ngram_size, max_spec_tokens);
+    const int64_t k = (int64_t)cand.size();
+    const int T = (int)(1 + k);
+    host[0] = gen.back();
+    for (int64_t c = 0; c < k; ++c) host[1 + c] = cand[c];
+    if (hipMemcpyAsync(dev, host, T * sizeof(int64_t), hipMemcpyHostToDevice, s) != hipSuccess) {
+      rc = -5;
+      break;
+    }
+    const int write_pos = (int)(seen % d.max_seq_len);
+    const int rope_pos = (int)(seen % d.rope_len);
+    if (k == 0) {
+      const int active = (int)std::min<int64_t>(seen + 1, d.max_seq_len);
+      rc = axm_runner_step(r, dev, 0, rope_pos, write_pos, active, stream, nullptr);
+    } else {
+      // Chain verification when the T slots do not wrap (prefix = write_pos), else the
+      // all-slots branch (mps_kernels.mm:3555-3620).
+      int depths[kMaxVerify];
+      unsigned long long masks[kMaxVerify];
+      for (int t = 0; t < T; ++t) {
+        depths[t] = t;
+        masks[t] = (t == 63) ? ~0ull : ((1ull << (t + 1)) - 1ull);
+      }
+      const bool chain = write_pos + T <= d.max_seq_len;
+      rc = verify_common(r, dev, T, rope_pos, write_pos, write_pos, depths, masks, chain, stream, nullptr);
+    }
+    if (rc) break;
+    launch_argmax(r->logits, T, d.vocab_size, dev + 64, s);
+    if (hipMemcpyAsync(host + 64, dev + 64, T * sizeof(int64_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+      rc = -5;
+      break;
+    }
+    ++calls;
+    if (k == 0) {
+      gen.push_back(host[64]);
+      seen += 1;
+      continue;
+    }
+    drafted += k;
+    int64_t acc = 0;
+    bool all_matched = true;
+    for (int64_t j = 0; j < k; ++j) {
+      const int64_t pred = host[64 + j];
+      gen.push_back(pred);
+      acc += 1;
+      if (pred != cand[j] || (int64_t)gen.size() >= target) {
+        all_matched = false;
+        break;
+      }
+    }
+    if (all_matched && (int64_t)gen.size() < target) {
+      gen.push_back(host[64 + k]);
+      acc += 1;
+    }
+    accepted_total += std::max<int64_t>(0, acc - 1);
+    seen += acc;
+  }
+  const double secs = std::chrono::duration<double>(std::chrono::high_resolution_clock::now() - t0).count();
+  (void)hipHostFree(host);
+  (void)hipFree(dev);
+  if (rc) {
+    if (rc == -5) axm_set_error("speculative_decode: device error");
+    return rc;
+  }
+  const int n = (int)std::min<int64_t>((int64_t)gen.size(), out_capacity);
+  for (int i = 0; i < n; ++i) out_tokens[i] = gen[i];
+  stats[0] = n;
+  stats[1] = seen;
+  stats[2] = calls;
+  stats[3] = drafted;
+  stats[4] = accepted_total;
+  std::memcpy(&stats[5], &secs, sizeof(double));
+  return 0;
 }

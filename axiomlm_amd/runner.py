@@ -228,6 +228,23 @@ class QuantizedDecodeRunner:
         self._keep_tokens = t
         return _RawBuffer.view(out.value, T * self.vocab_size, self.device).view(1, T, self.vocab_size)
 
+    def speculative_decode(self, initial_tokens, max_new_tokens: int, ngram_size: int, max_spec_tokens: int,
+                           start_pos: int):
+        """Native prompt-lookup speculative decoding (mps_kernels.mm:3639-3730).  Returns
+        (tokens, seen, model_forward_calls, drafted, accepted, seconds) like the reference."""
+        init = [int(t) for t in initial_tokens]
+        n = len(init)
+        cap = n + int(max_new_tokens)
+        a = (ctypes.c_int64 * n)(*init)
+        out = (ctypes.c_int64 * cap)()
+        stats = (ctypes.c_int64 * 6)()
+        rc = _lib.lib().axm_runner_speculative_decode(self._h, a, n, int(max_new_tokens), int(ngram_size),
+                                                      int(max_spec_tokens), int(start_pos), out, cap, stats,
+                                                      _lib.stream_of(self.device))
+        _lib.check(rc, "QuantizedDecodeRunner.speculative_decode")
+        secs = ctypes.cast(ctypes.byref(stats, 5 * 8), ctypes.POINTER(ctypes.c_double))[0]
+        return list(out[:stats[0]]), int(stats[1]), int(stats[2]), int(stats[3]), int(stats[4]), float(secs)
+
     def last_token(self) -> torch.Tensor:
         """int64 device view of the token id consumed by the latest step."""
         p = ctypes.c_void_p()

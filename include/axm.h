@@ -220,6 +220,16 @@ int axm_runner_verify_step(axm_runner_t r, const void* idx_dev, int T, int start
 int axm_runner_verify_tree_step(axm_runner_t r, const void* idx_dev, int T, int start_pos, int write_pos,
                                 int prefix_len, const int* depths_host, const uint64_t* masks_host, void* stream,
                                 void** logits_out);
+/* Native prompt-lookup speculative decoding with greedy acceptance: n-gram
+ * candidates from the token history are verified in one multi-token pass, the
+ * matching prefix plus one corrected / bonus token is kept.  Host arrays;
+ * out_tokens receives the whole sequence (initial + generated, capacity >=
+ * n_initial + max_new_tokens); stats = {n_tokens, seen, model_calls, drafted,
+ * accepted, seconds (double bits)}.  Replaces speculative_decode
+ * (mps_kernels.mm:3639-3730). */
+int axm_runner_speculative_decode(axm_runner_t r, const int64_t* initial_tokens, int n_initial, int max_new_tokens,
+                                  int ngram_size, int max_spec_tokens, int start_pos, int64_t* out_tokens,
+                                  int out_capacity, int64_t* stats, void* stream);
 /* Device int64 slot holding the token id consumed by the latest step. */
 int axm_runner_token_slot(axm_runner_t r, void** tok_out);
 /* Normalized final hidden state of the last call (fp16 [T][d]),

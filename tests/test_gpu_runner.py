@@ -371,3 +371,27 @@ def test_runner_verify_step_ring_wrap(dev):
     ref = model.forward_verify_ring(toks, ocache, seen, seen % S)
     for t in range(T):
         _check_logits(got[t], ref[t], f"ring verify token {t}")
+
+
+def test_runner_speculative_decode_matches_greedy(dev):
+    """Native prompt-lookup speculative decoding (mps_kernels.mm:3639-3730) is lossless
+    under greedy acceptance: its tokens equal plain greedy decoding by the oracle; a
+    repetitive prompt makes the n-gram lookup draft (drafted > 0, fewer model calls
+    than new tokens)."""
+    print("[runner_speculative]", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S)
+    rng = np.random.default_rng(14)
+    motif = rng.integers(0, cfg.vocab, 8).tolist()
+    prompt = motif * 3
+    run_steps(runner, cache, prompt[:-1], dev)
+    n_new = 40
+    toks, seen, calls, drafted, accepted, secs = runner.speculative_decode(prompt, n_new, 3, 8, len(prompt) - 1)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    ref_toks, _ = model.generate_greedy(prompt, n_new, ocache)
+    assert toks[:len(prompt)] == prompt
+    assert toks[len(prompt):] == list(ref_toks), (toks[len(prompt):], list(ref_toks))
+    assert seen == len(prompt) - 1 + n_new and calls <= n_new and drafted >= accepted >= 0 and secs > 0
+    print(f"[runner_speculative] calls={calls} drafted={drafted} accepted={accepted}", flush=True)
