@@ -9,6 +9,7 @@ import os
 
 import numpy as np
 
+from oracle import formats as fm
 from oracle import model as om
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "c1_q4.npz")
@@ -47,3 +48,17 @@ def named_packs(ow: om.OracleWeights) -> dict:
         for i, a in enumerate(lst):
             out[f"{key}{i}"] = a
     return out
+
+
+def marlin_near_tie_fraction(wm: np.ndarray, sb: np.ndarray, ref_p: np.ndarray, ref_s: np.ndarray, K: int,
+                             what: str = "") -> float:
+    """Fraction of (row, group) entries whose (scale, bias) differ from the reference pack;
+    asserts that wherever they agree the 4-bit codes agree bit for bit.  The MSE clip search
+    may pick another candidate only where two candidates' weighted errors tie up to fp32
+    summation order."""
+    same = np.all(sb.view(np.uint16) == ref_s.view(np.uint16), axis=-1)  # [tile, g, row]
+    agree = same.transpose(0, 2, 1).reshape(-1, K // 64)
+    cg = fm.unpack_marlin_codes(wm).reshape(-1, K // 64, 64)
+    cr = fm.unpack_marlin_codes(ref_p).reshape(-1, K // 64, 64)
+    assert np.array_equal(cg[agree], cr[agree]), what
+    return float(1.0 - same.mean())
