@@ -58,6 +58,11 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
          c_void_p],
     ),
+    "axm_rope_kv_cache_write": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+         c_int, c_int, c_int, c_int, c_int, c_void_p],
+    ),
     "axm_attention_num_splits": (c_int, [c_int, c_int, c_int]),
     "axm_attention_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "axm_gqa_flash_decode": (

@@ -28,7 +28,9 @@ HIP_FLAGS = [
     "-O3",
     "-fPIC",
     "-std=c++17",
-    "-ffp-contract=fast",
+    # Contraction into multiply-adds everywhere except code marked
+    # "#pragma clang fp contract(off)" (the rounded helpers of axm_common.h).
+    "-ffp-contract=fast-honor-pragmas",
     # Packed-fp32 VALU ops are disabled for all device code on this target.
     "-Xclang",
     "-target-feature",

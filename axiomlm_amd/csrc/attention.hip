@@ -29,21 +29,11 @@ constexpr float kNegBig = -1e30f;
 //   xs    = fp16(x / scale)                 (fp16 division)
 //   fp8   = e4m3fn(float(xs));   int4 = clamp(rne(xs), -8, 7)
 // ---------------------------------------------------------------------------
-__global__ void kv_write_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld,
-                                int write_pos, const int* __restrict__ write_pos_dev) {
-  const int lane = threadIdx.x;  // 64 lanes
+// Lane `lane` of one wave stores element g*64 + lane of the key (which = 0) or
+// value (which = 1) row of kv head h at `slot` (batch 0).  Quantized caches
+// need all 64 lanes of the wave on the same (row, group).
+__device__ __forceinline__ void kv_store_lane(const KvView& kv, int which, int h, int slot, int g, int lane, f16 x) {
   const int G = kv.hd / 64;
-  int idx = blockIdx.x;
-  const int g = idx % G;
-  idx /= G;
-  const int h = idx % kv.Hkv;
-  idx /= kv.Hkv;
-  const int which = idx % 2;  // 0 = k, 1 = v
-  const int t = idx / 2;
-  const int wp0 = write_pos_dev ? write_pos_dev[0] : write_pos;
-  const int slot = (wp0 + t) % kv.S;
-  const f16* src = (which == 0 ? k_rows : v_rows) + (size_t)t * ld + h * kv.hd + g * 64;
-  const f16 x = src[lane];
   const size_t row = (size_t)h * kv.S + slot;  // batch 0
   if (kv.kv_dtype == AXM_KV_FP16) {
     f16* dst = (f16*)(which == 0 ? kv.k : kv.v);
@@ -81,6 +71,72 @@ __global__ void kv_write_kernel(KvView kv, const f16* __restrict__ k_rows, const
       dst[row * (kv.hd / 2) + g * 32 + lane / 2] = (uint8_t)((qi & 0xF) | ((partner & 0xF) << 4));
     }
   }
+}
+
+__global__ void kv_write_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld,
+                                int write_pos, const int* __restrict__ write_pos_dev) {
+  const int lane = threadIdx.x;  // 64 lanes
+  const int G = kv.hd / 64;
+  int idx = blockIdx.x;
+  const int g = idx % G;
+  idx /= G;
+  const int h = idx % kv.Hkv;
+  idx /= kv.Hkv;
+  const int which = idx % 2;  // 0 = k, 1 = v
+  const int t = idx / 2;
+  const int wp0 = write_pos_dev ? write_pos_dev[0] : write_pos;
+  const int slot = (wp0 + t) % kv.S;
+  const f16* src = (which == 0 ? k_rows : v_rows) + (size_t)t * ld + h * kv.hd + g * 64;
+  kv_store_lane(kv, which, h, slot, g, lane, src[lane]);
+}
+
+// Fused bias + RoPE + KV-cache write of T tokens (rope_kv_cache_write_half_kernel,
+// metal_kernels.metal:991-1036; fp8/int4 :1110-1279; tree variants :2862-2918,
+// :1282-1473).  qkv [T][q_dim + 2 kv_dim] fp16, updated in place for the query
+// part: token t is rotated at pos[t]; its rotated key and its value go to slot
+// (write_pos + t) % S.  One wave per (token, 64-element chunk of the row).
+struct RopePositions {
+  int pos[64];
+};
+
+__global__ void __launch_bounds__(64) rope_kv_write_kernel(f16* __restrict__ qkv, const f16* __restrict__ bias,
+                                                           const float* __restrict__ freqs, RopePositions rp,
+                                                           int q_dim, int kv_dim, KvView kv, int write_pos) {
+  const int lane = threadIdx.x;
+  const int t = blockIdx.y;
+  const int qkv_dim = q_dim + 2 * kv_dim;
+  const int e = blockIdx.x * 64 + lane;
+  const int hd = kv.hd;
+  f16* row = qkv + (size_t)t * qkv_dim;
+  const int slot = (write_pos + t) % kv.S;
+  const bool quant = kv.kv_dtype != AXM_KV_FP16;
+  if (e >= qkv_dim) return;  // only the fp16 cache allows a partial last chunk
+  f16 x = row[e];
+  f16 xp = row[e ^ 1];
+  if (bias != nullptr) {
+    x = hadd(x, bias[e]);
+    xp = hadd(xp, bias[e ^ 1]);
+  }
+  if (e < q_dim + kv_dim) {
+    const int within = e < q_dim ? e : e - q_dim;
+    const int fi = (within % hd) >> 1;
+    const float* f = freqs + ((size_t)rp.pos[t] * (hd / 2) + fi) * 2;
+    const bool even = (e & 1) == 0;
+    x = even ? rope_out(x, xp, f[0], f[1], true) : rope_out(xp, x, f[0], f[1], false);
+  }
+  if (e < q_dim) {
+    row[e] = x;
+    return;
+  }
+  const int which = e < q_dim + kv_dim ? 0 : 1;
+  const int within = e - q_dim - which * kv_dim;
+  const int h = within / hd, c = within % hd;
+  if (!quant) {
+    f16* dst = (f16*)(which == 0 ? kv.k : kv.v);
+    dst[((size_t)h * kv.S + slot) * hd + c] = x;
+    return;
+  }
+  kv_store_lane(kv, which, h, slot, c / 64, lane, x);
 }
 
 // Dequantized key/value chunk: 8 consecutive elements starting at e0 of slot `slot`.
@@ -504,6 +560,39 @@ extern "C" int axm_kv_cache_write(const void* k_rows, const void* v_rows, int ld
                 write_pos);
   launch_kv_write(kv, (const f16*)k_rows, (const f16*)v_rows, ld_rows, T, write_pos, nullptr, (hipStream_t)stream);
   AXM_LAUNCH_CHECK("kv_cache_write");
+  return 0;
+}
+
+extern "C" int axm_rope_kv_cache_write(void* qkv, int T, const void* freqs, int rope_len, int start_pos,
+                                       const int* depths_host, const void* qkv_bias, void* k_cache, void* v_cache,
+                                       void* k_scales, void* v_scales, int kv_dtype, int q_dim, int kv_dim,
+                                       int head_dim, int max_seq_len, int write_pos, void* stream) {
+  KvView kv{k_cache, v_cache, (f16*)k_scales, (f16*)v_scales, kv_dtype, 1, 0, max_seq_len, head_dim};
+  AXM_CHECK_ARG(qkv && freqs && k_cache && v_cache, -1, "rope_kv_cache_write: null pointer");
+  AXM_CHECK_ARG(T >= 1 && T <= 64, -1, "rope_kv_cache_write: T=%d outside [1, 64]", T);
+  AXM_CHECK_ARG(head_dim >= 2 && head_dim % 2 == 0 && q_dim > 0 && kv_dim > 0 && q_dim % head_dim == 0 &&
+                    kv_dim % head_dim == 0,
+                -1, "rope_kv_cache_write: bad dims q_dim=%d kv_dim=%d head_dim=%d", q_dim, kv_dim, head_dim);
+  kv.Hkv = kv_dim / head_dim;
+  if (kv_dtype != AXM_KV_FP16) {
+    AXM_CHECK_ARG(kv_dtype == AXM_KV_FP8 || kv_dtype == AXM_KV_INT4, -1, "rope_kv_cache_write: bad kv dtype %d",
+                  kv_dtype);
+    AXM_CHECK_ARG(head_dim % 64 == 0 && k_scales && v_scales, -1,
+                  "rope_kv_cache_write: quantized caches need head_dim %% 64 == 0 and scale tensors");
+  }
+  AXM_CHECK_ARG(rope_len >= 1 && start_pos >= 0 && max_seq_len >= 1 && write_pos >= 0 && write_pos < max_seq_len, -1,
+                "rope_kv_cache_write: bad positions start_pos=%d write_pos=%d", start_pos, write_pos);
+  RopePositions rp{};
+  for (int t = 0; t < T; ++t) {
+    const int d = depths_host ? depths_host[t] : t;
+    AXM_CHECK_ARG(d >= 0, -1, "rope_kv_cache_write: negative depth at %d", t);
+    rp.pos[t] = (int)(((long long)start_pos + d) % rope_len);
+  }
+  const int qkv_dim = q_dim + 2 * kv_dim;
+  const dim3 grid((qkv_dim + 63) / 64, T);
+  hipLaunchKernelGGL(rope_kv_write_kernel, grid, dim3(64), 0, (hipStream_t)stream, (f16*)qkv, (const f16*)qkv_bias,
+                     (const float*)freqs, rp, q_dim, kv_dim, kv, write_pos);
+  AXM_LAUNCH_CHECK("rope_kv_cache_write");
   return 0;
 }
 

@@ -53,9 +53,32 @@ __device__ __forceinline__ f16 f2h(float f) { return (f16)f; }
 __device__ __forceinline__ f16 u16_as_h(uint16_t u) { return __builtin_bit_cast(f16, u); }
 __device__ __forceinline__ uint16_t h_as_u16(f16 h) { return __builtin_bit_cast(uint16_t, h); }
 
+// fp32 operations rounded one at a time: never fused into a multiply-add, so
+// sequences of them reproduce the CPU reference's rounding step for step.
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 // fp16 op emulation of torch CPU kernels: every elementwise op rounds to fp16.
-__device__ __forceinline__ f16 hadd(f16 a, f16 b) { return f2h(__fadd_rn(h2f(a), h2f(b))); }
-__device__ __forceinline__ f16 hmul(f16 a, f16 b) { return f2h(__fmul_rn(h2f(a), h2f(b))); }
+__device__ __forceinline__ f16 hadd(f16 a, f16 b) { return f2h(add_rn(h2f(a), h2f(b))); }
+__device__ __forceinline__ f16 hmul(f16 a, f16 b) { return f2h(mul_rn(h2f(a), h2f(b))); }
+
+// One output of the interleaved-pair RoPE rotation (x0, x1) by (c, s) as the
+// reference CPU path evaluates it (quant.py:970-980, modules.py:111-121): fp32
+// products and sum each rounded (no fused multiply-add), then one fp16 rounding.
+__device__ __forceinline__ f16 rope_out(f16 x0, f16 x1, float c, float s, bool even) {
+  const float a = h2f(x0), b = h2f(x1);
+  return even ? f2h(sub_rn(mul_rn(a, c), mul_rn(b, s))) : f2h(add_rn(mul_rn(a, s), mul_rn(b, c)));
+}
 
 // Torch-CPU fp16 RMSNorm scale (axiomlm/models/modules.py:41-43 evaluated on a
 // half model): mean of the fp16-rounded squares accumulated in fp32 and

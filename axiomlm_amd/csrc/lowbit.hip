@@ -25,13 +25,13 @@ __global__ void pack_affine_kernel(const void* __restrict__ w, int src_fp16, int
   const float mx = wave_max(x);
   float denom;
   if (src_fp16) {
-    denom = h2f(f2h(__fsub_rn(mx, mn)));  // fp16 subtraction; the 1e-8 clamp bound rounds to 0 in fp16
+    denom = h2f(f2h(sub_rn(mx, mn)));  // fp16 subtraction; the 1e-8 clamp bound rounds to 0 in fp16
   } else {
-    denom = fmaxf(__fsub_rn(mx, mn), 1e-8f);
+    denom = fmaxf(sub_rn(mx, mn), 1e-8f);
   }
   const f16 sc = f2h(__fdiv_rn(denom, qmax));
   const f16 bi = f2h(mn);
-  float q = __builtin_rintf(__fdiv_rn(__fsub_rn(x, h2f(bi)), fmaxf(h2f(sc), 1e-8f)));
+  float q = __builtin_rintf(__fdiv_rn(sub_rn(x, h2f(bi)), fmaxf(h2f(sc), 1e-8f)));
   q = fminf(fmaxf(q, 0.f), qmax);
   if (qmax > 3.5f) {
     codes[idx] = (uint8_t)q;

@@ -138,7 +138,7 @@ __global__ void embed_q8_kernel(const uint8_t* __restrict__ wq, const f16* __res
   for (int k = threadIdx.x; k < D; k += blockDim.x) {
     const float q = (float)wq[(size_t)tok * D + k];
     const f16* sbr = sb + ((size_t)tok * G + k / 64) * 2;
-    out[(size_t)t * D + k] = f2h(__fadd_rn(__fmul_rn(q, h2f(sbr[0])), h2f(sbr[1])));
+    out[(size_t)t * D + k] = f2h(add_rn(mul_rn(q, h2f(sbr[0])), h2f(sbr[1])));
   }
 }
 

@@ -300,7 +300,7 @@ __device__ void stage(const PArgs& a, const Smem& sm, const f16* src, int K, con
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
               const float qq = (float)((qv[e >> 2] >> (8 * (e & 3))) & 0xFFu);
-              v[e] = f2h(__fadd_rn(__fmul_rn(qq, s), b));
+              v[e] = f2h(add_rn(mul_rn(qq, s), b));
             }
           }
         }
@@ -563,10 +563,10 @@ __device__ void epilogue_qkv(const PArgs& a, const Smem& sm, const Phase& cur, c
       f16 out = h;
       if (row < q_dim + kv_dim) {
         const bool even = (row & 1) == 0;
-        const float x0 = even ? h2f(h) : partner;
-        const float x1 = even ? partner : h2f(h);
+        const f16 x0 = even ? h : f2h(partner);
+        const f16 x1 = even ? f2h(partner) : h;
         const float c = sm.fr[2 * (ul * 16 + j)], s = sm.fr[2 * (ul * 16 + j) + 1];
-        out = even ? f2h(x0 * c - x1 * s) : f2h(x0 * s + x1 * c);
+        out = rope_out(x0, x1, c, s, even);
       }
       if (row < q_dim) {
         st_dev2(rq, row * 2, out);

@@ -196,8 +196,7 @@ __device__ __forceinline__ void q4_epilogue(const Q4GemvArgs& a, int unit, int l
         const int rp = pos % a.rope_len;
         const float c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
         const float sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
-        const float x0 = h2f(h0), x1 = h2f(h1);
-        out = even ? f2h(x0 * c - x1 * sn) : f2h(x0 * sn + x1 * c);
+        out = rope_out(h0, h1, c, sn, even);
       }
       if (row < a.q_dim) {
         a.y[(size_t)mi * a.ldy + row] = out;
@@ -411,7 +410,7 @@ __global__ void q4m_dequant_kernel(const uint32_t* __restrict__ w, const f16x2* 
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const uint32_t q = (word >> (16 * half + 4 * s)) & 0xFu;
-        out[(size_t)row * K + 64 * g + 32 * j + 8 * s + r] = f2h(__fadd_rn(__fmul_rn((float)q, sc), bi));
+        out[(size_t)row * K + 64 * g + 32 * j + 8 * s + r] = f2h(add_rn(mul_rn((float)q, sc), bi));
       }
     }
   }
@@ -458,11 +457,11 @@ __global__ void __launch_bounds__(64) q4m_pack_rtn_kernel(const void* __restrict
   float denom;
   f16 sc_h;
   if (SRC_FP16) {
-    f16 d = f2h(__fsub_rn(mx, mn));  // fp16 subtraction; clamp(min=1e-8) is a no-op in fp16
+    f16 d = f2h(sub_rn(mx, mn));  // fp16 subtraction; clamp(min=1e-8) is a no-op in fp16
     denom = h2f(d);
     sc_h = f2h(__fdiv_rn(denom, 15.0f));
   } else {
-    denom = fmaxf(__fsub_rn(mx, mn), 1e-8f);
+    denom = fmaxf(sub_rn(mx, mn), 1e-8f);
     sc_h = f2h(__fdiv_rn(denom, 15.0f));
   }
   const f16 bi_h = f2h(mn);
@@ -470,7 +469,7 @@ __global__ void __launch_bounds__(64) q4m_pack_rtn_kernel(const void* __restrict
   const float bif = h2f(bi_h);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float q = __builtin_rintf(__fdiv_rn(__fsub_rn(vals[i], bif), scf));
+    float q = __builtin_rintf(__fdiv_rn(sub_rn(vals[i], bif), scf));
     q = fminf(fmaxf(q, 0.f), 15.f);
     qs[c][8 * sub + i] = (uint8_t)q;
   }
@@ -522,28 +521,28 @@ __global__ void __launch_bounds__(512) q4m_pack_mse_kernel(const void* __restric
   const bool has_ig = col_imp != nullptr;
   if (has_ig) {
     const float imp = col_imp[k];
-    const float ig2 = __fmul_rn(imp, imp);
+    const float ig2 = mul_rn(imp, imp);
     const float mean = __fdiv_rn(wave_sum(ig2), 64.f);
     ig = __fdiv_rn(ig2, fmaxf(mean, 1e-8f));
   }
   const float mn0 = -wave_max(-w);
   const float mx0 = wave_max(w);
-  const float mu = __fdiv_rn(wave_sum(has_ig ? __fmul_rn(w, ig) : w), 64.f);
+  const float mu = __fdiv_rn(wave_sum(has_ig ? mul_rn(w, ig) : w), 64.f);
 
   auto err_of = [&](float sc, float bi) {
-    float q = __builtin_rintf(__fdiv_rn(__fsub_rn(w, bi), fmaxf(sc, 1e-8f)));
+    float q = __builtin_rintf(__fdiv_rn(sub_rn(w, bi), fmaxf(sc, 1e-8f)));
     q = fminf(fmaxf(q, 0.f), 15.f);
-    const float diff = __fsub_rn(w, __fadd_rn(__fmul_rn(q, sc), bi));
-    const float e = __fmul_rn(diff, diff);
-    return wave_sum(has_ig ? __fmul_rn(ig, e) : e);
+    const float diff = sub_rn(w, add_rn(mul_rn(q, sc), bi));
+    const float e = mul_rn(diff, diff);
+    return wave_sum(has_ig ? mul_rn(ig, e) : e);
   };
 
   float best = INFINITY;
   float cur_mn = mn0;
   for (int i = 0; i < n_alpha; ++i) {
     const float a = alphas[i];
-    const float cand_mn = __fadd_rn(mu, __fmul_rn(a, __fsub_rn(mn0, mu)));
-    const float sc = h2f(f2h(__fdiv_rn(fmaxf(__fsub_rn(mx0, cand_mn), 1e-8f), 15.f)));
+    const float cand_mn = add_rn(mu, mul_rn(a, sub_rn(mn0, mu)));
+    const float sc = h2f(f2h(__fdiv_rn(fmaxf(sub_rn(mx0, cand_mn), 1e-8f), 15.f)));
     const float bi = h2f(f2h(cand_mn));
     const float e = err_of(sc, bi);
     if (e < best) {
@@ -552,12 +551,12 @@ __global__ void __launch_bounds__(512) q4m_pack_mse_kernel(const void* __restric
     }
   }
   best = INFINITY;
-  f16 best_sc = f2h(__fdiv_rn(fmaxf(__fsub_rn(mx0, cur_mn), 1e-8f), 15.f));
+  f16 best_sc = f2h(__fdiv_rn(fmaxf(sub_rn(mx0, cur_mn), 1e-8f), 15.f));
   f16 best_bi = f2h(cur_mn);
   for (int i = 0; i < n_alpha; ++i) {
     const float a = alphas[i];
-    const float cand_mx = __fadd_rn(mu, __fmul_rn(a, __fsub_rn(mx0, mu)));
-    const f16 sc_h = f2h(__fdiv_rn(fmaxf(__fsub_rn(cand_mx, cur_mn), 1e-8f), 15.f));
+    const float cand_mx = add_rn(mu, mul_rn(a, sub_rn(mx0, mu)));
+    const f16 sc_h = f2h(__fdiv_rn(fmaxf(sub_rn(cand_mx, cur_mn), 1e-8f), 15.f));
     const f16 bi_h = f2h(cur_mn);
     const float e = err_of(h2f(sc_h), h2f(bi_h));
     if (e < best) {
@@ -566,7 +565,7 @@ __global__ void __launch_bounds__(512) q4m_pack_mse_kernel(const void* __restric
       best_bi = bi_h;
     }
   }
-  float q = __builtin_rintf(__fdiv_rn(__fsub_rn(w, h2f(best_bi)), fmaxf(h2f(best_sc), 1e-8f)));
+  float q = __builtin_rintf(__fdiv_rn(sub_rn(w, h2f(best_bi)), fmaxf(h2f(best_sc), 1e-8f)));
   q = fminf(fmaxf(q, 0.f), 15.f);
   qs[c][lane] = (uint8_t)q;
   if (lane == 0) sb_out[((size_t)tile * KG + g) * 8 + c] = f16x2{best_sc, best_bi};

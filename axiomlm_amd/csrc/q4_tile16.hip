@@ -197,8 +197,7 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
         const int rp = pos % a.rope_len;
         const float c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
         const float sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
-        const float x0 = h2f(h0), x1 = h2f(h1);
-        out = even ? f2h(x0 * c - x1 * sn) : f2h(x0 * sn + x1 * c);
+        out = rope_out(h0, h1, c, sn, even);
       }
       if (row < a.q_dim) {
         a.y[(size_t)tok * a.ldy + row] = out;

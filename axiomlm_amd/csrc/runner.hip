@@ -101,8 +101,7 @@ __global__ void rope_tokens_kernel(const f16* __restrict__ qkv, int q_dim, int k
       const int fi = (within % hd) >> 1;
       const float c = freqs[((size_t)pos * half + fi) * 2 + 0];
       const float sn = freqs[((size_t)pos * half + fi) * 2 + 1];
-      const float x0 = h2f(src[e & ~1]), x1 = h2f(src[e | 1]);
-      out = (e & 1) == 0 ? f2h(x0 * c - x1 * sn) : f2h(x0 * sn + x1 * c);
+      out = rope_out(src[e & ~1], src[e | 1], c, sn, (e & 1) == 0);
     }
     if (e < q_dim)
       q[(size_t)t * q_dim + e] = out;

@@ -15,6 +15,9 @@ from .ops import (  # noqa: F401
     gqa_tree_verify_mps,
     quantize_kv_fp8,
     quantize_kv_int4,
+    rope_kv_cache_write,
+    rope_kv_cache_write_quantized,
+    rope_tree_kv_cache_write,
     swiglu_gate_up,
 )
 from .quant import (  # noqa: F401

@@ -8,6 +8,8 @@ axiomlm/kernels/quant.py:692-1008).  All compute runs in libaxm.so.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from .. import _lib
@@ -82,6 +84,71 @@ def dequantize_kv_int4(cache_int4: torch.Tensor, scales: torch.Tensor, head_dim:
     q1 = (((c >> 4) & 0x0F) ^ 0x08) - 8
     dq = torch.stack([q0, q1], dim=-1).to(torch.float16) * scales.unsqueeze(-1).unsqueeze(-1)
     return dq.view(*cache_int4.shape[:-1], hd)
+
+
+# ---------------------------------------------------------------------------
+# Fused bias + RoPE + KV-cache write (quant.py:896-1008; rope_kv_cache_write*_mps,
+# rope_tree_kv_*_mps, mps_kernels.mm:788-929, 1005-1140, 3961-3998)
+# ---------------------------------------------------------------------------
+def _rope_kv_write(who, qkv, freqs_cis, k_cache, v_cache, k_scales, v_scales, q_dim, kv_dim, head_dim, start_pos,
+                   write_pos, kv_dtype, qkv_bias, depths):
+    _lib.require_gpu(qkv, who)
+    code = _kv_code(kv_dtype)
+    if qkv.dtype != torch.float16 or not qkv.is_contiguous():
+        raise ValueError(f"{who}: qkv must be a contiguous fp16 tensor (updated in place)")
+    width = int(q_dim) + 2 * int(kv_dim)
+    if qkv.numel() % width:
+        raise ValueError(f"{who}: qkv has {qkv.numel()} elements, not a multiple of q_dim + 2 kv_dim = {width}")
+    T = qkv.numel() // width
+    if depths is not None and len(depths) != T:
+        raise ValueError(f"{who}: {len(depths)} tree depths for {T} tokens")
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("k_scales", k_scales), ("v_scales", v_scales)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{who}: {name} must be contiguous (written in place)")
+    if code and (k_scales is None or v_scales is None):
+        raise ValueError(f"{who}: quantized KV cache needs k_scales and v_scales")
+    fr = torch.view_as_real(freqs_cis) if freqs_cis.is_complex() else freqs_cis
+    fr = fr.to(device=qkv.device, dtype=torch.float32).contiguous()
+    S = k_cache.size(-2)
+    bias = qkv_bias.to(device=qkv.device, dtype=torch.float16).contiguous() if qkv_bias is not None else None
+    arr = (ctypes.c_int * T)(*[int(d) for d in depths]) if depths is not None else None
+    _lib.check(_lib.lib().axm_rope_kv_cache_write(
+        _lib.ptr(qkv), T, _lib.ptr(fr), fr.size(0), int(start_pos), arr, _lib.ptr(bias), _lib.ptr(k_cache),
+        _lib.ptr(v_cache), _lib.ptr(k_scales if code else None), _lib.ptr(v_scales if code else None), code,
+        int(q_dim), int(kv_dim), int(head_dim), S, int(write_pos), _lib.stream_of(qkv.device)), who)
+
+
+def rope_kv_cache_write_quantized(qkv: torch.Tensor, freqs_cis: torch.Tensor, k_cache: torch.Tensor,
+                                  v_cache: torch.Tensor, k_scales: torch.Tensor | None, v_scales: torch.Tensor | None,
+                                  q_dim: int, kv_dim: int, head_dim: int, start_pos: int, write_pos: int,
+                                  kv_dtype: str = "fp16", qkv_bias: torch.Tensor | None = None) -> None:
+    """Fused RoPE + KV-cache write of the qkv rows (1, T, q_dim + 2 kv_dim) (quant.py:896-1008):
+    the query part of qkv is biased and rotated in place; token t is rotated at
+    start_pos + t and its key / value land at slot write_pos + t of batch 0 (quantized
+    per 64-element group for "fp8" / "int4").  freqs_cis: complex (rope_len, hd/2) or its
+    real view (rope_len, hd/2, 2)."""
+    _rope_kv_write("rope_kv_cache_write_quantized", qkv, freqs_cis, k_cache, v_cache, k_scales, v_scales, q_dim,
+                   kv_dim, head_dim, start_pos, write_pos, kv_dtype, qkv_bias, None)
+
+
+def rope_kv_cache_write(qkv: torch.Tensor, freqs_cis: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        q_dim: int, kv_dim: int, head_dim: int, start_pos: int, write_pos: int,
+                        qkv_bias: torch.Tensor | None = None) -> None:
+    """fp16-cache form (rope_kv_cache_write_mps, mps_kernels.mm:788-815)."""
+    rope_kv_cache_write_quantized(qkv, freqs_cis, k_cache, v_cache, None, None, q_dim, kv_dim, head_dim, start_pos,
+                                  write_pos, "fp16", qkv_bias)
+
+
+def rope_tree_kv_cache_write(qkv: torch.Tensor, freqs_cis: torch.Tensor, k_cache: torch.Tensor,
+                             v_cache: torch.Tensor, tree_depths, q_dim: int, kv_dim: int, head_dim: int,
+                             start_pos: int, write_pos: int, qkv_bias: torch.Tensor | None = None,
+                             k_scales: torch.Tensor | None = None, v_scales: torch.Tensor | None = None,
+                             kv_dtype: str = "fp16") -> None:
+    """Tree form (rope_tree_kv_cache_write_mps / rope_tree_kv_write_{fp8,int4}_mps,
+    mps_kernels.mm:3961-3998, 1005-1140): node t is rotated at start_pos + tree_depths[t]
+    and written at slot write_pos + t; up to 64 nodes."""
+    _rope_kv_write("rope_tree_kv_cache_write", qkv, freqs_cis, k_cache, v_cache, k_scales, v_scales, q_dim, kv_dim,
+                   head_dim, start_pos, write_pos, kv_dtype, qkv_bias, list(tree_depths))
 
 
 # ---------------------------------------------------------------------------

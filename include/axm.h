@@ -129,6 +129,22 @@ int axm_kv_cache_write(const void* k_rows, const void* v_rows, int ld_rows, int 
                        void* k_scales, void* v_scales, int kv_dtype, int n_kv_head, int head_dim, int max_seq_len,
                        int write_pos, void* stream);
 
+/* Fused QKV bias + RoPE + KV-cache write for T <= 64 tokens, in place on
+ * qkv fp16 [T][q_dim + 2 kv_dim]: the (bias-added) query part is rotated in
+ * place; token t's rotated key and its value are stored (quantized for fp8 /
+ * int4 caches, 64-element groups) at slot (write_pos + t) % max_seq_len of batch
+ * 0; token t is rotated at (start_pos + depth[t]) % rope_len with depth[t] =
+ * depths_host[t] (tree variant) or t when depths_host is NULL.  freqs fp32
+ * [rope_len][head_dim/2][2]; qkv_bias fp16 [q_dim + 2 kv_dim] or NULL.  The key
+ * and value parts of qkv are left as they were.
+ * Replaces rope_kv_cache_write{,_fp8,_int4}_mps (mps_kernels.mm:788-929),
+ * rope_tree_kv_cache_write_mps (:3961-3998), rope_tree_kv_write_{fp8,int4}_mps
+ * (:1005-1140); Python entry rope_kv_cache_write_quantized (quant.py:896-1008). */
+int axm_rope_kv_cache_write(void* qkv, int T, const void* freqs, int rope_len, int start_pos, const int* depths_host,
+                            const void* qkv_bias, void* k_cache, void* v_cache, void* k_scales, void* v_scales,
+                            int kv_dtype, int q_dim, int kv_dim, int head_dim, int max_seq_len, int write_pos,
+                            void* stream);
+
 /* Split-KV GQA decode attention: q fp16 [B][Hq][hd] -> out fp16 [B][Hq][hd] over
  * slots [0, active_len).  num_splits <= 0 picks a split count
  * (axm_attention_num_splits).  workspace >= axm_attention_workspace_bytes().

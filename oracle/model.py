@@ -68,6 +68,25 @@ def apply_rope_fp16(x16: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.nda
     return np.stack([re, im], axis=-1).reshape(x16.shape).astype(F16)
 
 
+def rope_kv_rows(qkv16: np.ndarray, cos: np.ndarray, sin: np.ndarray, positions, q_dim: int, kv_dim: int, hd: int,
+                 bias: np.ndarray | None = None):
+    """CPU fallback of ``rope_kv_cache_write_quantized`` (quant.py:960-1008) for T token rows
+    qkv16 [T, q_dim + 2 kv_dim]: fp16 bias add, then query and key rotated at their
+    positions.  Returns (q [T, q_dim], k [Hkv, T, hd], v [Hkv, T, hd]) fp16; the caller stores
+    k / v with ``OracleKVCache.write`` (quantizing for fp8 / int4)."""
+    x = qkv16.astype(F16)
+    if bias is not None:
+        x = _h(x.astype(F32) + bias.astype(F32)[None, :]).astype(F16)
+    T = x.shape[0]
+    pos = np.asarray(positions, dtype=np.int64)
+    c, s_ = cos[pos], sin[pos]
+    q = x[:, :q_dim].reshape(T, -1, hd).transpose(1, 0, 2)
+    k = x[:, q_dim:q_dim + kv_dim].reshape(T, -1, hd).transpose(1, 0, 2)
+    v = x[:, q_dim + kv_dim:].reshape(T, -1, hd).transpose(1, 0, 2)
+    q = apply_rope_fp16(q, c, s_).transpose(1, 0, 2).reshape(T, q_dim)
+    return q, apply_rope_fp16(k, c, s_), np.ascontiguousarray(v)
+
+
 def repeat_kv(x: np.ndarray, n_rep: int) -> np.ndarray:
     return x if n_rep == 1 else np.repeat(x, n_rep, axis=-3)
 

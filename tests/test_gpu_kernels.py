@@ -546,3 +546,81 @@ def test_compact_tree_path_bit_exact(dev, kv):
             assert np.array_equal(gs[:, 1, 0].view(np.uint16), oc.vs.view(np.uint16))
         assert cache.total_seen_tokens == oc.total_seen_tokens
         assert cache.layer_seq_lens == oc.layer_seq_lens
+
+
+@pytest.mark.parametrize("kv", ["fp16", "fp8", "int4"])
+@pytest.mark.parametrize("case", ["decode", "tree_wrap", "bias_gqa"])
+def test_rope_kv_cache_write_bit_exact(dev, kv, case):
+    """Fused bias + RoPE + KV write (quant.py:896-1008, tree variants mps_kernels.mm:1005-1140,
+    3961-3998) against the oracle's CPU-path restatement: rotated queries in qkv, and every
+    cache byte and scale, bit for bit; the key / value part of qkv and all other slots untouched.
+    Cases: one decode token; a 6-node tree whose slots wrap around the ring end; a
+    biased GQA row block (8 query heads over 2 KV heads) with head_dim 64 (fp16) or 128."""
+    from axiomlm_amd.kernels import rope_kv_cache_write_quantized, rope_tree_kv_cache_write
+
+    print(f"[rope_kv_write] kv={kv} case={case}", flush=True)
+    rng = np.random.default_rng(13)
+    hd = 64 if (case == "bias_gqa" and kv == "fp16") else 128
+    Hq, Hkv = (8, 2) if case == "bias_gqa" else (4, 4)
+    S, rope_len = 40, 96
+    q_dim, kv_dim = Hq * hd, Hkv * hd
+    T_ = {"decode": 1, "tree_wrap": 6, "bias_gqa": 3}[case]
+    depths = [0, 1, 1, 2, 2, 3] if case == "tree_wrap" else list(range(T_))
+    start_pos, write_pos = {"decode": (17, 17), "tree_wrap": (90, 37), "bias_gqa": (5, 5)}[case]
+    cos, sin = om.rope_tables(hd, rope_len, 10000.0)
+    freqs = T(np.stack([cos, sin], -1).astype(F32), dev)
+    qkv0 = (rng.standard_normal((T_, q_dim + 2 * kv_dim)) * 2).astype(F16)
+    bias = (rng.standard_normal(q_dim + 2 * kv_dim) * 0.5).astype(F16) if case == "bias_gqa" else None
+
+    oc = om.OracleKVCache(S, 1, Hkv, hd, kv)
+    if kv == "fp16":
+        init = rng.standard_normal((2, Hkv, S, hd)).astype(F16)
+    else:
+        init = rng.integers(0, 256, (2, Hkv, S, oc.k.shape[-1]), dtype=np.uint8)
+    oc.k[0], oc.v[0] = init[0], init[1]
+    kc, vc = T(init[0][None], dev), T(init[1][None], dev)
+    ks = vs = None
+    if kv != "fp16":
+        sinit = rng.standard_normal((2, Hkv, S, hd // 64)).astype(F16)
+        oc.ks[0], oc.vs[0] = sinit[0], sinit[1]
+        ks, vs = T(sinit[0][None], dev), T(sinit[1][None], dev)
+
+    positions = [(start_pos + d) % rope_len for d in depths]
+    q_ref, k_ref, v_ref = om.rope_kv_rows(qkv0, cos, sin, positions, q_dim, kv_dim, hd, bias)
+    oc.write(0, [(write_pos + t) % S for t in range(T_)], k_ref, v_ref)
+
+    qkv = T(qkv0, dev)
+    if case == "tree_wrap":
+        rope_tree_kv_cache_write(qkv, freqs, kc, vc, depths, q_dim, kv_dim, hd, start_pos, write_pos,
+                                 k_scales=ks, v_scales=vs, kv_dtype=kv)
+    else:
+        rope_kv_cache_write_quantized(qkv.view(1, T_, -1), freqs, kc, vc, ks, vs, q_dim, kv_dim, hd, start_pos,
+                                      write_pos, kv, None if bias is None else T(bias, dev))
+    got = N(qkv)
+    assert np.array_equal(got[:, :q_dim].view(np.uint16), q_ref.view(np.uint16)), "rotated queries"
+    assert np.array_equal(got[:, q_dim:].view(np.uint16), qkv0[:, q_dim:].view(np.uint16)), "k/v part of qkv changed"
+    assert np.array_equal(N(kc)[0].view(np.uint8), oc.k[0].view(np.uint8)), "key cache"
+    assert np.array_equal(N(vc)[0].view(np.uint8), oc.v[0].view(np.uint8)), "value cache"
+    if kv != "fp16":
+        assert np.array_equal(N(ks)[0].view(np.uint16), oc.ks[0].view(np.uint16)), "key scales"
+        assert np.array_equal(N(vs)[0].view(np.uint16), oc.vs[0].view(np.uint16)), "value scales"
+
+
+def test_rope_kv_cache_write_rejects_bad_arguments(dev):
+    from axiomlm_amd.kernels import rope_kv_cache_write_quantized, rope_tree_kv_cache_write
+
+    print("[rope_kv_write_errors]", flush=True)
+    hd, S = 128, 16
+    freqs = torch.zeros((32, hd // 2, 2), dtype=torch.float32, device=dev)
+    kc = torch.zeros((1, 1, S, hd), dtype=torch.uint8, device=dev)
+    qkv = torch.zeros((1, 1, 3 * hd), dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError):  # quantized cache without scales
+        rope_kv_cache_write_quantized(qkv, freqs, kc, kc.clone(), None, None, hd, hd, hd, 0, 0, "fp8")
+    with pytest.raises(ValueError):  # depths do not match the token count
+        rope_tree_kv_cache_write(qkv, freqs, kc, kc.clone(), [0, 1], hd, hd, hd, 0, 0)
+    kc16 = torch.zeros((1, 1, S, hd), dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError):  # write slot outside the cache
+        rope_kv_cache_write_quantized(qkv, freqs, kc16, kc16.clone(), None, None, hd, hd, hd, 0, S)
+    with pytest.raises(RuntimeError):  # more than 64 tokens
+        q70 = torch.zeros((70, 3 * hd), dtype=torch.float16, device=dev)
+        rope_kv_cache_write_quantized(q70, freqs, kc16, kc16.clone(), None, None, hd, hd, hd, 0, 0)
