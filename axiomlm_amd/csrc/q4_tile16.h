@@ -37,6 +37,9 @@ struct T16Args {
   uint32_t unpack[4];  // nibble masks and fp16 magic exponents (set by t16_gemv_launch)
 };
 
+// Largest K (activation length) the tile16 GEMV stages.
+constexpr int kTile16MaxK = 16384;
+
 size_t t16_smem_bytes(int M, int NT, int K);
 void t16_prepare_attributes();
 // Picks split / grid (a.split is overwritten); M in [1, 4].

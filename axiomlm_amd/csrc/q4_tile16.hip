@@ -79,9 +79,50 @@ __global__ void repack_tile16_kernel(const uint32_t* __restrict__ wm, const f16x
 // ---------------------------------------------------------------------------
 // Activation staging: xs [M][K_pad] f16 (normalized if ln_w), zero block,
 // cx [M][2 KB] float2 (magic-offset-weighted sum, plain sum) per 64-group.
+//
+// Thread tid owns the 8-element vectors i = tid + r * kT16Threads of every row.
+// t16_load_x issues the activation (and norm weight) loads into registers
+// before the kernel issues its weight loads: a wave's loads complete in issue
+// order, so staging that loaded x only after the weight loads would first wait
+// for every weight chunk of the wave to arrive.
 // ---------------------------------------------------------------------------
+constexpr int kT16XV = 4;  // vectors per thread and row: K <= kT16XV * kT16Threads * 8 = 16384
+constexpr int kT16MaxK = kT16XV * kT16Threads * 8;
+static_assert(kT16MaxK == kTile16MaxK, "tile16 staging bound");
+
 template <int M>
-__device__ void t16_stage_x(const T16Args& a, f16* xs, f32x2* cx, float* red) {
+struct T16X {
+  f16x8 x[M][kT16XV];
+  f16x8 w[kT16XV];
+};
+
+template <int M>
+__device__ __forceinline__ void t16_load_x(const T16Args& a, T16X<M>& r) {
+  const int tid = threadIdx.x;
+  const int nv = a.K >> 3;
+#pragma unroll
+  for (int v = 0; v < kT16XV; ++v) {
+    const int i = tid + v * kT16Threads;
+    const bool ok = i < nv;
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) {
+      const f16x8* xr = reinterpret_cast<const f16x8*>(a.x + (size_t)mi * a.ldx);
+      f16x8 t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = f16(0);
+      if (ok) t = xr[i];
+      r.x[mi][v] = t;
+    }
+    f16x8 t;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = f16(0);
+    if (ok && a.ln_w != nullptr) t = reinterpret_cast<const f16x8*>(a.ln_w)[i];
+    r.w[v] = t;
+  }
+}
+
+template <int M>
+__device__ void t16_stage_x(const T16Args& a, const T16X<M>& r, f16* xs, f32x2* cx, float* red) {
   const int tid = threadIdx.x;
   const int K = a.K;
   const int nv = K >> 3;
@@ -92,13 +133,13 @@ __device__ void t16_stage_x(const T16Args& a, f16* xs, f32x2* cx, float* red) {
   if (a.ln_w != nullptr) {
 #pragma unroll
     for (int mi = 0; mi < M; ++mi) {
-      const f16x8* xr = reinterpret_cast<const f16x8*>(a.x + (size_t)mi * a.ldx);
       float s = 0.f;
-      for (int i = tid; i < nv; i += kT16Threads) {
-        const f16x8 v = xr[i];
+#pragma unroll
+      for (int v = 0; v < kT16XV; ++v) {
+        // Vectors past nv were loaded as zeros and add nothing.
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float f = h2f(v[e]);
+          const float f = h2f(r.x[mi][v][e]);
           s += h2f(f2h(f * f));
         }
       }
@@ -114,30 +155,26 @@ __device__ void t16_stage_x(const T16Args& a, f16* xs, f32x2* cx, float* red) {
       rinv[mi] = rms_inv_fp16(s, K, a.eps);
     }
   }
-  const f16x8* wr = reinterpret_cast<const f16x8*>(a.ln_w);
 #pragma unroll
   for (int mi = 0; mi < M; ++mi) {
-    const f16x8* xr = reinterpret_cast<const f16x8*>(a.x + (size_t)mi * a.ldx);
-    // nv_pad is a multiple of 16 (KB*128/8), so the 8-lane group reduction below
-    // always runs with full wave participation.
-    for (int i0 = 0; i0 < nv_pad; i0 += kT16Threads) {
-      const int i = i0 + tid;
-      f16x8 v;
+    // nv_pad is a multiple of 16 (KB*128/8) and the same for every thread, so
+    // the 8-lane group reduction below always runs with full wave participation.
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = f16(0);
+    for (int v = 0; v < kT16XV; ++v) {
+      if (v * kT16Threads >= nv_pad) break;
+      const int i = tid + v * kT16Threads;
+      f16x8 x = r.x[mi][v];
       if (i < nv) {
-        v = xr[i];
         if (a.ln_w != nullptr) {
-          const f16x8 w = wr[i];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = f2h(h2f(f2h(h2f(v[e]) * rinv[mi])) * h2f(w[e]));
+          for (int e = 0; e < 8; ++e) x[e] = f2h(h2f(f2h(h2f(x[e]) * rinv[mi])) * h2f(r.w[v][e]));
         }
-        if (a.x_norm_out != nullptr) reinterpret_cast<f16x8*>(a.x_norm_out + (size_t)mi * K)[i] = v;
+        if (a.x_norm_out != nullptr) reinterpret_cast<f16x8*>(a.x_norm_out + (size_t)mi * K)[i] = x;
       }
       float corr = 0.f, sum = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float f = h2f(v[e]);
+        const float f = h2f(x[e]);
         sum += f;
         corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
       }
@@ -145,7 +182,7 @@ __device__ void t16_stage_x(const T16Args& a, f16* xs, f32x2* cx, float* red) {
       corr = group_sum<8>(corr);
       sum = group_sum<8>(sum);
       if (i < nv_pad) {
-        reinterpret_cast<f16x8*>(xs + (size_t)mi * a.KB * 128)[i] = v;
+        reinterpret_cast<f16x8*>(xs + (size_t)mi * a.KB * 128)[i] = x;
         if ((tid & 7) == 0) cx[(size_t)mi * 2 * a.KB + (i >> 3)] = f32x2{corr, sum};
       }
     }
@@ -233,16 +270,35 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
 // ---------------------------------------------------------------------------
 // MFMA GEMV.  Unit = one tile16 (or a gate/up pair, NT = 2).  S = a.split
 // waves share a unit (split-K over kb); 8 / S units per workgroup pass.
-// S == 1 runs a persistent loop; S > 1 needs one pass (grid covers all units).
+// MODE kT16Loop (S == 1): waves loop over units, prefetching the next unit's
+// chunks.  Otherwise (S > 1) the grid covers all units in one pass with a
+// straight-line body; the modes are separate instantiations so that the
+// one-pass body has no loop back edge carrying loads in flight, which would
+// make the compiler wait for every outstanding load before the first chunk is
+// consumed.
+// kT16Wave (one pass, every chunk of the wave in flight at once, P >= chunks
+// per wave): a wave's (scale, bias) pairs for its my <= P chunks are one
+// contiguous my * 128-byte run, fetched with P / 8 16-byte loads per lane into
+// a wave-private LDS slot instead of one 8-byte load per chunk.
+// kT16OnePass: one pass with per-chunk scale loads and in-loop refills.
 // P kb-loads (1 KB per tile each) stay in flight per wave.
 // ---------------------------------------------------------------------------
-template <int M, int NT, int EPI, int P>
+constexpr int kT16Loop = 0;
+constexpr int kT16OnePass = 1;
+constexpr int kT16Wave = 2;
+constexpr int kT16WaveDepth = 8;  // chunks in flight per wave in kT16Wave
+
+template <int M, int NT, int EPI, int P, int MODE>
 __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
+  constexpr bool ONE = MODE != kT16Loop;
+  constexpr bool SBW = MODE == kT16Wave;
+  constexpr int QS = SBW ? P / 8 : 1;  // 16-byte scale loads per lane and tile (kT16Wave)
   extern __shared__ __align__(16) unsigned char smem[];
   f16* xs = reinterpret_cast<f16*>(smem);                                   // [M][KB*128]
   f16* zero = xs + (size_t)M * a.KB * 128;                                   // 16 halves of zeros
   f32x2* cx = reinterpret_cast<f32x2*>(zero + 16);                           // [M][2 KB]
   float* red = reinterpret_cast<float*>(cx + (size_t)M * 2 * a.KB);          // [waves][NT][4][64]
+  u32x2* sbw = reinterpret_cast<u32x2*>(red + kT16Waves * NT * 4 * 64);      // kT16Wave: [waves][NT][per][16]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -280,15 +336,42 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
       const int wo = ok ? (base * 64 + lane) * 16 : kOOB;
       const int so = ok ? (base * 16 + (lane & 15)) * 8 : kOOB;
       wr[j][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
-      sr[j][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+      if (!SBW) sr[j][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
     }
   };
 
   int it = 0;
   int unit = blockIdx.x * upw + slot;
+  T16X<M> xr;
+  t16_load_x<M>(a, xr);
+  // kT16Wave: the wave's (scale, bias) run; 16-byte vector v holds chunk v / 8,
+  // rows 2 (v % 8) and 2 (v % 8) + 1.  Issued before the weight loads so that
+  // storing it to LDS waits only for itself.
+  u32x4 sbv[NT][QS];
+  u32x2* my_sb = sbw + (size_t)wave * NT * per * 16;
+  if (SBW) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int q = 0; q < QS; ++q) {
+        const int v = q * 64 + lane;
+        const bool ok = unit < a.n_units && v < my * 8;
+        const int bo = ok ? (((unit + t * a.pair_offset) * a.KB + kb0) * 8 + v) * 16 : kOOB;
+        sbv[t][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, bo, 0, 0));
+      }
+  }
 #pragma unroll
   for (int j = 0; j < P; ++j) load(unit, j, j);
-  t16_stage_x<M>(a, xs, cx, red);
+  if (SBW) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int q = 0; q < QS; ++q) {
+        const int v = q * 64 + lane;
+        if (v < my * 8) *reinterpret_cast<u32x4*>(my_sb + (size_t)t * per * 16 + 2 * v) = sbv[t][q];
+      }
+  }
+  t16_stage_x<M>(a, xr, xs, cx, red);  // ends with a workgroup barrier
 
   // LDS addresses: A operand of this lane and (corr, sum) of its D tokens.
   const f16* xa = (tokA < M) ? xs + (size_t)tokA * a.KB * 128 + 8 * kq : zero;
@@ -302,10 +385,14 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
 #pragma unroll
       for (int vi = 0; vi < 4; ++vi) acc[t][vi] = 0.f;
 
-    for (int ci0 = 0; ci0 < my; ci0 += P) {
+    // kT16Wave: a single pass over the my <= P chunks already in flight.
+    const int n_pass = SBW ? 1 : (my + P - 1) / P;
+    for (int pass = 0; pass < n_pass; ++pass) {
+      const int ci0 = pass * P;
 #pragma unroll
       for (int j = 0; j < P; ++j) {
         const int ci = ci0 + j;
+        if (SBW && ci >= my) break;  // wave-uniform
         // Chunks past the range carry zero codes and zero scales: clamp the LDS
         // reads to a valid kb so they only ever multiply finite values by zero.
         const int kb = kb0 + min(ci, my - 1);
@@ -320,6 +407,10 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
             const int tok = min(4 * kq + vi, M - 1);
             cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (size_t)tok * 2 * a.KB + 2 * kb);
           }
+        }
+        if (SBW) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) sr[j][t] = my_sb[(size_t)t * per * 16 + ci * 16 + (lane & 15)];
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -342,17 +433,18 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
             }
           }
         }
-        load(unit, ci + P, j);
+        // kT16Wave has every chunk in flight already (my <= P).
+        if (!SBW) load(unit, ci + P, j);
       }
     }
 
     const int next_unit = (blockIdx.x + (it + 1) * gridDim.x) * upw + slot;
-    const bool more = (S == 1) && ((blockIdx.x + (it + 1) * gridDim.x) * upw < a.n_units);
+    const bool more = !ONE && ((blockIdx.x + (it + 1) * gridDim.x) * upw < a.n_units);
     if (more) {
 #pragma unroll
       for (int j = 0; j < P; ++j) load(next_unit, j, j);
     }
-    if (S > 1) {
+    if (ONE) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -372,7 +464,7 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
       }
     }
     if (sub == 0 && unit < a.n_units) t16_epilogue<M, NT, EPI>(a, unit, lane, acc);
-    if (!more) break;
+    if (ONE || !more) break;
     ++it;
     unit = next_unit;
   }
@@ -383,16 +475,29 @@ struct T16Depth {
   static constexpr int value = NT == 2 ? 4 : 8;
 };
 
-template <int M, int NT, int EPI>
-void t16_set_attr() {
-  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value>,
+template <int M, int NT, int EPI, int P, int MODE>
+void t16_set_attr_mode() {
+  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
     (void)hipGetLastError();
 }
 
 template <int M, int NT, int EPI>
-int t16_launch_one(const T16Args& a, int grid, size_t smem, hipStream_t s) {
-  hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value>), dim3(grid), dim3(kT16Threads), smem, s, a);
+void t16_set_attr() {
+  t16_set_attr_mode<M, NT, EPI, T16Depth<NT>::value, kT16Loop>();
+  t16_set_attr_mode<M, NT, EPI, T16Depth<NT>::value, kT16OnePass>();
+  t16_set_attr_mode<M, NT, EPI, kT16WaveDepth, kT16Wave>();
+}
+
+template <int M, int NT, int EPI>
+int t16_launch_one(const T16Args& a, int mode, int grid, size_t smem, hipStream_t s) {
+  const dim3 g(grid), b(kT16Threads);
+  if (mode == kT16Wave)
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, kT16WaveDepth, kT16Wave>), g, b, smem, s, a);
+  else if (mode == kT16OnePass)
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16OnePass>), g, b, smem, s, a);
+  else
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16Loop>), g, b, smem, s, a);
   return 0;
 }
 
@@ -423,9 +528,9 @@ void t16_prepare_attributes() {
 int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   t16_prepare_attributes();
   const int NT = (epi == Q4_EPI_SWIGLU) ? 2 : 1;
-  const size_t smem = t16_smem_bytes(M, NT, a.K);
-  if (smem > 160 * 1024 || M < 1 || M > 4) {
-    axm_set_error("tile16 gemv: M=%d K=%d needs %zu B of LDS", M, a.K, smem);
+  size_t smem = t16_smem_bytes(M, NT, a.K);
+  if (smem > 160 * 1024 || M < 1 || M > 4 || a.K > kT16MaxK) {
+    axm_set_error("tile16 gemv: M=%d K=%d unsupported (K <= %d, %zu B of LDS)", M, a.K, kT16MaxK, smem);
     return -2;
   }
   // Waves per unit: aim for ~8 waves per CU with >= 2 kb-loads per wave.
@@ -442,13 +547,23 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   const int upw = kT16Waves / S;
   int grid = (a.n_units + upw - 1) / upw;
   if (S == 1 && grid > 2 * cus) grid = 2 * cus;
+  // Chunks per wave; kT16Wave keeps all of them in flight (per <= depth).
+  const int per = (a.KB + S - 1) / S;
+  int mode = S == 1 ? kT16Loop : kT16OnePass;
+  if (S > 1 && per <= kT16WaveDepth) {
+    const size_t sb_lds = (size_t)kT16Waves * NT * per * 128;
+    if (smem + sb_lds <= 160 * 1024) {
+      mode = kT16Wave;
+      smem += sb_lds;
+    }
+  }
 #define AXM_T16_CASE(MM)                                                                 \
   case MM:                                                                               \
     switch (epi) {                                                                       \
-      case Q4_EPI_STORE: return t16_launch_one<MM, 1, Q4_EPI_STORE>(a, grid, smem, s);   \
-      case Q4_EPI_RESID: return t16_launch_one<MM, 1, Q4_EPI_RESID>(a, grid, smem, s);   \
-      case Q4_EPI_SWIGLU: return t16_launch_one<MM, 2, Q4_EPI_SWIGLU>(a, grid, smem, s); \
-      case Q4_EPI_QKV_ROPE: return t16_launch_one<MM, 1, Q4_EPI_QKV_ROPE>(a, grid, smem, s); \
+      case Q4_EPI_STORE: return t16_launch_one<MM, 1, Q4_EPI_STORE>(a, mode, grid, smem, s);   \
+      case Q4_EPI_RESID: return t16_launch_one<MM, 1, Q4_EPI_RESID>(a, mode, grid, smem, s);   \
+      case Q4_EPI_SWIGLU: return t16_launch_one<MM, 2, Q4_EPI_SWIGLU>(a, mode, grid, smem, s); \
+      case Q4_EPI_QKV_ROPE: return t16_launch_one<MM, 1, Q4_EPI_QKV_ROPE>(a, mode, grid, smem, s); \
     }                                                                                    \
     break;
   switch (M) {

@@ -632,9 +632,11 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
       r->m_dn.push_back(Mat{r->dn_w[i], r->dn_sb[i], nullptr, nullptr, d.d_model, d.hidden_dim});
     }
     r->m_lmh = Mat{d.lm_head_w, d.lm_head_sb, nullptr, nullptr, d.vocab_size, d.d_model};
-    // The gate/up pair shares a tile16 boundary when H % 16 == 0; otherwise keep the
-    // reference layout everywhere.
-    const bool t16 = d.hidden_dim % 16 == 0 && d.layout != 1;
+    // The gate/up pair shares a tile16 boundary when H % 16 == 0, and the tile16
+    // GEMV stages at most kTile16MaxK activations; otherwise keep the reference
+    // layout everywhere.
+    const bool t16 = d.hidden_dim % 16 == 0 && d.layout != 1 && d.hidden_dim <= kTile16MaxK &&
+                     d.d_model <= kTile16MaxK && d.n_head * d.head_dim <= kTile16MaxK;
     if (t16) {
       int rc = 0;
       for (int i = 0; i < L && rc == 0; ++i) {
