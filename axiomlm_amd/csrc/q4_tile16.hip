@@ -287,6 +287,7 @@ constexpr int kT16Loop = 0;
 constexpr int kT16OnePass = 1;
 constexpr int kT16Wave = 2;
 constexpr int kT16WaveDepth = 8;  // chunks in flight per wave in kT16Wave
+constexpr int kT16WavePre = 4;    // of which issued before the activation staging
 
 template <int M, int NT, int EPI, int P, int MODE>
 __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
@@ -360,8 +361,13 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
         sbv[t][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, bo, 0, 0));
       }
   }
+  // kT16Wave issues only the first PRE chunks before the staging barrier: a
+  // wave that blocks on a full memory queue while issuing its later loads
+  // would hold the whole workgroup at the barrier.  The rest are issued while
+  // the first chunks are consumed.
+  constexpr int PRE = SBW ? kT16WavePre : P;
 #pragma unroll
-  for (int j = 0; j < P; ++j) load(unit, j, j);
+  for (int j = 0; j < PRE; ++j) load(unit, j, j);
   if (SBW) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -392,6 +398,7 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
 #pragma unroll
       for (int j = 0; j < P; ++j) {
         const int ci = ci0 + j;
+        if (SBW && j + PRE < P) load(unit, j + PRE, j + PRE);
         if (SBW && ci >= my) break;  // wave-uniform
         // Chunks past the range carry zero codes and zero scales: clamp the LDS
         // reads to a valid kb so they only ever multiply finite values by zero.
