@@ -168,6 +168,75 @@ __device__ __forceinline__ void load_kv8(const void* base, const f16* scales, si
   }
 }
 
+// Raw 8-element key/value chunk (fp16: 16 B, fp8: 8 B, int4: 4 B) and its
+// group scale, fetched ahead of use; kv8_convert applies the same rounding as
+// load_kv8.
+template <int KVT>
+__device__ __forceinline__ u32x4 kv8_fetch(const void* base, const f16* scales, size_t row, int hd, int e0,
+                                           float& sc) {
+  u32x4 r = {0u, 0u, 0u, 0u};
+  sc = 1.f;
+  if (KVT == AXM_KV_FP16) {
+    r = *reinterpret_cast<const u32x4*>((const f16*)base + row * hd + e0);
+  } else if (KVT == AXM_KV_FP8) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>((const uint8_t*)base + row * hd + e0);
+    r.x = v.x;
+    r.y = v.y;
+    sc = h2f(scales[row * (hd / 64) + e0 / 64]);
+  } else {
+    r.x = *reinterpret_cast<const uint32_t*>((const uint8_t*)base + row * (hd / 2) + e0 / 2);
+    sc = h2f(scales[row * (hd / 64) + e0 / 64]);
+  }
+  return r;
+}
+
+template <int KVT>
+__device__ __forceinline__ void kv8_convert(u32x4 r, float sc, float out[8]) {
+  if (KVT == AXM_KV_FP16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = r[i];
+      const f16x2 h = as_h2(w);
+      out[2 * i] = h2f(h.x);
+      out[2 * i + 1] = h2f(h.y);
+    }
+  } else if (KVT == AXM_KV_FP8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = r[i >> 2];
+      out[i] = h2f(f2h(fp8e4m3fn_to_f32((w >> (8 * (i & 3))) & 0xFFu) * sc));
+    }
+  } else {
+    const uint32_t w = r.x;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = (int)(((w >> (4 * i)) & 0xFu) ^ 0x8u) - 8;
+      out[i] = h2f(f2h((float)q * sc));
+    }
+  }
+}
+
+// Sum over the LPT lanes that hold one key row (aligned groups of 8 or 16
+// lanes; hd = 64 or 128) with DPP lane permutes instead of LDS-routed
+// shuffles: xor 1 and xor 2 within each quad, then the 8-lane and 16-lane
+// mirrors pair each lane with the complementary half.
+template <int CTRL>
+__device__ __forceinline__ float dpp_sum_step(float v) {
+  const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+  return v + __builtin_bit_cast(float, o);
+}
+__device__ __forceinline__ float key_row_sum(float v, int lpt) {
+  if (lpt == 16 || lpt == 8) {
+    v = dpp_sum_step<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_sum_step<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_sum_step<0x141>(v);  // row_half_mirror
+    if (lpt == 16) v = dpp_sum_step<0x140>(v);  // row_mirror
+    return v;
+  }
+  for (int off = lpt / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 struct AttnParams {
   const f16* q;           // query rows, row r at q + r_off(r)
   KvView kv;
@@ -185,8 +254,12 @@ struct AttnParams {
 
 // Rows of one workgroup: decode -> (b, kv head, replica r) with r < n_rep;
 // tree -> (node u, kv head, replica) flattened, QR rows per workgroup.
-template <int KVT, int QR, bool TREE>
-__global__ void __launch_bounds__(kAttnThreads) attn_split_kernel(AttnParams p) {
+// NW waves per workgroup; each wave fetches the keys / values of U steps
+// (U * 64 / (hd / 8) keys) before consuming them, so a workgroup keeps
+// NW * U loads per lane pair in flight.
+template <int KVT, int QR, bool TREE, int NW, int U>
+__global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
+  constexpr int kThreads = NW * 64;
   const int hd = p.kv.hd;
   const int LPT = hd / 8;        // lanes per key
   const int KPW = 64 / LPT;      // keys per wave step
@@ -260,25 +333,35 @@ __global__ void __launch_bounds__(kAttnThreads) attn_split_kernel(AttnParams p) 
     for (int r = 0; r < QR; ++r) node_mask[r] = r < n_rows ? p.masks[(row_base + r) / p.n_rep] : 0ull;
   }
 
-  for (int kb = k_begin + wave * KPW; kb < k_end; kb += kAttnWaves * KPW) {
-    const int key = kb + sub;
-    const bool valid = key < k_end;
-    int slot = key;
-    if (TREE && key >= prefix) slot = (p.write_pos + (key - prefix)) % p.kv.S;
-    float kf[8], vf[8];
-    if (valid) {
-      load_kv8<KVT>(p.kv.k, p.kv.ks, head_row0 + slot, hd, e0, kf);
-      load_kv8<KVT>(p.kv.v, p.kv.vs, head_row0 + slot, hd, e0, vf);
-    } else {
+  for (int kb0 = k_begin + wave * KPW; kb0 < k_end; kb0 += NW * KPW * U) {
+    u32x4 kr[U], vr[U];
+    float ksc[U], vsc[U];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kf[i] = vf[i] = 0.f;
+    for (int u = 0; u < U; ++u) {
+      const int key = kb0 + u * NW * KPW + sub;
+      int slot = key;
+      if (TREE && key >= prefix) slot = (p.write_pos + (key - prefix)) % p.kv.S;
+      if (key < k_end) {
+        kr[u] = kv8_fetch<KVT>(p.kv.k, p.kv.ks, head_row0 + slot, hd, e0, ksc[u]);
+        vr[u] = kv8_fetch<KVT>(p.kv.v, p.kv.vs, head_row0 + slot, hd, e0, vsc[u]);
+      } else {
+        kr[u] = vr[u] = u32x4{0u, 0u, 0u, 0u};
+        ksc[u] = vsc[u] = 0.f;
+      }
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+    const int key = kb0 + u * NW * KPW + sub;
+    const bool valid = key < k_end;
+    float kf[8], vf[8];
+    kv8_convert<KVT>(kr[u], ksc[u], kf);
+    kv8_convert<KVT>(vr[u], vsc[u], vf);
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[r][i], kf[i], d);
-      for (int off = LPT / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+      d = key_row_sum(d, LPT);
       bool vis = valid && r < n_rows;
       if (TREE && key >= prefix) vis = vis && ((node_mask[r] >> (key - prefix)) & 1ull);
       const float s = vis ? d * p.scale_log2 : kNegBig;
@@ -289,6 +372,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_split_kernel(AttnParams p) 
       m[r] = m_new;
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[r][i] = __builtin_fmaf(o[r][i], alpha, pr * vf[i]);
+    }
     }
   }
 
@@ -311,7 +395,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_split_kernel(AttnParams p) 
   }
 
   // Merge the waves through LDS: [wave][r][2 + hd].
-  __shared__ float sm[kAttnWaves][QR][2 + 128];
+  __shared__ float sm[NW][QR][2 + 128];
   if (lane < LPT) {
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
@@ -325,15 +409,15 @@ __global__ void __launch_bounds__(kAttnThreads) attn_split_kernel(AttnParams p) 
   }
   __syncthreads();
   // Thread t handles (r, e) pairs.
-  for (int idx = threadIdx.x; idx < QR * hd; idx += kAttnThreads) {
+  for (int idx = threadIdx.x; idx < QR * hd; idx += kThreads) {
     const int r = idx / hd, e = idx % hd;
     if (r >= n_rows) continue;
     float mm = kNegBig;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) mm = fmaxf(mm, sm[w][r][0]);
+    for (int w = 0; w < NW; ++w) mm = fmaxf(mm, sm[w][r][0]);
     float ll = 0.f, oo = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float a = exp2f(sm[w][r][0] - mm);
       ll += sm[w][r][1] * a;
       oo += sm[w][r][2 + e] * a;
@@ -372,9 +456,17 @@ __global__ void attn_reduce_kernel(const float* __restrict__ ws, f16* __restrict
   if (e < hd) out[(size_t)row * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
 }
 
+// Decode uses 16 waves (8 for more than 2 rows per workgroup, which need the
+// registers) with 4 steps of loads in flight; tree verification keeps 4 waves,
+// one step.
 template <int KVT, int QR, bool TREE>
 void launch_attn_t(const AttnParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_split_kernel<KVT, QR, TREE>), grid, dim3(kAttnThreads), 0, s, p);
+  if constexpr (TREE) {
+    hipLaunchKernelGGL((attn_split_kernel<KVT, QR, TREE, kAttnWaves, 1>), grid, dim3(kAttnThreads), 0, s, p);
+  } else {
+    constexpr int nw = QR <= 2 ? 16 : 8;
+    hipLaunchKernelGGL((attn_split_kernel<KVT, QR, TREE, nw, 4>), grid, dim3(nw * 64), 0, s, p);
+  }
 }
 
 template <bool TREE>
@@ -420,10 +512,13 @@ size_t attn_workspace_bytes(int B, int Hq, int hd, int n_splits) {
 }
 
 int attn_choose_splits(int B, int Hkv, int active_len) {
-  // Aim for >= 2 workgroups per CU with >= 32 keys per split.
-  const int target_wg = 2 * axm_num_cus();
-  int splits = (target_wg + B * Hkv - 1) / (B * Hkv);
-  const int by_len = (active_len + 31) / 32;
+  // A decode workgroup (16 waves x 4 keys x 4 steps in flight = 256 keys per
+  // round) takes up to 1024 keys: short contexts need no split merge; longer
+  // ones split so that the workgroups still fill the chip.
+  int splits = (active_len + 1023) / 1024;
+  const int fill = (axm_num_cus() + B * Hkv - 1) / (B * Hkv);
+  if (splits > 1 && splits < fill) splits = fill;
+  const int by_len = (active_len + 255) / 256;
   if (splits > by_len) splits = by_len;
   if (splits > 64) splits = 64;
   if (splits < 1) splits = 1;
