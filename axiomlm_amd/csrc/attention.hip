@@ -286,6 +286,35 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
   }
   if (n_rows <= 0) return;
 
+  const int prefix = p.prefix_dev ? p.prefix_dev[0] : p.prefix_len;
+  const int n_keys = prefix + (TREE ? p.T : 0);
+  const int per = (n_keys + p.n_splits - 1) / p.n_splits;
+  const int k_begin = min(split * per, n_keys);
+  const int k_end = min(k_begin + per, n_keys);
+  const size_t head_row0 = ((size_t)b * p.kv.Hkv + kvh) * p.kv.S;
+
+  // Keys / values of U steps; the first batch is requested before the query
+  // rows so that the two latencies overlap.
+  u32x4 kr[U], vr[U];
+  float ksc[U], vsc[U];
+  auto fetch = [&](int kb0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = kb0 + u * NW * KPW + sub;
+      int slot = key;
+      if (TREE && key >= prefix) slot = (p.write_pos + (key - prefix)) % p.kv.S;
+      if (key < k_end) {
+        kr[u] = kv8_fetch<KVT>(p.kv.k, p.kv.ks, head_row0 + slot, hd, e0, ksc[u]);
+        vr[u] = kv8_fetch<KVT>(p.kv.v, p.kv.vs, head_row0 + slot, hd, e0, vsc[u]);
+      } else {
+        kr[u] = vr[u] = u32x4{0u, 0u, 0u, 0u};
+        ksc[u] = vsc[u] = 0.f;
+      }
+    }
+  };
+  int kb0 = k_begin + wave * KPW;
+  if (kb0 < k_end) fetch(kb0);
+
   // Global query-row index and query pointers.
   float q[QR][8];
   int qrow[QR];
@@ -311,12 +340,6 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
     }
   }
 
-  const int prefix = p.prefix_dev ? p.prefix_dev[0] : p.prefix_len;
-  const int n_keys = prefix + (TREE ? p.T : 0);
-  const int per = (n_keys + p.n_splits - 1) / p.n_splits;
-  const int k_begin = min(split * per, n_keys);
-  const int k_end = min(k_begin + per, n_keys);
-
   float m[QR], l[QR], o[QR][8];
 #pragma unroll
   for (int r = 0; r < QR; ++r) {
@@ -326,29 +349,13 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
     for (int i = 0; i < 8; ++i) o[r][i] = 0.f;
   }
 
-  const size_t head_row0 = ((size_t)b * p.kv.Hkv + kvh) * p.kv.S;
   uint64_t node_mask[QR];
   if (TREE) {
 #pragma unroll
     for (int r = 0; r < QR; ++r) node_mask[r] = r < n_rows ? p.masks[(row_base + r) / p.n_rep] : 0ull;
   }
 
-  for (int kb0 = k_begin + wave * KPW; kb0 < k_end; kb0 += NW * KPW * U) {
-    u32x4 kr[U], vr[U];
-    float ksc[U], vsc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int key = kb0 + u * NW * KPW + sub;
-      int slot = key;
-      if (TREE && key >= prefix) slot = (p.write_pos + (key - prefix)) % p.kv.S;
-      if (key < k_end) {
-        kr[u] = kv8_fetch<KVT>(p.kv.k, p.kv.ks, head_row0 + slot, hd, e0, ksc[u]);
-        vr[u] = kv8_fetch<KVT>(p.kv.v, p.kv.vs, head_row0 + slot, hd, e0, vsc[u]);
-      } else {
-        kr[u] = vr[u] = u32x4{0u, 0u, 0u, 0u};
-        ksc[u] = vsc[u] = 0.f;
-      }
-    }
+  for (; kb0 < k_end; kb0 += NW * KPW * U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
     const int key = kb0 + u * NW * KPW + sub;
@@ -374,6 +381,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
       for (int i = 0; i < 8; ++i) o[r][i] = __builtin_fmaf(o[r][i], alpha, pr * vf[i]);
     }
     }
+    if (kb0 + NW * KPW * U < k_end) fetch(kb0 + NW * KPW * U);
   }
 
   // Merge the KPW key sub-slots of the wave (lanes with equal e0).

@@ -276,24 +276,27 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
 // one-pass body has no loop back edge carrying loads in flight, which would
 // make the compiler wait for every outstanding load before the first chunk is
 // consumed.
-// kT16Wave (one pass, every chunk of the wave in flight at once, P >= chunks
-// per wave): a wave's (scale, bias) pairs for its my <= P chunks are one
-// contiguous my * 128-byte run, fetched with P / 8 16-byte loads per lane into
-// a wave-private LDS slot instead of one 8-byte load per chunk.
+// kT16Wave (one pass over at most kT16WaveMaxChunks chunks per wave, loads
+// kept in flight through a ring of P register slots): a wave's (scale, bias)
+// pairs for its my chunks are one contiguous my * 128-byte run, fetched with
+// two 16-byte loads per lane into a wave-private LDS slot instead of one
+// 8-byte load per chunk.
 // kT16OnePass: one pass with per-chunk scale loads and in-loop refills.
 // P kb-loads (1 KB per tile each) stay in flight per wave.
 // ---------------------------------------------------------------------------
 constexpr int kT16Loop = 0;
 constexpr int kT16OnePass = 1;
 constexpr int kT16Wave = 2;
-constexpr int kT16WaveDepth = 8;  // chunks in flight per wave in kT16Wave
-constexpr int kT16WavePre = 4;    // of which issued before the activation staging
+constexpr int kT16WaveDepth = 8;      // chunk register slots per wave in kT16Wave (a ring)
+constexpr int kT16WavePre = 4;        // chunks issued before the activation staging
+constexpr int kT16WaveMaxChunks = 16;  // chunks per wave kT16Wave handles
 
 template <int M, int NT, int EPI, int P, int MODE>
 __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
   constexpr bool ONE = MODE != kT16Loop;
   constexpr bool SBW = MODE == kT16Wave;
-  constexpr int QS = SBW ? P / 8 : 1;  // 16-byte scale loads per lane and tile (kT16Wave)
+  constexpr int QS = SBW ? kT16WaveMaxChunks / 8 : 1;  // 16-byte scale loads per lane and tile (kT16Wave)
+  constexpr int NJ = SBW ? kT16WaveMaxChunks : P;        // unrolled chunk slots per pass
   extern __shared__ __align__(16) unsigned char smem[];
   f16* xs = reinterpret_cast<f16*>(smem);                                   // [M][KB*128]
   f16* zero = xs + (size_t)M * a.KB * 128;                                   // 16 halves of zeros
@@ -391,14 +394,17 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
 #pragma unroll
       for (int vi = 0; vi < 4; ++vi) acc[t][vi] = 0.f;
 
-    // kT16Wave: a single pass over the my <= P chunks already in flight.
+    // kT16Wave: a single pass over its my <= kT16WaveMaxChunks chunks.
     const int n_pass = SBW ? 1 : (my + P - 1) / P;
     for (int pass = 0; pass < n_pass; ++pass) {
       const int ci0 = pass * P;
 #pragma unroll
-      for (int j = 0; j < P; ++j) {
-        const int ci = ci0 + j;
-        if (SBW && j + PRE < P) load(unit, j + PRE, j + PRE);
+      for (int jj = 0; jj < NJ; ++jj) {
+        // kT16Wave: chunk jj lives in ring slot jj % P; chunk jj + PRE is
+        // requested into the slot chunk jj + PRE - P freed.
+        const int j = jj % P;
+        const int ci = ci0 + jj;
+        if (SBW && jj + PRE < NJ && jj + PRE < my) load(unit, jj + PRE, (jj + PRE) % P);
         if (SBW && ci >= my) break;  // wave-uniform
         // Chunks past the range carry zero codes and zero scales: clamp the LDS
         // reads to a valid kb so they only ever multiply finite values by zero.
@@ -557,7 +563,7 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   // Chunks per wave; kT16Wave keeps all of them in flight (per <= depth).
   const int per = (a.KB + S - 1) / S;
   int mode = S == 1 ? kT16Loop : kT16OnePass;
-  if (S > 1 && per <= kT16WaveDepth) {
+  if (S > 1 && per <= kT16WaveMaxChunks) {
     const size_t sb_lds = (size_t)kT16Waves * NT * per * 128;
     if (smem + sb_lds <= 160 * 1024) {
       mode = kT16Wave;
