@@ -172,6 +172,17 @@ def time_gate_up_kernel(layers, c, dev, reps=200, n_copies=8):
     return avg_us, bytes_per_launch
 
 
+def gate_up_traffic():
+    """HBM bytes per gate/up launch measured with rocprofv3 FETCH_SIZE and WRITE_SIZE counters
+    (profiles/gate_up_traffic.json, written from two counter runs and a copy-kernel
+    calibration; the summary beside it gives the commands).  None when absent."""
+    path = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
 def cpu_baseline(layers, lnf, c, budget_s=20.0):
     """Oracle (reference CPU fallback semantics) on a bounded sample: whole decode-step layers of
     the 7B shape at context CTX0, repeated until ~budget_s, extrapolated to 32 layers + lm_head."""
@@ -230,6 +241,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 10 plain device copies of 256 MiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only build the model and time the gate/up kernel (short runs under counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs the decode step on one GPU only; multi-GPU sharding is a design "
@@ -239,12 +254,25 @@ def main():
     import torch
 
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        n = 256 << 20
+        src = torch.ones(n // 2, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_copy": n}), flush=True)
+        return
     c = CFG_7B
     t_build = time.perf_counter()
     runner, cache, layers, lnf = build_model(c, dev)
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t_build
     print(f"[bench] model built and packed in {t_build:.1f} s", file=sys.stderr, flush=True)
+    if args.kernel_only:
+        avg_us, bpl = time_gate_up_kernel(layers, c, dev, reps=20)
+        print(json.dumps({"gate_up_avg_launch_us": round(avg_us, 3), "bytes_per_launch": bpl}), flush=True)
+        return
     ms, wall, pos0 = time_decode(runner, cache, args.steps, args.warmup, dev)
     ms_per_step = ms / args.steps
     tok_s = 1000.0 / ms_per_step
@@ -282,13 +310,13 @@ def main():
             "step_hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": "t16_gemv_kernel<1,2,SWIGLU,4> (fused RMSNorm + gate/up Q4 GEMV on matrix cores + SwiGLU, 22016x4096)",
+            "kernel": "t16_gemv_kernel<1,2,2,8,2> (fused RMSNorm + gate/up Q4 GEMV on matrix cores + SwiGLU, 22016x4096)",
             "bound": "hbm",
             "achieved": round(ach, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": gate_up_traffic(),
             "avg_launch_us": round(avg_us, 3),
             "algorithmic_bytes_per_launch": bpl,
         },
