@@ -19,6 +19,7 @@ c_void_p = ctypes.c_void_p
 c_int = ctypes.c_int
 c_float = ctypes.c_float
 c_size_t = ctypes.c_size_t
+c_long = ctypes.c_long
 c_int64 = ctypes.c_int64
 
 _SIGNATURES = {
@@ -58,6 +59,7 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
          c_void_p],
     ),
+    "axm_dequantize_kv": (c_int, [c_void_p, c_void_p, c_int, c_long, c_int, c_void_p, c_void_p]),
     "axm_rope_kv_cache_write": (
         c_int,
         [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,

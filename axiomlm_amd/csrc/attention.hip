@@ -700,6 +700,51 @@ extern "C" int axm_rope_kv_cache_write(void* qkv, int T, const void* freqs, int 
 }
 
 // ---------------------------------------------------------------------------
+// KV dequantization (dequantize_kv_cache_{fp8,int4}_mps, mps_kernels.mm:930-1004;
+// dequantize_kv_fp8 / dequantize_kv_int4, quant.py:727-852): rows of hd codes
+// with hd/64 fp16 scales -> fp16, rounded as the reference does (fp8 -> fp16
+// exact then one rounding of the product; int4 (q ^ 8) - 8 times the scale).
+// One thread per 8 elements.
+// ---------------------------------------------------------------------------
+namespace {
+template <int KVT>
+__global__ void dequant_kv_kernel(const void* __restrict__ codes, const f16* __restrict__ scales, long rows, int hd,
+                                  f16* __restrict__ out) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = hd / 8;
+  if (i >= rows * per_row) return;
+  const long row = i / per_row;
+  const int e0 = (int)(i % per_row) * 8;
+  float v[8];
+  load_kv8<KVT>(codes, scales, (size_t)row, hd, e0, v);
+  f16x8 h;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) h[k] = f2h(v[k]);
+  *reinterpret_cast<f16x8*>(out + row * hd + e0) = h;
+}
+}  // namespace
+
+extern "C" int axm_dequantize_kv(const void* codes, const void* scales, int kv_dtype, long rows, int head_dim,
+                                 void* out, void* stream) {
+  AXM_CHECK_ARG(codes && scales && out, -1, "dequantize_kv: null pointer");
+  AXM_CHECK_ARG(kv_dtype == AXM_KV_FP8 || kv_dtype == AXM_KV_INT4, -1, "dequantize_kv: kv dtype %d is not quantized",
+                kv_dtype);
+  AXM_CHECK_ARG(rows >= 0 && head_dim >= 64 && head_dim % 64 == 0, -1, "dequantize_kv: bad shape rows=%ld hd=%d", rows,
+                head_dim);
+  if (rows == 0) return 0;
+  const long n = rows * (head_dim / 8);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (kv_dtype == AXM_KV_FP8)
+    hipLaunchKernelGGL(dequant_kv_kernel<AXM_KV_FP8>, grid, dim3(256), 0, (hipStream_t)stream, codes,
+                       (const f16*)scales, rows, head_dim, (f16*)out);
+  else
+    hipLaunchKernelGGL(dequant_kv_kernel<AXM_KV_INT4>, grid, dim3(256), 0, (hipStream_t)stream, codes,
+                       (const f16*)scales, rows, head_dim, (f16*)out);
+  AXM_LAUNCH_CHECK("dequantize_kv");
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
 // Tree-path KV compaction (compact_tree_kv_{half,fp8,int4}_kernel,
 // metal_kernels.metal:3145-3179 / :3875-3978; StaticKVCache.compact_tree_path,
 // axiomlm/engine/paged_cache.py:376-462): slot (wp + acc[m]) % S moves to

@@ -67,23 +67,30 @@ def quantize_kv_int4(k: torch.Tensor, v: torch.Tensor):
     return _quantize_rows(k, v, 2)
 
 
+def _dequantize_rows(codes: torch.Tensor, scales: torch.Tensor, hd: int, code: int, who: str) -> torch.Tensor:
+    _lib.require_gpu(codes, who)
+    c = codes.contiguous()
+    sc = scales.to(device=codes.device, dtype=torch.float16).contiguous()
+    width = hd if code == 1 else hd // 2
+    rows = c.numel() // width
+    if sc.numel() != rows * (hd // 64):
+        raise ValueError(f"{who}: {sc.numel()} scales for {rows} rows of head_dim {hd}")
+    out = torch.empty((*c.shape[:-1], hd), dtype=torch.float16, device=codes.device)
+    _lib.check(_lib.lib().axm_dequantize_kv(_lib.ptr(c), _lib.ptr(sc), code, rows, hd, _lib.ptr(out),
+                                            _lib.stream_of(codes.device)), who)
+    return out
+
+
 def dequantize_kv_fp8(cache_fp8: torch.Tensor, scales: torch.Tensor, head_dim: int | None = None) -> torch.Tensor:
-    """E4M3FN bytes -> fp16 (exact), times the fp16 scale (quant.py:727-768)."""
+    """E4M3FN bytes -> fp16 (exact), times the fp16 scale with one rounding (quant.py:727-768)."""
     hd = head_dim or cache_fp8.size(-1)
-    c = cache_fp8.contiguous()
-    f = c.view(torch.float8_e4m3fn).to(torch.float16)
-    g = f.view(*c.shape[:-1], -1, 64)
-    return (g * scales.unsqueeze(-1)).view(*c.shape[:-1], hd)
+    return _dequantize_rows(cache_fp8, scales, hd, 1, "dequantize_kv_fp8")
 
 
 def dequantize_kv_int4(cache_int4: torch.Tensor, scales: torch.Tensor, head_dim: int | None = None) -> torch.Tensor:
-    """Packed nibbles -> fp16 (quant.py:810-852)."""
+    """Packed nibbles ((n ^ 8) - 8) times the fp16 scale (quant.py:810-852)."""
     hd = head_dim or cache_int4.size(-1) * 2
-    c = cache_int4.view(*cache_int4.shape[:-1], -1, 32).to(torch.int32)
-    q0 = ((c & 0x0F) ^ 0x08) - 8
-    q1 = (((c >> 4) & 0x0F) ^ 0x08) - 8
-    dq = torch.stack([q0, q1], dim=-1).to(torch.float16) * scales.unsqueeze(-1).unsqueeze(-1)
-    return dq.view(*cache_int4.shape[:-1], hd)
+    return _dequantize_rows(cache_int4, scales, hd, 2, "dequantize_kv_int4")
 
 
 # ---------------------------------------------------------------------------

@@ -129,6 +129,13 @@ int axm_kv_cache_write(const void* k_rows, const void* v_rows, int ld_rows, int 
                        void* k_scales, void* v_scales, int kv_dtype, int n_kv_head, int head_dim, int max_seq_len,
                        int write_pos, void* stream);
 
+/* KV dequantization: rows x head_dim codes (fp8: u8 [rows][hd], int4: u8
+ * [rows][hd/2]) with fp16 scales [rows][hd/64] -> fp16 out [rows][hd].
+ * Replaces dequantize_kv_cache_{fp8,int4}_mps (mps_kernels.mm:930-1004) and the
+ * Python dequantize_kv_fp8 / dequantize_kv_int4 (quant.py:727-852). */
+int axm_dequantize_kv(const void* codes, const void* scales, int kv_dtype, long rows, int head_dim, void* out,
+                      void* stream);
+
 /* Fused QKV bias + RoPE + KV-cache write for T <= 64 tokens, in place on
  * qkv fp16 [T][q_dim + 2 kv_dim]: the (bias-added) query part is rotated in
  * place; token t's rotated key and its value are stored (quantized for fp8 /

@@ -624,3 +624,28 @@ def test_rope_kv_cache_write_rejects_bad_arguments(dev):
     with pytest.raises(RuntimeError):  # more than 64 tokens
         q70 = torch.zeros((70, 3 * hd), dtype=torch.float16, device=dev)
         rope_kv_cache_write_quantized(q70, freqs, kc16, kc16.clone(), None, None, hd, hd, hd, 0, 0)
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int4"])
+def test_dequantize_kv_bit_exact(dev, kind):
+    """axm_dequantize_kv (dequantize_kv_cache_{fp8,int4}_mps) against the oracle's
+    dequantizers (quant.py:727-852) on every byte value, including the fp8 NaN codes,
+    for a strided cache view: fp16 outputs bit for bit (NaN where the oracle has NaN)."""
+    from axiomlm_amd.kernels import dequantize_kv_fp8, dequantize_kv_int4
+
+    print(f"[dequantize_kv] kv={kind}", flush=True)
+    rng = np.random.default_rng(21)
+    Hkv, S, hd, n = 3, 40, 128, 33
+    width = hd if kind == "fp8" else hd // 2
+    codes = rng.integers(0, 256, (1, Hkv, S, width), dtype=np.uint8)
+    codes[0, 0, :2, :] = np.arange(256, dtype=np.uint8).reshape(2, 128)[:, :width]
+    scales = (rng.standard_normal((1, Hkv, S, hd // 64)) * 0.05).astype(F16)
+    tc, ts = T(codes, dev), T(scales, dev)
+    fn = dequantize_kv_fp8 if kind == "fp8" else dequantize_kv_int4
+    got = N(fn(tc[:, :, :n], ts[:, :, :n], hd))
+    ref_fn = fm.dequantize_kv_fp8 if kind == "fp8" else fm.dequantize_kv_int4
+    ref = ref_fn(codes[:, :, :n], scales[:, :, :n])
+    assert got.shape == ref.shape == (1, Hkv, n, hd)
+    nan = np.isnan(ref.astype(F32))
+    assert np.array_equal(np.isnan(got.astype(F32)), nan)
+    assert np.array_equal(got.view(np.uint16)[~nan], ref.view(np.uint16)[~nan])
