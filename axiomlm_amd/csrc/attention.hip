@@ -520,13 +520,14 @@ size_t attn_workspace_bytes(int B, int Hq, int hd, int n_splits) {
 }
 
 int attn_choose_splits(int B, int Hkv, int active_len) {
-  // A decode workgroup (16 waves x 4 keys x 4 steps in flight = 256 keys per
-  // round) takes up to 1024 keys: short contexts need no split merge; longer
-  // ones split so that the workgroups still fill the chip.
-  int splits = (active_len + 1023) / 1024;
-  const int fill = (axm_num_cus() + B * Hkv - 1) / (B * Hkv);
-  if (splits > 1 && splits < fill) splits = fill;
-  const int by_len = (active_len + 255) / 256;
+  // Measured with 16-wave decode workgroups (32 KV heads, hd 128): one
+  // workgroup per head is fastest up to 512 keys; beyond that a four-way split
+  // (128 workgroups) is fastest from 1k to 4k keys.  Fewer (batch x head) rows
+  // take proportionally more splits; every split keeps >= 128 keys.
+  const int rows = B * Hkv;
+  const int want_wg = active_len <= 512 ? 32 : 128;
+  int splits = (want_wg + rows - 1) / rows;
+  const int by_len = (active_len + 127) / 128;
   if (splits > by_len) splits = by_len;
   if (splits > 64) splits = 64;
   if (splits < 1) splits = 1;
