@@ -225,6 +225,16 @@ __device__ __forceinline__ float dpp_sum_step(float v) {
   const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
   return v + __builtin_bit_cast(float, o);
 }
+// Packed halves in the operand type of v_dot2_f32_f16 (products exact in fp32,
+// accumulated in fp32).
+typedef __fp16 dot_h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ dot_h2 as_dot_h2(uint32_t u) { return __builtin_bit_cast(dot_h2, u); }
+
+// 2^x with the bare v_exp_f32: softmax weights below 2^-126 of the running
+// maximum are flushed to zero instead of kept as denormals, which changes no
+// fp16 output.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float key_row_sum(float v, int lpt) {
   if (lpt == 16 || lpt == 8) {
     v = dpp_sum_step<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -317,6 +327,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
 
   // Global query-row index and query pointers.
   float q[QR][8];
+  dot_h2 qh[QR][4];  // the same query halves packed for v_dot2_f32_f16 (fp16 KV)
   int qrow[QR];
 #pragma unroll
   for (int r = 0; r < QR; ++r) {
@@ -334,9 +345,13 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
       const f16x8 v = *reinterpret_cast<const f16x8*>(p.q + (size_t)qrow[r] * hd + e0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) q[r][i] = h2f(v[i]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qh[r][i] = dot_h2{(__fp16)v[2 * i], (__fp16)v[2 * i + 1]};
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) q[r][i] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qh[r][i] = dot_h2{(__fp16)0.f, (__fp16)0.f};
     }
   }
 
@@ -356,30 +371,71 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
   }
 
   for (; kb0 < k_end; kb0 += NW * KPW * U) {
+    // Steps of this batch that hold at least one key of the range (wave-uniform);
+    // the scores of the batch are taken first so that the running maximum and
+    // the rescaling of (l, o) happen once per batch instead of once per key.
+    const int n_steps = min(U, (k_end - kb0 + NW * KPW - 1) / (NW * KPW));
+    float sc[QR][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-    const int key = kb0 + u * NW * KPW + sub;
-    const bool valid = key < k_end;
-    float kf[8], vf[8];
-    kv8_convert<KVT>(kr[u], ksc[u], kf);
-    kv8_convert<KVT>(vr[u], vsc[u], vf);
+      if (u < n_steps) {
+        const int key = kb0 + u * NW * KPW + sub;
+        const bool valid = key < k_end;
+        float kf[8];
+        if constexpr (KVT != AXM_KV_FP16) kv8_convert<KVT>(kr[u], ksc[u], kf);
+#pragma unroll
+        for (int r = 0; r < QR; ++r) {
+          float d = 0.f;
+          if constexpr (KVT == AXM_KV_FP16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) d = __builtin_amdgcn_fdot2(qh[r][i], as_dot_h2(kr[u][i]), d, false);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[r][i], kf[i], d);
+          }
+          d = key_row_sum(d, LPT);
+          bool vis = valid && r < n_rows;
+          if (TREE && key >= prefix) vis = vis && ((node_mask[r] >> (key - prefix)) & 1ull);
+          sc[r][u] = vis ? d * p.scale_log2 : kNegBig;
+        }
+      }
+    }
+    float vf[U][8];
+    if constexpr (KVT != AXM_KV_FP16) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (u < n_steps) kv8_convert<KVT>(vr[u], vsc[u], vf[u]);
+    }
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
-      float d = 0.f;
+      float m_new = m[r];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[r][i], kf[i], d);
-      d = key_row_sum(d, LPT);
-      bool vis = valid && r < n_rows;
-      if (TREE && key >= prefix) vis = vis && ((node_mask[r] >> (key - prefix)) & 1ull);
-      const float s = vis ? d * p.scale_log2 : kNegBig;
-      const float m_new = fmaxf(m[r], s);
-      const float alpha = exp2f(m[r] - m_new);
-      const float pr = vis ? exp2f(s - m_new) : 0.f;
-      l[r] = l[r] * alpha + pr;
+      for (int u = 0; u < U; ++u)
+        if (u < n_steps) m_new = fmaxf(m_new, sc[r][u]);
+      const float alpha = fast_exp2(m[r] - m_new);
+      float lsum = l[r] * alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[r][i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u < n_steps) {
+          const float pr = sc[r][u] == kNegBig ? 0.f : fast_exp2(sc[r][u] - m_new);
+          lsum += pr;
+          if constexpr (KVT == AXM_KV_FP16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const f16x2 vh = as_h2(vr[u][i]);
+              o[r][2 * i] = __builtin_fmaf(pr, h2f(vh.x), o[r][2 * i]);
+              o[r][2 * i + 1] = __builtin_fmaf(pr, h2f(vh.y), o[r][2 * i + 1]);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[r][i] = __builtin_fmaf(pr, vf[u][i], o[r][i]);
+          }
+        }
+      }
+      l[r] = lsum;
       m[r] = m_new;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[r][i] = __builtin_fmaf(o[r][i], alpha, pr * vf[i]);
-    }
     }
     if (kb0 + NW * KPW * U < k_end) fetch(kb0 + NW * KPW * U);
   }

@@ -375,8 +375,10 @@ def test_runner_verify_step_ring_wrap(dev):
 
 def test_runner_speculative_decode_matches_greedy(dev):
     """Native prompt-lookup speculative decoding (mps_kernels.mm:3639-3730) is lossless
-    under greedy acceptance: its tokens equal plain greedy decoding by the oracle; a
-    repetitive prompt makes the n-gram lookup draft (drafted > 0, fewer model calls
+    under greedy acceptance: every token it emits is the oracle's greedy choice given the
+    tokens before it, up to near-ties within the logit tolerance (the random-init C1 model
+    has top-2 logit gaps of one fp16 ulp at some steps, where either choice is greedy);
+    a repetitive prompt makes the n-gram lookup draft (drafted > 0, fewer model calls
     than new tokens)."""
     print("[runner_speculative]", flush=True)
     cfg, ow, cos, sin = c1_model()
@@ -389,9 +391,17 @@ def test_runner_speculative_decode_matches_greedy(dev):
     run_steps(runner, cache, prompt[:-1], dev)
     n_new = 40
     toks, seen, calls, drafted, accepted, secs = runner.speculative_decode(prompt, n_new, 3, 8, len(prompt) - 1)
-    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
-    ref_toks, _ = model.generate_greedy(prompt, n_new, ocache)
     assert toks[:len(prompt)] == prompt
-    assert toks[len(prompt):] == list(ref_toks), (toks[len(prompt):], list(ref_toks))
+    new_toks = toks[len(prompt):]
+    assert len(new_toks) == n_new
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    lg = model.forward(prompt, ocache)[-1].astype(F32)
+    ties = 0
+    for i, tk in enumerate(new_toks):
+        assert lg[tk] >= lg.max() - 2 * TOL, f"token {i}: {tk} scores {lg[tk]}, greedy max {lg.max()}"
+        ties += int(tk != int(np.argmax(lg)))
+        if i + 1 < n_new:
+            lg = model.forward([tk], ocache)[-1].astype(F32)
     assert seen == len(prompt) - 1 + n_new and calls <= n_new and drafted >= accepted >= 0 and secs > 0
-    print(f"[runner_speculative] calls={calls} drafted={drafted} accepted={accepted}", flush=True)
+    print(f"[runner_speculative] calls={calls} drafted={drafted} accepted={accepted} near-tie choices={ties}",
+          flush=True)
