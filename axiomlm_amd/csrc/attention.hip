@@ -252,6 +252,8 @@ struct AttnParams {
   KvView kv;
   f16* out;
   float* ws;              // partials [n_rows_total][n_splits][2 + hd]
+  f16* parts_o;           // decode, merged by the consumer: o / l per split [n_splits][rows][hd]
+  f32x2* parts_ml;        //   and (running max m, sum l) per split [n_splits][rows]
   int Hq, n_rep;
   int n_splits;
   int prefix_len;         // keys [0, prefix_len) (decode: active_len)
@@ -490,6 +492,11 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
       const int gr = (!TREE) ? (b * p.Hq + kvh * p.n_rep + row_base + r)
                              : (((row_base + r) / p.n_rep) * p.Hq + kvh * p.n_rep + (row_base + r) % p.n_rep);
       p.out[(size_t)gr * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+    } else if (!TREE && p.parts_o != nullptr) {
+      const int gr = b * p.Hq + kvh * p.n_rep + row_base + r;
+      const size_t rows_total = (size_t)p.kv.B * p.Hq;
+      p.parts_o[((size_t)split * rows_total + gr) * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+      if (e == 0) p.parts_ml[(size_t)split * rows_total + gr] = f32x2{mm, ll};
     } else {
       const int gr = (!TREE) ? (b * p.Hq + kvh * p.n_rep + row_base + r)
                              : (((row_base + r) / p.n_rep) * p.Hq + kvh * p.n_rep + (row_base + r) % p.n_rep);
@@ -588,6 +595,44 @@ int attn_choose_splits(int B, int Hkv, int active_len) {
   if (splits > 64) splits = 64;
   if (splits < 1) splits = 1;
   return splits;
+}
+
+int attn_parts_splits(int B, int Hkv, int active_len) {
+  // Split partials merged by the consumer cost no reduce launch, so the split
+  // count aims at one workgroup per CU (measured on 32 heads x 128: eight
+  // splits fastest from 250 to 1k keys) with >= 16 keys per split.
+  const int rows = B * Hkv;
+  int splits = 1;
+  while (splits < kAttnMaxParts && rows * splits < 256) splits <<= 1;
+  while (splits > 1 && active_len < 16 * splits) splits >>= 1;
+  return splits;
+}
+
+size_t attn_parts_bytes(int B, int Hq, int hd) {
+  return (size_t)kAttnMaxParts * B * Hq * (hd * sizeof(f16) + sizeof(f32x2));
+}
+
+int launch_flash_decode_parts(const f16* q, const KvView& kv, int Hq, int active_len, const int* active_len_dev,
+                              int n_splits, f16* parts_o, f32x2* parts_ml, hipStream_t s) {
+  if (n_splits < 2 || n_splits > kAttnMaxParts || parts_o == nullptr || parts_ml == nullptr) {
+    axm_set_error("flash_decode_parts: %d splits (2..%d) or null partial buffers", n_splits, kAttnMaxParts);
+    return -1;
+  }
+  AttnParams p{};
+  p.q = q;
+  p.kv = kv;
+  p.parts_o = parts_o;
+  p.parts_ml = parts_ml;
+  p.Hq = Hq;
+  p.n_rep = Hq / kv.Hkv;
+  p.n_splits = n_splits;
+  p.prefix_len = active_len;
+  p.prefix_dev = active_len_dev;
+  p.T = 0;
+  p.scale_log2 = kLog2e / sqrtf((float)kv.hd);
+  const int qr = pick_qr(p.n_rep);
+  dim3 grid(kv.B * kv.Hkv, n_splits, (p.n_rep + qr - 1) / qr);
+  return launch_attn_dispatch<false>(p, qr, grid, s);
 }
 
 int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,

@@ -50,6 +50,16 @@ int attn_choose_splits(int B, int Hkv, int active_len);
 int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,
                         int n_splits, float* ws, hipStream_t s);
 
+// The same decode attention with 2..kAttnMaxParts splits whose partials are
+// left for the consumer to merge (no reduce launch): parts_o [n_splits][B*Hq][hd]
+// holds each split's o / l in fp16, parts_ml [n_splits][B*Hq] its (max, sum);
+// the row is sum_s w_s o_s / sum_s w_s with w_s = l_s 2^(m_s - max_s m_s).
+constexpr int kAttnMaxParts = 8;
+int attn_parts_splits(int B, int Hkv, int active_len);
+size_t attn_parts_bytes(int B, int Hq, int hd);  // parts_o + parts_ml for kAttnMaxParts splits
+int launch_flash_decode_parts(const f16* q, const KvView& kv, int Hq, int active_len, const int* active_len_dev,
+                              int n_splits, f16* parts_o, f32x2* parts_ml, hipStream_t s);
+
 // Tree / multi-token verification attention (batch 0): T query tokens; prefix
 // slots [0, prefix_len) always visible; tree node j lives at slot
 // (write_pos + j) % S and is visible to node u iff bit j of mask[u] is set.

@@ -33,12 +33,23 @@ struct T16Args {
   long kv_stride_h;
   int max_seq;
   unsigned long long* argmax_keys;  // Q4_EPI_STORE, M == 1: per-unit ordered (logit, index) key
+  // Q4_EPI_RESID, M == 1, K <= kTile16PartsMaxK: when x_parts is set the
+  // activations are merged from decode-attention split partials instead of read
+  // from x: x[h hd + e] = sum_s w_s o_s[h hd + e] / sum_s w_s with
+  // w_s = l_s 2^(m_s - max_s m_s), (m_s, l_s) = x_ml[s][h], rounded once to fp16.
+  const f16* x_parts;  // [n_parts][K] fp16
+  const f32x2* x_ml;   // [n_parts][K / parts_hd]
+  int n_parts;         // 2..kTile16MaxParts
+  int parts_hd;        // elements per head (a multiple of 8)
   int split;           // waves per unit (set by t16_gemv_launch)
   uint32_t unpack[4];  // nibble masks and fp16 magic exponents (set by t16_gemv_launch)
 };
 
 // Largest K (activation length) the tile16 GEMV stages.
 constexpr int kTile16MaxK = 16384;
+// Limits of the split-partial activation source (one 8-element vector per thread).
+constexpr int kTile16PartsMaxK = 4096;
+constexpr int kTile16MaxParts = 8;
 
 size_t t16_smem_bytes(int M, int NT, int K);
 void t16_prepare_attributes();

@@ -121,6 +121,80 @@ __device__ __forceinline__ void t16_load_x(const T16Args& a, T16X<M>& r) {
   }
 }
 
+// Split-partial activation source (Q4_EPI_RESID, M == 1): thread tid owns the
+// 8 elements 8 tid.. of x.  Every partial slot is loaded unconditionally through
+// a bounded buffer descriptor (slots past n_parts read as zero) so that the
+// number of loads in flight before the weight loads is static.
+static_assert(kTile16PartsMaxK == kT16Threads * 8, "one partial vector per thread");
+struct T16Parts {
+  u32x4 o[kTile16MaxParts];
+  u32x2 ml[kTile16MaxParts];
+};
+
+__device__ __forceinline__ void t16_load_parts(const T16Args& a, T16Parts& pp) {
+  const int i = threadIdx.x;
+  const int heads = a.K / a.parts_hd;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.x_parts, (short)0, a.n_parts * a.K * (int)sizeof(f16), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.x_ml, (short)0, a.n_parts * heads * (int)sizeof(f32x2), 0x00020000);
+  const bool ok = i < (a.K >> 3);
+  const int h = (8 * i) / a.parts_hd;
+#pragma unroll
+  for (int sp = 0; sp < kTile16MaxParts; ++sp) {
+    const int oo = ok ? (sp * a.K + 8 * i) * (int)sizeof(f16) : 0x7FFFFFF0;
+    const int mo = ok ? (sp * heads + h) * (int)sizeof(f32x2) : 0x7FFFFFF0;
+    pp.o[sp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, oo, 0, 0));
+    pp.ml[sp] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, mo, 0, 0));
+  }
+}
+
+template <int M>
+__device__ __forceinline__ void t16_merge_parts(const T16Args& a, const T16Parts& pp, T16X<M>& r) {
+  constexpr float kNoScore = -1e30f;
+  // The (m, l) words are copied to scalars before the bit casts: a bit cast of an
+  // ext_vector element expression reads element 0.
+  float m[kTile16MaxParts], l[kTile16MaxParts];
+#pragma unroll
+  for (int sp = 0; sp < kTile16MaxParts; ++sp) {
+    const uint32_t mu = pp.ml[sp][0];
+    const uint32_t lu = pp.ml[sp][1];
+    m[sp] = __builtin_bit_cast(float, mu);
+    l[sp] = __builtin_bit_cast(float, lu);
+  }
+  float mx = kNoScore;
+#pragma unroll
+  for (int sp = 0; sp < kTile16MaxParts; ++sp)
+    if (sp < a.n_parts) mx = fmaxf(mx, m[sp]);
+  float wsum = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < kTile16MaxParts; ++sp) {
+    if (sp < a.n_parts) {
+      const float w = l[sp] * exp2f(m[sp] - mx);
+      wsum += w;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f16x2 h2 = as_h2(pp.o[sp][c]);
+        acc[2 * c] = __builtin_fmaf(w, h2f(h2.x), acc[2 * c]);
+        acc[2 * c + 1] = __builtin_fmaf(w, h2f(h2.y), acc[2 * c + 1]);
+      }
+    }
+  }
+  f16x8 x;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = f2h(wsum > 0.f ? acc[e] / wsum : 0.f);
+  const bool ok = (int)threadIdx.x < (a.K >> 3);
+#pragma unroll
+  for (int v = 0; v < kT16XV; ++v) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.x[0][v][e] = f16(0);
+    r.w[v] = r.x[0][v];
+  }
+  if (ok) r.x[0][0] = x;
+}
+
 template <int M>
 __device__ void t16_stage_x(const T16Args& a, const T16X<M>& r, f16* xs, f32x2* cx, float* red) {
   const int tid = threadIdx.x;
@@ -284,6 +358,11 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
 // kT16OnePass: one pass with per-chunk scale loads and in-loop refills.
 // P kb-loads (1 KB per tile each) stay in flight per wave.
 // ---------------------------------------------------------------------------
+// Residual epilogue whose activations are merged from attention split partials
+// (an instantiation of its own, M == 1 only, so that the plain residual GEMV
+// keeps its smaller register footprint).
+constexpr int kT16EpiResidParts = 16;
+
 constexpr int kT16Loop = 0;
 constexpr int kT16OnePass = 1;
 constexpr int kT16Wave = 2;
@@ -347,7 +426,14 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
   int it = 0;
   int unit = blockIdx.x * upw + slot;
   T16X<M> xr;
-  t16_load_x<M>(a, xr);
+  // Q4_EPI_RESID with one token may take its activations from attention split
+  // partials (merged after the weight loads are issued).
+  constexpr bool from_parts = EPI == kT16EpiResidParts;
+  T16Parts pp;
+  if (from_parts)
+    t16_load_parts(a, pp);
+  else
+    t16_load_x<M>(a, xr);
   // kT16Wave: the wave's (scale, bias) run; 16-byte vector v holds chunk v / 8,
   // rows 2 (v % 8) and 2 (v % 8) + 1.  Issued before the weight loads so that
   // storing it to LDS waits only for itself.
@@ -380,6 +466,7 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
         if (v < my * 8) *reinterpret_cast<u32x4*>(my_sb + (size_t)t * per * 16 + 2 * v) = sbv[t][q];
       }
   }
+  if (from_parts) t16_merge_parts<M>(a, pp, xr);
   t16_stage_x<M>(a, xr, xs, cx, red);  // ends with a workgroup barrier
 
   // LDS addresses: A operand of this lane and (corr, sum) of its D tokens.
@@ -476,7 +563,8 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
             }
       }
     }
-    if (sub == 0 && unit < a.n_units) t16_epilogue<M, NT, EPI>(a, unit, lane, acc);
+    if (sub == 0 && unit < a.n_units)
+      t16_epilogue<M, NT, (EPI == kT16EpiResidParts ? Q4_EPI_RESID : EPI)>(a, unit, lane, acc);
     if (ONE || !more) break;
     ++it;
     unit = next_unit;
@@ -536,6 +624,7 @@ void t16_prepare_attributes() {
   AXM_T16_ATTR(3)
   AXM_T16_ATTR(4)
 #undef AXM_T16_ATTR
+  t16_set_attr<1, 1, kT16EpiResidParts>();
 }
 
 int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
@@ -544,6 +633,15 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   size_t smem = t16_smem_bytes(M, NT, a.K);
   if (smem > 160 * 1024 || M < 1 || M > 4 || a.K > kT16MaxK) {
     axm_set_error("tile16 gemv: M=%d K=%d unsupported (K <= %d, %zu B of LDS)", M, a.K, kT16MaxK, smem);
+    return -2;
+  }
+  if (a.x_parts != nullptr &&
+      (M != 1 || epi != Q4_EPI_RESID || a.ln_w != nullptr || a.K > kTile16PartsMaxK || a.n_parts < 2 ||
+       a.n_parts > kTile16MaxParts || a.parts_hd <= 0 || a.parts_hd % 8 != 0 || a.K % a.parts_hd != 0 ||
+       a.x_ml == nullptr)) {
+    axm_set_error("tile16 gemv: split-partial activations need M=1, the residual epilogue, no norm, K <= %d, "
+                  "2..%d parts, head size %% 8 == 0 (M=%d K=%d parts=%d hd=%d)",
+                  kTile16PartsMaxK, kTile16MaxParts, M, a.K, a.n_parts, a.parts_hd);
     return -2;
   }
   // Waves per unit: aim for ~8 waves per CU with >= 2 kb-loads per wave.
@@ -579,6 +677,7 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
       case Q4_EPI_QKV_ROPE: return t16_launch_one<MM, 1, Q4_EPI_QKV_ROPE>(a, mode, grid, smem, s); \
     }                                                                                    \
     break;
+  if (a.x_parts != nullptr) return t16_launch_one<1, 1, kT16EpiResidParts>(a, mode, grid, smem, s);
   switch (M) {
     AXM_T16_CASE(1)
     AXM_T16_CASE(2)

@@ -146,6 +146,10 @@ struct GemvCall {
   long kv_stride_h = 0;
   int max_seq = 1;
   unsigned long long* argmax_keys = nullptr;
+  // tile16 O projection: activations merged from attention split partials.
+  const f16* x_parts = nullptr;
+  const f32x2* x_ml = nullptr;
+  int n_parts = 0, parts_hd = 0;
 };
 
 template <class A>
@@ -188,6 +192,10 @@ static int run_gemv(const Mat& m, int epi, int out_rows, const GemvCall& c, int 
     a.N_rows_alloc = m.N;
     a.n_units = (out_rows + 15) / 16;
     a.pair_offset = c.pair_rows / 16;
+    a.x_parts = c.x_parts;
+    a.x_ml = c.x_ml;
+    a.n_parts = c.n_parts;
+    a.parts_hd = c.parts_hd;
     return t16_gemv_launch(a, M, epi, s);
   }
   Q4GemvArgs a{};
@@ -222,6 +230,11 @@ struct axm_runner {
   unsigned long long* tree_mask = nullptr;  // [kMaxVerify]
   float* ws = nullptr;
   size_t ws_bytes = 0;
+  // Decode: attention split partials merged by the tile16 O projection (no
+  // reduce launch) when parts_ok.
+  bool parts_ok = false;
+  f16* parts_o = nullptr;
+  f32x2* parts_ml = nullptr;
   unsigned long long* argmax_keys = nullptr;  // per lm_head tile: ordered (logit, index) key
   int max_splits = 64;
   int mode = AXM_RUNNER_MODE_GRAPH;
@@ -243,7 +256,7 @@ struct axm_runner {
   ~axm_runner() {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
-    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys,
+    void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys, parts_o,
                     qkvbuf, tree_pos, tree_mask, p_layers, p_bar, p_head_cnt, p_tok_next, p_err};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
@@ -412,8 +425,13 @@ struct axm_runner {
       if (rc) return rc;
       if (d.kv_dtype != AXM_KV_FP16)
         launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
-      // 2. attention over slots [0, active_len).
-      rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
+      // 2. attention over slots [0, active_len); with parts_ok the split
+      // partials are merged while the O projection stages its activations.
+      const bool merge_in_o = parts_ok && n_splits > 1;
+      if (merge_in_o)
+        rc = launch_flash_decode_parts(q, kv, d.n_head, 0, params + P_ACTIVE, n_splits, parts_o, parts_ml, s);
+      else
+        rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
       if (rc) return rc;
       // 3. O projection, residual add into x.
       GemvCall o{};
@@ -421,6 +439,12 @@ struct axm_runner {
       o.ldx = q_dim;
       o.resid = x;
       o.ldr = D;
+      if (merge_in_o) {
+        o.x_parts = parts_o;
+        o.x_ml = parts_ml;
+        o.n_parts = n_splits;
+        o.parts_hd = d.head_dim;
+      }
       rc = run_gemv(m_o[i], Q4_EPI_RESID, D, o, 1, s);
       if (rc) return rc;
       // 4. gate/up with RMSNorm prologue and SwiGLU epilogue.
@@ -671,6 +695,7 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
       {(void**)&r->logits, (size_t)T * d.vocab_size * sizeof(f16)},
       {(void**)&r->norm, (size_t)T * d.d_model * sizeof(f16)},
       {(void**)&r->ws, r->ws_bytes > 0 ? r->ws_bytes : 256},
+      {(void**)&r->parts_o, attn_parts_bytes(1, d.n_head, d.head_dim)},
       {(void**)&r->argmax_keys, (size_t)((d.vocab_size + 7) / 8) * sizeof(unsigned long long)},
       {(void**)&r->qkvbuf, (size_t)T * r->qkv_dim * sizeof(f16)},
       {(void**)&r->tree_pos, kMaxVerify * sizeof(int)},
@@ -690,6 +715,11 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
     axm_set_error("runner_create: stream/memset setup failed");
     return -4;
   }
+  r->parts_ml = reinterpret_cast<f32x2*>(r->parts_o + (size_t)kAttnMaxParts * r->q_dim);
+  r->parts_ok = true;
+  for (const Mat& m : r->m_o) r->parts_ok = r->parts_ok && m.w16 != nullptr;
+  r->parts_ok = r->parts_ok && r->q_dim <= kTile16PartsMaxK && d.head_dim % 8 == 0 &&
+                kAttnMaxParts <= kTile16MaxParts;
   q4m_prepare_attributes();
   r->setup_persistent();
   *out = r;
@@ -758,7 +788,8 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
                      rope_pos, write_pos, active_len, r->argmax_keys, (d.vocab_size + 7) / 8);
   // Bucket the split count so that one graph covers a range of lengths.
-  int splits = attn_choose_splits(1, d.n_kv_head, active_len);
+  int splits = r->parts_ok ? attn_parts_splits(1, d.n_kv_head, active_len)
+                           : attn_choose_splits(1, d.n_kv_head, active_len);
   int bucket = 1;
   while (bucket < splits) bucket <<= 1;
   if (bucket > r->max_splits) bucket = r->max_splits;

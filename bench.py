@@ -106,11 +106,11 @@ def build_model(c, dev, seed=0):
     return runner, cache, layers, lnf
 
 
-def time_decode(runner, cache, steps, warmup, dev):
+def time_decode(runner, cache, steps, warmup, dev, ctx0=CTX0):
     """Greedy decode: argmax of step t (device) is the token of step t+1."""
     import torch
 
-    pos = CTX0
+    pos = ctx0
     runner.step(torch.zeros(1, dtype=torch.int64, device=dev), pos - 1, pos - 1, pos)
 
     def one(p):
@@ -241,6 +241,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--context", type=int, default=CTX0,
+                    help="tokens of synthetic context before the first timed step (default %(default)s)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain device copies of 256 MiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--kernel-only", action="store_true",
@@ -249,6 +251,10 @@ def main():
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs the decode step on one GPU only; multi-GPU sharding is a design "
                                    "note (DESIGN.md), so --gpus must be 1"}))
+        sys.exit(2)
+
+    if not 1 <= args.context or args.context + args.warmup + args.steps + 1 > MAX_SEQ:
+        print(json.dumps({"error": f"--context + --warmup + --steps must stay within the {MAX_SEQ}-slot cache"}))
         sys.exit(2)
 
     import torch
@@ -273,7 +279,7 @@ def main():
         avg_us, bpl = time_gate_up_kernel(layers, c, dev, reps=20)
         print(json.dumps({"gate_up_avg_launch_us": round(avg_us, 3), "bytes_per_launch": bpl}), flush=True)
         return
-    ms, wall, pos0 = time_decode(runner, cache, args.steps, args.warmup, dev)
+    ms, wall, pos0 = time_decode(runner, cache, args.steps, args.warmup, dev, args.context)
     ms_per_step = ms / args.steps
     tok_s = 1000.0 / ms_per_step
     mean_active = pos0 + (args.steps + 1) / 2.0
