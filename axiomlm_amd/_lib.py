@@ -40,6 +40,13 @@ _SIGNATURES = {
     "axm_qmv_q4_tile16_swiglu": (
         c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]
     ),
+    "axm_qmm_q4_tile16_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "axm_qmm_q4_tile16": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]
+    ),
+    "axm_qmm_q4_tile16_swiglu": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]
+    ),
     "axm_dequantize_q4_marlin": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "axm_pack_q4_marlin_rtn": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "axm_pack_q4_marlin_mse": (
@@ -67,6 +74,7 @@ _SIGNATURES = {
     ),
     "axm_attention_num_splits": (c_int, [c_int, c_int, c_int]),
     "axm_attention_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "axm_tree_attention_num_splits": (c_int, [c_int, c_int, c_int, c_int]),
     "axm_gqa_flash_decode": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -662,6 +662,220 @@ size_t tree_workspace_bytes(int T, int Hq, int hd, int n_splits) {
   return n_splits <= 1 ? 0 : (size_t)T * Hq * n_splits * (2 + hd) * sizeof(float);
 }
 
+// ---------------------------------------------------------------------------
+// Tree verification attention on the matrix cores.  The query rows of one KV
+// head (tree node u x replica r, up to 64 per workgroup, 16 per wave) attend
+// over 32-key blocks of [prefix keys | tree slots]:
+//   S = Q K^T   v_mfma_f32_16x16x32_f16, A = the wave's 16 query rows (loaded
+//               once), B = 16 keys x 32 dims straight from the cache rows
+//               (dequantized to fp16 with the reference rounding),
+//   masked online softmax on the D tile (a query row's 16 keys sit in the 16
+//               lanes of one DPP row, so row max / sum are DPP reductions),
+//   O += P V    A = P (fp16, through a wave-private LDS tile), B = the block's
+//               V staged transposed (dim-major) in LDS by the workgroup.
+// A key block is loaded once per workgroup for all its rows, instead of once
+// per few rows.  Partials over key splits use the decode layout
+// ([row][split][m, l, o]) and attn_reduce_kernel.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float v) {
+  const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+  return fmaxf(v, __builtin_bit_cast(float, o));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = dpp_max_step<0xB1>(v);
+  v = dpp_max_step<0x4E>(v);
+  v = dpp_max_step<0x141>(v);
+  return dpp_max_step<0x140>(v);
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_sum_step<0xB1>(v);
+  v = dpp_sum_step<0x4E>(v);
+  v = dpp_sum_step<0x141>(v);
+  return dpp_sum_step<0x140>(v);
+}
+
+constexpr int kTreeKeys = 32;    // keys per block (the k extent of one P V MFMA)
+constexpr int kTreeRows = 64;    // query rows per workgroup (four waves of 16)
+
+// 8 consecutive elements [e0, e0 + 8) of cache row `row` as fp16 (zeros when !ok).
+template <int KVT>
+__device__ __forceinline__ f16x8 kv_row8(const void* base, const f16* scales, size_t row, int hd, int e0, bool ok) {
+  f16x8 h;
+  if (!ok) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = f16(0);
+    return h;
+  }
+  float sc;
+  const u32x4 r = kv8_fetch<KVT>(base, scales, row, hd, e0, sc);
+  if (KVT == AXM_KV_FP16) return __builtin_bit_cast(f16x8, r);
+  float f[8];
+  kv8_convert<KVT>(r, sc, f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = f2h(f[i]);
+  return h;
+}
+
+template <int KVT, int HD>
+__global__ void __launch_bounds__(256) tree_mfma_kernel(AttnParams p) {
+  constexpr int KSTEPS = HD / 32;  // MFMA k-steps over the head dimension
+  constexpr int DT = HD / 16;      // 16-wide output dimension tiles
+  __shared__ __align__(16) f16 vt[HD][kTreeKeys];           // V block, dim-major
+  __shared__ __align__(16) f16 pt[4][16][kTreeKeys];        // per wave: P of its 16 rows
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int kvh = blockIdx.x;
+  const int R = p.T * p.n_rep;
+  const int row0 = blockIdx.y * kTreeRows + wave * 16;
+  const int split = blockIdx.z;
+  const int prefix = p.prefix_len;
+  const int n_keys = prefix + p.T;
+  const int per = (n_keys + p.n_splits - 1) / p.n_splits;
+  const int k_begin = min(split * per, n_keys);
+  const int k_end = min(k_begin + per, n_keys);
+  const size_t head_row0 = (size_t)kvh * p.kv.S;  // batch 0
+  auto grow = [&](int r) {  // global query row (node * Hq + query head) of row r < R
+    return (r / p.n_rep) * p.Hq + kvh * p.n_rep + (r % p.n_rep);
+  };
+  auto slot_of = [&](int key) { return key < prefix ? key : (p.write_pos + (key - prefix)) % p.kv.S; };
+
+  // A operand: query row row0 + l16, dims 32 c + 8 lq .. +7.
+  f16x8 qa[KSTEPS];
+  {
+    const int r = row0 + l16;
+#pragma unroll
+    for (int c = 0; c < KSTEPS; ++c) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qa[c][i] = f16(0);
+      if (r < R) qa[c] = *reinterpret_cast<const f16x8*>(p.q + (size_t)grow(r) * HD + 32 * c + 8 * lq);
+    }
+  }
+  // D-tile rows of this lane: row0 + 4 lq + v.
+  uint64_t mask[4];
+  bool row_ok[4];
+  float m[4], l[4];
+  f32x4 o[DT];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = row0 + 4 * lq + v;
+    row_ok[v] = r < R;
+    mask[v] = row_ok[v] ? p.masks[r / p.n_rep] : 0ull;
+    m[v] = kNegBig;
+    l[v] = 0.f;
+  }
+#pragma unroll
+  for (int d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb0 = k_begin; kb0 < k_end; kb0 += kTreeKeys) {
+    // Stage the block's V transposed: vector j covers key kb0 + j / (HD/8), dims 8 (j % (HD/8)).
+    constexpr int kVec = kTreeKeys * HD / 8;
+#pragma unroll
+    for (int j0 = 0; j0 < kVec; j0 += 256) {
+      const int j = j0 + threadIdx.x;
+      if (j < kVec) {
+        const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
+        const int key = kb0 + kk;
+        const f16x8 vv = kv_row8<KVT>(p.kv.v, p.kv.vs, head_row0 + slot_of(key), HD, e0, key < k_end);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vt[e0 + i][kk] = vv[i];
+      }
+    }
+    // S = Q K^T for the block's two 16-key halves.
+    f32x4 sc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int key = kb0 + 16 * h + l16;
+      const size_t row = head_row0 + slot_of(key);
+      sc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) {
+        const f16x8 kf = kv_row8<KVT>(p.kv.k, p.kv.ks, row, HD, 32 * c + 8 * lq, key < k_end);
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf, sc[h], 0, 0, 0);
+      }
+    }
+    // Mask, scale, online softmax per D-tile row; P to the wave's LDS tile.
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float s[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int key = kb0 + 16 * h + l16;
+        bool vis = row_ok[v] && key < k_end;
+        if (key >= prefix) vis = vis && ((mask[v] >> (key - prefix)) & 1ull);
+        s[h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
+      }
+      const float m_new = fmaxf(m[v], row16_max(fmaxf(s[0], s[1])));
+      const float alpha = fast_exp2(m[v] - m_new);
+      float pr[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) pr[h] = s[h] == kNegBig ? 0.f : fast_exp2(s[h] - m_new);
+      l[v] = l[v] * alpha + row16_sum(pr[0] + pr[1]);
+      m[v] = m_new;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) o[d][v] *= alpha;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) pt[wave][4 * lq + v][16 * h + l16] = f2h(pr[h]);
+    }
+    __syncthreads();  // V staged by every wave; P tiles written
+    // O += P V: A = P[row l16][keys 8 lq ..], B = V^T[dim 16 d + l16][keys 8 lq ..].
+    const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][l16][8 * lq]);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const f16x8 vb = *reinterpret_cast<const f16x8*>(&vt[16 * d + l16][8 * lq]);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
+    }
+    __syncthreads();  // before the next block overwrites vt / pt
+  }
+
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if (!row_ok[v]) continue;
+    const int gr = grow(row0 + 4 * lq + v);
+    if (p.n_splits == 1) {
+      const float inv = l[v] > 0.f ? 1.f / l[v] : 0.f;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) p.out[(size_t)gr * HD + 16 * d + l16] = f2h(l[v] > 0.f ? o[d][v] * inv : 0.f);
+    } else {
+      float* dst = p.ws + ((size_t)gr * p.n_splits + split) * (2 + HD);
+      if (l16 == 0) {
+        dst[0] = m[v];
+        dst[1] = l[v];
+      }
+#pragma unroll
+      for (int d = 0; d < DT; ++d) dst[2 + 16 * d + l16] = o[d][v];
+    }
+  }
+}
+
+template <int HD>
+int launch_tree_mfma(const AttnParams& p, dim3 grid, hipStream_t s) {
+  switch (p.kv.kv_dtype) {
+    case AXM_KV_FP16:
+      hipLaunchKernelGGL((tree_mfma_kernel<AXM_KV_FP16, HD>), grid, dim3(256), 0, s, p);
+      return 0;
+    case AXM_KV_FP8:
+      hipLaunchKernelGGL((tree_mfma_kernel<AXM_KV_FP8, HD>), grid, dim3(256), 0, s, p);
+      return 0;
+    case AXM_KV_INT4:
+      hipLaunchKernelGGL((tree_mfma_kernel<AXM_KV_INT4, HD>), grid, dim3(256), 0, s, p);
+      return 0;
+  }
+  axm_set_error("tree attention: bad kv dtype %d", p.kv.kv_dtype);
+  return -1;
+}
+
+int tree_choose_splits(int T, int Hq, int Hkv, int n_keys) {
+  // Workgroups of 64 query rows per KV head; splits of >= 64 keys until about
+  // one workgroup per CU.
+  const int rows = T * (Hq / Hkv);
+  const int wgs = Hkv * ((rows + kTreeRows - 1) / kTreeRows);
+  int splits = 1;
+  while (splits < 64 && wgs * splits * 2 <= 256 && n_keys >= 64 * splits * 2) splits *= 2;
+  return splits;
+}
+
 int launch_tree_attention(const f16* q, const KvView& kv, f16* out, int Hq, int T, int prefix_len, int write_pos,
                           const uint64_t* masks_dev, int n_splits, float* ws, hipStream_t s) {
   AttnParams p{};
@@ -678,9 +892,15 @@ int launch_tree_attention(const f16* q, const KvView& kv, f16* out, int Hq, int 
   p.masks = masks_dev;
   p.scale_log2 = kLog2e / sqrtf((float)kv.hd);
   const int rows = T * p.n_rep;
-  const int qr = pick_qr(rows);
-  dim3 grid(kv.Hkv * ((rows + qr - 1) / qr), n_splits, 1);
-  int rc = launch_attn_dispatch<true>(p, qr, grid, s);
+  int rc;
+  if (kv.B == 1 && (kv.hd == 64 || kv.hd == 128)) {
+    const dim3 grid(kv.Hkv, (rows + kTreeRows - 1) / kTreeRows, n_splits);
+    rc = kv.hd == 128 ? launch_tree_mfma<128>(p, grid, s) : launch_tree_mfma<64>(p, grid, s);
+  } else {
+    const int qr = pick_qr(rows);
+    dim3 grid(kv.Hkv * ((rows + qr - 1) / qr), n_splits, 1);
+    rc = launch_attn_dispatch<true>(p, qr, grid, s);
+  }
   if (rc) return rc;
   if (n_splits > 1)
     hipLaunchKernelGGL(attn_reduce_kernel, dim3(T * Hq), dim3(kv.hd), 0, s, ws, out, n_splits, kv.hd);
@@ -697,6 +917,11 @@ static int check_kv(const KvView& kv, const char* who) {
   AXM_CHECK_ARG(kv.kv_dtype == AXM_KV_FP16 || (kv.ks && kv.vs), -1, "%s: quantized cache needs scales", who);
   AXM_CHECK_ARG(kv.B > 0 && kv.Hkv > 0 && kv.S > 0, -1, "%s: bad cache shape", who);
   return 0;
+}
+
+extern "C" int axm_tree_attention_num_splits(int T, int n_head, int n_kv_head, int n_keys) {
+  if (T < 1 || n_kv_head < 1 || n_head < n_kv_head || n_keys < 1) return 1;
+  return tree_choose_splits(T, n_head, n_kv_head, n_keys);
 }
 
 extern "C" size_t axm_attention_workspace_bytes(int B, int n_query_rows_per_batch, int head_dim, int n_splits) {
@@ -744,7 +969,7 @@ extern "C" int axm_gqa_tree_verify(const void* q, const void* k_cache, const voi
   AXM_CHECK_ARG(n_head % n_kv_head == 0, -1, "gqa_tree_verify: n_head %% n_kv_head != 0");
   AXM_CHECK_ARG(prefix_len >= 0 && prefix_len <= max_seq_len, -1, "gqa_tree_verify: bad prefix_len %d", prefix_len);
   AXM_CHECK_ARG(write_pos >= 0 && write_pos < max_seq_len, -1, "gqa_tree_verify: bad write_pos %d", write_pos);
-  if (num_splits <= 0) num_splits = attn_choose_splits(1, n_kv_head * T, prefix_len + T);
+  if (num_splits <= 0) num_splits = tree_choose_splits(T, n_head, n_kv_head, prefix_len + T);
   const size_t need = tree_workspace_bytes(T, n_head, head_dim, num_splits);
   AXM_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace), -1,
                 "gqa_tree_verify: workspace of %zu bytes needed, %zu given", need, workspace_bytes);

@@ -1,0 +1,374 @@
+// Multi-token tile16 GEMM (M <= 16 tokens) for gfx950: the verify / prefill
+// steps of the decode runner and the qmm entry points.
+//
+// The decode GEMV (q4_tile16.hip) fills only 1..4 of the 16 token rows of the
+// v_mfma_f32_16x16x32_f16 A operand; here all 16 rows carry tokens, so every
+// weight chunk (16 rows x 128 k, 1 KB) is read from HBM once for up to 16
+// tokens and the nibble unpack is shared by all of them.  Per chunk and tile a
+// wave issues the same four MFMAs as the GEMV and applies (scale, bias) of the
+// two 64-groups to the four tokens its lanes hold in the D tile.
+//
+// The activations of all 16 token rows for the workgroup's K range are staged
+// in LDS, so K is split across workgroups (grid.y) into ranges of at most
+// kTile16GemmMaxChunks chunks; with more than one range each workgroup writes
+// its fp32 partial tile and t16g_reduce_kernel sums the ranges in order and
+// applies the epilogue.  Activations come in normalized (the runner runs the
+// RMSNorm first, with the same rounding as the GEMV prologue).
+#include "kernels.h"
+#include "q4_tile16.h"
+#include "t16_device.h"
+
+namespace {
+
+constexpr int kGThreads = 512;
+constexpr int kGWaves = kGThreads / 64;
+constexpr int kGTok = kTile16GemmTokens;
+constexpr int kGP = 8;  // chunk loads in flight per wave (ring of register slots)
+constexpr int kGOOB = 0x7FFFFFF0;
+// Staging: (token, 8-element vector) pairs per thread.
+constexpr int kGStagePerThread = kGTok * kTile16GemmMaxChunks * 16 / kGThreads;
+static_assert(kGStagePerThread * kGThreads == kGTok * kTile16GemmMaxChunks * 16, "staging split");
+
+size_t gemm_smem_bytes(int kbps, int NT) {
+  return (size_t)kGTok * kbps * 128 * sizeof(f16) + (size_t)kGTok * 2 * kbps * sizeof(f32x2) +
+         (size_t)kGWaves * NT * 4 * 64 * sizeof(float);
+}
+
+// One output element of the epilogue (identical arithmetic to the GEMV's):
+// v0 the gate / plain accumulator, v1 the up accumulator (SwiGLU).
+template <int EPI>
+__device__ __forceinline__ void t16g_store(const T16Args& a, int tok, int row, float v0, float v1) {
+  if (EPI == Q4_EPI_SWIGLU) {
+    const f16 g = f2h(v0);
+    const f16 u = f2h(v1);
+    const f16 sg = f2h(t16_silu(h2f(g)));
+    a.y[(size_t)tok * a.ldy + row] = f2h(h2f(sg) * h2f(u));
+  } else {
+    f16 h = f2h(v0);
+    if (a.bias != nullptr) h = f2h(h2f(h) + h2f(a.bias[row]));
+    if (EPI == Q4_EPI_STORE) {
+      a.y[(size_t)tok * a.ldy + row] = h;
+    } else {
+      f16* xr = a.resid + (size_t)tok * a.ldr + row;
+      *xr = f2h(h2f(*xr) + h2f(h));
+    }
+  }
+}
+
+template <int NT, int EPI>
+__global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int kbps = a.kb_per_split;
+  const int kbA = blockIdx.y * kbps;                  // first chunk of this K range
+  const int kbN = min(a.KB, kbA + kbps) - kbA;        // chunks in it (>= 1)
+  f16* xs = reinterpret_cast<f16*>(smem);                                      // [16][kbN * 128]
+  f32x2* cx = reinterpret_cast<f32x2*>(xs + (size_t)kGTok * kbps * 128);       // [16][2 kbN]
+  float* red = reinterpret_cast<float*>(cx + (size_t)kGTok * 2 * kbps);        // [waves][NT][4][64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int S = a.split;
+  const int upw = kGWaves / S;
+  const int sub = wave % S;
+  const int slot = wave / S;
+  const int per = (kbN + S - 1) / S;
+  const int c0 = sub * per;                    // chunk offset of this wave within the range
+  const int my = max(0, min(per, kbN - c0));   // chunks of this wave
+  const int unit = blockIdx.x * upw + slot;
+  const int kq = lane >> 4;
+  const Unpack U{to_vgpr(a.unpack[0]), to_vgpr(a.unpack[1]), a.unpack[2], a.unpack[3]};
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w16, (short)0, (int)a.w16_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.sb16, (short)0, (int)a.sb16_bytes, 0x00020000);
+
+  u32x4 wr[kGP][NT];
+  u32x2 sr[kGP][NT];
+  auto load = [&](int ci, int j) {
+    const bool ok = unit < a.n_units && ci < my;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int base = (unit + t * a.pair_offset) * a.KB + kbA + c0 + ci;
+      const int wo = ok ? (base * 64 + lane) * 16 : kGOOB;
+      const int so = ok ? (base * 16 + (lane & 15)) * 8 : kGOOB;
+      wr[j][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
+      sr[j][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+    }
+  };
+  // The first weight chunks go out before the activation loads: both are one
+  // memory latency away and the activations are needed first only after the
+  // staging barrier.
+#pragma unroll
+  for (int j = 0; j < kGP; ++j) load(j, j);
+
+  // Stage x[0..15][kbA*128 .. +kbN*128) (tokens >= M and k >= K as zeros) and
+  // per 64-group the magic-offset-weighted and plain sums.  Pair p of thread
+  // tid is (token p / nvec, vector p % nvec); nvec is a multiple of 8, so the
+  // eight vectors of a group sit in eight consecutive lanes of one wave.
+  const int nvec = kbN * 16;
+  f16x8 xv[kGStagePerThread];
+#pragma unroll
+  for (int i = 0; i < kGStagePerThread; ++i) {
+    const int p = tid + i * kGThreads;
+    const int tok = p / nvec, v = p - tok * nvec;
+    const int k = kbA * 128 + 8 * v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv[i][e] = f16(0);
+    if (tok < a.M_tokens && k < a.K) xv[i] = *reinterpret_cast<const f16x8*>(a.x + (size_t)tok * a.ldx + k);
+  }
+#pragma unroll
+  for (int i = 0; i < kGStagePerThread; ++i) {
+    const int p = tid + i * kGThreads;
+    if (p >= kGTok * nvec) break;  // whole waves (nvec * 16 is a multiple of 64)
+    const int tok = p / nvec, v = p - tok * nvec;
+    float corr = 0.f, sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = h2f(xv[i][e]);
+      sum += f;
+      corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
+    }
+    corr = group_sum<8>(corr);
+    sum = group_sum<8>(sum);
+    *reinterpret_cast<f16x8*>(xs + (size_t)tok * kbN * 128 + 8 * v) = xv[i];
+    if ((tid & 7) == 0) cx[(size_t)tok * 2 * kbN + (v >> 3)] = f32x2{corr, sum};
+  }
+  __syncthreads();
+
+  // A operand: token lane % 16 (rows past M are zeros), k sub-block lane / 16.
+  const f16* xa = xs + (size_t)(lane & 15) * kbN * 128 + 8 * kq;
+  float acc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int vi = 0; vi < 4; ++vi) acc[t][vi] = 0.f;
+
+  for (int ci0 = 0; ci0 < my; ci0 += kGP) {
+#pragma unroll
+    for (int jj = 0; jj < kGP; ++jj) {
+      const int ci = ci0 + jj;
+      if (ci >= my) break;  // wave-uniform
+      const int kb = c0 + ci;  // chunk within the staged range
+      const f16* xk = xa + kb * 128;
+      f16x8 A[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) A[c] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * c));
+      f32x4 cxv[4];
+#pragma unroll
+      for (int vi = 0; vi < 4; ++vi)
+        cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (size_t)(4 * kq + vi) * 2 * kbN + 2 * kb);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+        f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], unpack_word(wr[jj][t][0], U), z4, 0, 0, 0);
+        f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], unpack_word(wr[jj][t][2], U), z4, 0, 0, 0);
+        d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], unpack_word(wr[jj][t][1], U), d0, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], unpack_word(wr[jj][t][3], U), d1, 0, 0, 0);
+        const f16x2 sb0 = as_h2(sr[jj][t][0]);
+        const f16x2 sb1 = as_h2(sr[jj][t][1]);
+#pragma unroll
+        for (int vi = 0; vi < 4; ++vi) {
+          float r = acc[t][vi];
+          r = __builtin_fmaf(h2f(sb0.x), d0[vi] - cxv[vi][0], r);
+          r = __builtin_fmaf(h2f(sb0.y), cxv[vi][1], r);
+          r = __builtin_fmaf(h2f(sb1.x), d1[vi] - cxv[vi][2], r);
+          r = __builtin_fmaf(h2f(sb1.y), cxv[vi][3], r);
+          acc[t][vi] = r;
+        }
+      }
+      load(ci + kGP, jj);
+    }
+  }
+
+  // Sum the S partial tiles of a unit in wave order.
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int vi = 0; vi < 4; ++vi) red[((wave * NT + t) * 4 + vi) * 64 + lane] = acc[t][vi];
+  __syncthreads();
+  if (sub != 0 || unit >= a.n_units) return;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int vi = 0; vi < 4; ++vi) {
+      float s = 0.f;
+      for (int w = wave; w < wave + S; ++w) s += red[((w * NT + t) * 4 + vi) * 64 + lane];
+      acc[t][vi] = s;
+    }
+  const int j = lane & 15;
+  if (gridDim.y == 1) {
+    const int row = unit * 16 + j;
+#pragma unroll
+    for (int vi = 0; vi < 4; ++vi) {
+      const int tok = 4 * kq + vi;
+      if (tok < a.M_tokens && row < a.N) t16g_store<EPI>(a, tok, row, acc[0][vi], acc[NT - 1][vi]);
+    }
+  } else {
+    // Partial tile of this K range: [split][token][column], column = tile * 16 + row in tile.
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int col = (unit + t * a.pair_offset) * 16 + j;
+#pragma unroll
+      for (int vi = 0; vi < 4; ++vi)
+        a.part_ws[((size_t)blockIdx.y * kGTok + 4 * kq + vi) * a.part_cols + col] = acc[t][vi];
+    }
+  }
+}
+
+// Sums the K-range partials in range order and applies the epilogue: one thread
+// per (token, output row).
+template <int EPI>
+__global__ void t16g_reduce_kernel(T16Args a, int n_splits, int up_col) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int tok = (int)(idx / a.N), row = (int)(idx % a.N);
+  if (tok >= a.M_tokens) return;
+  float v0 = 0.f, v1 = 0.f;
+  for (int sp = 0; sp < n_splits; ++sp) {
+    const float* p = a.part_ws + ((size_t)sp * kGTok + tok) * a.part_cols;
+    v0 += p[row];
+    if (EPI == Q4_EPI_SWIGLU) v1 += p[up_col + row];
+  }
+  t16g_store<EPI>(a, tok, row, v0, v1);
+}
+
+template <int NT, int EPI>
+void t16g_attr(size_t smem) {
+  static size_t set = 0;
+  if (smem <= set) return;
+  if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)smem) == hipSuccess)
+    set = smem;
+  else
+    (void)hipGetLastError();
+}
+
+int gemm_splits(int KB) { return (KB + kTile16GemmMaxChunks - 1) / kTile16GemmMaxChunks; }
+
+}  // namespace
+
+size_t t16_gemm16_ws_bytes(int K, int n_units, int NT) {
+  const int KB = (K + 127) / 128;
+  const int splits = gemm_splits(KB);
+  return splits <= 1 ? 0 : (size_t)splits * kGTok * n_units * 16 * NT * sizeof(float);
+}
+
+int t16_gemm16_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s) {
+  if (M < 1 || M > kGTok || a.ln_w != nullptr || a.argmax_keys != nullptr || a.x_parts != nullptr ||
+      (epi != Q4_EPI_STORE && epi != Q4_EPI_RESID && epi != Q4_EPI_SWIGLU) || a.K <= 0 || a.K % 64 != 0) {
+    axm_set_error("tile16 gemm: M=%d (1..%d), epi=%d, K=%d unsupported (normalized activations, store / "
+                  "residual / SwiGLU epilogues)", M, kGTok, epi, a.K);
+    return -2;
+  }
+  const int NT = epi == Q4_EPI_SWIGLU ? 2 : 1;
+  a.KB = (a.K + 127) / 128;
+  const int splits = gemm_splits(a.KB);
+  const int kbps = (a.KB + splits - 1) / splits;
+  const size_t need = t16_gemm16_ws_bytes(a.K, a.n_units, NT);
+  if (need > 0 && (ws == nullptr || ws_bytes < need)) {
+    axm_set_error("tile16 gemm: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    return -1;
+  }
+  // Waves per unit: about 8 waves per CU over all K ranges, >= 2 chunks per wave.
+  const int cus = axm_num_cus();
+  int S = 1;
+  while (S < kGWaves && a.n_units * S * splits < 8 * cus && kbps >= 4 * S) S *= 2;
+  a.split = S;
+  a.M_tokens = M;
+  a.kb_per_split = kbps;
+  a.part_ws = ws;
+  a.part_cols = a.n_units * 16 * NT;
+  a.w16_bytes = t16_weight_bytes(a.N_rows_alloc, a.K);
+  a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K);
+  a.unpack[0] = 0x000F000Fu;
+  a.unpack[1] = 0x00F000F0u;
+  a.unpack[2] = 0x64006400u;
+  a.unpack[3] = 0x54005400u;
+  const int upw = kGWaves / S;
+  const dim3 grid((a.n_units + upw - 1) / upw, splits);
+  const size_t smem = gemm_smem_bytes(kbps, NT);
+  switch (epi) {
+    case Q4_EPI_STORE:
+      t16g_attr<1, Q4_EPI_STORE>(smem);
+      hipLaunchKernelGGL((t16g_kernel<1, Q4_EPI_STORE>), grid, dim3(kGThreads), smem, s, a);
+      break;
+    case Q4_EPI_RESID:
+      t16g_attr<1, Q4_EPI_RESID>(smem);
+      hipLaunchKernelGGL((t16g_kernel<1, Q4_EPI_RESID>), grid, dim3(kGThreads), smem, s, a);
+      break;
+    default:
+      t16g_attr<2, Q4_EPI_SWIGLU>(smem);
+      hipLaunchKernelGGL((t16g_kernel<2, Q4_EPI_SWIGLU>), grid, dim3(kGThreads), smem, s, a);
+      break;
+  }
+  if (splits > 1) {
+    const long n = (long)M * a.N;
+    const dim3 rg((unsigned)((n + 255) / 256));
+    const int up_col = a.pair_offset * 16;
+    if (epi == Q4_EPI_STORE)
+      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_STORE>, rg, dim3(256), 0, s, a, splits, up_col);
+    else if (epi == Q4_EPI_RESID)
+      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_RESID>, rg, dim3(256), 0, s, a, splits, up_col);
+    else
+      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_SWIGLU>, rg, dim3(256), 0, s, a, splits, up_col);
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI: multi-token GEMM on tile16 copies (16 tokens per weight pass).
+// ---------------------------------------------------------------------------
+extern "C" size_t axm_qmm_q4_tile16_workspace_bytes(int K, int N, int swiglu) {
+  if (K <= 0 || N <= 0) return 0;
+  return t16_gemm16_ws_bytes(K, (N + 15) / 16, swiglu ? 2 : 1);
+}
+
+static int qmm_tile16_rows(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
+                           int N, int epi, void* ws, size_t ws_bytes, hipStream_t s) {
+  for (int m0 = 0; m0 < M; m0 += kTile16GemmTokens) {
+    const int mc = (M - m0) < kTile16GemmTokens ? (M - m0) : kTile16GemmTokens;
+    T16Args a{};
+    a.x = (const f16*)x + (size_t)m0 * K;
+    a.ldx = K;
+    a.w16 = (const u32x4*)w16;
+    a.sb16 = (const u32x2*)sb16;
+    a.K = K;
+    a.N = N;
+    a.n_units = (N + 15) / 16;
+    if (epi == Q4_EPI_SWIGLU) {
+      a.N_rows_alloc = 2 * N;
+      a.pair_offset = N / 16;
+    } else {
+      a.N_rows_alloc = N;
+    }
+    a.y = (f16*)y + (size_t)m0 * N;
+    a.ldy = N;
+    a.bias = (const f16*)bias;
+    const int rc = t16_gemm16_launch(a, mc, epi, (float*)ws, ws_bytes, s);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+extern "C" int axm_qmm_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M,
+                                 int K, int N, void* workspace, size_t workspace_bytes, void* stream) {
+  AXM_CHECK_ARG(x && w16 && sb16 && y, -1, "qmm_q4_tile16: null pointer");
+  AXM_CHECK_ARG(K > 0 && K % 64 == 0 && N > 0 && M >= 1, -1, "qmm_q4_tile16: bad shape M=%d K=%d N=%d", M, K, N);
+  const int rc = qmm_tile16_rows(x, w16, sb16, bias, y, M, K, N, Q4_EPI_STORE, workspace, workspace_bytes,
+                                 (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("qmm_q4_tile16");
+  return 0;
+}
+
+extern "C" int axm_qmm_q4_tile16_swiglu(const void* x_normed, const void* gu16, const void* gusb16, void* y, int M,
+                                        int K, int H, void* workspace, size_t workspace_bytes, void* stream) {
+  AXM_CHECK_ARG(x_normed && gu16 && gusb16 && y, -1, "qmm_q4_tile16_swiglu: null pointer");
+  AXM_CHECK_ARG(K > 0 && K % 64 == 0 && H > 0 && H % 16 == 0 && M >= 1, -1,
+                "qmm_q4_tile16_swiglu: bad shape M=%d K=%d H=%d (H %% 16 == 0)", M, K, H);
+  const int rc = qmm_tile16_rows(x_normed, gu16, gusb16, nullptr, y, M, K, H, Q4_EPI_SWIGLU, workspace,
+                                 workspace_bytes, (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("qmm_q4_tile16_swiglu");
+  return 0;
+}

@@ -491,6 +491,39 @@ struct axm_runner {
 
   // GEMV over T token rows in launches of at most 4 rows.
   int gemv_rows(const Mat& m, int epi, int out_rows, GemvCall c, int T, hipStream_t s) {
+    if (m.w16 != nullptr && T > 4 && c.argmax_keys == nullptr && c.q_dim == 0 &&
+        (epi == Q4_EPI_STORE || epi == Q4_EPI_RESID || epi == Q4_EPI_SWIGLU)) {
+      // Multi-token GEMM: 16 tokens per weight pass, activations normalized first
+      // (into x_norm_out when the caller wants them, else into the norm scratch).
+      for (int t0 = 0; t0 < T; t0 += kTile16GemmTokens) {
+        const int mc = (T - t0) < kTile16GemmTokens ? (T - t0) : kTile16GemmTokens;
+        const f16* xin = c.x + (size_t)t0 * c.ldx;
+        if (c.ln_w != nullptr) {
+          f16* nrm = (c.x_norm_out ? c.x_norm_out : norm) + (size_t)t0 * c.ldx;
+          launch_rmsnorm(xin, c.ln_w, nrm, mc, m.K, c.eps, s);
+          xin = nrm;
+        }
+        T16Args a{};
+        a.x = xin;
+        a.ldx = c.ldx;
+        a.w16 = (const u32x4*)m.w16;
+        a.sb16 = (const u32x2*)m.sb16;
+        a.K = m.K;
+        a.KB = (m.K + 127) / 128;
+        a.N = out_rows;
+        a.N_rows_alloc = m.N;
+        a.n_units = (out_rows + 15) / 16;
+        a.pair_offset = c.pair_rows / 16;
+        a.y = c.y ? c.y + (size_t)t0 * c.ldy : nullptr;
+        a.ldy = c.ldy;
+        a.bias = c.bias;
+        a.resid = c.resid ? c.resid + (size_t)t0 * c.ldr : nullptr;
+        a.ldr = c.ldr;
+        const int rc = t16_gemm16_launch(a, mc, epi, ws, ws_bytes, s);
+        if (rc) return rc;
+      }
+      return 0;
+    }
     for (int t0 = 0; t0 < T; t0 += 4) {
       const int mc = (T - t0) < 4 ? (T - t0) : 4;
       GemvCall cc = c;
@@ -531,7 +564,7 @@ struct axm_runner {
                          tree_pos, q, kvst);
       launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, T, write_pos, nullptr, s);
       if (tree) {
-        const int splits = attn_choose_splits(T, d.n_kv_head, prefix + T);
+        const int splits = tree_choose_splits(T, d.n_head, d.n_kv_head, prefix + T);
         rc = launch_tree_attention(q, kv, attn_y, d.n_head, T, prefix, write_pos, (const uint64_t*)tree_mask, splits, ws,
                                    s);
       } else {
@@ -682,6 +715,15 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
   r->qkv_dim = r->q_dim + 2 * r->kv_dim;
   const int T = r->d.max_tokens;
   r->ws_bytes = attn_workspace_bytes(T, d.n_head, d.head_dim, r->max_splits);
+  if (r->m_o.size() == (size_t)L && r->m_o[0].w16 != nullptr) {
+    // Partial tiles of the multi-token GEMM share the attention workspace.
+    const size_t g[] = {t16_gemm16_ws_bytes(d.d_model, r->qkv_dim / 16 + ((r->qkv_dim % 16) != 0), 1),
+                        t16_gemm16_ws_bytes(r->q_dim, (d.d_model + 15) / 16, 1),
+                        t16_gemm16_ws_bytes(d.d_model, d.hidden_dim / 16, 2),
+                        t16_gemm16_ws_bytes(d.hidden_dim, (d.d_model + 15) / 16, 1),
+                        t16_gemm16_ws_bytes(d.d_model, (d.vocab_size + 15) / 16, 1)};
+    for (size_t b : g) r->ws_bytes = b > r->ws_bytes ? b : r->ws_bytes;
+  }
   struct {
     void** p;
     size_t bytes;

@@ -32,6 +32,7 @@ from .quant import (  # noqa: F401
     pack_linear_q8_g64,
     pack_linear_ternary,
     qmm_q4_marlin,
+    qmm_q4_tile16,
     qmm_q8_g64,
     qmv_q4_marlin,
     qmv_q8_g64,

@@ -245,8 +245,8 @@ def gqa_tree_verify_mps(
         qc = q.reshape(T, n_head, head_dim).contiguous()
     qc = qc.to(torch.float16)
     masks = _masks_tensor(tree_mask, T, q.device)
-    splits = int(num_splits) if num_splits and num_splits > 0 else _lib.lib().axm_attention_num_splits(
-        1, Hkv * T, int(prefix_len) + T)
+    splits = int(num_splits) if num_splits and num_splits > 0 else _lib.lib().axm_tree_attention_num_splits(
+        T, n_head, Hkv, int(prefix_len) + T)
     ws_bytes = _lib.lib().axm_attention_workspace_bytes(T, n_head, head_dim, splits)
     ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=q.device) if ws_bytes else None
     out = torch.empty_like(qc)

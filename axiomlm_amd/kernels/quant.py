@@ -154,18 +154,36 @@ def repack_q4_marlin_tile16(w_marlin, sb_marlin, N: int, K: int) -> tuple[torch.
     return w16, sb16
 
 
+def _qmm_workspace(K: int, N: int, swiglu: bool, device):
+    n = _lib.lib().axm_qmm_q4_tile16_workspace_bytes(K, N, int(swiglu))
+    return (torch.empty(n, dtype=torch.uint8, device=device) if n else None), n
+
+
 def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
-    """y = x @ W^T (+ bias) on a tile16 copy made by :func:`repack_q4_marlin_tile16`."""
+    """y = x @ W^T (+ bias) on a tile16 copy made by :func:`repack_q4_marlin_tile16`: the
+    decode GEMV for up to 4 rows, the multi-token GEMM (16 rows per weight pass) beyond."""
     _lib.require_gpu(x, "qmv_q4_tile16")
     K = x.size(-1)
     M = x.numel() // K
     N = int(out_features)
     y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
     b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
-    _lib.check(_lib.lib().axm_qmv_q4_tile16(_lib.ptr(x.contiguous()), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b),
-                                            _lib.ptr(y), M, K, N, _lib.stream_of(x.device)),
-               "qmv_q4_tile16")
+    xc = x.contiguous()
+    if M <= 4:
+        _lib.check(_lib.lib().axm_qmv_q4_tile16(_lib.ptr(xc), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b),
+                                                _lib.ptr(y), M, K, N, _lib.stream_of(x.device)),
+                   "qmv_q4_tile16")
+        return y
+    ws, n = _qmm_workspace(K, N, False, x.device)
+    _lib.check(_lib.lib().axm_qmm_q4_tile16(_lib.ptr(xc), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b), _lib.ptr(y),
+                                            M, K, N, _lib.ptr(ws), n, _lib.stream_of(x.device)),
+               "qmm_q4_tile16")
     return y
+
+
+def qmm_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
+    """Multi-token form of :func:`qmv_q4_tile16` (the qmm_q4_marlin role, quant.py:664-684)."""
+    return qmv_q4_tile16(x, w16, sb16, out_features, bias)
 
 
 def _swiglu_call(fn, name, x, ln_w, eps, w, sb, H):
@@ -188,8 +206,26 @@ def qmv_q4_marlin_swiglu(x, ln_w, eps: float, gu_w, gu_sb, H: int) -> torch.Tens
 
 
 def qmv_q4_tile16_swiglu(x, ln_w, eps: float, gu16, gusb16, H: int) -> torch.Tensor:
-    """:func:`qmv_q4_marlin_swiglu` on the tile16 copy of the packed [W_gate; W_up] (H % 16 == 0)."""
-    return _swiglu_call(_lib.lib().axm_qmv_q4_tile16_swiglu, "qmv_q4_tile16_swiglu", x, ln_w, eps, gu16, gusb16, H)
+    """:func:`qmv_q4_marlin_swiglu` on the tile16 copy of the packed [W_gate; W_up] (H % 16 == 0);
+    more than 4 rows are normalized first and go through the multi-token GEMM."""
+    K = x.size(-1)
+    M = x.numel() // K
+    if M <= 4:
+        return _swiglu_call(_lib.lib().axm_qmv_q4_tile16_swiglu, "qmv_q4_tile16_swiglu", x, ln_w, eps, gu16, gusb16,
+                            H)
+    from .ops import fused_rmsnorm
+
+    _lib.require_gpu(x, "qmv_q4_tile16_swiglu")
+    if x.dtype != torch.float16:
+        raise RuntimeError("qmv_q4_tile16_swiglu: x must be float16")
+    xn = (fused_rmsnorm(x.reshape(M, K), ln_w, eps) if ln_w is not None else x.reshape(M, K)).contiguous()
+    y = torch.empty((*x.shape[:-1], int(H)), dtype=torch.float16, device=x.device)
+    ws, n = _qmm_workspace(K, int(H), True, x.device)
+    _lib.check(_lib.lib().axm_qmm_q4_tile16_swiglu(_lib.ptr(xn), _lib.ptr(gu16.contiguous()),
+                                                   _lib.ptr(gusb16.contiguous()), _lib.ptr(y), M, K, int(H),
+                                                   _lib.ptr(ws), n, _lib.stream_of(x.device)),
+               "qmm_q4_tile16_swiglu")
+    return y
 
 
 # ---------------------------------------------------------------------------

@@ -1,0 +1,273 @@
+"""Measurements of the BASELINE configurations other than the headline decode line.
+
+`bench.py` prints the one JSON line the driver reads (Q4 7B-shape decode tok/s).
+This script measures the remaining configurations on one MI355X, one JSON line
+per case, each against the HBM roofline (8 TB/s) with its algorithmic bytes:
+
+  c2  single decoder layer at Llama-7B shapes (RMSNorm, QKV, O, gate/up + SwiGLU,
+      down; MARLIN Q4 G64 re-tiled for the matrix cores) at M = 1, 4, 16 tokens
+  c3  split-K decode attention, B 8, 32 query / 8 KV heads, hd 128, INT4 and FP8
+      KV at 1k / 8k / 32k keys, and the 4096-slot ring buffer after 10k tokens
+  c4  BitNet ternary and affine 2-bit GEMVs at the FFN shapes (4096 -> 11008,
+      11008 -> 4096), batch 1
+  c5  speculative tree verification, 7B shape, FP8 KV, prefix 2048, a 64-node
+      tree (depth 6, branching 4,4,2,2,1,1): one runner.verify_tree_step
+
+Kernels are timed from a captured HIP graph of back-to-back calls (no host
+launch gaps), rotating over enough weight / cache copies that the stream does
+not sit in the 256 MB last-level cache.  Weights are random-init N(0, 0.02),
+activations and KV N(0, 1).
+
+    python bench_configs.py [c2 c3 c4 c5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+
+import bench
+
+HBM_PEAK_GBS = bench.HBM_PEAK_GBS
+MFMA_PEAK_F16_TFLOPS = 2500.0
+COLD_POOL_BYTES = 600 << 20  # > 2x the 256 MB last-level cache
+
+
+def _graph_time_us(fn, n_calls: int, replays: int = 5) -> float:
+    """Average device time of fn(i) over n_calls calls captured in one graph."""
+    import torch
+
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_calls):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / (replays * n_calls)
+
+
+def _line(config, case, avg_us, nbytes, extra=None):
+    gbs = nbytes / (avg_us * 1e-6) / 1e9
+    out = {"config": config, "case": case, "avg_us": round(avg_us, 3), "algorithmic_bytes": int(nbytes),
+           "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if extra:
+        out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+def run_c2(dev):
+    import torch
+
+    from axiomlm_amd.kernels import (fused_rmsnorm, pack_linear_q4_marlin, qmv_q4_tile16, qmv_q4_tile16_swiglu,
+                                     repack_q4_marlin_tile16)
+
+    c = bench.CFG_7B
+    d, H = c["d"], c["hidden"]
+    qkv_rows = (c["n_head"] + 2 * c["n_kv_head"]) * c["hd"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+
+    def packed(n, k):
+        w = (torch.randn(n, k, generator=g, device=dev) * 0.02).half()
+        p, s = pack_linear_q4_marlin(w, clip_search=False)
+        return repack_q4_marlin_tile16(p, s, n, k)
+
+    layer_bytes = bench.layer_weight_bytes(c)
+    n_copies = max(2, COLD_POOL_BYTES // layer_bytes + 1)
+    layers = [dict(qkv=packed(qkv_rows, d), o=packed(d, d), gu=packed(2 * H, d), dn=packed(d, H),
+                   ln1=(1 + 0.1 * torch.randn(d, generator=g, device=dev)).half(),
+                   ln2=(1 + 0.1 * torch.randn(d, generator=g, device=dev)).half()) for _ in range(n_copies)]
+    for M in (1, 4, 16):
+        x = torch.randn(M, d, generator=g, device=dev).half()
+
+        def layer(i):
+            L = layers[i % n_copies]
+            xn = fused_rmsnorm(x, L["ln1"], 1e-5)
+            q = qmv_q4_tile16(xn, *L["qkv"], qkv_rows)
+            o = qmv_q4_tile16(q[:, :d].contiguous(), *L["o"], d)
+            h = qmv_q4_tile16_swiglu(x + o, L["ln2"], 1e-5, *L["gu"], H)
+            return qmv_q4_tile16(h, *L["dn"], d)
+
+        us = _graph_time_us(layer, 2 * n_copies)
+        nbytes = layer_bytes + M * (d + qkv_rows + d + d + d + 2 * H + H + d) * 2
+        _line("C2", f"layer M={M}", us, nbytes, {"tokens_per_s_per_layer": round(M / (us * 1e-6), 1),
+                                                 "weight_copies": n_copies})
+
+
+def run_c3(dev):
+    import torch
+
+    from axiomlm_amd.kernels import gqa_flash_decode_mps, quantize_kv_fp8, quantize_kv_int4
+
+    B, Hq, Hkv, hd = 8, 32, 8, 128
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    per_key = {"int4": 136, "fp8": 264}
+    cases = [(L, L) for L in (1024, 8192, 32768)] + [(4096, "ring")]
+    for kind in ("int4", "fp8"):
+        quant = quantize_kv_int4 if kind == "int4" else quantize_kv_fp8
+        for L, label in cases:
+            nbytes = B * Hkv * L * per_key[kind] + 2 * B * Hq * hd * 2
+            n_copies = max(1, min(16, COLD_POOL_BYTES // (B * Hkv * L * per_key[kind]) + 1))
+            caches = []
+            for _ in range(n_copies):
+                k = torch.randn(B, Hkv, L, hd, generator=g, device=dev).half()
+                v = torch.randn(B, Hkv, L, hd, generator=g, device=dev).half()
+                kc, ks, vc, vs = quant(k, v)
+                del k, v
+                caches.append((kc, vc, ks, vs))
+            q = torch.randn(B, Hq, 1, hd, generator=g, device=dev).half()
+
+            def attn(i):
+                kc, vc, ks, vs = caches[i % n_copies]
+                return gqa_flash_decode_mps(q, kc, vc, L, 0, ks, vs, kind)
+
+            us = _graph_time_us(attn, max(8, 2 * n_copies))
+            case = f"{kind} L={L}" if label != "ring" else f"{kind} ring S=4096 after 10k tokens (all slots valid)"
+            _line("C3", case, us, nbytes, {"cache_copies": n_copies})
+            del caches
+            torch.cuda.empty_cache()
+
+
+def run_c4(dev):
+    import torch
+
+    from axiomlm_amd.kernels import pack_linear_q2_k, pack_linear_ternary, qmv_q2_k, qmv_ternary
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    for fmt in ("ternary", "q2"):
+        for N, K in ((11008, 4096), (4096, 11008)):
+            if fmt == "ternary":
+                codes = torch.multinomial(torch.tensor([0.25, 0.5, 0.25], device=dev), N * K, replacement=True,
+                                          generator=g).view(N, K).to(torch.float16) - 1
+                w = codes * 0.02
+                packs = [pack_linear_ternary(w) for _ in range(1)]
+                fn, per_w = qmv_ternary, 0.28125
+            else:
+                w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+                packs = [pack_linear_q2_k(w) for _ in range(1)]
+                fn, per_w = qmv_q2_k, 0.3125
+            wb = int(N * K * per_w)
+            n_copies = max(2, COLD_POOL_BYTES // wb + 1)
+            packs = [tuple(t.clone() for t in packs[0]) for _ in range(n_copies)]
+            x = torch.randn(1, K, generator=g, device=dev).half()
+
+            def gemv(i):
+                p, s = packs[i % n_copies]
+                return fn(x, p, s)
+
+            us = _graph_time_us(gemv, 2 * n_copies)
+            _line("C4", f"{fmt} {K}->{N} M=1", us, wb + (K + N) * 2, {"weight_copies": n_copies})
+            del packs
+            torch.cuda.empty_cache()
+
+
+def run_c5(dev):
+    import torch
+
+    from axiomlm_amd.cache import StaticKVCache
+    from axiomlm_amd.kernels import pack_linear_q4_marlin, pack_linear_q8_g64, quantize_kv_fp8
+    from axiomlm_amd.runner import QuantizedDecodeRunner
+    from axiomlm_amd.tree import build_branching_tree
+
+    c = bench.CFG_7B
+    d, H, L, hd = c["d"], c["hidden"], c["n_layer"], c["hd"]
+    prefix, S, T = 2048, 2048 + 128, 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+
+    def randn(*shape, std=0.02):
+        return (torch.randn(*shape, generator=g, device=dev) * std).half()
+
+    def q4(n, k):
+        return pack_linear_q4_marlin(randn(n, k), clip_search=False)
+
+    qkv_rows = (c["n_head"] + 2 * c["n_kv_head"]) * hd
+    lay = {k: [] for k in ("ln1", "ln2", "qkv", "o", "gu", "dn")}
+    for _ in range(L):
+        lay["ln1"].append((1 + randn(d, std=0.1).float()).half())
+        lay["ln2"].append((1 + randn(d, std=0.1).float()).half())
+        lay["qkv"].append(q4(qkv_rows, d))
+        lay["o"].append(q4(d, d))
+        lay["gu"].append(q4(2 * H, d))
+        lay["dn"].append(q4(d, H))
+    lmh_p, lmh_s = q4(c["vocab"], d)
+    wte_p, wte_s = pack_linear_q8_g64(randn(c["vocab"], d))
+    lnf = (1 + randn(d, std=0.1).float()).half()
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    fr = torch.outer(torch.arange(4 * S, dtype=torch.float32), inv)
+    freqs = torch.stack([fr.cos(), fr.sin()], dim=-1).to(dev)
+    cache = StaticKVCache(1, S, L, c["n_kv_head"], hd, device=dev, cache_dtype="fp8")
+    for li in range(L):
+        k = torch.randn(1, c["n_kv_head"], S, hd, generator=g, device=dev).half()
+        v = torch.randn(1, c["n_kv_head"], S, hd, generator=g, device=dev).half()
+        kc, ks, vc, vs = quantize_kv_fp8(k, v)
+        cache.cache[li, 0].copy_(kc)
+        cache.cache[li, 1].copy_(vc)
+        cache.scales[li, 0].copy_(ks)
+        cache.scales[li, 1].copy_(vs)
+    runner = QuantizedDecodeRunner(
+        None, lmh_p, lmh_s, freqs, lay["ln1"], [p for p, _ in lay["qkv"]], [s for _, s in lay["qkv"]],
+        [p for p, _ in lay["o"]], [s for _, s in lay["o"]], lay["ln2"], [p for p, _ in lay["gu"]],
+        [s for _, s in lay["gu"]], [p for p, _ in lay["dn"]], [s for _, s in lay["dn"]], lnf, cache.k_caches,
+        cache.v_caches, c["n_head"], c["n_kv_head"], hd, True, 1e-5, [], c["vocab"], wte_p=wte_p, wte_s=wte_s,
+        k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype="fp8", max_tokens=T)
+    tree = build_branching_tree([4, 4, 2, 2, 1, 1], max_nodes=T)
+    assert tree["num_nodes"] == T
+    toks = torch.randint(0, c["vocab"], (1, T), generator=g, device=dev)
+    depths, masks = tree["tree_depths"], tree["tree_mask"]
+
+    def verify():
+        return runner.verify_tree_step(toks, prefix, prefix, prefix, depths, masks)
+
+    for _ in range(3):
+        verify()
+    torch.cuda.synchronize()
+    reps = 10
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        verify()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / reps
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    w_bytes = L * bench.layer_weight_bytes(c) + bench.q4_bytes(c["vocab"], d)
+    kv_bytes = L * 2 * c["n_kv_head"] * (prefix + T) * (hd + 2 * (hd // 64))
+    flops = 2.0 * T * (L * (qkv_rows * d + d * d + 2 * H * d + d * H) + c["vocab"] * d)
+    _line("C5", f"verify_tree_step T={T} prefix={prefix} fp8 KV", us, w_bytes + kv_bytes,
+          {"mfma_frac_f16": round(flops / (us * 1e-6) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4),
+           "tree_nodes_per_s": round(T / (us * 1e-6), 1), "host_wall_us": round(wall * 1e6, 1)})
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("configs", nargs="*", default=["c2", "c3", "c4", "c5"])
+    args = ap.parse_args()
+    import torch
+
+    dev = torch.device("cuda", 0)
+    runs = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}
+    for name in args.configs:
+        if name not in runs:
+            sys.exit(f"unknown config {name!r}; choose from {sorted(runs)}")
+        print(f"[bench_configs] {name}", file=sys.stderr, flush=True)
+        runs[name](dev)
+        torch.cuda.empty_cache()
+
+
+if __name__ == "__main__":
+    main()

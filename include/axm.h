@@ -55,6 +55,19 @@ int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb16, const vo
  * H % 16 == 0): the runner's MLP-input launch (transformer.py:1178-1189). */
 int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const void* gu16, const void* gusb16,
                              void* y, int M, int K, int H, void* stream);
+/* Multi-token GEMM on the tile16 copy: y[M][N] = x @ W^T (+ bias) with every weight
+ * chunk streamed once per 16 tokens (the M > 8 path of qmm_q4_marlin_mps: kernels
+ * qmm_q4_marlin_m8_apple_kernel / qmm_q4_marlin_apple_kernel, metal_kernels.metal:
+ * 2268-2684; dispatch mps_kernels.mm:1272-1312; CPU form quant.py:664-684).  K is
+ * split across workgroups; `workspace` holds the fp32 partial tiles
+ * (axm_qmm_q4_tile16_workspace_bytes; 0 bytes when K <= 2048). */
+size_t axm_qmm_q4_tile16_workspace_bytes(int K, int N, int swiglu);
+int axm_qmm_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
+                      int N, void* workspace, size_t workspace_bytes, void* stream);
+/* silu(g) * u over the tile16 [W_gate; W_up] copy for M tokens whose activations are
+ * already RMS-normalized (the multi-token MLP input, transformer.py:1178-1189). */
+int axm_qmm_q4_tile16_swiglu(const void* x_normed, const void* gu16, const void* gusb16, void* y, int M, int K,
+                             int H, void* workspace, size_t workspace_bytes, void* stream);
 /* Row-major fp16 [N][K] dequantization (axiomlm/kernels/quant.py:597-634). */
 int axm_dequantize_q4_marlin(const void* w_marlin, const void* sb_marlin, void* out, int K, int N, void* stream);
 /* Round-to-nearest packer, clip_search=False (axiomlm/kernels/quant.py:447-494, 573-593).
@@ -164,9 +177,14 @@ int axm_gqa_flash_decode(const void* q, const void* k_cache, const void* v_cache
                          int head_dim, int max_seq_len, int active_len, int num_splits, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* Key splits the tree-verification attention picks for num_splits <= 0 (T nodes,
+ * n_keys = prefix_len + T); the split heuristic of gqa_tree_verify_*_mps
+ * (mps_kernels.mm:1508-1631) re-derived for 64-row matrix-core workgroups. */
+int axm_tree_attention_num_splits(int T, int n_head, int n_kv_head, int n_keys);
 /* Bitmask tree-verification attention (batch 0): q fp16 [T][Hq][hd], T <= 64,
  * masks uint64 [T] (device) ancestor bitmasks.  Prefix slots [0, prefix_len)
- * are visible to every node; node j lives at slot (write_pos + j) % S.
+ * are visible to every node; node j lives at slot (write_pos + j) % S.  Q K^T and
+ * P V run as v_mfma_f32_16x16x32_f16 tiles (hd 64 / 128).
  * workspace >= axm_attention_workspace_bytes(T, Hq, hd, num_splits).
  * Replaces gqa_tree_verify{,_fp8,_int4}_mps (mps_kernels.mm:1508-1631, 1908-2038,
  * 4111-4249; Python entry axiomlm/kernels/ops.py:657-797); masks are widened

@@ -199,6 +199,53 @@ def test_tile16_qmv_matches_oracle(dev, M, N_, K, bias):
     assert err.max() <= 2e-3, f"max rel err {err.max()}"
 
 
+@pytest.mark.parametrize(
+    "M,N_,K,bias",
+    [(5, 96, 256, True), (16, 13, 192, False), (17, 768, 704, False), (37, 1408, 4096, True), (64, 4096, 11008, False),
+     (16, 12288, 4096, False), (8, 32000, 4096, False)],
+)
+def test_tile16_qmm_matches_oracle(dev, M, N_, K, bias):
+    """Multi-token GEMM (16 tokens per weight pass, K split over workgroups above 2048
+    with fp32 partial tiles summed in order) vs the oracle's dequantize-then-matmul; the
+    same bound as the GEMV (fp32 accumulation order and the fp16 output rounding)."""
+    from axiomlm_amd.kernels import qmm_q4_tile16, repack_q4_marlin_tile16
+
+    print(f"[tile16_qmm] M={M} N={N_} K={K} bias={bias}", flush=True)
+    rng = np.random.default_rng(M * 7 + N_ + K)
+    w = (rng.standard_normal((N_, K)) * 0.02).astype(F16)
+    x = rng.standard_normal((M, K)).astype(F16)
+    b = (rng.standard_normal(N_) * 0.1).astype(F16) if bias else None
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    ref = fm.qmv_q4_marlin(x, wm, sb, N_, b).astype(F32)
+    w16, sb16 = repack_q4_marlin_tile16(T(wm, dev), T(sb, dev), N_, K)
+    got = N(qmm_q4_tile16(T(x, dev), w16, sb16, N_, None if b is None else T(b, dev))).astype(F32)
+    err = np.abs(got - ref) / (1.0 + np.abs(ref))
+    assert err.max() <= 2e-3, f"max rel err {err.max()}"
+
+
+@pytest.mark.parametrize("M,K,H,norm", [(16, 4096, 11008, True), (9, 256, 704, False), (33, 704, 256, True)])
+def test_tile16_qmm_swiglu_matches_oracle(dev, M, K, H, norm):
+    """RMSNorm -> [W_gate; W_up] multi-token GEMM -> silu(g) * u; bound as for the
+    single-launch GEMV form below."""
+    from axiomlm_amd.kernels import qmv_q4_tile16_swiglu, repack_q4_marlin_tile16
+    from oracle import model as om
+
+    print(f"[tile16_qmm_swiglu] M={M} K={K} H={H} norm={norm}", flush=True)
+    rng = np.random.default_rng(K + H + M)
+    w = (rng.standard_normal((2 * H, K)) * 0.02).astype(F16)
+    x = rng.standard_normal((M, K)).astype(F16)
+    ln = (1.0 + 0.1 * rng.standard_normal(K)).astype(F16) if norm else None
+    wm, sb = fm.pack_linear_q4_marlin(w, clip_search=False)
+    h = om.rmsnorm_fp16(x, ln, 1e-5) if norm else x
+    gu = fm.qmv_q4_marlin(h, wm, sb, 2 * H).astype(F32)
+    g, u = gu[:, :H], gu[:, H:]
+    ref = (((g / (1 + np.exp(-g))).astype(F16).astype(F32)) * u).astype(F16).astype(F32)
+    w16, sb16 = repack_q4_marlin_tile16(T(wm, dev), T(sb, dev), 2 * H, K)
+    got = N(qmv_q4_tile16_swiglu(T(x, dev), None if ln is None else T(ln, dev), 1e-5, w16, sb16, H)).astype(F32)
+    bound = 4e-3 * (1 + np.abs(g)) * (1 + np.abs(u))
+    assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) - bound)}"
+
+
 @pytest.mark.parametrize("layout", ["marlin", "tile16"])
 @pytest.mark.parametrize("M,K,H,norm", [(1, 256, 704, True), (3, 704, 256, False), (1, 4096, 11008, True),
                                         (4, 1024, 512, True)])
