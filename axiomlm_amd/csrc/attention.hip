@@ -190,8 +190,26 @@ __device__ __forceinline__ u32x4 kv8_fetch(const void* base, const f16* scales, 
   return r;
 }
 
-template <int KVT>
+// HW: fp8 codes through v_cvt_pk_f32_fp8 (OCP E4M3FN on gfx950; every finite
+// code converts exactly, so the result equals the table-free decode below for
+// all non-NaN codes).  The attention kernels use it; the dequantization entry
+// point keeps the bitwise decode so that NaN codes keep their exact pattern.
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+template <int KVT, bool HW = false>
 __device__ __forceinline__ void kv8_convert(u32x4 r, float sc, float out[8]) {
+  if (KVT == AXM_KV_FP8 && HW) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t word = r[w];
+      const f32x2_hw lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
+      const f32x2_hw hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
+      out[4 * w + 0] = h2f(f2h(lo.x * sc));
+      out[4 * w + 1] = h2f(f2h(lo.y * sc));
+      out[4 * w + 2] = h2f(f2h(hi.x * sc));
+      out[4 * w + 3] = h2f(f2h(hi.y * sc));
+    }
+    return;
+  }
   if (KVT == AXM_KV_FP16) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -384,7 +402,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
         const int key = kb0 + u * NW * KPW + sub;
         const bool valid = key < k_end;
         float kf[8];
-        if constexpr (KVT != AXM_KV_FP16) kv8_convert<KVT>(kr[u], ksc[u], kf);
+        if constexpr (KVT != AXM_KV_FP16) kv8_convert<KVT, true>(kr[u], ksc[u], kf);
 #pragma unroll
         for (int r = 0; r < QR; ++r) {
           float d = 0.f;
@@ -406,7 +424,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
     if constexpr (KVT != AXM_KV_FP16) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (u < n_steps) kv8_convert<KVT>(vr[u], vsc[u], vf[u]);
+        if (u < n_steps) kv8_convert<KVT, true>(vr[u], vsc[u], vf[u]);
     }
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
@@ -698,31 +716,45 @@ __device__ __forceinline__ float row16_sum(float v) {
 constexpr int kTreeKeys = 32;    // keys per block (the k extent of one P V MFMA)
 constexpr int kTreeRows = 64;    // query rows per workgroup (four waves of 16)
 
-// 8 consecutive elements [e0, e0 + 8) of cache row `row` as fp16 (zeros when !ok).
-template <int KVT>
-__device__ __forceinline__ f16x8 kv_row8(const void* base, const f16* scales, size_t row, int hd, int e0, bool ok) {
-  f16x8 h;
-  if (!ok) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = f16(0);
-    return h;
-  }
+// 8 consecutive elements [e0, e0 + 8) of a cache row: raw codes (+ group scale)
+// fetched ahead of use, converted to fp16 with the reference rounding.
+struct KvRaw8 {
+  u32x4 r;
   float sc;
-  const u32x4 r = kv8_fetch<KVT>(base, scales, row, hd, e0, sc);
-  if (KVT == AXM_KV_FP16) return __builtin_bit_cast(f16x8, r);
-  float f[8];
-  kv8_convert<KVT>(r, sc, f);
+};
+template <int KVT>
+__device__ __forceinline__ KvRaw8 kv_fetch8(const void* base, const f16* scales, size_t row, int hd, int e0, bool ok) {
+  KvRaw8 f;
+  f.r = u32x4{0u, 0u, 0u, 0u};
+  f.sc = 0.f;
+  if (ok) f.r = kv8_fetch<KVT>(base, scales, row, hd, e0, f.sc);
+  return f;
+}
+template <int KVT>
+__device__ __forceinline__ f16x8 kv_half8(const KvRaw8& f) {
+  if (KVT == AXM_KV_FP16) return __builtin_bit_cast(f16x8, f.r);
+  float x[8];
+  kv8_convert<KVT, true>(f.r, f.sc, x);
+  f16x8 h;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) h[i] = f2h(f[i]);
+  for (int i = 0; i < 8; ++i) h[i] = f2h(x[i]);
   return h;
 }
 
 template <int KVT, int HD>
-__global__ void __launch_bounds__(256) tree_mfma_kernel(AttnParams p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) tree_mfma_kernel(AttnParams p) {
   constexpr int KSTEPS = HD / 32;  // MFMA k-steps over the head dimension
   constexpr int DT = HD / 16;      // 16-wide output dimension tiles
-  __shared__ __align__(16) f16 vt[HD][kTreeKeys];           // V block, dim-major
-  __shared__ __align__(16) f16 pt[4][16][kTreeKeys];        // per wave: P of its 16 rows
+  constexpr int kVec = kTreeKeys * HD / 8;        // 8-element V vectors per key block
+  constexpr int kVPT = (kVec + 255) / 256;        // of them per thread
+  // V block, dim-major, and per wave the P tile of its 16 rows.  Both store
+  // row r's 8-key unit u at unit u ^ swz(r), so that the transposing 2-byte
+  // writes of rows 8 (V) or 4 (P) apart fall in different banks, while a
+  // 16-byte operand read still covers whole units of one contiguous 1 KB tile.
+  __shared__ __align__(16) f16 vt[HD * kTreeKeys];
+  __shared__ __align__(16) f16 pt[4][16 * kTreeKeys];
+  auto vt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 3) & 3)) << 3) + (key & 7); };
+  auto pt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 2) & 3)) << 3) + (key & 7); };
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
@@ -740,6 +772,29 @@ __global__ void __launch_bounds__(256) tree_mfma_kernel(AttnParams p) {
     return (r / p.n_rep) * p.Hq + kvh * p.n_rep + (r % p.n_rep);
   };
   auto slot_of = [&](int key) { return key < prefix ? key : (p.write_pos + (key - prefix)) % p.kv.S; };
+
+  // Key / value fetches of one block: this lane's K B-operand fragments (keys
+  // kb0 + 16 h + l16, dims 32 c + 8 lq) and this thread's V vectors.
+  KvRaw8 kraw[2][KSTEPS], vraw[kVPT];
+  auto fetch = [&](int kb0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int key = kb0 + 16 * h + l16;
+      const size_t row = head_row0 + slot_of(key);
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c)
+        kraw[h][c] = kv_fetch8<KVT>(p.kv.k, p.kv.ks, row, HD, 32 * c + 8 * lq, key < k_end);
+    }
+#pragma unroll
+    for (int i = 0; i < kVPT; ++i) {
+      const int j = i * 256 + threadIdx.x;
+      const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
+      const int key = kb0 + kk;
+      vraw[i] = kv_fetch8<KVT>(p.kv.v, p.kv.vs, head_row0 + slot_of(key), HD, e0, j < kVec && key < k_end);
+    }
+  };
+  // The first block's keys and values are requested before the query rows.
+  if (k_begin < k_end) fetch(k_begin);
 
   // A operand: query row row0 + l16, dims 32 c + 8 lq .. +7.
   f16x8 qa[KSTEPS];
@@ -769,31 +824,32 @@ __global__ void __launch_bounds__(256) tree_mfma_kernel(AttnParams p) {
   for (int d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int kb0 = k_begin; kb0 < k_end; kb0 += kTreeKeys) {
-    // Stage the block's V transposed: vector j covers key kb0 + j / (HD/8), dims 8 (j % (HD/8)).
-    constexpr int kVec = kTreeKeys * HD / 8;
+    // Convert this block's fetches, then request the next block's.
+    f16x8 kf[2][KSTEPS], vv[kVPT];
 #pragma unroll
-    for (int j0 = 0; j0 < kVec; j0 += 256) {
-      const int j = j0 + threadIdx.x;
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(kraw[h][c]);
+#pragma unroll
+    for (int i = 0; i < kVPT; ++i) vv[i] = kv_half8<KVT>(vraw[i]);
+    if (kb0 + kTreeKeys < k_end) fetch(kb0 + kTreeKeys);
+    // Stage V transposed: vector j covers key kb0 + j / (HD/8), dims 8 (j % (HD/8)).
+#pragma unroll
+    for (int i = 0; i < kVPT; ++i) {
+      const int j = i * 256 + threadIdx.x;
       if (j < kVec) {
         const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
-        const int key = kb0 + kk;
-        const f16x8 vv = kv_row8<KVT>(p.kv.v, p.kv.vs, head_row0 + slot_of(key), HD, e0, key < k_end);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vt[e0 + i][kk] = vv[i];
+        for (int e = 0; e < 8; ++e) vt[vt_at(e0 + e, kk)] = vv[i][e];
       }
     }
     // S = Q K^T for the block's two 16-key halves.
     f32x4 sc[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int key = kb0 + 16 * h + l16;
-      const size_t row = head_row0 + slot_of(key);
       sc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) {
-        const f16x8 kf = kv_row8<KVT>(p.kv.k, p.kv.ks, row, HD, 32 * c + 8 * lq, key < k_end);
-        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf, sc[h], 0, 0, 0);
-      }
+      for (int c = 0; c < KSTEPS; ++c) sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf[h][c], sc[h], 0, 0, 0);
     }
     // Mask, scale, online softmax per D-tile row; P to the wave's LDS tile.
 #pragma unroll
@@ -816,14 +872,14 @@ __global__ void __launch_bounds__(256) tree_mfma_kernel(AttnParams p) {
 #pragma unroll
       for (int d = 0; d < DT; ++d) o[d][v] *= alpha;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) pt[wave][4 * lq + v][16 * h + l16] = f2h(pr[h]);
+      for (int h = 0; h < 2; ++h) pt[wave][pt_at(4 * lq + v, 16 * h + l16)] = f2h(pr[h]);
     }
     __syncthreads();  // V staged by every wave; P tiles written
     // O += P V: A = P[row l16][keys 8 lq ..], B = V^T[dim 16 d + l16][keys 8 lq ..].
-    const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][l16][8 * lq]);
+    const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][pt_at(l16, 8 * lq)]);
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
-      const f16x8 vb = *reinterpret_cast<const f16x8*>(&vt[16 * d + l16][8 * lq]);
+      const f16x8 vb = *reinterpret_cast<const f16x8*>(&vt[vt_at(16 * d + l16, 8 * lq)]);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
     }
     __syncthreads();  // before the next block overwrites vt / pt
@@ -868,11 +924,11 @@ int launch_tree_mfma(const AttnParams& p, dim3 grid, hipStream_t s) {
 
 int tree_choose_splits(int T, int Hq, int Hkv, int n_keys) {
   // Workgroups of 64 query rows per KV head; splits of >= 64 keys until about
-  // one workgroup per CU.
+  // two workgroups per CU.
   const int rows = T * (Hq / Hkv);
   const int wgs = Hkv * ((rows + kTreeRows - 1) / kTreeRows);
   int splits = 1;
-  while (splits < 64 && wgs * splits * 2 <= 256 && n_keys >= 64 * splits * 2) splits *= 2;
+  while (splits < 64 && wgs * splits * 2 <= 512 && n_keys >= 64 * splits * 2) splits *= 2;
   return splits;
 }
 

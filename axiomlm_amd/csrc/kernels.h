@@ -66,5 +66,5 @@ int launch_flash_decode_parts(const f16* q, const KvView& kv, int Hq, int active
 int launch_tree_attention(const f16* q, const KvView& kv, f16* out, int Hq, int T, int prefix_len, int write_pos,
                           const uint64_t* masks_dev, int n_splits, float* ws, hipStream_t s);
 size_t tree_workspace_bytes(int T, int Hq, int hd, int n_splits);
-// Key splits for tree attention (about one 64-row workgroup per CU, >= 64 keys each).
+// Key splits for tree attention (about two 64-row workgroups per CU, >= 64 keys each).
 int tree_choose_splits(int T, int Hq, int Hkv, int n_keys);

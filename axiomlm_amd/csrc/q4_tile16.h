@@ -65,12 +65,11 @@ int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* 
 // Multi-token GEMM over the same tile16 weights for M in [1, 16] tokens (the 16
 // rows of the MFMA A operand): every weight chunk is streamed once for all M
 // tokens.  Activations must be normalized already (a.ln_w == nullptr); epi is
-// Q4_EPI_STORE (+ bias), Q4_EPI_RESID or Q4_EPI_SWIGLU.  K is split across
-// workgroups so that each stages at most kTile16GemmMaxChunks chunks of x; with
-// more than one split the partial tiles go to ws (t16_gemm16_ws_bytes) and a
-// reduce launch applies the epilogue.
+// Q4_EPI_STORE (+ bias), Q4_EPI_RESID or Q4_EPI_SWIGLU.  K is split across at
+// most kTile16GemmMaxSplits workgroups; with more than one split the partial
+// tiles go to ws (t16_gemm16_ws_bytes) and a reduce launch applies the epilogue.
 constexpr int kTile16GemmTokens = 16;
-constexpr int kTile16GemmMaxChunks = 16;
+constexpr int kTile16GemmMaxSplits = 16;
 size_t t16_gemm16_ws_bytes(int K, int n_units, int NT);
 int t16_gemm16_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s);
 size_t t16_weight_bytes(int N, int K);

@@ -8,12 +8,13 @@
 // wave issues the same four MFMAs as the GEMV and applies (scale, bias) of the
 // two 64-groups to the four tokens its lanes hold in the D tile.
 //
-// The activations of all 16 token rows for the workgroup's K range are staged
-// in LDS, so K is split across workgroups (grid.y) into ranges of at most
-// kTile16GemmMaxChunks chunks; with more than one range each workgroup writes
-// its fp32 partial tile and t16g_reduce_kernel sums the ranges in order and
-// applies the epilogue.  Activations come in normalized (the runner runs the
-// RMSNorm first, with the same rounding as the GEMV prologue).
+// A wave owns one unit for the workgroup's K split, so the eight waves of a
+// workgroup cover 128 output rows and share one staged copy of the activations
+// (16 tokens, kGRC chunks at a time, double-buffered).  K is split across
+// workgroups until the grid covers the CUs; with more than one split each
+// workgroup writes its fp32 partial tile and t16g_reduce_kernel sums the splits
+// in order and applies the epilogue.  Activations come in normalized (the
+// runner runs the RMSNorm first, with the same rounding as the GEMV prologue).
 #include "kernels.h"
 #include "q4_tile16.h"
 #include "t16_device.h"
@@ -21,17 +22,33 @@
 namespace {
 
 constexpr int kGThreads = 512;
-constexpr int kGWaves = kGThreads / 64;
+constexpr int kGWaves = kGThreads / 64;   // one tile16 unit per wave
 constexpr int kGTok = kTile16GemmTokens;
-constexpr int kGP = 8;  // chunk loads in flight per wave (ring of register slots)
+constexpr int kGRC = 8;                   // chunks (128 k) per staged activation range
 constexpr int kGOOB = 0x7FFFFFF0;
-// Staging: (token, 8-element vector) pairs per thread.
-constexpr int kGStagePerThread = kGTok * kTile16GemmMaxChunks * 16 / kGThreads;
-static_assert(kGStagePerThread * kGThreads == kGTok * kTile16GemmMaxChunks * 16, "staging split");
+constexpr int kGStageVec = kGTok * kGRC * 16;                  // 8-element vectors per range
+constexpr int kGStagePerThread = kGStageVec / kGThreads;       // 4
+static_assert(kGStagePerThread * kGThreads == kGStageVec, "staging split");
 
-size_t gemm_smem_bytes(int kbps, int NT) {
-  return (size_t)kGTok * kbps * 128 * sizeof(f16) + (size_t)kGTok * 2 * kbps * sizeof(f32x2) +
-         (size_t)kGWaves * NT * 4 * 64 * sizeof(float);
+// Staged rows are padded by 16 bytes (activations) and 16 bytes (group sums) so
+// that the A-operand reads of the 16 token rows (and the group-sum reads of the
+// four rows a lane holds) do not all fall into the same LDS banks.
+constexpr int kGXRow = kGRC * 128 + 8;   // halves per staged activation row
+constexpr int kGCRow = 2 * kGRC + 2;     // (corr, sum) pairs per staged row
+constexpr size_t kGXsHalves = (size_t)kGTok * kGXRow;
+constexpr size_t kGCxPairs = (size_t)kGTok * kGCRow;
+
+size_t gemm_smem_bytes() { return 2 * (kGXsHalves * sizeof(f16) + kGCxPairs * sizeof(f32x2)); }
+
+// Workgroups per K split: a unit per wave, eight per workgroup; split K until
+// about one workgroup per CU, keeping >= kGRC chunks per split.
+int gemm_splits(int KB, int n_units) {
+  const int wg = (n_units + kGWaves - 1) / kGWaves;
+  int splits = (axm_num_cus() + wg / 2) / wg;
+  const int max_splits = KB / kGRC > 0 ? KB / kGRC : 1;
+  if (splits > max_splits) splits = max_splits;
+  if (splits > kTile16GemmMaxSplits) splits = kTile16GemmMaxSplits;
+  return splits < 1 ? 1 : splits;
 }
 
 // One output element of the epilogue (identical arithmetic to the GEMV's):
@@ -55,147 +72,158 @@ __device__ __forceinline__ void t16g_store(const T16Args& a, int tok, int row, f
   }
 }
 
+// Each wave owns one unit (16 rows, or a gate/up pair) over the workgroup's K
+// split.  The split's activations of all 16 token rows are staged range by
+// range (kGRC chunks, double-buffered in LDS: range r + 1 is loaded while range
+// r is consumed), and the weight chunks of range r + 1 are requested into the
+// register slots that range r's chunks free, so the weight stream does not stop
+// at range boundaries.
 template <int NT, int EPI>
 __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int kbps = a.kb_per_split;
-  const int kbA = blockIdx.y * kbps;                  // first chunk of this K range
-  const int kbN = min(a.KB, kbA + kbps) - kbA;        // chunks in it (>= 1)
-  f16* xs = reinterpret_cast<f16*>(smem);                                      // [16][kbN * 128]
-  f32x2* cx = reinterpret_cast<f32x2*>(xs + (size_t)kGTok * kbps * 128);       // [16][2 kbN]
-  float* red = reinterpret_cast<float*>(cx + (size_t)kGTok * 2 * kbps);        // [waves][NT][4][64]
+  f16* xs0 = reinterpret_cast<f16*>(smem);                         // [2][16][kGXRow]
+  f32x2* cx0 = reinterpret_cast<f32x2*>(xs0 + 2 * kGXsHalves);     // [2][16][kGCRow]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int S = a.split;
-  const int upw = kGWaves / S;
-  const int sub = wave % S;
-  const int slot = wave / S;
-  const int per = (kbN + S - 1) / S;
-  const int c0 = sub * per;                    // chunk offset of this wave within the range
-  const int my = max(0, min(per, kbN - c0));   // chunks of this wave
-  const int unit = blockIdx.x * upw + slot;
   const int kq = lane >> 4;
+  const int unit = blockIdx.x * kGWaves + wave;
+  const int kbA = blockIdx.y * a.kb_per_split;
+  const int kbN = min(a.KB, kbA + a.kb_per_split) - kbA;  // chunks of this split (>= 1)
+  const int n_ranges = (kbN + kGRC - 1) / kGRC;
   const Unpack U{to_vgpr(a.unpack[0]), to_vgpr(a.unpack[1]), a.unpack[2], a.unpack[3]};
   const __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.w16, (short)0, (int)a.w16_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.sb16, (short)0, (int)a.sb16_bytes, 0x00020000);
 
-  u32x4 wr[kGP][NT];
-  u32x2 sr[kGP][NT];
-  auto load = [&](int ci, int j) {
-    const bool ok = unit < a.n_units && ci < my;
+  u32x4 wr[kGRC][NT];
+  u32x2 sr[kGRC][NT];
+  // Chunk c of range r into slot c (zeros past the split or the matrix).
+  auto load = [&](int r, int c) {
+    const int kl = r * kGRC + c;
+    const bool ok = unit < a.n_units && kl < kbN;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int base = (unit + t * a.pair_offset) * a.KB + kbA + c0 + ci;
+      const int base = (unit + t * a.pair_offset) * a.KB + kbA + kl;
       const int wo = ok ? (base * 64 + lane) * 16 : kGOOB;
       const int so = ok ? (base * 16 + (lane & 15)) * 8 : kGOOB;
-      wr[j][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
-      sr[j][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+      wr[c][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
+      sr[c][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
     }
   };
-  // The first weight chunks go out before the activation loads: both are one
-  // memory latency away and the activations are needed first only after the
-  // staging barrier.
-#pragma unroll
-  for (int j = 0; j < kGP; ++j) load(j, j);
-
-  // Stage x[0..15][kbA*128 .. +kbN*128) (tokens >= M and k >= K as zeros) and
-  // per 64-group the magic-offset-weighted and plain sums.  Pair p of thread
-  // tid is (token p / nvec, vector p % nvec); nvec is a multiple of 8, so the
-  // eight vectors of a group sit in eight consecutive lanes of one wave.
-  const int nvec = kbN * 16;
+  // Activations of range r: vector v = tid + i * threads is (token v / (16 kGRC),
+  // vector v % (16 kGRC) of the range); eight consecutive lanes hold a 64-group.
+  // Buffer loads with out-of-range offsets (tokens >= M, k past the split or K,
+  // ranges past the last) read zeros, so every load is issued unconditionally
+  // and the compiler can count the loads in flight exactly.
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.M_tokens * a.ldx * (int)sizeof(f16), 0x00020000);
+  // With 512 threads and 128 vectors per token row, thread tid stages vector
+  // tid % 128 of token rows tid / 128 + 4 i.
+  static_assert(kGThreads == 4 * 16 * kGRC && kGStagePerThread == 4, "staging map");
+  const int svi = tid & (16 * kGRC - 1);
+  const int stok = tid / (16 * kGRC);
   f16x8 xv[kGStagePerThread];
+  auto stage_load = [&](int r) {
+    const int k = (kbA + r * kGRC) * 128 + 8 * svi;
+    const int kok = (int)(k < a.K) & (int)(8 * svi < (kbN - r * kGRC) * 128);
 #pragma unroll
-  for (int i = 0; i < kGStagePerThread; ++i) {
-    const int p = tid + i * kGThreads;
-    const int tok = p / nvec, v = p - tok * nvec;
-    const int k = kbA * 128 + 8 * v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xv[i][e] = f16(0);
-    if (tok < a.M_tokens && k < a.K) xv[i] = *reinterpret_cast<const f16x8*>(a.x + (size_t)tok * a.ldx + k);
-  }
-#pragma unroll
-  for (int i = 0; i < kGStagePerThread; ++i) {
-    const int p = tid + i * kGThreads;
-    if (p >= kGTok * nvec) break;  // whole waves (nvec * 16 is a multiple of 64)
-    const int tok = p / nvec, v = p - tok * nvec;
-    float corr = 0.f, sum = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float f = h2f(xv[i][e]);
-      sum += f;
-      corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
+    for (int i = 0; i < kGStagePerThread; ++i) {
+      const int tok = stok + 4 * i;
+      // Branch-free select of the offset (a conditional here became divergent
+      // control flow with full memory waits inside it).
+      const int m = -(kok & (int)(tok < a.M_tokens));
+      const int off = (((tok * a.ldx + k) * (int)sizeof(f16)) & m) | (kGOOB & ~m);
+      xv[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
     }
-    corr = group_sum<8>(corr);
-    sum = group_sum<8>(sum);
-    *reinterpret_cast<f16x8*>(xs + (size_t)tok * kbN * 128 + 8 * v) = xv[i];
-    if ((tid & 7) == 0) cx[(size_t)tok * 2 * kbN + (v >> 3)] = f32x2{corr, sum};
-  }
+  };
+  auto stage_store = [&](int buf) {
+    f16* xs = xs0 + buf * kGXsHalves;
+    f32x2* cx = cx0 + buf * kGCxPairs;
+#pragma unroll
+    for (int i = 0; i < kGStagePerThread; ++i) {
+      const int tok = stok + 4 * i, vi = svi;
+      float corr = 0.f, sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = h2f(xv[i][e]);
+        sum += f;
+        corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
+      }
+      corr = group_sum<8>(corr);
+      sum = group_sum<8>(sum);
+      *reinterpret_cast<f16x8*>(xs + (size_t)tok * kGXRow + 8 * vi) = xv[i];
+      if ((tid & 7) == 0) cx[tok * kGCRow + (vi >> 3)] = f32x2{corr, sum};
+    }
+  };
+
+  // Weights of range 0 first, then its activations (both one latency away).
+#pragma unroll
+  for (int c = 0; c < kGRC; ++c) load(0, c);
+  stage_load(0);
+  stage_store(0);
   __syncthreads();
 
-  // A operand: token lane % 16 (rows past M are zeros), k sub-block lane / 16.
-  const f16* xa = xs + (size_t)(lane & 15) * kbN * 128 + 8 * kq;
   float acc[NT][4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int vi = 0; vi < 4; ++vi) acc[t][vi] = 0.f;
 
-  for (int ci0 = 0; ci0 < my; ci0 += kGP) {
+  for (int r = 0; r < n_ranges; ++r) {
+    // The next range's weights are requested unconditionally (past the last
+    // range they read zeros and are never used); its activations only when it
+    // exists.
+    const bool more = r + 1 < n_ranges;
+    if (more) stage_load(r + 1);
+    const f16* xs = xs0 + (r & 1) * kGXsHalves;
+    const f32x2* cx = cx0 + (r & 1) * kGCxPairs;
+    // A operand: token lane % 16 (rows past M are zeros), k sub-block lane / 16.
+    const f16* xa = xs + (size_t)(lane & 15) * kGXRow + 8 * kq;
+    // Only the last range of a split can be partial (uniform across the
+    // workgroup); keeping the guard makes each chunk its own block, which the
+    // register allocator needs.
+    const int n_here = min(kGRC, kbN - r * kGRC);
 #pragma unroll
-    for (int jj = 0; jj < kGP; ++jj) {
-      const int ci = ci0 + jj;
-      if (ci >= my) break;  // wave-uniform
-      const int kb = c0 + ci;  // chunk within the staged range
-      const f16* xk = xa + kb * 128;
-      f16x8 A[4];
+    for (int c = 0; c < kGRC; ++c) {
+      if (c < n_here) {
+        const f16* xk = xa + c * 128;
+        f16x8 A[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) A[c] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * c));
-      f32x4 cxv[4];
+        for (int q = 0; q < 4; ++q) A[q] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * q));
+        f32x4 cxv[4];
 #pragma unroll
-      for (int vi = 0; vi < 4; ++vi)
-        cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (size_t)(4 * kq + vi) * 2 * kbN + 2 * kb);
+        for (int vi = 0; vi < 4; ++vi)
+          cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (4 * kq + vi) * kGCRow + 2 * c);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-        f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], unpack_word(wr[jj][t][0], U), z4, 0, 0, 0);
-        f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], unpack_word(wr[jj][t][2], U), z4, 0, 0, 0);
-        d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], unpack_word(wr[jj][t][1], U), d0, 0, 0, 0);
-        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], unpack_word(wr[jj][t][3], U), d1, 0, 0, 0);
-        const f16x2 sb0 = as_h2(sr[jj][t][0]);
-        const f16x2 sb1 = as_h2(sr[jj][t][1]);
+        for (int t = 0; t < NT; ++t) {
+          const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+          f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], unpack_word(wr[c][t][0], U), z4, 0, 0, 0);
+          f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], unpack_word(wr[c][t][2], U), z4, 0, 0, 0);
+          d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], unpack_word(wr[c][t][1], U), d0, 0, 0, 0);
+          d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], unpack_word(wr[c][t][3], U), d1, 0, 0, 0);
+          const f16x2 sb0 = as_h2(sr[c][t][0]);
+          const f16x2 sb1 = as_h2(sr[c][t][1]);
 #pragma unroll
-        for (int vi = 0; vi < 4; ++vi) {
-          float r = acc[t][vi];
-          r = __builtin_fmaf(h2f(sb0.x), d0[vi] - cxv[vi][0], r);
-          r = __builtin_fmaf(h2f(sb0.y), cxv[vi][1], r);
-          r = __builtin_fmaf(h2f(sb1.x), d1[vi] - cxv[vi][2], r);
-          r = __builtin_fmaf(h2f(sb1.y), cxv[vi][3], r);
-          acc[t][vi] = r;
+          for (int vi = 0; vi < 4; ++vi) {
+            float x = acc[t][vi];
+            x = __builtin_fmaf(h2f(sb0.x), d0[vi] - cxv[vi][0], x);
+            x = __builtin_fmaf(h2f(sb0.y), cxv[vi][1], x);
+            x = __builtin_fmaf(h2f(sb1.x), d1[vi] - cxv[vi][2], x);
+            x = __builtin_fmaf(h2f(sb1.y), cxv[vi][3], x);
+            acc[t][vi] = x;
+          }
         }
       }
-      load(ci + kGP, jj);
+      load(r + 1, c);
     }
+    if (more) stage_store((r + 1) & 1);
+    __syncthreads();
   }
 
-  // Sum the S partial tiles of a unit in wave order.
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int vi = 0; vi < 4; ++vi) red[((wave * NT + t) * 4 + vi) * 64 + lane] = acc[t][vi];
-  __syncthreads();
-  if (sub != 0 || unit >= a.n_units) return;
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int vi = 0; vi < 4; ++vi) {
-      float s = 0.f;
-      for (int w = wave; w < wave + S; ++w) s += red[((w * NT + t) * 4 + vi) * 64 + lane];
-      acc[t][vi] = s;
-    }
+  if (unit >= a.n_units) return;
   const int j = lane & 15;
   if (gridDim.y == 1) {
     const int row = unit * 16 + j;
@@ -205,7 +233,7 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
       if (tok < a.M_tokens && row < a.N) t16g_store<EPI>(a, tok, row, acc[0][vi], acc[NT - 1][vi]);
     }
   } else {
-    // Partial tile of this K range: [split][token][column], column = tile * 16 + row in tile.
+    // Partial tile of this K split: [split][token][column], column = tile * 16 + row in tile.
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int col = (unit + t * a.pair_offset) * 16 + j;
@@ -216,7 +244,7 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   }
 }
 
-// Sums the K-range partials in range order and applies the epilogue: one thread
+// Sums the K-split partials in split order and applies the epilogue: one thread
 // per (token, output row).
 template <int EPI>
 __global__ void t16g_reduce_kernel(T16Args a, int n_splits, int up_col) {
@@ -233,23 +261,20 @@ __global__ void t16g_reduce_kernel(T16Args a, int n_splits, int up_col) {
 }
 
 template <int NT, int EPI>
-void t16g_attr(size_t smem) {
-  static size_t set = 0;
-  if (smem <= set) return;
+void t16g_attr() {
+  static bool set = false;
+  if (set) return;
+  set = true;
   if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)smem) == hipSuccess)
-    set = smem;
-  else
+                          (int)gemm_smem_bytes()) != hipSuccess)
     (void)hipGetLastError();
 }
-
-int gemm_splits(int KB) { return (KB + kTile16GemmMaxChunks - 1) / kTile16GemmMaxChunks; }
 
 }  // namespace
 
 size_t t16_gemm16_ws_bytes(int K, int n_units, int NT) {
   const int KB = (K + 127) / 128;
-  const int splits = gemm_splits(KB);
+  const int splits = gemm_splits(KB, n_units);
   return splits <= 1 ? 0 : (size_t)splits * kGTok * n_units * 16 * NT * sizeof(float);
 }
 
@@ -262,18 +287,14 @@ int t16_gemm16_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hip
   }
   const int NT = epi == Q4_EPI_SWIGLU ? 2 : 1;
   a.KB = (a.K + 127) / 128;
-  const int splits = gemm_splits(a.KB);
+  const int splits = gemm_splits(a.KB, a.n_units);
   const int kbps = (a.KB + splits - 1) / splits;
   const size_t need = t16_gemm16_ws_bytes(a.K, a.n_units, NT);
   if (need > 0 && (ws == nullptr || ws_bytes < need)) {
     axm_set_error("tile16 gemm: workspace of %zu bytes needed, %zu given", need, ws_bytes);
     return -1;
   }
-  // Waves per unit: about 8 waves per CU over all K ranges, >= 2 chunks per wave.
-  const int cus = axm_num_cus();
-  int S = 1;
-  while (S < kGWaves && a.n_units * S * splits < 8 * cus && kbps >= 4 * S) S *= 2;
-  a.split = S;
+  a.split = 1;
   a.M_tokens = M;
   a.kb_per_split = kbps;
   a.part_ws = ws;
@@ -284,20 +305,19 @@ int t16_gemm16_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hip
   a.unpack[1] = 0x00F000F0u;
   a.unpack[2] = 0x64006400u;
   a.unpack[3] = 0x54005400u;
-  const int upw = kGWaves / S;
-  const dim3 grid((a.n_units + upw - 1) / upw, splits);
-  const size_t smem = gemm_smem_bytes(kbps, NT);
+  const dim3 grid((a.n_units + kGWaves - 1) / kGWaves, splits);
+  const size_t smem = gemm_smem_bytes();
   switch (epi) {
     case Q4_EPI_STORE:
-      t16g_attr<1, Q4_EPI_STORE>(smem);
+      t16g_attr<1, Q4_EPI_STORE>();
       hipLaunchKernelGGL((t16g_kernel<1, Q4_EPI_STORE>), grid, dim3(kGThreads), smem, s, a);
       break;
     case Q4_EPI_RESID:
-      t16g_attr<1, Q4_EPI_RESID>(smem);
+      t16g_attr<1, Q4_EPI_RESID>();
       hipLaunchKernelGGL((t16g_kernel<1, Q4_EPI_RESID>), grid, dim3(kGThreads), smem, s, a);
       break;
     default:
-      t16g_attr<2, Q4_EPI_SWIGLU>(smem);
+      t16g_attr<2, Q4_EPI_SWIGLU>();
       hipLaunchKernelGGL((t16g_kernel<2, Q4_EPI_SWIGLU>), grid, dim3(kGThreads), smem, s, a);
       break;
   }

@@ -89,25 +89,30 @@ __global__ void set_tree_kernel(TreeParams p, int T, int* pos_dev, unsigned long
 __global__ void rope_tokens_kernel(const f16* __restrict__ qkv, int q_dim, int kv_dim, int hd,
                                    const float* __restrict__ freqs, const int* __restrict__ pos_dev,
                                    f16* __restrict__ q, f16* __restrict__ kv) {
-  const int t = blockIdx.x;
+  // Thread (token blockIdx.y, vector i): elements 8 i .. 8 i + 7 (four rotation
+  // pairs of one head; q_dim, kv_dim and hd are multiples of 8).
+  const int t = blockIdx.y;
   const int qkv_dim = q_dim + 2 * kv_dim;
-  const f16* src = qkv + (size_t)t * qkv_dim;
-  const int pos = pos_dev[t];
-  const int half = hd / 2;
-  for (int e = threadIdx.x; e < qkv_dim; e += blockDim.x) {
-    f16 out = src[e];
-    if (e < q_dim + kv_dim) {
-      const int within = e < q_dim ? e : e - q_dim;
-      const int fi = (within % hd) >> 1;
-      const float c = freqs[((size_t)pos * half + fi) * 2 + 0];
-      const float sn = freqs[((size_t)pos * half + fi) * 2 + 1];
-      out = rope_out(src[e & ~1], src[e | 1], c, sn, (e & 1) == 0);
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (8 * i >= qkv_dim) return;
+  const int e = 8 * i;
+  const f16x8 v = *reinterpret_cast<const f16x8*>(qkv + (size_t)t * qkv_dim + e);
+  f16x8 out = v;
+  if (e < q_dim + kv_dim) {
+    const int within = e < q_dim ? e : e - q_dim;
+    const int fi = (within % hd) >> 1;
+    const float* f = freqs + ((size_t)pos_dev[t] * (hd / 2) + fi) * 2;
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) {
+      const float c = f[2 * pr], sn = f[2 * pr + 1];
+      out[2 * pr] = rope_out(v[2 * pr], v[2 * pr + 1], c, sn, true);
+      out[2 * pr + 1] = rope_out(v[2 * pr], v[2 * pr + 1], c, sn, false);
     }
-    if (e < q_dim)
-      q[(size_t)t * q_dim + e] = out;
-    else
-      kv[(size_t)t * 2 * kv_dim + (e - q_dim)] = out;
   }
+  if (e < q_dim)
+    *reinterpret_cast<f16x8*>(q + (size_t)t * q_dim + e) = out;
+  else
+    *reinterpret_cast<f16x8*>(kv + (size_t)t * 2 * kv_dim + (e - q_dim)) = out;
 }
 
 }  // namespace
@@ -495,14 +500,15 @@ struct axm_runner {
         (epi == Q4_EPI_STORE || epi == Q4_EPI_RESID || epi == Q4_EPI_SWIGLU)) {
       // Multi-token GEMM: 16 tokens per weight pass, activations normalized first
       // (into x_norm_out when the caller wants them, else into the norm scratch).
+      const f16* xall = c.x;
+      if (c.ln_w != nullptr) {
+        f16* nrm = c.x_norm_out ? c.x_norm_out : norm;
+        launch_rmsnorm(c.x, c.ln_w, nrm, T, m.K, c.eps, s);
+        xall = nrm;
+      }
       for (int t0 = 0; t0 < T; t0 += kTile16GemmTokens) {
         const int mc = (T - t0) < kTile16GemmTokens ? (T - t0) : kTile16GemmTokens;
-        const f16* xin = c.x + (size_t)t0 * c.ldx;
-        if (c.ln_w != nullptr) {
-          f16* nrm = (c.x_norm_out ? c.x_norm_out : norm) + (size_t)t0 * c.ldx;
-          launch_rmsnorm(xin, c.ln_w, nrm, mc, m.K, c.eps, s);
-          xin = nrm;
-        }
+        const f16* xin = xall + (size_t)t0 * c.ldx;
         T16Args a{};
         a.x = xin;
         a.ldx = c.ldx;
@@ -560,8 +566,8 @@ struct axm_runner {
       a.eps = d.eps;
       int rc = gemv_rows(m_qkv[i], Q4_EPI_STORE, qkv_dim, a, T, s);
       if (rc) return rc;
-      hipLaunchKernelGGL(rope_tokens_kernel, dim3(T), dim3(256), 0, s, qkvbuf, q_dim, kv_dim, d.head_dim, d.freqs,
-                         tree_pos, q, kvst);
+      hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, T), dim3(256), 0, s, qkvbuf, q_dim,
+                         kv_dim, d.head_dim, d.freqs, tree_pos, q, kvst);
       launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, T, write_pos, nullptr, s);
       if (tree) {
         const int splits = tree_choose_splits(T, d.n_head, d.n_kv_head, prefix + T);

@@ -207,6 +207,11 @@ def gqa_flash_decode_mps(
 
 
 def _masks_tensor(tree_mask, T: int, device) -> torch.Tensor:
+    if isinstance(tree_mask, torch.Tensor) and tree_mask.device == device and tree_mask.dtype == torch.int64:
+        # uint64 bit patterns already on the device (no host round trip)
+        if tree_mask.numel() != T:
+            raise ValueError(f"tree_mask has {tree_mask.numel()} entries for {T} nodes")
+        return tree_mask.contiguous()
     if isinstance(tree_mask, torch.Tensor):
         vals = [int(x) for x in tree_mask.cpu().tolist()]
     else:

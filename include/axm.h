@@ -60,7 +60,7 @@ int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const v
  * qmm_q4_marlin_m8_apple_kernel / qmm_q4_marlin_apple_kernel, metal_kernels.metal:
  * 2268-2684; dispatch mps_kernels.mm:1272-1312; CPU form quant.py:664-684).  K is
  * split across workgroups; `workspace` holds the fp32 partial tiles
- * (axm_qmm_q4_tile16_workspace_bytes; 0 bytes when K <= 2048). */
+ * (axm_qmm_q4_tile16_workspace_bytes; 0 bytes when K <= 4096). */
 size_t axm_qmm_q4_tile16_workspace_bytes(int K, int N, int swiglu);
 int axm_qmm_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
                       int N, void* workspace, size_t workspace_bytes, void* stream);

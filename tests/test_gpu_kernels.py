@@ -202,7 +202,7 @@ def test_tile16_qmv_matches_oracle(dev, M, N_, K, bias):
 @pytest.mark.parametrize(
     "M,N_,K,bias",
     [(5, 96, 256, True), (16, 13, 192, False), (17, 768, 704, False), (37, 1408, 4096, True), (64, 4096, 11008, False),
-     (16, 12288, 4096, False), (8, 32000, 4096, False)],
+     (16, 12288, 4096, False), (8, 32000, 4096, False), (20, 96, 5120, True)],
 )
 def test_tile16_qmm_matches_oracle(dev, M, N_, K, bias):
     """Multi-token GEMM (16 tokens per weight pass, K split over workgroups above 2048
@@ -223,7 +223,8 @@ def test_tile16_qmm_matches_oracle(dev, M, N_, K, bias):
     assert err.max() <= 2e-3, f"max rel err {err.max()}"
 
 
-@pytest.mark.parametrize("M,K,H,norm", [(16, 4096, 11008, True), (9, 256, 704, False), (33, 704, 256, True)])
+@pytest.mark.parametrize("M,K,H,norm", [(16, 4096, 11008, True), (9, 256, 704, False), (33, 704, 256, True),
+                                        (12, 4608, 256, True)])
 def test_tile16_qmm_swiglu_matches_oracle(dev, M, K, H, norm):
     """RMSNorm -> [W_gate; W_up] multi-token GEMM -> silu(g) * u; bound as for the
     single-launch GEMV form below."""
