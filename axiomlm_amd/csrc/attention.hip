@@ -391,6 +391,18 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
   }
 
   for (; kb0 < k_end; kb0 += NW * KPW * U) {
+    // This batch's keys / values; the next batch is requested before they are
+    // consumed, so one batch of loads is always in flight.
+    u32x4 kcur[U], vcur[U];
+    float kscur[U], vscur[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      kcur[u] = kr[u];
+      vcur[u] = vr[u];
+      kscur[u] = ksc[u];
+      vscur[u] = vsc[u];
+    }
+    if (kb0 + NW * KPW * U < k_end) fetch(kb0 + NW * KPW * U);
     // Steps of this batch that hold at least one key of the range (wave-uniform);
     // the scores of the batch are taken first so that the running maximum and
     // the rescaling of (l, o) happen once per batch instead of once per key.
@@ -402,13 +414,13 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
         const int key = kb0 + u * NW * KPW + sub;
         const bool valid = key < k_end;
         float kf[8];
-        if constexpr (KVT != AXM_KV_FP16) kv8_convert<KVT, true>(kr[u], ksc[u], kf);
+        if constexpr (KVT != AXM_KV_FP16) kv8_convert<KVT, true>(kcur[u], kscur[u], kf);
 #pragma unroll
         for (int r = 0; r < QR; ++r) {
           float d = 0.f;
           if constexpr (KVT == AXM_KV_FP16) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) d = __builtin_amdgcn_fdot2(qh[r][i], as_dot_h2(kr[u][i]), d, false);
+            for (int i = 0; i < 4; ++i) d = __builtin_amdgcn_fdot2(qh[r][i], as_dot_h2(kcur[u][i]), d, false);
           } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[r][i], kf[i], d);
@@ -424,7 +436,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
     if constexpr (KVT != AXM_KV_FP16) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (u < n_steps) kv8_convert<KVT, true>(vr[u], vsc[u], vf[u]);
+        if (u < n_steps) kv8_convert<KVT, true>(vcur[u], vscur[u], vf[u]);
     }
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
@@ -444,7 +456,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
           if constexpr (KVT == AXM_KV_FP16) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const f16x2 vh = as_h2(vr[u][i]);
+              const f16x2 vh = as_h2(vcur[u][i]);
               o[r][2 * i] = __builtin_fmaf(pr, h2f(vh.x), o[r][2 * i]);
               o[r][2 * i + 1] = __builtin_fmaf(pr, h2f(vh.y), o[r][2 * i + 1]);
             }
@@ -457,7 +469,6 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
       l[r] = lsum;
       m[r] = m_new;
     }
-    if (kb0 + NW * KPW * U < k_end) fetch(kb0 + NW * KPW * U);
   }
 
   // Merge the KPW key sub-slots of the wave (lanes with equal e0).
@@ -605,10 +616,12 @@ int attn_choose_splits(int B, int Hkv, int active_len) {
   // workgroup per head is fastest up to 512 keys; beyond that a four-way split
   // (128 workgroups) is fastest from 1k to 4k keys.  Fewer (batch x head) rows
   // take proportionally more splits; every split keeps >= 128 keys.
+  // Long contexts take about four workgroups per CU (>= 256 keys each) so that
+  // enough key batches are in flight.
   const int rows = B * Hkv;
-  const int want_wg = active_len <= 512 ? 32 : 128;
+  const int want_wg = active_len <= 512 ? 32 : (active_len <= 4096 ? 128 : 4 * axm_num_cus());
   int splits = (want_wg + rows - 1) / rows;
-  const int by_len = (active_len + 127) / 128;
+  const int by_len = active_len <= 4096 ? (active_len + 127) / 128 : (active_len + 255) / 256;
   if (splits > by_len) splits = by_len;
   if (splits > 64) splits = 64;
   if (splits < 1) splits = 1;
