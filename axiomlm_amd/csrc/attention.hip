@@ -666,6 +666,8 @@ int launch_flash_decode_parts(const f16* q, const KvView& kv, int Hq, int active
   return launch_attn_dispatch<false>(p, qr, grid, s);
 }
 
+int launch_decode_mfma(const AttnParams& p, dim3 grid, hipStream_t s);
+
 int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,
                         int n_splits, float* ws, hipStream_t s) {
   AttnParams p{};
@@ -680,9 +682,14 @@ int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int ac
   p.prefix_dev = active_len_dev;
   p.T = 0;
   p.scale_log2 = kLog2e / sqrtf((float)kv.hd);
-  const int qr = pick_qr(p.n_rep);
-  dim3 grid(kv.B * kv.Hkv, n_splits, (p.n_rep + qr - 1) / qr);
-  int rc = launch_attn_dispatch<false>(p, qr, grid, s);
+  int rc;
+  if (p.n_rep >= 2 && p.n_rep <= 16 && (kv.hd == 64 || kv.hd == 128)) {
+    rc = launch_decode_mfma(p, dim3(kv.B * kv.Hkv, n_splits), s);
+  } else {
+    const int qr = pick_qr(p.n_rep);
+    dim3 grid(kv.B * kv.Hkv, n_splits, (p.n_rep + qr - 1) / qr);
+    rc = launch_attn_dispatch<false>(p, qr, grid, s);
+  }
   if (rc) return rc;
   if (n_splits > 1)
     hipLaunchKernelGGL(attn_reduce_kernel, dim3(kv.B * Hq), dim3(kv.hd), 0, s, ws, out, n_splits, kv.hd);
@@ -729,25 +736,60 @@ __device__ __forceinline__ float row16_sum(float v) {
 constexpr int kTreeKeys = 32;    // keys per block (the k extent of one P V MFMA)
 constexpr int kTreeRows = 64;    // query rows per workgroup (four waves of 16)
 
-// 8 consecutive elements [e0, e0 + 8) of a cache row: raw codes (+ group scale)
-// fetched ahead of use, converted to fp16 with the reference rounding.
+// 8 consecutive elements [e0, e0 + 8) of a cache row: raw codes and the raw
+// fp16 group scale, fetched ahead of use through bounded buffer descriptors
+// over one head's slots (an out-of-range offset reads zeros, so fetches of keys
+// past the range need no branch), converted to fp16 with the reference
+// rounding only when consumed.  A conditional fetch, or converting the scale
+// at the fetch, made the compiler wait for each load right after issuing it.
 struct KvRaw8 {
   u32x4 r;
-  float sc;
+  uint32_t sc;  // fp16 bits in the low half
+};
+struct KvHead {
+  __amdgpu_buffer_rsrc_t codes, scales;
 };
 template <int KVT>
-__device__ __forceinline__ KvRaw8 kv_fetch8(const void* base, const f16* scales, size_t row, int hd, int e0, bool ok) {
+__device__ __forceinline__ int kv_row_bytes(int hd) {
+  return KVT == AXM_KV_FP16 ? hd * 2 : (KVT == AXM_KV_FP8 ? hd : hd / 2);
+}
+template <int KVT>
+__device__ __forceinline__ KvHead kv_head(const void* base, const f16* scales, size_t head_row0, int S, int hd) {
+  KvHead h;
+  const int rb = kv_row_bytes<KVT>(hd);
+  h.codes = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)base + head_row0 * rb), (short)0, S * rb,
+                                              0x00020000);
+  h.scales = h.codes;
+  if (KVT != AXM_KV_FP16)
+    h.scales = __builtin_amdgcn_make_buffer_rsrc((void*)(scales + head_row0 * (hd / 64)), (short)0,
+                                                 S * (hd / 64) * 2, 0x00020000);
+  return h;
+}
+template <int KVT>
+__device__ __forceinline__ KvRaw8 kv_fetch8(const KvHead& h, int slot, int hd, int e0, bool ok) {
+  constexpr int kOff = 0x7FFFFFF0;
+  const int rb = kv_row_bytes<KVT>(hd);
   KvRaw8 f;
   f.r = u32x4{0u, 0u, 0u, 0u};
-  f.sc = 0.f;
-  if (ok) f.r = kv8_fetch<KVT>(base, scales, row, hd, e0, f.sc);
+  f.sc = 0u;
+  if (KVT == AXM_KV_FP16) {
+    f.r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(h.codes, ok ? slot * rb + e0 * 2 : kOff, 0, 0));
+  } else if (KVT == AXM_KV_FP8) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(h.codes, ok ? slot * rb + e0 : kOff, 0, 0));
+    f.r.x = v.x;
+    f.r.y = v.y;
+  } else {
+    f.r.x = __builtin_amdgcn_raw_buffer_load_b32(h.codes, ok ? slot * rb + e0 / 2 : kOff, 0, 0);
+  }
+  if (KVT != AXM_KV_FP16)
+    f.sc = __builtin_amdgcn_raw_buffer_load_b16(h.scales, ok ? (slot * (hd / 64) + e0 / 64) * 2 : kOff, 0, 0);
   return f;
 }
 template <int KVT>
 __device__ __forceinline__ f16x8 kv_half8(const KvRaw8& f) {
   if (KVT == AXM_KV_FP16) return __builtin_bit_cast(f16x8, f.r);
   float x[8];
-  kv8_convert<KVT, true>(f.r, f.sc, x);
+  kv8_convert<KVT, true>(f.r, h2f(u16_as_h((uint16_t)f.sc)), x);
   f16x8 h;
 #pragma unroll
   for (int i = 0; i < 8; ++i) h[i] = f2h(x[i]);
@@ -789,21 +831,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   // Key / value fetches of one block: this lane's K B-operand fragments (keys
   // kb0 + 16 h + l16, dims 32 c + 8 lq) and this thread's V vectors.
   KvRaw8 kraw[2][KSTEPS], vraw[kVPT];
+  const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, p.kv.S, HD);
+  const KvHead vh = kv_head<KVT>(p.kv.v, p.kv.vs, head_row0, p.kv.S, HD);
   auto fetch = [&](int kb0) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int key = kb0 + 16 * h + l16;
-      const size_t row = head_row0 + slot_of(key);
+      const int slot = slot_of(key);
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c)
-        kraw[h][c] = kv_fetch8<KVT>(p.kv.k, p.kv.ks, row, HD, 32 * c + 8 * lq, key < k_end);
+      for (int c = 0; c < KSTEPS; ++c) kraw[h][c] = kv_fetch8<KVT>(kh, slot, HD, 32 * c + 8 * lq, key < k_end);
     }
 #pragma unroll
     for (int i = 0; i < kVPT; ++i) {
       const int j = i * 256 + threadIdx.x;
       const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
       const int key = kb0 + kk;
-      vraw[i] = kv_fetch8<KVT>(p.kv.v, p.kv.vs, head_row0 + slot_of(key), HD, e0, j < kVec && key < k_end);
+      vraw[i] = kv_fetch8<KVT>(vh, slot_of(key), HD, e0, j < kVec && key < k_end);
     }
   };
   // The first block's keys and values are requested before the query rows.
@@ -932,6 +975,188 @@ int launch_tree_mfma(const AttnParams& p, dim3 grid, hipStream_t s) {
       return 0;
   }
   axm_set_error("tree attention: bad kv dtype %d", p.kv.kv_dtype);
+  return -1;
+}
+
+// ---------------------------------------------------------------------------
+// Batched GQA decode attention on the matrix cores: the n_rep (2..16) query
+// heads of one (batch, KV head) are the rows of one 16-row MFMA tile, so every
+// key / value row loaded serves all of them through q K^T and P V tiles instead
+// of n_rep vector dot products.  A workgroup is one (batch, KV head, split);
+// its four waves take interleaved 32-key blocks of the split independently
+// (wave-private transposed V and P tiles, no barrier in the loop) and merge
+// their (m, l, o) through LDS at the end.
+// ---------------------------------------------------------------------------
+template <int KVT, int HD>
+__global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
+  constexpr int KSTEPS = HD / 32;
+  constexpr int DT = HD / 16;
+  constexpr int kVPL = kTreeKeys * HD / 8 / 64;  // 8-element V vectors per lane and block
+  __shared__ __align__(16) f16 vt[4][HD * kTreeKeys];
+  __shared__ __align__(16) f16 pt[4][16 * kTreeKeys];
+  __shared__ float mrg[4][16][2 + HD];
+  auto vt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 3) & 3)) << 3) + (key & 7); };
+  auto pt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 2) & 3)) << 3) + (key & 7); };
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int b = blockIdx.x / p.kv.Hkv, kvh = blockIdx.x % p.kv.Hkv;
+  const int R = p.n_rep;
+  const int split = blockIdx.y;
+  const int n_keys = p.prefix_dev ? p.prefix_dev[0] : p.prefix_len;
+  const int per = (n_keys + p.n_splits - 1) / p.n_splits;
+  const int k_begin = min(split * per, n_keys);
+  const int k_end = min(k_begin + per, n_keys);
+  const size_t head_row0 = ((size_t)b * p.kv.Hkv + kvh) * p.kv.S;
+  const size_t qrow0 = (size_t)b * p.Hq + (size_t)kvh * p.n_rep;  // global query row of replica 0
+
+  KvRaw8 kraw[2][KSTEPS], vraw[kVPL];
+  const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, p.kv.S, HD);
+  const KvHead vh = kv_head<KVT>(p.kv.v, p.kv.vs, head_row0, p.kv.S, HD);
+  auto fetch = [&](int kb0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int key = kb0 + 16 * h + l16;
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) kraw[h][c] = kv_fetch8<KVT>(kh, key, HD, 32 * c + 8 * lq, key < k_end);
+    }
+#pragma unroll
+    for (int i = 0; i < kVPL; ++i) {
+      const int j = i * 64 + lane;
+      const int key = kb0 + j / (HD / 8), e0 = 8 * (j % (HD / 8));
+      vraw[i] = kv_fetch8<KVT>(vh, key, HD, e0, key < k_end);
+    }
+  };
+  const int kb_first = k_begin + kTreeKeys * wave;
+  if (kb_first < k_end) fetch(kb_first);
+
+  f16x8 qa[KSTEPS];
+#pragma unroll
+  for (int c = 0; c < KSTEPS; ++c) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qa[c][i] = f16(0);
+    if (l16 < R) qa[c] = *reinterpret_cast<const f16x8*>(p.q + (qrow0 + l16) * HD + 32 * c + 8 * lq);
+  }
+  bool row_ok[4];
+  float m[4], l[4];
+  f32x4 o[DT];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    row_ok[v] = 4 * lq + v < R;
+    m[v] = kNegBig;
+    l[v] = 0.f;
+  }
+#pragma unroll
+  for (int d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb0 = kb_first; kb0 < k_end; kb0 += 4 * kTreeKeys) {
+    f16x8 kf[2][KSTEPS], vv[kVPL];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(kraw[h][c]);
+#pragma unroll
+    for (int i = 0; i < kVPL; ++i) vv[i] = kv_half8<KVT>(vraw[i]);
+    if (kb0 + 4 * kTreeKeys < k_end) fetch(kb0 + 4 * kTreeKeys);
+#pragma unroll
+    for (int i = 0; i < kVPL; ++i) {
+      const int j = i * 64 + lane;
+      const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[wave][vt_at(e0 + e, kk)] = vv[i][e];
+    }
+    f32x4 sc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf[h][c], sc[h], 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float s2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool vis = row_ok[v] && kb0 + 16 * h + l16 < k_end;
+        s2[h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
+      }
+      const float m_new = fmaxf(m[v], row16_max(fmaxf(s2[0], s2[1])));
+      const float alpha = fast_exp2(m[v] - m_new);
+      float pr[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) pr[h] = s2[h] == kNegBig ? 0.f : fast_exp2(s2[h] - m_new);
+      l[v] = l[v] * alpha + row16_sum(pr[0] + pr[1]);
+      m[v] = m_new;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) o[d][v] *= alpha;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) pt[wave][pt_at(4 * lq + v, 16 * h + l16)] = f2h(pr[h]);
+    }
+    // The wave reads back its own LDS writes: DS operations of one wave complete
+    // in order, and the reads below wait for them.
+    const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][pt_at(l16, 8 * lq)]);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const f16x8 vb = *reinterpret_cast<const f16x8*>(&vt[wave][vt_at(16 * d + l16, 8 * lq)]);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
+    }
+  }
+
+  // Merge the four waves' (m, l, o) per query row.
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int row = 4 * lq + v;
+    if (l16 == 0) {
+      mrg[wave][row][0] = m[v];
+      mrg[wave][row][1] = l[v];
+    }
+#pragma unroll
+    for (int d = 0; d < DT; ++d) mrg[wave][row][2 + 16 * d + l16] = o[d][v];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < R * HD; t += 256) {
+    const int row = t / HD, e = t % HD;
+    float mm = kNegBig;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mm = fmaxf(mm, mrg[w][row][0]);
+    float ll = 0.f, oo = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float a = fast_exp2(mrg[w][row][0] - mm);
+      ll += mrg[w][row][1] * a;
+      oo += mrg[w][row][2 + e] * a;
+    }
+    const size_t gr = qrow0 + row;
+    if (p.n_splits == 1) {
+      p.out[gr * HD + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+    } else {
+      float* dst = p.ws + (gr * p.n_splits + split) * (2 + HD);
+      if (e == 0) {
+        dst[0] = mm;
+        dst[1] = ll;
+      }
+      dst[2 + e] = oo;
+    }
+  }
+}
+
+int launch_decode_mfma(const AttnParams& p, dim3 grid, hipStream_t s) {
+  const int hd = p.kv.hd;
+  switch (p.kv.kv_dtype) {
+    case AXM_KV_FP16:
+      if (hd == 128) hipLaunchKernelGGL((decode_mfma_kernel<AXM_KV_FP16, 128>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((decode_mfma_kernel<AXM_KV_FP16, 64>), grid, dim3(256), 0, s, p);
+      return 0;
+    case AXM_KV_FP8:
+      if (hd == 128) hipLaunchKernelGGL((decode_mfma_kernel<AXM_KV_FP8, 128>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((decode_mfma_kernel<AXM_KV_FP8, 64>), grid, dim3(256), 0, s, p);
+      return 0;
+    case AXM_KV_INT4:
+      if (hd == 128) hipLaunchKernelGGL((decode_mfma_kernel<AXM_KV_INT4, 128>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((decode_mfma_kernel<AXM_KV_INT4, 64>), grid, dim3(256), 0, s, p);
+      return 0;
+  }
+  axm_set_error("decode attention: bad kv dtype %d", p.kv.kv_dtype);
   return -1;
 }
 
