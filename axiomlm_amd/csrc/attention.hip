@@ -168,28 +168,8 @@ __device__ __forceinline__ void load_kv8(const void* base, const f16* scales, si
   }
 }
 
-// Raw 8-element key/value chunk (fp16: 16 B, fp8: 8 B, int4: 4 B) and its
-// group scale, fetched ahead of use; kv8_convert applies the same rounding as
-// load_kv8.
-template <int KVT>
-__device__ __forceinline__ u32x4 kv8_fetch(const void* base, const f16* scales, size_t row, int hd, int e0,
-                                           float& sc) {
-  u32x4 r = {0u, 0u, 0u, 0u};
-  sc = 1.f;
-  if (KVT == AXM_KV_FP16) {
-    r = *reinterpret_cast<const u32x4*>((const f16*)base + row * hd + e0);
-  } else if (KVT == AXM_KV_FP8) {
-    const u32x2 v = *reinterpret_cast<const u32x2*>((const uint8_t*)base + row * hd + e0);
-    r.x = v.x;
-    r.y = v.y;
-    sc = h2f(scales[row * (hd / 64) + e0 / 64]);
-  } else {
-    r.x = *reinterpret_cast<const uint32_t*>((const uint8_t*)base + row * (hd / 2) + e0 / 2);
-    sc = h2f(scales[row * (hd / 64) + e0 / 64]);
-  }
-  return r;
-}
-
+// A raw 8-element key/value chunk (fp16: 16 B, fp8: 8 B, int4: 4 B) and its fp16
+// group scale become eight fp32 values with the rounding of load_kv8.
 // HW: fp8 codes through v_cvt_pk_f32_fp8 (OCP E4M3FN on gfx950; every finite
 // code converts exactly, so the result equals the table-free decode below for
 // all non-NaN codes).  The attention kernels use it; the dequantization entry
@@ -232,6 +212,66 @@ __device__ __forceinline__ void kv8_convert(u32x4 r, float sc, float out[8]) {
       out[i] = h2f(f2h((float)q * sc));
     }
   }
+}
+
+// 8 consecutive elements [e0, e0 + 8) of a cache row: raw codes and the raw
+// fp16 group scale, fetched ahead of use through bounded buffer descriptors
+// over one head's slots (an out-of-range offset reads zeros, so fetches of keys
+// past the range need no branch), converted to fp16 with the reference
+// rounding only when consumed.  A conditional fetch, or converting the scale
+// at the fetch, made the compiler wait for each load right after issuing it.
+struct KvRaw8 {
+  u32x4 r;
+  uint32_t sc;  // fp16 bits in the low half
+};
+struct KvHead {
+  __amdgpu_buffer_rsrc_t codes, scales;
+};
+template <int KVT>
+__device__ __forceinline__ int kv_row_bytes(int hd) {
+  return KVT == AXM_KV_FP16 ? hd * 2 : (KVT == AXM_KV_FP8 ? hd : hd / 2);
+}
+template <int KVT>
+__device__ __forceinline__ KvHead kv_head(const void* base, const f16* scales, size_t head_row0, int S, int hd) {
+  KvHead h;
+  const int rb = kv_row_bytes<KVT>(hd);
+  h.codes = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)base + head_row0 * rb), (short)0, S * rb,
+                                              0x00020000);
+  h.scales = h.codes;
+  if (KVT != AXM_KV_FP16)
+    h.scales = __builtin_amdgcn_make_buffer_rsrc((void*)(scales + head_row0 * (hd / 64)), (short)0,
+                                                 S * (hd / 64) * 2, 0x00020000);
+  return h;
+}
+template <int KVT>
+__device__ __forceinline__ KvRaw8 kv_fetch8(const KvHead& h, int slot, int hd, int e0, bool ok) {
+  constexpr int kOff = 0x7FFFFFF0;
+  const int rb = kv_row_bytes<KVT>(hd);
+  KvRaw8 f;
+  f.r = u32x4{0u, 0u, 0u, 0u};
+  f.sc = 0u;
+  if (KVT == AXM_KV_FP16) {
+    f.r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(h.codes, ok ? slot * rb + e0 * 2 : kOff, 0, 0));
+  } else if (KVT == AXM_KV_FP8) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(h.codes, ok ? slot * rb + e0 : kOff, 0, 0));
+    f.r.x = v.x;
+    f.r.y = v.y;
+  } else {
+    f.r.x = __builtin_amdgcn_raw_buffer_load_b32(h.codes, ok ? slot * rb + e0 / 2 : kOff, 0, 0);
+  }
+  if (KVT != AXM_KV_FP16)
+    f.sc = __builtin_amdgcn_raw_buffer_load_b16(h.scales, ok ? (slot * (hd / 64) + e0 / 64) * 2 : kOff, 0, 0);
+  return f;
+}
+template <int KVT>
+__device__ __forceinline__ f16x8 kv_half8(const KvRaw8& f) {
+  if (KVT == AXM_KV_FP16) return __builtin_bit_cast(f16x8, f.r);
+  float x[8];
+  kv8_convert<KVT, true>(f.r, h2f(u16_as_h((uint16_t)f.sc)), x);
+  f16x8 h;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = f2h(x[i]);
+  return h;
 }
 
 // Sum over the LPT lanes that hold one key row (aligned groups of 8 or 16
@@ -326,20 +366,21 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
   // Keys / values of U steps; the first batch is requested before the query
   // rows so that the two latencies overlap.
   u32x4 kr[U], vr[U];
-  float ksc[U], vsc[U];
+  uint32_t ksc[U], vsc[U];  // raw fp16 group scales
+  const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, p.kv.S, hd);
+  const KvHead vh = kv_head<KVT>(p.kv.v, p.kv.vs, head_row0, p.kv.S, hd);
   auto fetch = [&](int kb0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int key = kb0 + u * NW * KPW + sub;
       int slot = key;
       if (TREE && key >= prefix) slot = (p.write_pos + (key - prefix)) % p.kv.S;
-      if (key < k_end) {
-        kr[u] = kv8_fetch<KVT>(p.kv.k, p.kv.ks, head_row0 + slot, hd, e0, ksc[u]);
-        vr[u] = kv8_fetch<KVT>(p.kv.v, p.kv.vs, head_row0 + slot, hd, e0, vsc[u]);
-      } else {
-        kr[u] = vr[u] = u32x4{0u, 0u, 0u, 0u};
-        ksc[u] = vsc[u] = 0.f;
-      }
+      const KvRaw8 fk = kv_fetch8<KVT>(kh, slot, hd, e0, key < k_end);
+      const KvRaw8 fv = kv_fetch8<KVT>(vh, slot, hd, e0, key < k_end);
+      kr[u] = fk.r;
+      ksc[u] = fk.sc;
+      vr[u] = fv.r;
+      vsc[u] = fv.sc;
     }
   };
   int kb0 = k_begin + wave * KPW;
@@ -394,7 +435,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
     // This batch's keys / values; the next batch is requested before they are
     // consumed, so one batch of loads is always in flight.
     u32x4 kcur[U], vcur[U];
-    float kscur[U], vscur[U];
+    uint32_t kscur[U], vscur[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       kcur[u] = kr[u];
@@ -414,7 +455,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
         const int key = kb0 + u * NW * KPW + sub;
         const bool valid = key < k_end;
         float kf[8];
-        if constexpr (KVT != AXM_KV_FP16) kv8_convert<KVT, true>(kcur[u], kscur[u], kf);
+        if constexpr (KVT != AXM_KV_FP16) kv8_convert<KVT, true>(kcur[u], h2f(u16_as_h((uint16_t)kscur[u])), kf);
 #pragma unroll
         for (int r = 0; r < QR; ++r) {
           float d = 0.f;
@@ -436,7 +477,7 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
     if constexpr (KVT != AXM_KV_FP16) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (u < n_steps) kv8_convert<KVT, true>(vcur[u], vscur[u], vf[u]);
+        if (u < n_steps) kv8_convert<KVT, true>(vcur[u], h2f(u16_as_h((uint16_t)vscur[u])), vf[u]);
     }
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
@@ -735,66 +776,6 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 constexpr int kTreeKeys = 32;    // keys per block (the k extent of one P V MFMA)
 constexpr int kTreeRows = 64;    // query rows per workgroup (four waves of 16)
-
-// 8 consecutive elements [e0, e0 + 8) of a cache row: raw codes and the raw
-// fp16 group scale, fetched ahead of use through bounded buffer descriptors
-// over one head's slots (an out-of-range offset reads zeros, so fetches of keys
-// past the range need no branch), converted to fp16 with the reference
-// rounding only when consumed.  A conditional fetch, or converting the scale
-// at the fetch, made the compiler wait for each load right after issuing it.
-struct KvRaw8 {
-  u32x4 r;
-  uint32_t sc;  // fp16 bits in the low half
-};
-struct KvHead {
-  __amdgpu_buffer_rsrc_t codes, scales;
-};
-template <int KVT>
-__device__ __forceinline__ int kv_row_bytes(int hd) {
-  return KVT == AXM_KV_FP16 ? hd * 2 : (KVT == AXM_KV_FP8 ? hd : hd / 2);
-}
-template <int KVT>
-__device__ __forceinline__ KvHead kv_head(const void* base, const f16* scales, size_t head_row0, int S, int hd) {
-  KvHead h;
-  const int rb = kv_row_bytes<KVT>(hd);
-  h.codes = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)base + head_row0 * rb), (short)0, S * rb,
-                                              0x00020000);
-  h.scales = h.codes;
-  if (KVT != AXM_KV_FP16)
-    h.scales = __builtin_amdgcn_make_buffer_rsrc((void*)(scales + head_row0 * (hd / 64)), (short)0,
-                                                 S * (hd / 64) * 2, 0x00020000);
-  return h;
-}
-template <int KVT>
-__device__ __forceinline__ KvRaw8 kv_fetch8(const KvHead& h, int slot, int hd, int e0, bool ok) {
-  constexpr int kOff = 0x7FFFFFF0;
-  const int rb = kv_row_bytes<KVT>(hd);
-  KvRaw8 f;
-  f.r = u32x4{0u, 0u, 0u, 0u};
-  f.sc = 0u;
-  if (KVT == AXM_KV_FP16) {
-    f.r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(h.codes, ok ? slot * rb + e0 * 2 : kOff, 0, 0));
-  } else if (KVT == AXM_KV_FP8) {
-    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(h.codes, ok ? slot * rb + e0 : kOff, 0, 0));
-    f.r.x = v.x;
-    f.r.y = v.y;
-  } else {
-    f.r.x = __builtin_amdgcn_raw_buffer_load_b32(h.codes, ok ? slot * rb + e0 / 2 : kOff, 0, 0);
-  }
-  if (KVT != AXM_KV_FP16)
-    f.sc = __builtin_amdgcn_raw_buffer_load_b16(h.scales, ok ? (slot * (hd / 64) + e0 / 64) * 2 : kOff, 0, 0);
-  return f;
-}
-template <int KVT>
-__device__ __forceinline__ f16x8 kv_half8(const KvRaw8& f) {
-  if (KVT == AXM_KV_FP16) return __builtin_bit_cast(f16x8, f.r);
-  float x[8];
-  kv8_convert<KVT, true>(f.r, h2f(u16_as_h((uint16_t)f.sc)), x);
-  f16x8 h;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) h[i] = f2h(x[i]);
-  return h;
-}
 
 template <int KVT, int HD>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) tree_mfma_kernel(AttnParams p) {
