@@ -43,7 +43,7 @@ struct T16Args {
   int parts_hd;        // elements per head (a multiple of 8)
   int split;           // waves per unit (set by t16_gemv_launch)
   uint32_t unpack[4];  // nibble masks and fp16 magic exponents (set by t16_gemv_launch)
-  // Multi-token GEMM (t16_gemm16_launch): tokens, chunks of K per grid.y split,
+  // Multi-token GEMM (t16_gemm_launch): tokens, chunks of K per grid.y split,
   // fp32 partial tiles [splits][16][part_cols] when K is split across workgroups.
   int M_tokens;
   int kb_per_split;
@@ -62,15 +62,16 @@ void t16_prepare_attributes();
 // Picks split / grid (a.split is overwritten); M in [1, 4].
 int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s);
 int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16, hipStream_t s);
-// Multi-token GEMM over the same tile16 weights for M in [1, 16] tokens (the 16
-// rows of the MFMA A operand): every weight chunk is streamed once for all M
+// Multi-token GEMM over the same tile16 weights for M in [1, 64] tokens (one to
+// four 16-row MFMA A tiles): every weight chunk is streamed once for all M
 // tokens.  Activations must be normalized already (a.ln_w == nullptr); epi is
 // Q4_EPI_STORE (+ bias), Q4_EPI_RESID or Q4_EPI_SWIGLU.  K is split across at
 // most kTile16GemmMaxSplits workgroups; with more than one split the partial
-// tiles go to ws (t16_gemm16_ws_bytes) and a reduce launch applies the epilogue.
-constexpr int kTile16GemmTokens = 16;
+// tiles go to ws (t16_gemm_ws_bytes, enough for any M) and a reduce launch
+// applies the epilogue.
+constexpr int kTile16GemmMaxTokens = 64;
 constexpr int kTile16GemmMaxSplits = 16;
-size_t t16_gemm16_ws_bytes(int K, int n_units, int NT);
-int t16_gemm16_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s);
+size_t t16_gemm_ws_bytes(int K, int n_units, int NT);
+int t16_gemm_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s);
 size_t t16_weight_bytes(int N, int K);
 size_t t16_sb_bytes(int N, int K);

@@ -1,16 +1,17 @@
-// Multi-token tile16 GEMM (M <= 16 tokens) for gfx950: the verify / prefill
-// steps of the decode runner and the qmm entry points.
+// Multi-token tile16 GEMM (M <= 64 tokens per launch) for gfx950: the verify /
+// prefill steps of the decode runner and the qmm entry points.
 //
 // The decode GEMV (q4_tile16.hip) fills only 1..4 of the 16 token rows of the
-// v_mfma_f32_16x16x32_f16 A operand; here all 16 rows carry tokens, so every
-// weight chunk (16 rows x 128 k, 1 KB) is read from HBM once for up to 16
-// tokens and the nibble unpack is shared by all of them.  Per chunk and tile a
-// wave issues the same four MFMAs as the GEMV and applies (scale, bias) of the
-// two 64-groups to the four tokens its lanes hold in the D tile.
+// v_mfma_f32_16x16x32_f16 A operand; here MB tiles of 16 token rows each carry
+// tokens, so every weight chunk (16 rows x 128 k, 1 KB) is read from HBM once
+// for up to 16 MB tokens and its nibble unpack (the B operand) is shared by all
+// of them.  Per chunk and token tile a wave issues the same four MFMAs as the
+// GEMV and applies (scale, bias) of the two 64-groups to the four tokens its
+// lanes hold in the D tile.
 //
 // A wave owns one unit for the workgroup's K split, so the eight waves of a
 // workgroup cover 128 output rows and share one staged copy of the activations
-// (16 tokens, kGRC chunks at a time, double-buffered).  K is split across
+// (16 MB tokens, RC chunks at a time, double-buffered).  K is split across
 // workgroups until the grid covers the CUs; with more than one split each
 // workgroup writes its fp32 partial tile and t16g_reduce_kernel sums the splits
 // in order and applies the epilogue.  Activations come in normalized (the
@@ -23,32 +24,51 @@ namespace {
 
 constexpr int kGThreads = 512;
 constexpr int kGWaves = kGThreads / 64;   // one tile16 unit per wave
-constexpr int kGTok = kTile16GemmTokens;
-constexpr int kGRC = 8;                   // chunks (128 k) per staged activation range
 constexpr int kGOOB = 0x7FFFFFF0;
-constexpr int kGStageVec = kGTok * kGRC * 16;                  // 8-element vectors per range
-constexpr int kGStagePerThread = kGStageVec / kGThreads;       // 4
-static_assert(kGStagePerThread * kGThreads == kGStageVec, "staging split");
 
-// Staged rows are padded by 16 bytes (activations) and 16 bytes (group sums) so
-// that the A-operand reads of the 16 token rows (and the group-sum reads of the
-// four rows a lane holds) do not all fall into the same LDS banks.
-constexpr int kGXRow = kGRC * 128 + 8;   // halves per staged activation row
-constexpr int kGCRow = 2 * kGRC + 2;     // (corr, sum) pairs per staged row
-constexpr size_t kGXsHalves = (size_t)kGTok * kGXRow;
-constexpr size_t kGCxPairs = (size_t)kGTok * kGCRow;
+// Shapes of one instantiation: MB token tiles (16 MB tokens per weight pass)
+// and RC chunks (128 k) per staged activation range.  Staged rows are padded by
+// 16 bytes (activations) and 16 bytes (group sums) so that the A-operand reads
+// of 16 token rows (and the group-sum reads of the four rows a lane holds) do
+// not all fall into the same LDS banks.
+template <int MB, int RC>
+struct GemmShape {
+  static constexpr int TOK = 16 * MB;
+  static constexpr int XROW = RC * 128 + 8;             // halves per staged activation row
+  static constexpr int CROW = 2 * RC + 2;               // (corr, sum) pairs per staged row
+  static constexpr size_t XS = (size_t)TOK * XROW;      // halves per buffer
+  static constexpr size_t CX = (size_t)TOK * CROW;      // pairs per buffer
+  static constexpr int VPR = 16 * RC;                   // 8-element vectors per token row and range
+  static constexpr int RPP = kGThreads / VPR;           // token rows staged per pass of the workgroup
+  static constexpr int PER = TOK / RPP;                 // vectors staged per thread
+  static constexpr size_t smem = 2 * (XS * sizeof(f16) + CX * sizeof(f32x2));
+  static_assert(RPP * VPR == kGThreads && PER * RPP == TOK, "staging map");
+  static_assert(smem <= 160 * 1024, "LDS");
+};
 
-size_t gemm_smem_bytes() { return 2 * (kGXsHalves * sizeof(f16) + kGCxPairs * sizeof(f32x2)); }
+// The three instantiations by tokens per launch: 16 tokens stage 8 chunks per
+// range (an 8-deep weight ring) and keep the GEMV's arithmetic; 32 and 64
+// tokens stage 4 (LDS holds two 64-token ranges of 4 chunks, 143 KB, and the
+// shorter ring bounds the SwiGLU form's registers) and dequantize each chunk
+// once for all of their token tiles (DQ).
+struct GemmCfg {
+  int mb, rc;
+};
+GemmCfg gemm_cfg(int M) {
+  if (M <= 16) return {1, 8};
+  if (M <= 32) return {2, 4};
+  return {4, 4};
+}
 
 // Workgroups per K split: a unit per wave, eight per workgroup.  The kernel
 // needs 140-200 VGPRs, so one 8-wave workgroup is resident per CU: K is split
 // as far as the grid still fits one round of workgroups (a grid even one
 // workgroup past the CU count runs a second round, e.g. 7B gate/up at M=16:
-// 172 workgroups 21 us, 258 workgroups 32 us), keeping >= kGRC chunks per split.
-int gemm_splits(int KB, int n_units) {
+// 172 workgroups 21 us, 258 workgroups 32 us), keeping >= RC chunks per split.
+int gemm_splits(int KB, int n_units, int rc) {
   const int wg = (n_units + kGWaves - 1) / kGWaves;
   int splits = axm_num_cus() / wg;
-  const int max_splits = KB / kGRC > 0 ? KB / kGRC : 1;
+  const int max_splits = KB / rc > 0 ? KB / rc : 1;
   if (splits > max_splits) splits = max_splits;
   if (splits > kTile16GemmMaxSplits) splits = kTile16GemmMaxSplits;
   return splits < 1 ? 1 : splits;
@@ -76,16 +96,26 @@ __device__ __forceinline__ void t16g_store(const T16Args& a, int tok, int row, f
 }
 
 // Each wave owns one unit (16 rows, or a gate/up pair) over the workgroup's K
-// split.  The split's activations of all 16 token rows are staged range by
-// range (kGRC chunks, double-buffered in LDS: range r + 1 is loaded while range
-// r is consumed), and the weight chunks of range r + 1 are requested into the
+// split.  The split's activations of all 16 MB token rows are staged range by
+// range (RC chunks, double-buffered in LDS: range r + 1 is loaded while range r
+// is consumed), and the weight chunks of range r + 1 are requested into the
 // register slots that range r's chunks free, so the weight stream does not stop
 // at range boundaries.
-template <int NT, int EPI>
+//
+// DQ selects how (scale, bias) enter.  DQ = false (the GEMV's arithmetic): the
+// MFMAs take the raw magic-exponent fp16 nibbles, and per 64-group and token
+// the corrections sum_x(magic) and bias * sum_x come from group sums staged
+// with the activations.  DQ = true: every weight is dequantized once per chunk
+// to fp16 q * scale + bias (one rounding, the "dequantize to half, then MMA"
+// of the reference's multi-token kernel) and the MFMAs accumulate the dot
+// products directly, so a token tile costs its four A reads and four MFMAs and
+// no per-tile vector math.
+template <int NT, int EPI, int MB, int RC, bool DQ>
 __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
+  using G = GemmShape<MB, RC>;
   extern __shared__ __align__(16) unsigned char smem[];
-  f16* xs0 = reinterpret_cast<f16*>(smem);                         // [2][16][kGXRow]
-  f32x2* cx0 = reinterpret_cast<f32x2*>(xs0 + 2 * kGXsHalves);     // [2][16][kGCRow]
+  f16* xs0 = reinterpret_cast<f16*>(smem);                     // [2][TOK][XROW]
+  f32x2* cx0 = reinterpret_cast<f32x2*>(xs0 + 2 * G::XS);      // [2][TOK][CROW]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -94,18 +124,18 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   const int unit = blockIdx.x * kGWaves + wave;
   const int kbA = blockIdx.y * a.kb_per_split;
   const int kbN = min(a.KB, kbA + a.kb_per_split) - kbA;  // chunks of this split (>= 1)
-  const int n_ranges = (kbN + kGRC - 1) / kGRC;
+  const int n_ranges = (kbN + RC - 1) / RC;
   const Unpack U{to_vgpr(a.unpack[0]), to_vgpr(a.unpack[1]), a.unpack[2], a.unpack[3]};
   const __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.w16, (short)0, (int)a.w16_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.sb16, (short)0, (int)a.sb16_bytes, 0x00020000);
 
-  u32x4 wr[kGRC][NT];
-  u32x2 sr[kGRC][NT];
+  u32x4 wr[RC][NT];
+  u32x2 sr[RC][NT];
   // Chunk c of range r into slot c (zeros past the split or the matrix).
   auto load = [&](int r, int c) {
-    const int kl = r * kGRC + c;
+    const int kl = r * RC + c;
     const bool ok = unit < a.n_units && kl < kbN;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -116,25 +146,22 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
       sr[c][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
     }
   };
-  // Activations of range r: vector v = tid + i * threads is (token v / (16 kGRC),
-  // vector v % (16 kGRC) of the range); eight consecutive lanes hold a 64-group.
+  // Activations of range r: thread tid stages vector svi = tid % VPR of token
+  // rows stok + RPP i (i < PER); eight consecutive lanes hold a 64-group.
   // Buffer loads with out-of-range offsets (tokens >= M, k past the split or K,
   // ranges past the last) read zeros, so every load is issued unconditionally
   // and the compiler can count the loads in flight exactly.
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.M_tokens * a.ldx * (int)sizeof(f16), 0x00020000);
-  // With 512 threads and 128 vectors per token row, thread tid stages vector
-  // tid % 128 of token rows tid / 128 + 4 i.
-  static_assert(kGThreads == 4 * 16 * kGRC && kGStagePerThread == 4, "staging map");
-  const int svi = tid & (16 * kGRC - 1);
-  const int stok = tid / (16 * kGRC);
-  f16x8 xv[kGStagePerThread];
+  const int svi = tid & (G::VPR - 1);
+  const int stok = tid / G::VPR;
+  f16x8 xv[G::PER];
   auto stage_load = [&](int r) {
-    const int k = (kbA + r * kGRC) * 128 + 8 * svi;
-    const int kok = (int)(k < a.K) & (int)(8 * svi < (kbN - r * kGRC) * 128);
+    const int k = (kbA + r * RC) * 128 + 8 * svi;
+    const int kok = (int)(k < a.K) & (int)(8 * svi < (kbN - r * RC) * 128);
 #pragma unroll
-    for (int i = 0; i < kGStagePerThread; ++i) {
-      const int tok = stok + 4 * i;
+    for (int i = 0; i < G::PER; ++i) {
+      const int tok = stok + G::RPP * i;
       // Branch-free select of the offset (a conditional here became divergent
       // control flow with full memory waits inside it).
       const int m = -(kok & (int)(tok < a.M_tokens));
@@ -143,37 +170,39 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
     }
   };
   auto stage_store = [&](int buf) {
-    f16* xs = xs0 + buf * kGXsHalves;
-    f32x2* cx = cx0 + buf * kGCxPairs;
+    f16* xs = xs0 + buf * G::XS;
+    f32x2* cx = cx0 + buf * G::CX;
 #pragma unroll
-    for (int i = 0; i < kGStagePerThread; ++i) {
-      const int tok = stok + 4 * i, vi = svi;
+    for (int i = 0; i < G::PER; ++i) {
+      const int tok = stok + G::RPP * i, vi = svi;
       float corr = 0.f, sum = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < 8 * !DQ; ++e) {
         const float f = h2f(xv[i][e]);
         sum += f;
         corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
       }
-      corr = group_sum<8>(corr);
-      sum = group_sum<8>(sum);
-      *reinterpret_cast<f16x8*>(xs + (size_t)tok * kGXRow + 8 * vi) = xv[i];
-      if ((tid & 7) == 0) cx[tok * kGCRow + (vi >> 3)] = f32x2{corr, sum};
+      *reinterpret_cast<f16x8*>(xs + (size_t)tok * G::XROW + 8 * vi) = xv[i];
+      if (!DQ) {
+        corr = group_sum<8>(corr);
+        sum = group_sum<8>(sum);
+        if ((tid & 7) == 0) cx[tok * G::CROW + (vi >> 3)] = f32x2{corr, sum};
+      }
     }
   };
 
   // Weights of range 0 first, then its activations (both one latency away).
 #pragma unroll
-  for (int c = 0; c < kGRC; ++c) load(0, c);
+  for (int c = 0; c < RC; ++c) load(0, c);
   stage_load(0);
   stage_store(0);
   __syncthreads();
 
-  float acc[NT][4];
+  f32x4 acc[NT][MB];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int vi = 0; vi < 4; ++vi) acc[t][vi] = 0.f;
+    for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int r = 0; r < n_ranges; ++r) {
     // The next range's weights are requested unconditionally (past the last
@@ -181,42 +210,80 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
     // exists.
     const bool more = r + 1 < n_ranges;
     if (more) stage_load(r + 1);
-    const f16* xs = xs0 + (r & 1) * kGXsHalves;
-    const f32x2* cx = cx0 + (r & 1) * kGCxPairs;
-    // A operand: token lane % 16 (rows past M are zeros), k sub-block lane / 16.
-    const f16* xa = xs + (size_t)(lane & 15) * kGXRow + 8 * kq;
+    const f16* xs = xs0 + (r & 1) * G::XS;
+    const f32x2* cx = cx0 + (r & 1) * G::CX;
+    // A operand: token 16 mb + lane % 16 (rows past M are zeros), k sub-block lane / 16.
+    const f16* xa = xs + (size_t)(lane & 15) * G::XROW + 8 * kq;
     // Only the last range of a split can be partial (uniform across the
     // workgroup); keeping the guard makes each chunk its own block, which the
     // register allocator needs.
-    const int n_here = min(kGRC, kbN - r * kGRC);
+    const int n_here = min(RC, kbN - r * RC);
 #pragma unroll
-    for (int c = 0; c < kGRC; ++c) {
-      if (c < n_here) {
-        const f16* xk = xa + c * 128;
-        f16x8 A[4];
+    for (int c = 0; c < RC; ++c) {
+      if (c < n_here && DQ) {
+        // Word q of a lane holds 8 k of group q / 2; its unpacked elements are
+        // 1024 + n or 64 + n (pattern of unpack_word), subtracted exactly.
+        const f16x8 magic = {(f16)1024.f, (f16)1024.f, (f16)64.f, (f16)64.f,
+                             (f16)1024.f, (f16)1024.f, (f16)64.f, (f16)64.f};
+        f16x8 B[NT][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) A[q] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * q));
-        f32x4 cxv[4];
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int vi = 0; vi < 4; ++vi)
-          cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (4 * kq + vi) * kGCRow + 2 * c);
+          for (int q = 0; q < 4; ++q) {
+            const f16x2 sb = as_h2(sr[c][t][q >> 1]);
+            const f16x8 sc = {sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x, sb.x};
+            const f16x8 bi = {sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y};
+            B[t][q] = __builtin_elementwise_fma(unpack_word(wr[c][t][q], U) - magic, sc, bi);
+          }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const f16* xk = xa + (size_t)16 * mb * G::XROW + c * 128;
+          f16x8 A[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) A[q] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * q));
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[q], B[t][q], acc[t][mb], 0, 0, 0);
+        }
+      } else if (c < n_here) {
+        // The chunk's B fragments are unpacked once for all token tiles.
+        f16x8 B[NT][4];
+        f16x2 sb[NT][2];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-          f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], unpack_word(wr[c][t][0], U), z4, 0, 0, 0);
-          f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], unpack_word(wr[c][t][2], U), z4, 0, 0, 0);
-          d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], unpack_word(wr[c][t][1], U), d0, 0, 0, 0);
-          d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], unpack_word(wr[c][t][3], U), d1, 0, 0, 0);
-          const f16x2 sb0 = as_h2(sr[c][t][0]);
-          const f16x2 sb1 = as_h2(sr[c][t][1]);
 #pragma unroll
-          for (int vi = 0; vi < 4; ++vi) {
-            float x = acc[t][vi];
-            x = __builtin_fmaf(h2f(sb0.x), d0[vi] - cxv[vi][0], x);
-            x = __builtin_fmaf(h2f(sb0.y), cxv[vi][1], x);
-            x = __builtin_fmaf(h2f(sb1.x), d1[vi] - cxv[vi][2], x);
-            x = __builtin_fmaf(h2f(sb1.y), cxv[vi][3], x);
-            acc[t][vi] = x;
+          for (int q = 0; q < 4; ++q) B[t][q] = unpack_word(wr[c][t][q], U);
+          sb[t][0] = as_h2(sr[c][t][0]);
+          sb[t][1] = as_h2(sr[c][t][1]);
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const f16* xk = xa + (size_t)16 * mb * G::XROW + c * 128;
+          f16x8 A[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) A[q] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * q));
+          f32x4 cxv[4];
+#pragma unroll
+          for (int vi = 0; vi < 4; ++vi)
+            cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (16 * mb + 4 * kq + vi) * G::CROW + 2 * c);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[t][0], z4, 0, 0, 0);
+            f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], B[t][2], z4, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], B[t][1], d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], B[t][3], d1, 0, 0, 0);
+#pragma unroll
+            for (int vi = 0; vi < 4; ++vi) {
+              float x = acc[t][mb][vi];
+              x = __builtin_fmaf(h2f(sb[t][0].x), d0[vi] - cxv[vi][0], x);
+              x = __builtin_fmaf(h2f(sb[t][0].y), cxv[vi][1], x);
+              x = __builtin_fmaf(h2f(sb[t][1].x), d1[vi] - cxv[vi][2], x);
+              x = __builtin_fmaf(h2f(sb[t][1].y), cxv[vi][3], x);
+              acc[t][mb][vi] = x;
+            }
           }
         }
       }
@@ -231,68 +298,96 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   if (gridDim.y == 1) {
     const int row = unit * 16 + j;
 #pragma unroll
-    for (int vi = 0; vi < 4; ++vi) {
-      const int tok = 4 * kq + vi;
-      if (tok < a.M_tokens && row < a.N) t16g_store<EPI>(a, tok, row, acc[0][vi], acc[NT - 1][vi]);
-    }
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int vi = 0; vi < 4; ++vi) {
+        const int tok = 16 * mb + 4 * kq + vi;
+        if (tok < a.M_tokens && row < a.N) t16g_store<EPI>(a, tok, row, acc[0][mb][vi], acc[NT - 1][mb][vi]);
+      }
   } else {
     // Partial tile of this K split: [split][token][column], column = tile * 16 + row in tile.
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int col = (unit + t * a.pair_offset) * 16 + j;
 #pragma unroll
-      for (int vi = 0; vi < 4; ++vi)
-        a.part_ws[((size_t)blockIdx.y * kGTok + 4 * kq + vi) * a.part_cols + col] = acc[t][vi];
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int vi = 0; vi < 4; ++vi)
+          a.part_ws[((size_t)blockIdx.y * G::TOK + 16 * mb + 4 * kq + vi) * a.part_cols + col] = acc[t][mb][vi];
     }
   }
 }
 
 // Sums the K-split partials in split order and applies the epilogue: one thread
-// per (token, output row).
+// per (token, output row); tok_stride = token rows per split in the workspace.
 template <int EPI>
-__global__ void t16g_reduce_kernel(T16Args a, int n_splits, int up_col) {
+__global__ void t16g_reduce_kernel(T16Args a, int n_splits, int up_col, int tok_stride) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const int tok = (int)(idx / a.N), row = (int)(idx % a.N);
   if (tok >= a.M_tokens) return;
   float v0 = 0.f, v1 = 0.f;
   for (int sp = 0; sp < n_splits; ++sp) {
-    const float* p = a.part_ws + ((size_t)sp * kGTok + tok) * a.part_cols;
+    const float* p = a.part_ws + ((size_t)sp * tok_stride + tok) * a.part_cols;
     v0 += p[row];
     if (EPI == Q4_EPI_SWIGLU) v1 += p[up_col + row];
   }
   t16g_store<EPI>(a, tok, row, v0, v1);
 }
 
-template <int NT, int EPI>
-void t16g_attr() {
+template <int NT, int EPI, int MB, int RC, bool DQ>
+void t16g_launch_shape(const T16Args& a, dim3 grid, hipStream_t s) {
+  using G = GemmShape<MB, RC>;
   static bool set = false;
-  if (set) return;
-  set = true;
-  if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)gemm_smem_bytes()) != hipSuccess)
-    (void)hipGetLastError();
+  if (!set) {
+    set = true;
+    if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI, MB, RC, DQ>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)G::smem) != hipSuccess)
+      (void)hipGetLastError();
+  }
+  hipLaunchKernelGGL((t16g_kernel<NT, EPI, MB, RC, DQ>), grid, dim3(kGThreads), G::smem, s, a);
+}
+
+// The (MB, RC, DQ) triples here are the ones gemm_cfg returns.
+template <int NT, int EPI>
+void t16g_launch_epi(const T16Args& a, GemmCfg cfg, dim3 grid, hipStream_t s) {
+  if (cfg.mb == 1)
+    t16g_launch_shape<NT, EPI, 1, 8, false>(a, grid, s);
+  else if (cfg.mb == 2)
+    t16g_launch_shape<NT, EPI, 2, 4, true>(a, grid, s);
+  else
+    t16g_launch_shape<NT, EPI, 4, 4, true>(a, grid, s);
+}
+
+size_t gemm_ws_bytes_cfg(int KB, int n_units, int NT, GemmCfg cfg) {
+  const int splits = gemm_splits(KB, n_units, cfg.rc);
+  return splits <= 1 ? 0 : (size_t)splits * 16 * cfg.mb * n_units * 16 * NT * sizeof(float);
 }
 
 }  // namespace
 
-size_t t16_gemm16_ws_bytes(int K, int n_units, int NT) {
+size_t t16_gemm_ws_bytes(int K, int n_units, int NT) {
   const int KB = (K + 127) / 128;
-  const int splits = gemm_splits(KB, n_units);
-  return splits <= 1 ? 0 : (size_t)splits * kGTok * n_units * 16 * NT * sizeof(float);
+  size_t need = 0;
+  for (int m = 16; m <= kTile16GemmMaxTokens; m *= 2) {
+    const size_t b = gemm_ws_bytes_cfg(KB, n_units, NT, gemm_cfg(m));
+    if (b > need) need = b;
+  }
+  return need;
 }
 
-int t16_gemm16_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s) {
-  if (M < 1 || M > kGTok || a.ln_w != nullptr || a.argmax_keys != nullptr || a.x_parts != nullptr ||
+int t16_gemm_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s) {
+  if (M < 1 || M > kTile16GemmMaxTokens || a.ln_w != nullptr || a.argmax_keys != nullptr || a.x_parts != nullptr ||
       (epi != Q4_EPI_STORE && epi != Q4_EPI_RESID && epi != Q4_EPI_SWIGLU) || a.K <= 0 || a.K % 64 != 0) {
     axm_set_error("tile16 gemm: M=%d (1..%d), epi=%d, K=%d unsupported (normalized activations, store / "
-                  "residual / SwiGLU epilogues)", M, kGTok, epi, a.K);
+                  "residual / SwiGLU epilogues)", M, kTile16GemmMaxTokens, epi, a.K);
     return -2;
   }
   const int NT = epi == Q4_EPI_SWIGLU ? 2 : 1;
+  const GemmCfg cfg = gemm_cfg(M);
   a.KB = (a.K + 127) / 128;
-  const int splits = gemm_splits(a.KB, a.n_units);
+  const int splits = gemm_splits(a.KB, a.n_units, cfg.rc);
   const int kbps = (a.KB + splits - 1) / splits;
-  const size_t need = t16_gemm16_ws_bytes(a.K, a.n_units, NT);
+  const size_t need = gemm_ws_bytes_cfg(a.KB, a.n_units, NT, cfg);
   if (need > 0 && (ws == nullptr || ws_bytes < need)) {
     axm_set_error("tile16 gemm: workspace of %zu bytes needed, %zu given", need, ws_bytes);
     return -1;
@@ -309,47 +404,44 @@ int t16_gemm16_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hip
   a.unpack[2] = 0x64006400u;
   a.unpack[3] = 0x54005400u;
   const dim3 grid((a.n_units + kGWaves - 1) / kGWaves, splits);
-  const size_t smem = gemm_smem_bytes();
   switch (epi) {
     case Q4_EPI_STORE:
-      t16g_attr<1, Q4_EPI_STORE>();
-      hipLaunchKernelGGL((t16g_kernel<1, Q4_EPI_STORE>), grid, dim3(kGThreads), smem, s, a);
+      t16g_launch_epi<1, Q4_EPI_STORE>(a, cfg, grid, s);
       break;
     case Q4_EPI_RESID:
-      t16g_attr<1, Q4_EPI_RESID>();
-      hipLaunchKernelGGL((t16g_kernel<1, Q4_EPI_RESID>), grid, dim3(kGThreads), smem, s, a);
+      t16g_launch_epi<1, Q4_EPI_RESID>(a, cfg, grid, s);
       break;
     default:
-      t16g_attr<2, Q4_EPI_SWIGLU>();
-      hipLaunchKernelGGL((t16g_kernel<2, Q4_EPI_SWIGLU>), grid, dim3(kGThreads), smem, s, a);
+      t16g_launch_epi<2, Q4_EPI_SWIGLU>(a, cfg, grid, s);
       break;
   }
   if (splits > 1) {
     const long n = (long)M * a.N;
     const dim3 rg((unsigned)((n + 255) / 256));
     const int up_col = a.pair_offset * 16;
+    const int ts = 16 * cfg.mb;
     if (epi == Q4_EPI_STORE)
-      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_STORE>, rg, dim3(256), 0, s, a, splits, up_col);
+      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_STORE>, rg, dim3(256), 0, s, a, splits, up_col, ts);
     else if (epi == Q4_EPI_RESID)
-      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_RESID>, rg, dim3(256), 0, s, a, splits, up_col);
+      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_RESID>, rg, dim3(256), 0, s, a, splits, up_col, ts);
     else
-      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_SWIGLU>, rg, dim3(256), 0, s, a, splits, up_col);
+      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_SWIGLU>, rg, dim3(256), 0, s, a, splits, up_col, ts);
   }
   return 0;
 }
 
 // ---------------------------------------------------------------------------
-// C ABI: multi-token GEMM on tile16 copies (16 tokens per weight pass).
+// C ABI: multi-token GEMM on tile16 copies (up to 64 tokens per weight pass).
 // ---------------------------------------------------------------------------
 extern "C" size_t axm_qmm_q4_tile16_workspace_bytes(int K, int N, int swiglu) {
   if (K <= 0 || N <= 0) return 0;
-  return t16_gemm16_ws_bytes(K, (N + 15) / 16, swiglu ? 2 : 1);
+  return t16_gemm_ws_bytes(K, (N + 15) / 16, swiglu ? 2 : 1);
 }
 
 static int qmm_tile16_rows(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
                            int N, int epi, void* ws, size_t ws_bytes, hipStream_t s) {
-  for (int m0 = 0; m0 < M; m0 += kTile16GemmTokens) {
-    const int mc = (M - m0) < kTile16GemmTokens ? (M - m0) : kTile16GemmTokens;
+  for (int m0 = 0; m0 < M; m0 += kTile16GemmMaxTokens) {
+    const int mc = (M - m0) < kTile16GemmMaxTokens ? (M - m0) : kTile16GemmMaxTokens;
     T16Args a{};
     a.x = (const f16*)x + (size_t)m0 * K;
     a.ldx = K;
@@ -367,7 +459,7 @@ static int qmm_tile16_rows(const void* x, const void* w16, const void* sb16, con
     a.y = (f16*)y + (size_t)m0 * N;
     a.ldy = N;
     a.bias = (const f16*)bias;
-    const int rc = t16_gemm16_launch(a, mc, epi, (float*)ws, ws_bytes, s);
+    const int rc = t16_gemm_launch(a, mc, epi, (float*)ws, ws_bytes, s);
     if (rc) return rc;
   }
   return 0;

@@ -498,7 +498,7 @@ struct axm_runner {
   int gemv_rows(const Mat& m, int epi, int out_rows, GemvCall c, int T, hipStream_t s) {
     if (m.w16 != nullptr && T > 4 && c.argmax_keys == nullptr && c.q_dim == 0 &&
         (epi == Q4_EPI_STORE || epi == Q4_EPI_RESID || epi == Q4_EPI_SWIGLU)) {
-      // Multi-token GEMM: 16 tokens per weight pass, activations normalized first
+      // Multi-token GEMM: up to 64 tokens per weight pass, activations normalized first
       // (into x_norm_out when the caller wants them, else into the norm scratch).
       const f16* xall = c.x;
       if (c.ln_w != nullptr) {
@@ -506,8 +506,8 @@ struct axm_runner {
         launch_rmsnorm(c.x, c.ln_w, nrm, T, m.K, c.eps, s);
         xall = nrm;
       }
-      for (int t0 = 0; t0 < T; t0 += kTile16GemmTokens) {
-        const int mc = (T - t0) < kTile16GemmTokens ? (T - t0) : kTile16GemmTokens;
+      for (int t0 = 0; t0 < T; t0 += kTile16GemmMaxTokens) {
+        const int mc = (T - t0) < kTile16GemmMaxTokens ? (T - t0) : kTile16GemmMaxTokens;
         const f16* xin = xall + (size_t)t0 * c.ldx;
         T16Args a{};
         a.x = xin;
@@ -525,7 +525,7 @@ struct axm_runner {
         a.bias = c.bias;
         a.resid = c.resid ? c.resid + (size_t)t0 * c.ldr : nullptr;
         a.ldr = c.ldr;
-        const int rc = t16_gemm16_launch(a, mc, epi, ws, ws_bytes, s);
+        const int rc = t16_gemm_launch(a, mc, epi, ws, ws_bytes, s);
         if (rc) return rc;
       }
       return 0;
@@ -723,11 +723,11 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
   r->ws_bytes = attn_workspace_bytes(T, d.n_head, d.head_dim, r->max_splits);
   if (r->m_o.size() == (size_t)L && r->m_o[0].w16 != nullptr) {
     // Partial tiles of the multi-token GEMM share the attention workspace.
-    const size_t g[] = {t16_gemm16_ws_bytes(d.d_model, r->qkv_dim / 16 + ((r->qkv_dim % 16) != 0), 1),
-                        t16_gemm16_ws_bytes(r->q_dim, (d.d_model + 15) / 16, 1),
-                        t16_gemm16_ws_bytes(d.d_model, d.hidden_dim / 16, 2),
-                        t16_gemm16_ws_bytes(d.hidden_dim, (d.d_model + 15) / 16, 1),
-                        t16_gemm16_ws_bytes(d.d_model, (d.vocab_size + 15) / 16, 1)};
+    const size_t g[] = {t16_gemm_ws_bytes(d.d_model, r->qkv_dim / 16 + ((r->qkv_dim % 16) != 0), 1),
+                        t16_gemm_ws_bytes(r->q_dim, (d.d_model + 15) / 16, 1),
+                        t16_gemm_ws_bytes(d.d_model, d.hidden_dim / 16, 2),
+                        t16_gemm_ws_bytes(d.hidden_dim, (d.d_model + 15) / 16, 1),
+                        t16_gemm_ws_bytes(d.d_model, (d.vocab_size + 15) / 16, 1)};
     for (size_t b : g) r->ws_bytes = b > r->ws_bytes ? b : r->ws_bytes;
   }
   struct {

@@ -56,11 +56,13 @@ int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb16, const vo
 int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const void* gu16, const void* gusb16,
                              void* y, int M, int K, int H, void* stream);
 /* Multi-token GEMM on the tile16 copy: y[M][N] = x @ W^T (+ bias) with every weight
- * chunk streamed once per 16 tokens (the M > 8 path of qmm_q4_marlin_mps: kernels
+ * chunk streamed once per 64 tokens (the M > 8 path of qmm_q4_marlin_mps: kernels
  * qmm_q4_marlin_m8_apple_kernel / qmm_q4_marlin_apple_kernel, metal_kernels.metal:
- * 2268-2684; dispatch mps_kernels.mm:1272-1312; CPU form quant.py:664-684).  K is
- * split across workgroups; `workspace` holds the fp32 partial tiles
- * (axm_qmm_q4_tile16_workspace_bytes; 0 bytes when K <= 4096). */
+ * 2268-2684; dispatch mps_kernels.mm:1272-1312; CPU form quant.py:664-684).  Up to
+ * 16 tokens per launch keep the GEMV's arithmetic; 17-64 tokens dequantize each
+ * weight to fp16 q * scale + bias before the MFMAs (as the reference's kernel does).
+ * K is split across workgroups; `workspace` holds the fp32 partial tiles
+ * (axm_qmm_q4_tile16_workspace_bytes: enough for any M, 0 when no split is used). */
 size_t axm_qmm_q4_tile16_workspace_bytes(int K, int N, int swiglu);
 int axm_qmm_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
                       int N, void* workspace, size_t workspace_bytes, void* stream);

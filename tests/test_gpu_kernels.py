@@ -202,12 +202,14 @@ def test_tile16_qmv_matches_oracle(dev, M, N_, K, bias):
 @pytest.mark.parametrize(
     "M,N_,K,bias",
     [(5, 96, 256, True), (16, 13, 192, False), (17, 768, 704, False), (37, 1408, 4096, True), (64, 4096, 11008, False),
-     (16, 12288, 4096, False), (8, 32000, 4096, False), (20, 96, 5120, True)],
+     (16, 12288, 4096, False), (8, 32000, 4096, False), (20, 96, 5120, True), (32, 4608, 4096, False),
+     (48, 12288, 4096, True), (70, 640, 1024, True), (131, 256, 512, False)],
 )
 def test_tile16_qmm_matches_oracle(dev, M, N_, K, bias):
-    """Multi-token GEMM (16 tokens per weight pass, K split over workgroups above 2048
-    with fp32 partial tiles summed in order) vs the oracle's dequantize-then-matmul; the
-    same bound as the GEMV (fp32 accumulation order and the fp16 output rounding)."""
+    """Multi-token GEMM (one to four 16-token MFMA tiles per weight pass, up to 64
+    tokens per launch, K split over workgroups with fp32 partial tiles summed in order)
+    vs the oracle's dequantize-then-matmul; the same bound as the GEMV (fp32
+    accumulation order and the fp16 output rounding)."""
     from axiomlm_amd.kernels import qmm_q4_tile16, repack_q4_marlin_tile16
 
     print(f"[tile16_qmm] M={M} N={N_} K={K} bias={bias}", flush=True)
@@ -224,7 +226,7 @@ def test_tile16_qmm_matches_oracle(dev, M, N_, K, bias):
 
 
 @pytest.mark.parametrize("M,K,H,norm", [(16, 4096, 11008, True), (9, 256, 704, False), (33, 704, 256, True),
-                                        (12, 4608, 256, True)])
+                                        (12, 4608, 256, True), (24, 1024, 512, False), (64, 4096, 11008, True)])
 def test_tile16_qmm_swiglu_matches_oracle(dev, M, K, H, norm):
     """RMSNorm -> [W_gate; W_up] multi-token GEMM -> silu(g) * u; bound as for the
     single-launch GEMV form below."""
