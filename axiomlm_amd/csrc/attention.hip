@@ -73,11 +73,15 @@ __device__ __forceinline__ void kv_store_lane(const KvView& kv, int which, int h
   }
 }
 
-__global__ void kv_write_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld,
-                                int write_pos, const int* __restrict__ write_pos_dev) {
-  const int lane = threadIdx.x;  // 64 lanes
+// Four waves per workgroup, one (token, k|v, kv head, 64-group) per wave.
+constexpr int kKvWriteWaves = 4;
+__global__ void __launch_bounds__(kKvWriteWaves * 64)
+    kv_write_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld, int write_pos,
+                    const int* __restrict__ write_pos_dev, int n_items) {
+  const int lane = threadIdx.x & 63;
   const int G = kv.hd / 64;
-  int idx = blockIdx.x;
+  int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
+  if (idx >= n_items) return;
   const int g = idx % G;
   idx /= G;
   const int h = idx % kv.Hkv;
@@ -580,21 +584,43 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnParams p) {
   }
 }
 
-// Merge split partials: one block per query row, hd threads.
+// Merges the split partials of one query row: wave 0 takes the splits' (m, l)
+// (one split per lane, in steps of 64), forms the global max, the weights
+// 2^(m_s - max) (kept in LDS) and the total l; then thread e sums its output
+// element over the splits in order, all split loads independent.
+// Launch: max(hd, 64) threads rounded to whole waves, (n_splits + 1) floats of LDS.
 __global__ void attn_reduce_kernel(const float* __restrict__ ws, f16* __restrict__ out, int n_splits, int hd) {
+  extern __shared__ float a_sh[];
   const int row = blockIdx.x;
   const int e = threadIdx.x;
-  const float* base = ws + (size_t)row * n_splits * (2 + hd);
-  float mm = kNegBig;
-  for (int s = 0; s < n_splits; ++s) mm = fmaxf(mm, base[(size_t)s * (2 + hd)]);
-  float ll = 0.f, oo = 0.f;
-  for (int s = 0; s < n_splits; ++s) {
-    const float* ps = base + (size_t)s * (2 + hd);
-    const float a = exp2f(ps[0] - mm);
-    ll += ps[1] * a;
-    oo += ps[2 + e] * a;
+  const size_t st = 2 + hd;
+  const float* base = ws + (size_t)row * n_splits * st;
+  if (e < 64) {
+    float mm = kNegBig;
+    for (int sp = e; sp < n_splits; sp += 64) mm = fmaxf(mm, base[sp * st]);
+    mm = wave_max(mm);
+    float ll = 0.f;
+    for (int sp = e; sp < n_splits; sp += 64) {
+      const float a = exp2f(base[sp * st] - mm);
+      a_sh[sp] = a;
+      ll += base[sp * st + 1] * a;
+    }
+    ll = wave_sum(ll);
+    if (e == 0) a_sh[n_splits] = ll;
   }
-  if (e < hd) out[(size_t)row * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+  __syncthreads();
+  if (e >= hd) return;
+  const float ll = a_sh[n_splits];
+  float oo = 0.f;
+#pragma unroll 8
+  for (int sp = 0; sp < n_splits; ++sp) oo += base[sp * st + 2 + e] * a_sh[sp];
+  out[(size_t)row * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+}
+
+void launch_attn_reduce(const float* ws, f16* out, int rows, int n_splits, int hd, hipStream_t s) {
+  const int threads = ((hd > 64 ? hd : 64) + 63) / 64 * 64;
+  hipLaunchKernelGGL(attn_reduce_kernel, dim3(rows), dim3(threads), (n_splits + 1) * sizeof(float), s, ws, out,
+                     n_splits, hd);
 }
 
 // Decode uses 16 waves (8 for more than 2 rows per workgroup, which need the
@@ -642,9 +668,10 @@ int pick_qr(int rows) {
 int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int ld_rows, int T, int write_pos,
                     const int* write_pos_dev, hipStream_t s) {
   const int G = kv.hd / 64;
-  const unsigned blocks = (unsigned)T * 2 * kv.Hkv * G;
-  hipLaunchKernelGGL(kv_write_kernel, dim3(blocks), dim3(64), 0, s, kv, k_rows, v_rows, ld_rows, write_pos,
-                     write_pos_dev);
+  const int items = T * 2 * kv.Hkv * G;
+  const unsigned blocks = (unsigned)((items + kKvWriteWaves - 1) / kKvWriteWaves);
+  hipLaunchKernelGGL(kv_write_kernel, dim3(blocks), dim3(kKvWriteWaves * 64), 0, s, kv, k_rows, v_rows, ld_rows,
+                     write_pos, write_pos_dev, items);
   return 0;
 }
 
@@ -733,7 +760,7 @@ int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int ac
   }
   if (rc) return rc;
   if (n_splits > 1)
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3(kv.B * Hq), dim3(kv.hd), 0, s, ws, out, n_splits, kv.hd);
+    launch_attn_reduce(ws, out, kv.B * Hq, n_splits, kv.hd, s);
   return 0;
 }
 
@@ -1178,7 +1205,7 @@ int launch_tree_attention(const f16* q, const KvView& kv, f16* out, int Hq, int 
   }
   if (rc) return rc;
   if (n_splits > 1)
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3(T * Hq), dim3(kv.hd), 0, s, ws, out, n_splits, kv.hd);
+    launch_attn_reduce(ws, out, T * Hq, n_splits, kv.hd, s);
   return 0;
 }
 

@@ -40,6 +40,60 @@ __global__ void __launch_bounds__(kNormThreads)
   }
 }
 
+// Row-vectorized forms of the two norms (same per-element rounding) for rows of
+// D % 8 == 0, D <= 8 * kNormThreads * kNormVec with 16-byte aligned rows: every
+// thread loads its 8-element vectors once, keeps them in registers across the
+// block reduction and writes the normalized vectors.  ADD: x = half(x + r) first.
+constexpr int kNormVec = 4;
+template <bool ADD>
+__global__ void __launch_bounds__(kNormThreads)
+    rmsnorm_vec_kernel(f16* __restrict__ x, const f16* __restrict__ r, const f16* __restrict__ w,
+                       f16* __restrict__ y, int D, float eps) {
+  __shared__ float red[kNormThreads / 64];
+  const int nv = D / 8;
+  f16x8* xr = reinterpret_cast<f16x8*>(x + (size_t)blockIdx.x * D);
+  const f16x8* rr = reinterpret_cast<const f16x8*>(r + (size_t)blockIdx.x * D);
+  f16x8* yr = reinterpret_cast<f16x8*>(y + (size_t)blockIdx.x * D);
+  const f16x8* wr = reinterpret_cast<const f16x8*>(w);
+  f16x8 v[kNormVec];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormVec; ++i) {
+    const int j = threadIdx.x + i * kNormThreads;
+    if (j < nv) {
+      v[i] = xr[j];
+      if (ADD) {
+        const f16x8 rv = rr[j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = f2h(h2f(v[i][e]) + h2f(rv[e]));
+        xr[j] = v[i];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = h2f(v[i][e]);
+        s += h2f(f2h(f * f));
+      }
+    }
+  }
+  const float rinv = rms_inv_fp16(block_sum_256(s, red), D, eps);
+#pragma unroll
+  for (int i = 0; i < kNormVec; ++i) {
+    const int j = threadIdx.x + i * kNormThreads;
+    if (j < nv) {
+      const f16x8 wv = wr[j];
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = f2h(h2f(f2h(h2f(v[i][e]) * rinv)) * h2f(wv[e]));
+      yr[j] = o;
+    }
+  }
+}
+
+bool norm_vec_ok(const void* x, const void* r, const void* w, const void* y, int D) {
+  const uintptr_t al = (uintptr_t)x | (uintptr_t)r | (uintptr_t)w | (uintptr_t)y;
+  return D % 8 == 0 && D <= 8 * kNormThreads * kNormVec && (al & 15) == 0;
+}
+
 // x = half(x + r);  y = rmsnorm(x)   (transformer.py:1176-1178)
 __global__ void __launch_bounds__(kNormThreads)
     add_rmsnorm_kernel(f16* __restrict__ x, const f16* __restrict__ r, const f16* __restrict__ w,
@@ -216,11 +270,18 @@ __global__ void __launch_bounds__(kQ8Threads)
 }  // namespace
 
 int launch_rmsnorm(const f16* x, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, w, y, D, eps);
+  if (norm_vec_ok(x, x, w, y, D))
+    hipLaunchKernelGGL(rmsnorm_vec_kernel<false>, dim3(rows), dim3(kNormThreads), 0, s, (f16*)x, (const f16*)nullptr,
+                       w, y, D, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, w, y, D, eps);
   return 0;
 }
 int launch_add_rmsnorm(f16* x, const f16* r, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s) {
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, r, w, y, D, eps);
+  if (norm_vec_ok(x, r, w, y, D))
+    hipLaunchKernelGGL(rmsnorm_vec_kernel<true>, dim3(rows), dim3(kNormThreads), 0, s, x, r, w, y, D, eps);
+  else
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, r, w, y, D, eps);
   return 0;
 }
 int launch_swiglu(const f16* gu, f16* y, int rows, int H, hipStream_t s) {

@@ -326,6 +326,7 @@ __global__ void t16g_reduce_kernel(T16Args a, int n_splits, int up_col, int tok_
   const int tok = (int)(idx / a.N), row = (int)(idx % a.N);
   if (tok >= a.M_tokens) return;
   float v0 = 0.f, v1 = 0.f;
+#pragma unroll 4
   for (int sp = 0; sp < n_splits; ++sp) {
     const float* p = a.part_ws + ((size_t)sp * tok_stride + tok) * a.part_cols;
     v0 += p[row];

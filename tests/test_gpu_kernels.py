@@ -391,15 +391,35 @@ def test_ternary_and_q2_pack_bit_exact(dev, src):
 # ---------------------------------------------------------------------------
 # norms / activations / argmax
 # ---------------------------------------------------------------------------
-def test_rmsnorm_bit_exact(dev):
+@pytest.mark.parametrize("rows,D", [(5, 4096), (64, 4096), (3, 704), (2, 100), (2, 8200)])
+def test_rmsnorm_bit_exact(dev, rows, D):
+    """Row-vectorized kernel (D % 8 == 0, D <= 8192) and the element loop (D = 100, 8200)."""
     from axiomlm_amd.kernels import fused_rmsnorm
 
-    rng = np.random.default_rng(4)
-    x = rng.standard_normal((5, 4096)).astype(F16)
-    w = (1 + 0.1 * rng.standard_normal(4096)).astype(F16)
+    rng = np.random.default_rng(4 + D)
+    x = rng.standard_normal((rows, D)).astype(F16)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(F16)
     ref = om.rmsnorm_fp16(x, w, 1e-5)
     got = N(fused_rmsnorm(T(x, dev), T(w, dev), 1e-5))
     # the fp32 mean may round differently in rare cases (summation order): allow 1 ulp on <0.1% of rows
+    d = np.abs(got.view(np.uint16).astype(np.int32) - ref.view(np.uint16).astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3
+
+
+@pytest.mark.parametrize("rows,D", [(4, 4096), (3, 100)])
+def test_add_rmsnorm_bit_exact(dev, rows, D):
+    """x += r in place (fp16 add, bit-exact), then RMSNorm of the new x (same bound as above)."""
+    from axiomlm_amd.kernels import add_rmsnorm_infer
+
+    rng = np.random.default_rng(40 + D)
+    x = rng.standard_normal((rows, D)).astype(F16)
+    r = rng.standard_normal((rows, D)).astype(F16)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(F16)
+    xs = (x.astype(F32) + r.astype(F32)).astype(F16)
+    ref = om.rmsnorm_fp16(xs, w, 1e-5)
+    xt = T(x, dev)
+    got = N(add_rmsnorm_infer(xt, T(r, dev), T(w, dev), 1e-5))
+    assert np.array_equal(N(xt).view(np.uint16), xs.view(np.uint16))
     d = np.abs(got.view(np.uint16).astype(np.int32) - ref.view(np.uint16).astype(np.int32))
     assert d.max() <= 1 and (d > 0).mean() < 1e-3
 
