@@ -49,6 +49,11 @@ struct T16Args {
   int kb_per_split;
   float* part_ws;
   int part_cols;
+  // Q4_EPI_RESID: when post_ln_w is set, the updated residual rows are also
+  // RMS-normalized (weight post_ln_w, eps) into post_norm_out [M][N] (the input
+  // of the next normed GEMM), fused into the split reduce when K is split.
+  const f16* post_ln_w;
+  f16* post_norm_out;
 };
 
 // Largest K (activation length) the tile16 GEMV stages.

@@ -51,22 +51,30 @@ struct GemmShape {
 // tokens stage 4 (LDS holds two 64-token ranges of 4 chunks, 143 KB, and the
 // shorter ring bounds the SwiGLU form's registers) and dequantize each chunk
 // once for all of their token tiles (DQ).
+// upw = units per wave of the store epilogue at 64 tokens: two adjacent units
+// share each A fragment read from LDS, as the gate / up pair of the SwiGLU form
+// always does.  Measured in the 7B verify step it sped up the QKV and lm_head
+// GEMMs (19.4 -> 16.7 us) but slowed the residual O / down GEMMs (13.2 -> 14.4
+// us: their K splits double, leaving O on 128 workgroups), which keep one.
 struct GemmCfg {
-  int mb, rc;
+  int mb, rc, upw;
 };
 GemmCfg gemm_cfg(int M) {
-  if (M <= 16) return {1, 8};
-  if (M <= 32) return {2, 4};
-  return {4, 4};
+  if (M <= 16) return {1, 8, 1};
+  if (M <= 32) return {2, 4, 1};
+  return {4, 4, 2};
 }
+// Units per wave / partial-tile columns per unit of an (epilogue, config).
+int gemm_upw(int epi, GemmCfg cfg) { return epi == Q4_EPI_STORE ? cfg.upw : 1; }
+int gemm_cols_per_unit(int epi) { return epi == Q4_EPI_SWIGLU ? 2 * 16 : 16; }
 
-// Workgroups per K split: a unit per wave, eight per workgroup.  The kernel
+// Workgroups per K split: upw units per wave, eight waves per workgroup.  The kernel
 // needs 140-200 VGPRs, so one 8-wave workgroup is resident per CU: K is split
 // as far as the grid still fits one round of workgroups (a grid even one
 // workgroup past the CU count runs a second round, e.g. 7B gate/up at M=16:
 // 172 workgroups 21 us, 258 workgroups 32 us), keeping >= RC chunks per split.
-int gemm_splits(int KB, int n_units, int rc) {
-  const int wg = (n_units + kGWaves - 1) / kGWaves;
+int gemm_splits(int KB, int n_units, int rc, int upw) {
+  const int wg = (n_units + kGWaves * upw - 1) / (kGWaves * upw);
   int splits = axm_num_cus() / wg;
   const int max_splits = KB / rc > 0 ? KB / rc : 1;
   if (splits > max_splits) splits = max_splits;
@@ -95,8 +103,8 @@ __device__ __forceinline__ void t16g_store(const T16Args& a, int tok, int row, f
   }
 }
 
-// Each wave owns one unit (16 rows, or a gate/up pair) over the workgroup's K
-// split.  The split's activations of all 16 MB token rows are staged range by
+// Each wave owns NT weight tiles over the workgroup's K split: a gate/up pair
+// (SwiGLU) or NT adjacent units (store / residual epilogues).  The split's activations of all 16 MB token rows are staged range by
 // range (RC chunks, double-buffered in LDS: range r + 1 is loaded while range r
 // is consumed), and the weight chunks of range r + 1 are requested into the
 // register slots that range r's chunks free, so the weight stream does not stop
@@ -121,7 +129,9 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kq = lane >> 4;
-  const int unit = blockIdx.x * kGWaves + wave;
+  constexpr bool kPair = EPI == Q4_EPI_SWIGLU;
+  const int unit = (blockIdx.x * kGWaves + wave) * (kPair ? 1 : NT);  // first unit of the wave
+  const int tstride = kPair ? a.pair_offset : 1;                      // unit step between tiles
   const int kbA = blockIdx.y * a.kb_per_split;
   const int kbN = min(a.KB, kbA + a.kb_per_split) - kbA;  // chunks of this split (>= 1)
   const int n_ranges = (kbN + RC - 1) / RC;
@@ -136,10 +146,10 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   // Chunk c of range r into slot c (zeros past the split or the matrix).
   auto load = [&](int r, int c) {
     const int kl = r * RC + c;
-    const bool ok = unit < a.n_units && kl < kbN;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int base = (unit + t * a.pair_offset) * a.KB + kbA + kl;
+      const bool ok = unit + (kPair ? 0 : t) < a.n_units && kl < kbN;
+      const int base = (unit + t * tstride) * a.KB + kbA + kl;
       const int wo = ok ? (base * 64 + lane) * 16 : kGOOB;
       const int so = ok ? (base * 16 + (lane & 15)) * 8 : kGOOB;
       wr[c][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
@@ -293,22 +303,27 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
     __syncthreads();
   }
 
-  if (unit >= a.n_units) return;
   const int j = lane & 15;
   if (gridDim.y == 1) {
-    const int row = unit * 16 + j;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int t = 0; t < (kPair ? 1 : NT); ++t) {
+      if (unit + t >= a.n_units) break;
+      const int row = (unit + t) * 16 + j;
 #pragma unroll
-      for (int vi = 0; vi < 4; ++vi) {
-        const int tok = 16 * mb + 4 * kq + vi;
-        if (tok < a.M_tokens && row < a.N) t16g_store<EPI>(a, tok, row, acc[0][mb][vi], acc[NT - 1][mb][vi]);
-      }
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int vi = 0; vi < 4; ++vi) {
+          const int tok = 16 * mb + 4 * kq + vi;
+          if (tok < a.M_tokens && row < a.N)
+            t16g_store<EPI>(a, tok, row, acc[t][mb][vi], acc[kPair ? NT - 1 : t][mb][vi]);
+        }
+    }
   } else {
     // Partial tile of this K split: [split][token][column], column = tile * 16 + row in tile.
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int col = (unit + t * a.pair_offset) * 16 + j;
+      if (unit + (kPair ? 0 : t) >= a.n_units) break;
+      const int col = (unit + t * tstride) * 16 + j;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -335,6 +350,68 @@ __global__ void t16g_reduce_kernel(T16Args a, int n_splits, int up_col, int tok_
   t16g_store<EPI>(a, tok, row, v0, v1);
 }
 
+// Residual epilogue over the split partials of whole token rows, then RMSNorm of
+// each updated row into post_norm_out: one 1024-thread workgroup per token,
+// thread tid owns the 4-row vectors tid + 1024 i (N % 4 == 0, N <= 16384,
+// 8-byte aligned rows), so each thread issues one 16-byte partial load per split
+// and vector.  The arithmetic is t16g_reduce_kernel's followed by the norm
+// kernel's.
+constexpr int kRnThreads = 1024;
+constexpr int kRnVec = 4;
+__global__ void __launch_bounds__(kRnThreads) t16g_reduce_resid_norm_kernel(T16Args a, int n_splits, int tok_stride) {
+  __shared__ float red[kRnThreads / 64];
+  const int tok = blockIdx.x;
+  const int nv = a.N / 4;
+  f16* xr = a.resid + (size_t)tok * a.ldr;
+  f16x4 xv[kRnVec];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRnVec; ++i) {
+    const int j = threadIdx.x + i * kRnThreads;
+    if (j < nv) {
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int sp = 0; sp < n_splits; ++sp)
+        v += *reinterpret_cast<const f32x4*>(a.part_ws + ((size_t)sp * tok_stride + tok) * a.part_cols + 4 * j);
+      f16x4 xo = *reinterpret_cast<const f16x4*>(xr + 4 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f16 h = f2h(v[e]);
+        if (a.bias != nullptr) h = f2h(h2f(h) + h2f(a.bias[4 * j + e]));
+        xo[e] = f2h(h2f(xo[e]) + h2f(h));
+        const float f = h2f(xo[e]);
+        ss += h2f(f2h(f * f));
+      }
+      *reinterpret_cast<f16x4*>(xr + 4 * j) = xo;
+      xv[i] = xo;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRnThreads / 64; ++w) tot += red[w];
+  const float rinv = rms_inv_fp16(tot, a.N, a.eps);
+  f16* yr = a.post_norm_out + (size_t)tok * a.N;
+#pragma unroll
+  for (int i = 0; i < kRnVec; ++i) {
+    const int j = threadIdx.x + i * kRnThreads;
+    if (j < nv) {
+      const f16x4 wv = *reinterpret_cast<const f16x4*>(a.post_ln_w + 4 * j);
+      f16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = f2h(h2f(f2h(h2f(xv[i][e]) * rinv)) * h2f(wv[e]));
+      *reinterpret_cast<f16x4*>(yr + 4 * j) = o;
+    }
+  }
+}
+
+bool post_norm_fusable(const T16Args& a) {
+  const uintptr_t al = (uintptr_t)a.resid | (uintptr_t)a.post_ln_w | (uintptr_t)a.post_norm_out;
+  return a.N % 4 == 0 && a.N <= 4 * kRnThreads * kRnVec && a.ldr % 4 == 0 && (al & 7) == 0;
+}
+
 template <int NT, int EPI, int MB, int RC, bool DQ>
 void t16g_launch_shape(const T16Args& a, dim3 grid, hipStream_t s) {
   using G = GemmShape<MB, RC>;
@@ -348,29 +425,33 @@ void t16g_launch_shape(const T16Args& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((t16g_kernel<NT, EPI, MB, RC, DQ>), grid, dim3(kGThreads), G::smem, s, a);
 }
 
-// The (MB, RC, DQ) triples here are the ones gemm_cfg returns.
-template <int NT, int EPI>
+// The (MB, RC, DQ, units per wave) shapes here are the ones gemm_cfg returns.
+template <int EPI>
 void t16g_launch_epi(const T16Args& a, GemmCfg cfg, dim3 grid, hipStream_t s) {
+  constexpr int P = EPI == Q4_EPI_SWIGLU ? 2 : 1;  // tiles per unit
   if (cfg.mb == 1)
-    t16g_launch_shape<NT, EPI, 1, 8, false>(a, grid, s);
+    t16g_launch_shape<P, EPI, 1, 8, false>(a, grid, s);
   else if (cfg.mb == 2)
-    t16g_launch_shape<NT, EPI, 2, 4, true>(a, grid, s);
+    t16g_launch_shape<P, EPI, 2, 4, true>(a, grid, s);
+  else if (gemm_upw(EPI, cfg) == 1)
+    t16g_launch_shape<P, EPI, 4, 4, true>(a, grid, s);
   else
-    t16g_launch_shape<NT, EPI, 4, 4, true>(a, grid, s);
+    t16g_launch_shape<2, EPI, 4, 4, true>(a, grid, s);
 }
 
-size_t gemm_ws_bytes_cfg(int KB, int n_units, int NT, GemmCfg cfg) {
-  const int splits = gemm_splits(KB, n_units, cfg.rc);
-  return splits <= 1 ? 0 : (size_t)splits * 16 * cfg.mb * n_units * 16 * NT * sizeof(float);
+size_t gemm_ws_bytes_cfg(int KB, int n_units, int epi, GemmCfg cfg) {
+  const int splits = gemm_splits(KB, n_units, cfg.rc, gemm_upw(epi, cfg));
+  return splits <= 1 ? 0 : (size_t)splits * 16 * cfg.mb * n_units * gemm_cols_per_unit(epi) * sizeof(float);
 }
 
 }  // namespace
 
 size_t t16_gemm_ws_bytes(int K, int n_units, int NT) {
   const int KB = (K + 127) / 128;
+  const int epi = NT == 2 ? Q4_EPI_SWIGLU : Q4_EPI_STORE;
   size_t need = 0;
   for (int m = 16; m <= kTile16GemmMaxTokens; m *= 2) {
-    const size_t b = gemm_ws_bytes_cfg(KB, n_units, NT, gemm_cfg(m));
+    const size_t b = gemm_ws_bytes_cfg(KB, n_units, epi, gemm_cfg(m));
     if (b > need) need = b;
   }
   return need;
@@ -378,17 +459,19 @@ size_t t16_gemm_ws_bytes(int K, int n_units, int NT) {
 
 int t16_gemm_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s) {
   if (M < 1 || M > kTile16GemmMaxTokens || a.ln_w != nullptr || a.argmax_keys != nullptr || a.x_parts != nullptr ||
-      (epi != Q4_EPI_STORE && epi != Q4_EPI_RESID && epi != Q4_EPI_SWIGLU) || a.K <= 0 || a.K % 64 != 0) {
+      (epi != Q4_EPI_STORE && epi != Q4_EPI_RESID && epi != Q4_EPI_SWIGLU) || a.K <= 0 || a.K % 64 != 0 ||
+      (a.post_ln_w != nullptr && (epi != Q4_EPI_RESID || a.post_norm_out == nullptr || a.ldr != a.N))) {
     axm_set_error("tile16 gemm: M=%d (1..%d), epi=%d, K=%d unsupported (normalized activations, store / "
-                  "residual / SwiGLU epilogues)", M, kTile16GemmMaxTokens, epi, a.K);
+                  "residual / SwiGLU epilogues, post-norm only with the residual one over contiguous rows)", M,
+                  kTile16GemmMaxTokens, epi, a.K);
     return -2;
   }
-  const int NT = epi == Q4_EPI_SWIGLU ? 2 : 1;
   const GemmCfg cfg = gemm_cfg(M);
+  const int upw = gemm_upw(epi, cfg);
   a.KB = (a.K + 127) / 128;
-  const int splits = gemm_splits(a.KB, a.n_units, cfg.rc);
+  const int splits = gemm_splits(a.KB, a.n_units, cfg.rc, upw);
   const int kbps = (a.KB + splits - 1) / splits;
-  const size_t need = gemm_ws_bytes_cfg(a.KB, a.n_units, NT, cfg);
+  const size_t need = gemm_ws_bytes_cfg(a.KB, a.n_units, epi, cfg);
   if (need > 0 && (ws == nullptr || ws_bytes < need)) {
     axm_set_error("tile16 gemm: workspace of %zu bytes needed, %zu given", need, ws_bytes);
     return -1;
@@ -397,30 +480,44 @@ int t16_gemm_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipSt
   a.M_tokens = M;
   a.kb_per_split = kbps;
   a.part_ws = ws;
-  a.part_cols = a.n_units * 16 * NT;
+  a.part_cols = a.n_units * gemm_cols_per_unit(epi);
   a.w16_bytes = t16_weight_bytes(a.N_rows_alloc, a.K);
   a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K);
   a.unpack[0] = 0x000F000Fu;
   a.unpack[1] = 0x00F000F0u;
   a.unpack[2] = 0x64006400u;
   a.unpack[3] = 0x54005400u;
-  const dim3 grid((a.n_units + kGWaves - 1) / kGWaves, splits);
+  const dim3 grid((a.n_units + kGWaves * upw - 1) / (kGWaves * upw), splits);
   switch (epi) {
     case Q4_EPI_STORE:
-      t16g_launch_epi<1, Q4_EPI_STORE>(a, cfg, grid, s);
+      t16g_launch_epi<Q4_EPI_STORE>(a, cfg, grid, s);
       break;
     case Q4_EPI_RESID:
-      t16g_launch_epi<1, Q4_EPI_RESID>(a, cfg, grid, s);
+      t16g_launch_epi<Q4_EPI_RESID>(a, cfg, grid, s);
       break;
     default:
-      t16g_launch_epi<2, Q4_EPI_SWIGLU>(a, cfg, grid, s);
+      t16g_launch_epi<Q4_EPI_SWIGLU>(a, cfg, grid, s);
       break;
+  }
+  const int ts = 16 * cfg.mb;
+  if (a.post_ln_w != nullptr) {
+    // Residual rows then their RMSNorm: one fused launch over the partials, or
+    // the norm kernel after an unsplit GEMM (and as the general fallback).
+    if (splits > 1 && post_norm_fusable(a)) {
+      hipLaunchKernelGGL(t16g_reduce_resid_norm_kernel, dim3(M), dim3(kRnThreads), 0, s, a, splits, ts);
+      return 0;
+    }
+    if (splits > 1) {
+      const long n = (long)M * a.N;
+      hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_RESID>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a,
+                         splits, 0, ts);
+    }
+    return launch_rmsnorm(a.resid, a.post_ln_w, a.post_norm_out, M, a.N, a.eps, s);
   }
   if (splits > 1) {
     const long n = (long)M * a.N;
     const dim3 rg((unsigned)((n + 255) / 256));
     const int up_col = a.pair_offset * 16;
-    const int ts = 16 * cfg.mb;
     if (epi == Q4_EPI_STORE)
       hipLaunchKernelGGL(t16g_reduce_kernel<Q4_EPI_STORE>, rg, dim3(256), 0, s, a, splits, up_col, ts);
     else if (epi == Q4_EPI_RESID)

@@ -155,6 +155,10 @@ struct GemvCall {
   const f16* x_parts = nullptr;
   const f32x2* x_ml = nullptr;
   int n_parts = 0, parts_hd = 0;
+  // RESID: RMSNorm (weight post_ln_w, eps) of the updated residual rows into
+  // post_norm_out, the input of the next normed GEMM.
+  const f16* post_ln_w = nullptr;
+  f16* post_norm_out = nullptr;
 };
 
 template <class A>
@@ -525,6 +529,9 @@ struct axm_runner {
         a.bias = c.bias;
         a.resid = c.resid ? c.resid + (size_t)t0 * c.ldr : nullptr;
         a.ldr = c.ldr;
+        a.post_ln_w = c.post_ln_w;
+        a.post_norm_out = c.post_ln_w ? c.post_norm_out + (size_t)t0 * out_rows : nullptr;
+        a.eps = c.eps;
         const int rc = t16_gemm_launch(a, mc, epi, ws, ws_bytes, s);
         if (rc) return rc;
       }
@@ -540,6 +547,7 @@ struct axm_runner {
       const int rc = run_gemv(m, epi, out_rows, cc, mc, s);
       if (rc) return rc;
     }
+    if (c.post_ln_w != nullptr) return launch_rmsnorm(c.resid, c.post_ln_w, c.post_norm_out, T, out_rows, c.eps, s);
     return 0;
   }
 
@@ -550,6 +558,11 @@ struct axm_runner {
   // attends over all S slots, as the reference does in that case.
   int enqueue_verify(const int64_t* idx_dev, int T, int write_pos, int prefix, bool tree, hipStream_t s) {
     const int D = d.d_model, H = d.hidden_dim;
+    // Multi-token GEMMs take normalized activations: there the residual GEMMs
+    // (O, down) also write the RMSNorm of the rows they update into `norm` for
+    // the next GEMM (fused into their split reduce), instead of a norm launch
+    // per normed GEMM.  Up to 4 tokens keep the GEMVs' fused norm prologue.
+    const bool post = T > 4;
     if (d.wte_format == 0)
       launch_embed_f16((const f16*)d.wte, idx_dev, nullptr, x, T, D, d.vocab_size, s);
     else
@@ -557,12 +570,12 @@ struct axm_runner {
     for (int i = 0; i < d.n_layer; ++i) {
       KvView kv = kv_view(i);
       GemvCall a{};
-      a.x = x;
+      a.x = post && i > 0 ? norm : x;
       a.ldx = D;
       a.y = qkvbuf;
       a.ldy = qkv_dim;
       a.bias = (const f16*)qkv_b[i];
-      a.ln_w = (const f16*)ln1[i];
+      a.ln_w = post && i > 0 ? nullptr : (const f16*)ln1[i];
       a.eps = d.eps;
       int rc = gemv_rows(m_qkv[i], Q4_EPI_STORE, qkv_dim, a, T, s);
       if (rc) return rc;
@@ -585,14 +598,19 @@ struct axm_runner {
       o.ldx = q_dim;
       o.resid = x;
       o.ldr = D;
+      if (post) {
+        o.post_ln_w = (const f16*)ln2[i];
+        o.post_norm_out = norm;
+        o.eps = d.eps;
+      }
       rc = gemv_rows(m_o[i], Q4_EPI_RESID, D, o, T, s);
       if (rc) return rc;
       GemvCall g{};
-      g.x = x;
+      g.x = post ? norm : x;
       g.ldx = D;
       g.y = hbuf;
       g.ldy = H;
-      g.ln_w = (const f16*)ln2[i];
+      g.ln_w = post ? nullptr : (const f16*)ln2[i];
       g.eps = d.eps;
       g.pair_rows = H;
       rc = gemv_rows(m_gu[i], Q4_EPI_SWIGLU, H, g, T, s);
@@ -602,21 +620,26 @@ struct axm_runner {
       dn.ldx = H;
       dn.resid = x;
       dn.ldr = D;
+      if (post) {
+        dn.post_ln_w = (const f16*)(i + 1 < d.n_layer ? ln1[i + 1] : d.lnf_w);
+        dn.post_norm_out = norm;
+        dn.eps = d.eps;
+      }
       rc = gemv_rows(m_dn[i], Q4_EPI_RESID, D, dn, T, s);
       if (rc) return rc;
     }
     if (d.lm_head_format == 0) {
       GemvCall l{};
-      l.x = x;
+      l.x = post ? norm : x;
       l.ldx = D;
       l.y = logits;
       l.ldy = d.vocab_size;
-      l.ln_w = (const f16*)d.lnf_w;
+      l.ln_w = post ? nullptr : (const f16*)d.lnf_w;
       l.eps = d.eps;
-      l.x_norm_out = norm;
+      l.x_norm_out = post ? nullptr : norm;
       return gemv_rows(m_lmh, Q4_EPI_STORE, d.vocab_size, l, T, s);
     }
-    launch_rmsnorm(x, (const f16*)d.lnf_w, norm, T, D, d.eps, s);
+    if (!post) launch_rmsnorm(x, (const f16*)d.lnf_w, norm, T, D, d.eps, s);
     return launch_q8_gemv(norm, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, T, D,
                           d.vocab_size, nullptr, 0.f, s);
   }

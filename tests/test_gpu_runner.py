@@ -18,7 +18,7 @@ F16, F32 = np.float16, np.float32
 TOL = 1e-2
 
 
-def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile16", mode=None):
+def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile16", mode=None, max_tokens=32):
     from axiomlm_amd.cache import StaticKVCache
     from axiomlm_amd.runner import QuantizedDecodeRunner
 
@@ -32,7 +32,8 @@ def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile1
         [t(x) for x in ow.ln2], [t(x) for x in ow.gu_p], [t(x) for x in ow.gu_s], [t(x) for x in ow.wd_p],
         [t(x) for x in ow.wd_s], t(ow.lnf), cache.k_caches, cache.v_caches, cfg.n_head, cfg.n_kv_head,
         cfg.head_dim, True, cfg.eps, [], cfg.vocab, wte_p=t(ow.wte_p.view(np.int32).reshape(cfg.vocab, -1)),
-        wte_s=t(ow.wte_sb), k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv, layout=layout)
+        wte_s=t(ow.wte_sb), k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv, layout=layout,
+        max_tokens=max_tokens)
     if mode is not None:
         r.set_mode(mode)
     return r, cache
@@ -314,6 +315,37 @@ def test_runner_verify_step_chain(dev):
     rng = np.random.default_rng(11)
     _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 10).tolist(), dev)
     for T in (5, 17):
+        seen = cache.total_seen_tokens[0]
+        toks = rng.integers(0, cfg.vocab, T).tolist()
+        got = runner.verify_step(torch.tensor([toks], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
+        ref = model.forward(toks, ocache, return_all_logits=True)
+        cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
+        cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
+        for t in range(T):
+            _check_logits(got[t], ref[t], f"verify T={T} token {t}")
+    tok = int(rng.integers(0, cfg.vocab))
+    got = run_steps(runner, cache, [tok], dev)[0]
+    _check_logits(got, model.forward([tok], ocache)[-1], "step after verify")
+
+
+def test_runner_verify_step_split_gemms(dev):
+    """verify_step on a wider model (d 1024, head 128, MLP 2816) whose multi-token GEMMs
+    split K at 40 and 20 tokens: the residual GEMMs' fused split-reduce + RMSNorm (the
+    next GEMM's input), the two-unit store form and the 32-token form, against the
+    oracle's multi-token forward, then a decode step."""
+    print("[runner_verify_split_gemms]", flush=True)
+    cfg = om.OracleConfig(n_layer=2, n_head=8, n_kv_head=8, d_model=1024, hidden=2816, vocab=1024, eps=1e-5,
+                          block_size=256)
+    W = om.make_float_weights(cfg, seed=3)
+    ow = om.pack_model_rtn(cfg, W)
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, 10000.0)
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, max_tokens=64)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    rng = np.random.default_rng(14)
+    _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 6).tolist(), dev)
+    for T in (40, 20):
         seen = cache.total_seen_tokens[0]
         toks = rng.integers(0, cfg.vocab, T).tolist()
         got = runner.verify_step(torch.tensor([toks], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
