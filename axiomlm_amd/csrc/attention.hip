@@ -94,6 +94,85 @@ __global__ void __launch_bounds__(kKvWriteWaves * 64)
   kv_store_lane(kv, which, h, slot, g, lane, src[lane]);
 }
 
+// Row form of the KV write: one wave per (token, k|v, kv head); lane l holds the
+// EPL = hd / 64 consecutive elements EPL l .. EPL l + EPL - 1 (one vector load),
+// so a 64-group spans 64 / EPL lanes and its maximum is taken by shuffles within
+// them.  Per element the arithmetic is kv_store_lane's.
+template <int EPL>
+__global__ void __launch_bounds__(kKvWriteWaves * 64)
+    kv_write_row_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld,
+                        int write_pos, const int* __restrict__ write_pos_dev, int n_items) {
+  constexpr int LPG = 64 / EPL;  // lanes per 64-group
+  typedef _Float16 hvec __attribute__((ext_vector_type(EPL)));
+  const int lane = threadIdx.x & 63;
+  int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
+  if (idx >= n_items) return;
+  const int h = idx % kv.Hkv;
+  idx /= kv.Hkv;
+  const int which = idx & 1;
+  const int t = idx >> 1;
+  const int wp0 = write_pos_dev ? write_pos_dev[0] : write_pos;
+  const int slot = (wp0 + t) % kv.S;
+  const hvec xv = *reinterpret_cast<const hvec*>((which == 0 ? k_rows : v_rows) + (size_t)t * ld + h * kv.hd +
+                                                 EPL * lane);
+  const size_t row = (size_t)h * kv.S + slot;  // batch 0
+  if (kv.kv_dtype == AXM_KV_FP16) {
+    *reinterpret_cast<hvec*>((f16*)(which == 0 ? kv.k : kv.v) + row * kv.hd + EPL * lane) = xv;
+    return;
+  }
+  float ax = fabsf(h2f(xv[0]));  // seeded like wave_max (an all-NaN group keeps a NaN maximum)
+#pragma unroll
+  for (int e = 1; e < EPL; ++e) ax = fmaxf(ax, fabsf(h2f(xv[e])));
+#pragma unroll
+  for (int off = LPG / 2; off > 0; off >>= 1) ax = fmaxf(ax, __shfl_xor(ax, off, 64));
+  const float div = kv.kv_dtype == AXM_KV_FP8 ? 448.0f : 7.0f;
+  const f16 sc = f2h(__fdiv_rn(ax, div));
+  const float scf = h2f(sc);
+  if (lane % LPG == 0) (which == 0 ? kv.ks : kv.vs)[row * (kv.hd / 64) + lane / LPG] = sc;
+  float q[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float xf = h2f(xv[e]);
+    if (scf == 0.f)
+      q[e] = (xf == 0.f) ? __builtin_bit_cast(float, 0xFFC00000u) : xf / scf;
+    else
+      q[e] = h2f(f2h(__fdiv_rn(xf, scf)));
+  }
+  uint8_t* dst = (uint8_t*)(which == 0 ? kv.k : kv.v);
+  if (kv.kv_dtype == AXM_KV_FP8) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) packed |= (uint32_t)fp8e4m3fn_from_f32(q[e]) << (8 * e);
+    uint8_t* d = dst + row * kv.hd + EPL * lane;
+    if (EPL == 1) *d = (uint8_t)packed;
+    else if (EPL == 2) *reinterpret_cast<uint16_t*>(d) = (uint16_t)packed;
+    else *reinterpret_cast<uint32_t*>(d) = packed;
+    return;
+  }
+  int qi[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    if (q[e] != q[e]) {
+      qi[e] = 0;  // NaN -> int8 conversion yields 0 on the reference CPU path
+    } else {
+      const float r = fminf(fmaxf(__builtin_rintf(q[e]), -8.f), 7.f);
+      qi[e] = (int)r;
+    }
+  }
+  if (EPL == 1) {
+    const int partner = __shfl_xor(qi[0], 1, 64);
+    if ((lane & 1) == 0) dst[row * (kv.hd / 2) + lane / 2] = (uint8_t)((qi[0] & 0xF) | ((partner & 0xF) << 4));
+  } else {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < EPL / 2; ++e)
+      packed |= (uint32_t)((qi[2 * e] & 0xF) | ((qi[2 * e + 1] & 0xF) << 4)) << (8 * e);
+    uint8_t* d = dst + row * (kv.hd / 2) + EPL / 2 * lane;
+    if (EPL == 2) *d = (uint8_t)packed;
+    else *reinterpret_cast<uint16_t*>(d) = (uint16_t)packed;
+  }
+}
+
 // Fused bias + RoPE + KV-cache write of T tokens (rope_kv_cache_write_half_kernel,
 // metal_kernels.metal:991-1036; fp8/int4 :1110-1279; tree variants :2862-2918,
 // :1282-1473).  qkv [T][q_dim + 2 kv_dim] fp16, updated in place for the query
@@ -668,6 +747,23 @@ int pick_qr(int rows) {
 int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int ld_rows, int T, int write_pos,
                     const int* write_pos_dev, hipStream_t s) {
   const int G = kv.hd / 64;
+  const int epl = G;  // elements per lane of the row form
+  const uintptr_t al = (uintptr_t)k_rows | (uintptr_t)v_rows;
+  if ((epl == 1 || epl == 2 || epl == 4) && ld_rows % epl == 0 && al % (2 * epl) == 0) {
+    const int items = T * 2 * kv.Hkv;
+    const unsigned blocks = (unsigned)((items + kKvWriteWaves - 1) / kKvWriteWaves);
+    const dim3 b(kKvWriteWaves * 64);
+    if (epl == 1)
+      hipLaunchKernelGGL(kv_write_row_kernel<1>, dim3(blocks), b, 0, s, kv, k_rows, v_rows, ld_rows, write_pos,
+                         write_pos_dev, items);
+    else if (epl == 2)
+      hipLaunchKernelGGL(kv_write_row_kernel<2>, dim3(blocks), b, 0, s, kv, k_rows, v_rows, ld_rows, write_pos,
+                         write_pos_dev, items);
+    else
+      hipLaunchKernelGGL(kv_write_row_kernel<4>, dim3(blocks), b, 0, s, kv, k_rows, v_rows, ld_rows, write_pos,
+                         write_pos_dev, items);
+    return 0;
+  }
   const int items = T * 2 * kv.Hkv * G;
   const unsigned blocks = (unsigned)((items + kKvWriteWaves - 1) / kKvWriteWaves);
   hipLaunchKernelGGL(kv_write_kernel, dim3(blocks), dim3(kKvWriteWaves * 64), 0, s, kv, k_rows, v_rows, ld_rows,

@@ -443,13 +443,15 @@ def test_swiglu_and_argmax(dev):
 # ---------------------------------------------------------------------------
 # KV quantization
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("hd", [64, 128])
 @pytest.mark.parametrize("kind", ["fp8", "int4"])
-def test_kv_quantize_bit_exact(dev, kind):
+def test_kv_quantize_bit_exact(dev, kind, hd):
+    """Row-form KV write: 1 or 2 elements per lane for the cache's head sizes 64 / 128."""
     from axiomlm_amd.kernels import quantize_kv_fp8, quantize_kv_int4
 
-    rng = np.random.default_rng(6)
-    k = rng.standard_normal((2, 8, 33, 128)).astype(F16)
-    v = (rng.standard_normal((2, 8, 33, 128)) * 3).astype(F16)
+    rng = np.random.default_rng(6 + hd)
+    k = rng.standard_normal((2, 8, 33, hd)).astype(F16)
+    v = (rng.standard_normal((2, 8, 33, hd)) * 3).astype(F16)
     k[0, 0, 0, :64] = 0  # all-zero group -> NaN codes on the reference path
     v[1, 2, 3, :] = F16(1e-7)  # subnormal group
     fn = quantize_kv_fp8 if kind == "fp8" else quantize_kv_int4
