@@ -13,6 +13,8 @@
 // every key/value byte is read exactly once per workgroup.  Softmax is online
 // in the exp2 domain with fp32 state; partial (m, l, o) per split are merged by
 // a second kernel (or written directly when there is a single split).
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace {
@@ -932,29 +934,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   };
   auto slot_of = [&](int key) { return key < prefix ? key : (p.write_pos + (key - prefix)) % p.kv.S; };
 
-  // Key / value fetches of one block: this lane's K B-operand fragments (keys
-  // kb0 + 16 h + l16, dims 32 c + 8 lq) and this thread's V vectors.
-  KvRaw8 kraw[2][KSTEPS], vraw[kVPT];
+  // Key / value fetches of one block into register buffer b (two blocks are in
+  // flight): this lane's K B-operand fragments (keys kb0 + 16 h + l16, dims
+  // 32 c + 8 lq) and this thread's V vectors.  Keys at or past k_end read zeros
+  // (out-of-range offsets), so every fetch is issued unconditionally and the
+  // compiler counts the loads in flight exactly.
+  KvRaw8 kraw[2][2][KSTEPS], vraw[2][kVPT];
   const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, p.kv.S, HD);
   const KvHead vh = kv_head<KVT>(p.kv.v, p.kv.vs, head_row0, p.kv.S, HD);
-  auto fetch = [&](int kb0) {
+  auto fetch = [&](int kb0, auto bc) {
+    constexpr int b = decltype(bc)::value;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int key = kb0 + 16 * h + l16;
       const int slot = slot_of(key);
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) kraw[h][c] = kv_fetch8<KVT>(kh, slot, HD, 32 * c + 8 * lq, key < k_end);
+      for (int c = 0; c < KSTEPS; ++c) kraw[b][h][c] = kv_fetch8<KVT>(kh, slot, HD, 32 * c + 8 * lq, key < k_end);
     }
 #pragma unroll
     for (int i = 0; i < kVPT; ++i) {
       const int j = i * 256 + threadIdx.x;
       const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
       const int key = kb0 + kk;
-      vraw[i] = kv_fetch8<KVT>(vh, slot_of(key), HD, e0, j < kVec && key < k_end);
+      vraw[b][i] = kv_fetch8<KVT>(vh, slot_of(key), HD, e0, j < kVec && key < k_end);
     }
   };
-  // The first block's keys and values are requested before the query rows.
-  if (k_begin < k_end) fetch(k_begin);
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  // The first two blocks' keys and values are requested before the query rows.
+  fetch(k_begin, B0{});
+  fetch(k_begin + kTreeKeys, B1{});
 
   // A operand: query row row0 + l16, dims 32 c + 8 lq .. +7.
   f16x8 qa[KSTEPS];
@@ -983,16 +992,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
 #pragma unroll
   for (int d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb0 = k_begin; kb0 < k_end; kb0 += kTreeKeys) {
-    // Convert this block's fetches, then request the next block's.
+  // One key block from register buffer b, whose registers then take the block
+  // two ahead.
+  auto block = [&](int kb0, auto bc) {
+    constexpr int b = decltype(bc)::value;
     f16x8 kf[2][KSTEPS], vv[kVPT];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(kraw[h][c]);
+      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(kraw[b][h][c]);
 #pragma unroll
-    for (int i = 0; i < kVPT; ++i) vv[i] = kv_half8<KVT>(vraw[i]);
-    if (kb0 + kTreeKeys < k_end) fetch(kb0 + kTreeKeys);
+    for (int i = 0; i < kVPT; ++i) vv[i] = kv_half8<KVT>(vraw[b][i]);
+    fetch(kb0 + 2 * kTreeKeys, bc);
     // Stage V transposed: vector j covers key kb0 + j / (HD/8), dims 8 (j % (HD/8)).
 #pragma unroll
     for (int i = 0; i < kVPT; ++i) {
@@ -1043,6 +1054,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
     }
     __syncthreads();  // before the next block overwrites vt / pt
+  };
+  for (int kb0 = k_begin; kb0 < k_end; kb0 += 2 * kTreeKeys) {
+    block(kb0, B0{});
+    if (kb0 + kTreeKeys < k_end) block(kb0 + kTreeKeys, B1{});
   }
 
 #pragma unroll
