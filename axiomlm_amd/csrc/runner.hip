@@ -35,9 +35,21 @@ constexpr int kTokenOffset = 72;
 // Token source: idx_dev[0] if non-null, else tok_host if >= 0, else the greedy
 // argmax of the previous step's logits, reduced here from the per-tile keys the
 // lm_head launch wrote (largest fp16 logit, lowest index on ties).
+//
+// With `emb` set the same workgroup also gathers the token's embedding row into
+// emb->x (the first kernel of the decode graph otherwise), with the arithmetic
+// of embed_f16_kernel / embed_q8_kernel: 16 elements per thread and pass.
+struct EmbedArgs {
+  const void* wte;    // fp16 [V][D] (format 0) or Q8 codes u8 [V][D] (format 1)
+  const f16* wte_sb;  // Q8: (scale, bias) fp16 [V][D / 64][2]
+  int format;
+  int D, V;           // D % 64 == 0
+  f16* x;
+};
 __global__ void __launch_bounds__(256) set_params_kernel(int* params, const int64_t* idx_dev, int64_t tok_host,
                                                          int rope_pos, int write_pos, int active_len,
-                                                         const unsigned long long* keys, int n_keys) {
+                                                         const unsigned long long* keys, int n_keys,
+                                                         EmbedArgs emb) {
   __shared__ unsigned long long red[4];
   int64_t tok = 0;
   if (idx_dev == nullptr && tok_host < 0) {
@@ -63,6 +75,34 @@ __global__ void __launch_bounds__(256) set_params_kernel(int* params, const int6
     params[P_ROPE] = rope_pos;
     params[P_WRITE] = write_pos;
     params[P_ACTIVE] = active_len;
+  }
+  if (emb.x == nullptr) return;
+  // Out-of-range token ids produce a zero row (params[P_TOKEN] is the int cast,
+  // as the embed kernels read it).
+  const long t = (long)(int)tok;
+  const bool ok = t >= 0 && t < emb.V;
+  for (int k0 = 16 * threadIdx.x; k0 < emb.D; k0 += 16 * 256) {
+    f16x8 o[2];
+    if (!ok) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[0][e] = o[1][e] = f16(0);
+    } else if (emb.format == 0) {
+      const f16x8* src = reinterpret_cast<const f16x8*>((const f16*)emb.wte + (size_t)t * emb.D + k0);
+      o[0] = src[0];
+      o[1] = src[1];
+    } else {
+      const u32x4 c = *reinterpret_cast<const u32x4*>((const uint8_t*)emb.wte + (size_t)t * emb.D + k0);
+      const f16* sbr = emb.wte_sb + ((size_t)t * (emb.D / 64) + k0 / 64) * 2;
+      const float sc = h2f(sbr[0]), bi = h2f(sbr[1]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float q = (float)((c[e >> 2] >> (8 * (e & 3))) & 0xFFu);
+        o[e >> 3][e & 7] = f2h(add_rn(mul_rn(q, sc), bi));
+      }
+    }
+    f16x8* dst = reinterpret_cast<f16x8*>(emb.x + k0);
+    dst[0] = o[0];
+    dst[1] = o[1];
   }
 }
 
@@ -350,7 +390,7 @@ struct axm_runner {
     if (idx_dev == nullptr && tok_host < 0 && !tok_next_valid) {
       // Greedy feedback after a step of another mode: reduce its argmax keys first.
       hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, params, (const int64_t*)nullptr, (int64_t)-1,
-                         rope_pos, write_pos, active_len, argmax_keys, (d.vocab_size + 7) / 8);
+                         rope_pos, write_pos, active_len, argmax_keys, (d.vocab_size + 7) / 8, EmbedArgs{});
       a.idx_dev = a.tok_used;
     }
     a.rope_pos = rope_pos;
@@ -390,15 +430,11 @@ struct axm_runner {
   }
 
   // Enqueue the whole single-token step on stream s (no host synchronization).
+  // The decode step after set_params_kernel, which has written the token's
+  // embedding row into x.
   int enqueue_step(int n_splits, hipStream_t s) {
     const int D = d.d_model;
     const int H = d.hidden_dim;
-    // Embedding gather of params[P_TOKEN].
-    if (d.wte_format == 0)
-      launch_embed_f16((const f16*)d.wte, nullptr, params + P_TOKEN, x, 1, D, d.vocab_size, s);
-    else
-      launch_embed_q8((const uint8_t*)d.wte, (const f16*)d.wte_sb, nullptr, params + P_TOKEN, x, 1, D,
-                      d.vocab_size, s);
 
     for (int i = 0; i < d.n_layer; ++i) {
       KvView kv = kv_view(i);
@@ -856,8 +892,10 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
     return 0;
   }
   r->tok_next_valid = false;
+  // The step's token and its embedding row (the graph starts at layer 0).
+  const EmbedArgs emb{d.wte, (const f16*)d.wte_sb, d.wte_format, d.d_model, d.vocab_size, r->x};
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
-                     rope_pos, write_pos, active_len, r->argmax_keys, (d.vocab_size + 7) / 8);
+                     rope_pos, write_pos, active_len, r->argmax_keys, (d.vocab_size + 7) / 8, emb);
   // Bucket the split count so that one graph covers a range of lengths.
   int splits = r->parts_ok ? attn_parts_splits(1, d.n_kv_head, active_len)
                            : attn_choose_splits(1, d.n_kv_head, active_len);
