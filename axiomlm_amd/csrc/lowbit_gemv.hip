@@ -7,8 +7,10 @@
 // (scale) or (scale, bias) fp16 entry per row and 64-column group.
 //
 // Mapping: 4 waves per workgroup, kRows rows per wave; lane l handles groups
-// g = l, l + 64, ...  One 16-byte load per (row, group) brings all 64 codes of
-// the group.  Each 32-bit word holds the codes of columns 16d .. 16d+15 and is
+// g = l, l + 64, ... (ITERS of them, K <= ITERS * 4096).  One 16-byte load per
+// (row, group) brings all 64 codes of the group; a lane requests the codes and
+// scales of all its groups before the workgroup stages the activations, so the
+// weight stream and the staging overlap.  Each 32-bit word holds the codes of columns 16d .. 16d+15 and is
 // expanded in pairs: pair p takes the fields at bits 2p and 16 + 2p (columns
 // 16d + p and 16d + p + 8), moves them into bits 8-9 of each half and ORs the
 // fp16 exponent of 4.0, giving the exact halves (4 + v, 4 + v').  The
@@ -41,7 +43,7 @@ __device__ __forceinline__ f16x2 code_pair(uint32_t w, int p) {
 
 // xs: [M][K] fp16, each 16-column block stored as pairs (k, k+8), k = 0..7.
 // gs: [M][K/64] fp32 group sums of x.
-template <int FMT, int M>
+template <int FMT, int M, int ITERS>
 __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __restrict__ x, int K, int N,
                                                                 const uint8_t* __restrict__ w,
                                                                 const f16* __restrict__ s, const f16* __restrict__ bias,
@@ -52,62 +54,89 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
   const int tid = threadIdx.x;
   const int KG = K / 64;
   const int nblk = K / 16;
-  for (int m = 0; m < M; ++m) {
-    for (int b0 = 0; b0 < nblk; b0 += kLbThreads) {
-      const int b = b0 + tid;
-      float part = 0.f;
-      if (b < nblk) {
-        const f16x8 lo = *reinterpret_cast<const f16x8*>(x + (size_t)m * K + 16 * b);
-        const f16x8 hi = *reinterpret_cast<const f16x8*>(x + (size_t)m * K + 16 * b + 8);
-        f16x8 p0, p1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p0[2 * i] = lo[i];
-          p0[2 * i + 1] = hi[i];
-          p1[2 * i] = lo[4 + i];
-          p1[2 * i + 1] = hi[4 + i];
-          part += h2f(lo[i]) + h2f(hi[i]) + h2f(lo[4 + i]) + h2f(hi[4 + i]);
-        }
-        reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[0] = p0;
-        reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[1] = p1;
-      }
-      // Four consecutive blocks form one group (nblk is a multiple of 4).
-      part += __shfl_xor(part, 1, 64);
-      part += __shfl_xor(part, 2, 64);
-      if (b < nblk && (b & 3) == 0) gs[m * KG + b / 4] = part;
-    }
-  }
-  __syncthreads();
-
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int row0 = (blockIdx.x * (kLbThreads / 64) + wave) * kLbRows;
   const size_t row_bytes = (size_t)K / 4;
+
+  // Activation vectors of this thread (blocks tid + 256 i, i < ITERS: K / 16
+  // blocks of 16 columns), requested first: a wave's loads complete in issue
+  // order, so the staging below then waits only for these.  Blocks past the row
+  // are clamped and masked.
+  f16x8 xlo[M][ITERS], xhi[M][ITERS];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) {
+      const int b = min(tid + kLbThreads * i, nblk - 1);
+      xlo[m][i] = *reinterpret_cast<const f16x8*>(x + (size_t)m * K + 16 * b);
+      xhi[m][i] = *reinterpret_cast<const f16x8*>(x + (size_t)m * K + 16 * b + 8);
+    }
+  // Then the codes and scales of every (row, group) of this lane (groups past
+  // the row are clamped to the last one and skipped below).
+  u32x4 cw[ITERS][kLbRows];
+  float sc[ITERS][kLbRows], bi[ITERS][kLbRows];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int g = min(lane + 64 * it, KG - 1);
+#pragma unroll
+    for (int r = 0; r < kLbRows; ++r) {
+      const int row = min(row0 + r, N - 1);
+      cw[it][r] = *reinterpret_cast<const u32x4*>(w + (size_t)row * row_bytes + 16 * g);
+      if (FMT == 0) {
+        sc[it][r] = h2f(s[(size_t)row * KG + g]);
+        bi[it][r] = 0.f;
+      } else {
+        const f16x2 v = *reinterpret_cast<const f16x2*>(s + ((size_t)row * KG + g) * 2);
+        sc[it][r] = h2f(v.x);
+        bi[it][r] = h2f(v.y);
+      }
+    }
+  }
+  // Stage the activations in pair order with their group sums.
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) {
+      const int b = tid + kLbThreads * i;
+      const f16x8 lo = xlo[m][i], hi = xhi[m][i];
+      f16x8 p0, p1;
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        p0[2 * j] = lo[j];
+        p0[2 * j + 1] = hi[j];
+        p1[2 * j] = lo[4 + j];
+        p1[2 * j + 1] = hi[4 + j];
+        part += h2f(lo[j]) + h2f(hi[j]) + h2f(lo[4 + j]) + h2f(hi[4 + j]);
+      }
+      // Four consecutive blocks form one group (nblk is a multiple of 4).
+      part += __shfl_xor(part, 1, 64);
+      part += __shfl_xor(part, 2, 64);
+      if (b < nblk) {
+        reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[0] = p0;
+        reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[1] = p1;
+        if ((b & 3) == 0) gs[m * KG + b / 4] = part;
+      }
+    }
+  }
+  __syncthreads();
+
   float yacc[kLbRows][M];
 #pragma unroll
   for (int r = 0; r < kLbRows; ++r)
 #pragma unroll
     for (int m = 0; m < M; ++m) yacc[r][m] = 0.f;
 
-  for (int g = lane; g < KG; g += 64) {
-    u32x4 cw[kLbRows];
-    float sc[kLbRows], bi[kLbRows];
 #pragma unroll
-    for (int r = 0; r < kLbRows; ++r) {
-      const int row = min(row0 + r, N - 1);
-      cw[r] = *reinterpret_cast<const u32x4*>(w + (size_t)row * row_bytes + 16 * g);
-      if (FMT == 0) {
-        sc[r] = h2f(s[(size_t)row * KG + g]);
-        bi[r] = 0.f;
-      } else {
-        const f16x2 v = *reinterpret_cast<const f16x2*>(s + ((size_t)row * KG + g) * 2);
-        sc[r] = h2f(v.x);
-        bi[r] = h2f(v.y);
-      }
-      if (FMT == 0) {
+  for (int it = 0; it < ITERS; ++it) {
+    const int g = lane + 64 * it;
+    if (g >= KG) break;
+    if (FMT == 0) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) cw[r][d] = ternary_to_offset(cw[r][d]);
-      }
+      for (int r = 0; r < kLbRows; ++r)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) cw[it][r][d] = ternary_to_offset(cw[it][r][d]);
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
@@ -127,13 +156,13 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
             // ext_vector element expression reads element 0 with this compiler.
             const uint32_t xw = xv[2 * d + p / 4][p % 4];
             const f16x2 xpair = as_h2(xw);
-            acc = __builtin_amdgcn_fdot2(xpair, code_pair(cw[r][d], p), acc, false);
+            acc = __builtin_amdgcn_fdot2(xpair, code_pair(cw[it][r][d], p), acc, false);
           }
         }
         if (FMT == 0)
-          yacc[r][m] = __builtin_fmaf(sc[r], acc - 5.f * gsum, yacc[r][m]);
+          yacc[r][m] = __builtin_fmaf(sc[it][r], acc - 5.f * gsum, yacc[r][m]);
         else
-          yacc[r][m] = __builtin_fmaf(sc[r], acc - 4.f * gsum, __builtin_fmaf(bi[r], gsum, yacc[r][m]));
+          yacc[r][m] = __builtin_fmaf(sc[it][r], acc - 4.f * gsum, __builtin_fmaf(bi[it][r], gsum, yacc[r][m]));
       }
     }
   }
@@ -151,25 +180,42 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
   }
 }
 
-template <int FMT, int M>
-int lowbit_launch(const f16* x, int K, int N, const uint8_t* w, const f16* s, const f16* bias, f16* y,
-                  hipStream_t st) {
+template <int FMT, int M, int ITERS>
+int lowbit_launch_iters(const f16* x, int K, int N, const uint8_t* w, const f16* s, const f16* bias, f16* y,
+                        hipStream_t st) {
   const size_t smem = (size_t)M * K * sizeof(f16) + (size_t)M * (K / 64) * sizeof(float);
   if (smem > 160 * 1024) {
     axm_set_error("lowbit gemv: K=%d needs %zu B of LDS", K, smem);
     return -2;
   }
   if (smem > 64 * 1024 &&
-      hipFuncSetAttribute((const void*)lowbit_gemv_kernel<FMT, M>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)smem) != hipSuccess) {
+      hipFuncSetAttribute((const void*)lowbit_gemv_kernel<FMT, M, ITERS>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess) {
     (void)hipGetLastError();
     axm_set_error("lowbit gemv: cannot reserve %zu B of LDS", smem);
     return -2;
   }
   const int rows_per_block = (kLbThreads / 64) * kLbRows;
   const int grid = (N + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((lowbit_gemv_kernel<FMT, M>), dim3(grid), dim3(kLbThreads), smem, st, x, K, N, w, s, bias, y);
+  hipLaunchKernelGGL((lowbit_gemv_kernel<FMT, M, ITERS>), dim3(grid), dim3(kLbThreads), smem, st, x, K, N, w, s,
+                     bias, y);
   return 0;
+}
+
+// Groups per lane: K / 64 groups over 64 lanes, up to 8 (K <= 32768).
+template <int FMT, int M>
+int lowbit_launch(const f16* x, int K, int N, const uint8_t* w, const f16* s, const f16* bias, f16* y,
+                  hipStream_t st) {
+  const int iters = (K / 64 + 63) / 64;
+  switch (iters) {
+    case 1: return lowbit_launch_iters<FMT, M, 1>(x, K, N, w, s, bias, y, st);
+    case 2: return lowbit_launch_iters<FMT, M, 2>(x, K, N, w, s, bias, y, st);
+    case 3: return lowbit_launch_iters<FMT, M, 3>(x, K, N, w, s, bias, y, st);
+    case 4: return lowbit_launch_iters<FMT, M, 4>(x, K, N, w, s, bias, y, st);
+  }
+  if (iters <= 8) return lowbit_launch_iters<FMT, M, 8>(x, K, N, w, s, bias, y, st);
+  axm_set_error("lowbit gemv: K=%d above 32768", K);
+  return -2;
 }
 
 template <int FMT>
