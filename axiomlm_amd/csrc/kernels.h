@@ -57,8 +57,9 @@ int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int ac
 constexpr int kAttnMaxParts = 8;
 int attn_parts_splits(int B, int Hkv, int active_len);
 size_t attn_parts_bytes(int B, int Hq, int hd);  // parts_o + parts_ml for kAttnMaxParts splits
+// short_splits: at most 64 keys per split (the launch shape for such splits).
 int launch_flash_decode_parts(const f16* q, const KvView& kv, int Hq, int active_len, const int* active_len_dev,
-                              int n_splits, f16* parts_o, f32x2* parts_ml, hipStream_t s);
+                              int n_splits, f16* parts_o, f32x2* parts_ml, bool short_splits, hipStream_t s);
 
 // Tree / multi-token verification attention (batch 0): T query tokens; prefix
 // slots [0, prefix_len) always visible; tree node j lives at slot

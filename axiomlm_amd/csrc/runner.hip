@@ -432,7 +432,7 @@ struct axm_runner {
   // Enqueue the whole single-token step on stream s (no host synchronization).
   // The decode step after set_params_kernel, which has written the token's
   // embedding row into x.
-  int enqueue_step(int n_splits, hipStream_t s) {
+  int enqueue_step(int n_splits, bool short_splits, hipStream_t s) {
     const int D = d.d_model;
     const int H = d.hidden_dim;
 
@@ -474,7 +474,8 @@ struct axm_runner {
       // partials are merged while the O projection stages its activations.
       const bool merge_in_o = parts_ok && n_splits > 1;
       if (merge_in_o)
-        rc = launch_flash_decode_parts(q, kv, d.n_head, 0, params + P_ACTIVE, n_splits, parts_o, parts_ml, s);
+        rc = launch_flash_decode_parts(q, kv, d.n_head, 0, params + P_ACTIVE, n_splits, parts_o, parts_ml,
+                                       short_splits, s);
       else
         rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
       if (rc) return rc;
@@ -902,18 +903,22 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
   int bucket = 1;
   while (bucket < splits) bucket <<= 1;
   if (bucket > r->max_splits) bucket = r->max_splits;
+  // Splits of at most 64 keys use a smaller attention launch shape; the graph
+  // key carries that choice next to the split bucket.
+  const bool short_splits = active_len <= 64 * bucket;
+  const int key = 2 * bucket + (short_splits ? 1 : 0);
   if (r->mode == AXM_RUNNER_MODE_EAGER) {
-    int rc = r->enqueue_step(bucket, s);
+    int rc = r->enqueue_step(bucket, short_splits, s);
     if (rc) return rc;
   } else {
-    auto it = r->graphs.find(bucket);
+    auto it = r->graphs.find(key);
     if (it == r->graphs.end()) {
       hipGraph_t g = nullptr;
       if (hipStreamBeginCapture(r->cap_stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
         axm_set_error("runner_step: stream capture failed to start");
         return -5;
       }
-      int rc = r->enqueue_step(bucket, r->cap_stream);
+      int rc = r->enqueue_step(bucket, short_splits, r->cap_stream);
       hipError_t e = hipStreamEndCapture(r->cap_stream, &g);
       if (rc) {
         if (g) (void)hipGraphDestroy(g);
@@ -930,7 +935,7 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
         axm_set_error("runner_step: graph instantiate failed: %s", hipGetErrorString(e));
         return -5;
       }
-      it = r->graphs.emplace(bucket, ge).first;
+      it = r->graphs.emplace(key, ge).first;
     }
     if (hipGraphLaunch(it->second, s) != hipSuccess) {
       axm_set_error("runner_step: graph launch failed");
