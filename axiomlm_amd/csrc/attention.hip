@@ -101,25 +101,15 @@ __global__ void __launch_bounds__(kKvWriteWaves * 64)
 // so a 64-group spans 64 / EPL lanes and its maximum is taken by shuffles within
 // them.  Per element the arithmetic is kv_store_lane's.
 template <int EPL>
-__global__ void __launch_bounds__(kKvWriteWaves * 64)
-    kv_write_row_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld,
-                        int write_pos, const int* __restrict__ write_pos_dev, int n_items) {
+using kv_hvec = _Float16 __attribute__((ext_vector_type(EPL)));
+
+template <int EPL>
+__device__ __forceinline__ void kv_row_store(const KvView& kv, int which, int h, int slot, int lane,
+                                             kv_hvec<EPL> xv) {
   constexpr int LPG = 64 / EPL;  // lanes per 64-group
-  typedef _Float16 hvec __attribute__((ext_vector_type(EPL)));
-  const int lane = threadIdx.x & 63;
-  int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
-  if (idx >= n_items) return;
-  const int h = idx % kv.Hkv;
-  idx /= kv.Hkv;
-  const int which = idx & 1;
-  const int t = idx >> 1;
-  const int wp0 = write_pos_dev ? write_pos_dev[0] : write_pos;
-  const int slot = (wp0 + t) % kv.S;
-  const hvec xv = *reinterpret_cast<const hvec*>((which == 0 ? k_rows : v_rows) + (size_t)t * ld + h * kv.hd +
-                                                 EPL * lane);
   const size_t row = (size_t)h * kv.S + slot;  // batch 0
   if (kv.kv_dtype == AXM_KV_FP16) {
-    *reinterpret_cast<hvec*>((f16*)(which == 0 ? kv.k : kv.v) + row * kv.hd + EPL * lane) = xv;
+    *reinterpret_cast<kv_hvec<EPL>*>((f16*)(which == 0 ? kv.k : kv.v) + row * kv.hd + EPL * lane) = xv;
     return;
   }
   float ax = fabsf(h2f(xv[0]));  // seeded like wave_max (an all-NaN group keeps a NaN maximum)
@@ -173,6 +163,58 @@ __global__ void __launch_bounds__(kKvWriteWaves * 64)
     if (EPL == 2) *d = (uint8_t)packed;
     else *reinterpret_cast<uint16_t*>(d) = (uint16_t)packed;
   }
+}
+
+template <int EPL>
+__global__ void __launch_bounds__(kKvWriteWaves * 64)
+    kv_write_row_kernel(KvView kv, const f16* __restrict__ k_rows, const f16* __restrict__ v_rows, int ld,
+                        int write_pos, const int* __restrict__ write_pos_dev, int n_items) {
+  const int lane = threadIdx.x & 63;
+  int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
+  if (idx >= n_items) return;
+  const int h = idx % kv.Hkv;
+  idx /= kv.Hkv;
+  const int which = idx & 1;
+  const int t = idx >> 1;
+  const int wp0 = write_pos_dev ? write_pos_dev[0] : write_pos;
+  const int slot = (wp0 + t) % kv.S;
+  const kv_hvec<EPL> xv = *reinterpret_cast<const kv_hvec<EPL>*>((which == 0 ? k_rows : v_rows) + (size_t)t * ld +
+                                                                 h * kv.hd + EPL * lane);
+  kv_row_store<EPL>(kv, which, h, slot, lane, xv);
+}
+
+// RoPE + KV write of T tokens in one launch (head size 128): one wave per
+// (token, head row) of qkv [T][q_dim + 2 kv_dim] (bias already added); lane l
+// holds rotation pair l.  Query rows are rotated at pos_dev[t] into q
+// [T][q_dim], key rows rotated and value rows as they are go to slot
+// (write_pos + t) % S (the arithmetic of the RoPE kernel and of kv_row_store).
+__global__ void __launch_bounds__(kKvWriteWaves * 64)
+    rope_kv_row_kernel(KvView kv, const f16* __restrict__ qkv, int Hq, int T, const float* __restrict__ freqs,
+                       const int* __restrict__ pos_dev, f16* __restrict__ q, int write_pos) {
+  constexpr int HD = 128;
+  const int lane = threadIdx.x & 63;
+  const int rows = Hq + 2 * kv.Hkv;
+  const int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
+  if (idx >= T * rows) return;
+  const int t = idx / rows, r = idx % rows;
+  const int q_dim = Hq * HD, kv_dim = kv.Hkv * HD;
+  const f16x2 v = *reinterpret_cast<const f16x2*>(qkv + (size_t)t * (q_dim + 2 * kv_dim) + (size_t)r * HD + 2 * lane);
+  kv_hvec<2> out;
+  if (r < Hq + kv.Hkv) {
+    const float* f = freqs + ((size_t)pos_dev[t] * (HD / 2) + lane) * 2;
+    out[0] = rope_out(v[0], v[1], f[0], f[1], true);
+    out[1] = rope_out(v[0], v[1], f[0], f[1], false);
+  } else {
+    out[0] = v[0];
+    out[1] = v[1];
+  }
+  if (r < Hq) {
+    *reinterpret_cast<kv_hvec<2>*>(q + (size_t)t * q_dim + (size_t)r * HD + 2 * lane) = out;
+    return;
+  }
+  const int which = r < Hq + kv.Hkv ? 0 : 1;
+  const int h = r - Hq - which * kv.Hkv;
+  kv_row_store<2>(kv, which, h, (write_pos + t) % kv.S, lane, out);
 }
 
 // Fused bias + RoPE + KV-cache write of T tokens (rope_kv_cache_write_half_kernel,
@@ -778,6 +820,18 @@ int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int 
   const unsigned blocks = (unsigned)((items + kKvWriteWaves - 1) / kKvWriteWaves);
   hipLaunchKernelGGL(kv_write_kernel, dim3(blocks), dim3(kKvWriteWaves * 64), 0, s, kv, k_rows, v_rows, ld_rows,
                      write_pos, write_pos_dev, items);
+  return 0;
+}
+
+int launch_rope_kv_write(const KvView& kv, const f16* qkv, int Hq, int T, const float* freqs, const int* pos_dev,
+                         f16* q, int write_pos, hipStream_t s) {
+  if (kv.hd != 128 || ((uintptr_t)qkv & 3) != 0 || ((uintptr_t)q & 3) != 0) {
+    axm_set_error("rope_kv_write: head size %d (128) or misaligned rows", kv.hd);
+    return -2;
+  }
+  const int items = T * (Hq + 2 * kv.Hkv);
+  hipLaunchKernelGGL(rope_kv_row_kernel, dim3((unsigned)((items + kKvWriteWaves - 1) / kKvWriteWaves)),
+                     dim3(kKvWriteWaves * 64), 0, s, kv, qkv, Hq, T, freqs, pos_dev, q, write_pos);
   return 0;
 }
 

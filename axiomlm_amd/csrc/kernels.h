@@ -41,6 +41,12 @@ struct KvView {
 // (batch 0).  write_pos_dev overrides write_pos when non-null.
 int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int ld_rows, int T, int write_pos,
                     const int* write_pos_dev, hipStream_t s);
+// RoPE of the query and key rows of qkv [T][Hq hd + 2 Hkv hd] (token t at
+// pos_dev[t], freqs as the runner holds them) with the queries into q
+// [T][Hq hd] and the keys / values written at slots (write_pos + t) % S, in one
+// launch; head size 128 only (-2 otherwise).
+int launch_rope_kv_write(const KvView& kv, const f16* qkv, int Hq, int T, const float* freqs, const int* pos_dev,
+                         f16* q, int write_pos, hipStream_t s);
 
 // Split-KV decode attention over slots [0, active_len) of every batch entry.
 // q: [B][Hq][hd] fp16, out: [B][Hq][hd] fp16.  ws: workspace of

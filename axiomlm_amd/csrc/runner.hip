@@ -616,9 +616,15 @@ struct axm_runner {
       a.eps = d.eps;
       int rc = gemv_rows(m_qkv[i], Q4_EPI_STORE, qkv_dim, a, T, s);
       if (rc) return rc;
-      hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, T), dim3(256), 0, s, qkvbuf, q_dim,
-                         kv_dim, d.head_dim, d.freqs, tree_pos, q, kvst);
-      launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, T, write_pos, nullptr, s);
+      if (d.head_dim == 128) {
+        // RoPE and the cache write in one launch.
+        rc = launch_rope_kv_write(kv, qkvbuf, d.n_head, T, d.freqs, tree_pos, q, write_pos, s);
+        if (rc) return rc;
+      } else {
+        hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, T), dim3(256), 0, s, qkvbuf, q_dim,
+                           kv_dim, d.head_dim, d.freqs, tree_pos, q, kvst);
+        launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, T, write_pos, nullptr, s);
+      }
       if (tree) {
         const int splits = tree_choose_splits(T, d.n_head, d.n_kv_head, prefix + T);
         rc = launch_tree_attention(q, kv, attn_y, d.n_head, T, prefix, write_pos, (const uint64_t*)tree_mask, splits, ws,

@@ -328,12 +328,14 @@ def test_runner_verify_step_chain(dev):
     _check_logits(got, model.forward([tok], ocache)[-1], "step after verify")
 
 
-def test_runner_verify_step_split_gemms(dev):
+@pytest.mark.parametrize("kv", ["fp16", "fp8"])
+def test_runner_verify_step_split_gemms(dev, kv):
     """verify_step on a wider model (d 1024, head 128, MLP 2816) whose multi-token GEMMs
     split K at 40 and 20 tokens: the residual GEMMs' fused split-reduce + RMSNorm (the
-    next GEMM's input), the two-unit store form and the 32-token form, against the
-    oracle's multi-token forward, then a decode step."""
-    print("[runner_verify_split_gemms]", flush=True)
+    next GEMM's input), the two-unit store form, the 32-token form and the one-launch
+    RoPE + cache write of head size 128, against the oracle's multi-token forward, then
+    a decode step."""
+    print(f"[runner_verify_split_gemms] kv={kv}", flush=True)
     cfg = om.OracleConfig(n_layer=2, n_head=8, n_kv_head=8, d_model=1024, hidden=2816, vocab=1024, eps=1e-5,
                           block_size=256)
     W = om.make_float_weights(cfg, seed=3)
@@ -341,21 +343,41 @@ def test_runner_verify_step_split_gemms(dev):
     cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, 10000.0)
     model = om.OracleModel(cfg, ow, cos, sin)
     S = 128
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, max_tokens=64)
-    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, kv, max_tokens=64)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv)
+    # fp8: the oracle reads the GPU's cache codes (a rounding-boundary code flip
+    # moves logits by more than the bound; see the quantized-KV step test), so
+    # each GPU call runs first and the oracle repeats it on the loaded cache.
+    frozen = kv != "fp16"
+    ocache.frozen = frozen
+
+    def sync(seen):
+        _load_gpu_cache(ocache, cache)
+        ocache.total_seen_tokens[:] = [seen] * cfg.n_layer
+        ocache.layer_seq_lens[:] = [seen] * cfg.n_layer
+
     rng = np.random.default_rng(14)
-    _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 6).tolist(), dev)
+    prefix = rng.integers(0, cfg.vocab, 6).tolist()
+    if frozen:
+        run_steps(runner, cache, prefix, dev)
+    else:
+        _prefill(runner, cache, ocache, model, prefix, dev)
     for T in (40, 20):
         seen = cache.total_seen_tokens[0]
         toks = rng.integers(0, cfg.vocab, T).tolist()
         got = runner.verify_step(torch.tensor([toks], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
+        if frozen:
+            sync(seen)
         ref = model.forward(toks, ocache, return_all_logits=True)
         cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
         cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
         for t in range(T):
             _check_logits(got[t], ref[t], f"verify T={T} token {t}")
+    seen = cache.total_seen_tokens[0]
     tok = int(rng.integers(0, cfg.vocab))
     got = run_steps(runner, cache, [tok], dev)[0]
+    if frozen:
+        sync(seen)
     _check_logits(got, model.forward([tok], ocache)[-1], "step after verify")
 
 
