@@ -13,13 +13,17 @@ Pinning (see tests/test_oracle_*.py):
     (quant.py:462-463) on random matrices.
   * RTN codes: brute-force optimality (each code is the nearest lattice point)
     and closed-form scale/bias on hand-built groups.
-  * MSE clip search (quant.py:495-571): golden vectors written by
-    tests/golden/make_golden.py from the reference implementation.
+  * MSE clip search (quant.py:495-571): SHA-256 of every C1 pack written by
+    tests/golden/make_golden_c1.py from the reference implementation
+    (tests/test_oracle_golden.py).
   * Ternary / Q2: reference KATs (tests/test_phase3_task33_bitnet_q2k.py:62-129)
     and byte-per-weight constants (:321-324).
   * FP8 E4M3FN: all 65536 fp16 inputs against torch's own cast (the library
     the reference calls, quant.py:719, 766).
-  * INT4 KV: closed form + exact round trip on lattice inputs.
+  * INT4 KV: closed form, exact round trip on lattice inputs, and torch's own
+    round / clamp / int8 cast (quant.py:789-803) on exact .5 ties, all-zero
+    (NaN-code) groups, subnormal groups and every fp16 quotient in [-8.5, 8.5]
+    (tests/test_oracle_model.py).
 """
 
 from __future__ import annotations

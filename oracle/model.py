@@ -12,11 +12,23 @@ Follows the CPU path of a half-precision AxiomLM model:
 
 Every fp16 op rounds to fp16; matmuls and SDPA accumulate in fp32 and round once.
 
-Pinning: the closed forms are checked in tests/test_oracle_model.py (RMSNorm vs a
-float64 evaluation, RoPE rotation preserving pair norms, SDPA vs a direct
-softmax, ring-buffer counters 67/32 from the reference tests), and the whole
-forward against golden logits / greedy tokens written from the reference by
-tests/golden/make_golden.py.
+This module is test infrastructure: only tests/, the smoke check and the CPU
+baseline of bench.py use it, as the checker.
+
+Pinning (tests/test_oracle_model.py unless noted):
+  * RMSNorm against a float64 evaluation, SDPA against equal-score / dominant-key
+    closed forms, a float64 softmax and key gathering, RoPE pair norms and angles;
+  * ``forward`` (decode, 32-token prefill, 64 greedy tokens) against golden logits
+    written from the reference by tests/golden/make_golden_c1.py
+    (tests/test_oracle_golden.py);
+  * ``OracleKVCache.update`` in ring mode, ``forward_tree`` and
+    ``forward_verify_ring`` against a brute-force model with explicit per-query
+    key sets over a flat token history (sliding window, prefix + ancestors at
+    seen + depth, all S slots), ``forward_tree`` against ``forward`` over each
+    node's ancestor path and over a chain, the reference ring counters 67 / 32
+    and 25 / 16;
+  * ``compact_tree_path`` against a gather from a snapshot (overlapping and
+    wrapping slots, a non-monotonic accepted list).
 """
 
 from __future__ import annotations
