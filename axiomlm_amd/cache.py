@@ -16,7 +16,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .kernels.ops import KV_CODES, dequantize_kv_fp8, dequantize_kv_int4
+from .kernels.ops import KV_CODES, compact_tree_kv, dequantize_kv_fp8, dequantize_kv_int4
 
 
 class StaticKVCache:
@@ -142,18 +142,9 @@ class StaticKVCache:
     def compact_tree_path(self, write_pos: int, accepted_indices: list[int], new_total_seen: int | None = None):
         """Move accepted tree slots (write_pos + a[m]) % S to (write_pos + m) % S in every layer
         with one race-free HIP pass (paged_cache.py:376-462)."""
-        n = len(accepted_indices)
-        if n > 0 and not all(int(a) == m for m, a in enumerate(accepted_indices)):
-            _lib.require_gpu(self.cache, "compact_tree_path")
-            if not self.cache.is_contiguous() or (self.scales is not None and not self.scales.is_contiguous()):
-                raise RuntimeError("compact_tree_path: cache and scales must be contiguous")
-            L, two, B, H, S = self.cache.shape[:5]
-            slot_bytes = self.cache.shape[5] * self.cache.element_size()
-            halves = self.scales.shape[5] if self.scales is not None else 0
-            arr = (ctypes.c_int * n)(*[int(a) for a in accepted_indices])
-            _lib.check(_lib.lib().axm_compact_tree_kv(
-                _lib.ptr(self.cache), _lib.ptr(self.scales), L * two * B * H, S, slot_bytes, halves, int(write_pos),
-                arr, n, _lib.stream_of(self.cache.device)), "compact_tree_path")
+        if self.scales is not None and not self.scales.is_contiguous():
+            raise RuntimeError("compact_tree_path: cache and scales must be contiguous")
+        compact_tree_kv(self.cache, self.scales, write_pos, accepted_indices)
         if new_total_seen is not None:
             active = min(new_total_seen, self.max_seq_len)
             self.total_seen_tokens[:] = [new_total_seen] * self.n_layer

@@ -269,6 +269,33 @@ def gqa_tree_verify_mps(
 
 
 # ---------------------------------------------------------------------------
+# Tree-path KV compaction (compact_tree_kv{,_quant}_mps, mps_kernels.mm:4066-4110, 4251-4295)
+# ---------------------------------------------------------------------------
+def compact_tree_kv(cache: torch.Tensor, scales: torch.Tensor | None, write_pos: int, accepted_indices) -> None:
+    """Move slot (write_pos + a[m]) % S to (write_pos + m) % S in every (layer, k|v, batch,
+    head) row block of a 6-D StaticKVCache tensor (L, 2, B, Hkv, S, width) and, for FP8 /
+    INT4 caches, of its scales (L, 2, B, Hkv, S, hd/64); one race-free pass, up to 64
+    accepted nodes."""
+    acc = [int(a) for a in accepted_indices]
+    n = len(acc)
+    if n == 0 or all(a == m for m, a in enumerate(acc)):
+        return
+    _lib.require_gpu(cache, "compact_tree_kv")
+    if cache.dim() != 6 or not cache.is_contiguous():
+        raise ValueError("compact_tree_kv expects a contiguous 6-D StaticKVCache tensor")
+    if scales is not None and (scales.dim() != 6 or not scales.is_contiguous() or
+                               tuple(scales.shape[:5]) != tuple(cache.shape[:5])):
+        raise ValueError("compact_tree_kv: scales must be a contiguous 6-D tensor over the same slots")
+    L, two, B, H, S = cache.shape[:5]
+    slot_bytes = cache.shape[5] * cache.element_size()
+    halves = scales.shape[5] if scales is not None else 0
+    arr = (ctypes.c_int * n)(*acc)
+    _lib.check(_lib.lib().axm_compact_tree_kv(_lib.ptr(cache), _lib.ptr(scales), L * two * B * H, S, slot_bytes,
+                                              halves, int(write_pos), arr, n, _lib.stream_of(cache.device)),
+               "compact_tree_kv")
+
+
+# ---------------------------------------------------------------------------
 # Norms / activations / argmax
 # ---------------------------------------------------------------------------
 def fused_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

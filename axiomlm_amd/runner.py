@@ -89,6 +89,7 @@ class QuantizedDecodeRunner:
         kv_code = KV_CODES[kv_dtype]
         self.kv_dtype = kv_dtype
         self.max_seq_len = int(k_cs[0].shape[-2])
+        self.rope_len = int(freqs.shape[0])
 
         def first_batch(t):
             return keep(t[0] if t.dim() == 4 else t)

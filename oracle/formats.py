@@ -169,17 +169,34 @@ def pack_linear_q4_marlin(weight: np.ndarray, clip_search: bool = True, col_impo
     return interleave_marlin(q, scale, bias)
 
 
+def _marlin_group_order():
+    """Position in a group's 512 (lane, word, half, s) nibbles of each (row c, column k) code:
+    the nibble at bits 16*half + 4*s of word j of lane l holds row c0(l) + half, column
+    32 j + 8 s + r(l) (quant.py:573-593)."""
+    r_idx, c0_idx = marlin_lane_maps()
+    order = np.empty((8, 64), dtype=np.int64)
+    for lane in range(32):
+        for j in range(2):
+            for half in range(2):
+                for s in range(4):
+                    order[c0_idx[lane] + half, 32 * j + 8 * s + r_idx[lane]] = ((lane * 2 + j) * 2 + half) * 4 + s
+    return order.reshape(-1)
+
+
+_MARLIN_ORDER = _marlin_group_order()
+
+
 def unpack_marlin_codes(w_marlin: np.ndarray):
     """Inverse interleave: codes [N_pad, K] (uint8), quant.py:597-625."""
     nt, KG, _, _ = w_marlin.shape
-    r_idx, c0_idx = marlin_lane_maps()
-    w = w_marlin.view(np.uint32).astype(np.int64)[..., None]  # (nt, KG, 32, 2, 1)
-    q_c0 = (w >> np.array([0, 4, 8, 12])) & 0xF
-    q_c1 = (w >> np.array([16, 20, 24, 28])) & 0xF
-    q_cr = np.zeros((nt, KG, 8, 8, 2, 4), dtype=np.int64)
-    q_cr[:, :, c0_idx, r_idx] = q_c0
-    q_cr[:, :, c0_idx + 1, r_idx] = q_c1
-    return q_cr.transpose(0, 2, 1, 4, 5, 3).reshape(nt * 8, KG * 64).astype(np.uint8)
+    w = w_marlin.view(np.uint32)
+    # nibbles as (tile, group, lane, word, half, s)
+    nib = np.empty((nt, KG, 32, 2, 2, 4), dtype=np.uint8)
+    for half in range(2):
+        for s in range(4):
+            nib[..., half, s] = (w >> np.uint32(16 * half + 4 * s)) & np.uint32(0xF)
+    q = nib.reshape(nt, KG, 512)[:, :, _MARLIN_ORDER].reshape(nt, KG, 8, 64)
+    return np.ascontiguousarray(q.transpose(0, 2, 1, 3)).reshape(nt * 8, KG * 64)
 
 
 def dequantize_q4_marlin(w_marlin: np.ndarray, sb_marlin: np.ndarray, K: int, out_features: int | None = None):

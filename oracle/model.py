@@ -268,12 +268,31 @@ class OracleWeights:
     c_attn_b: list = field(default_factory=list)
 
 
-def qlin(x16, wp, wsb, out_features, bias=None):
-    """Transformer._qlin (transformer.py:1010-1034)."""
+_DEQ_MEMO: dict = {}
+
+
+def _dequantized(wp, wsb, K, out_features):
+    """fp16 weights of a packed matrix, memoized per packed array (the entry keeps the
+    arrays alive, so an id is never reused while its entry exists)."""
+    key = (id(wp), id(wsb), K, out_features)
+    hit = _DEQ_MEMO.get(key)
+    if hit is not None and hit[0] is wp and hit[1] is wsb:
+        return hit[2]
     if wp.ndim == 4:
-        return fm.qmv_q4_marlin(x16, wp, wsb, out_features, bias)
+        w = fm.dequantize_q4_marlin(wp, wsb, K, out_features)
+    else:
+        w = fm.dequantize_q8_g64(wp, wsb, K)
+    if sum(e[2].nbytes for e in _DEQ_MEMO.values()) + w.nbytes > (1 << 30):
+        _DEQ_MEMO.clear()
+    _DEQ_MEMO[key] = (wp, wsb, w)
+    return w
+
+
+def qlin(x16, wp, wsb, out_features, bias=None):
+    """Transformer._qlin (transformer.py:1010-1034): the CPU fallback dequantizes the
+    packed weights to fp16 (quant.py:656-661, 597-634 / 72-129), then F.linear."""
     K = x16.shape[-1]
-    w = fm.dequantize_q8_g64(wp, wsb, K)
+    w = _dequantized(wp, wsb, K, out_features)
     y = fm.linear_fp16(x16, w)
     if bias is not None:
         y = (y.astype(F32) + bias.astype(F32)).astype(F16)

@@ -18,22 +18,34 @@ F16, F32 = np.float16, np.float32
 TOL = 1e-2
 
 
-def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile16", mode=None, max_tokens=32):
+def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile16", mode=None, max_tokens=32,
+                 wte16=False):
+    """Runner over the oracle's packs.  A 2-D (Q8_G64) lm_head goes in as the reference's int32
+    [V, d/4] view; ``wte16`` passes the embedding as an fp16 table (the reference's ``wte_emb``,
+    here the Q8 rows dequantized, so both paths embed identical values) instead of Q8 rows;
+    ``ow.c_attn_b`` becomes ``c_attn_bs``."""
     from axiomlm_amd.cache import StaticKVCache
     from axiomlm_amd.runner import QuantizedDecodeRunner
+
+    from oracle import formats as fm
 
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     cache = StaticKVCache(1, S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, device=dev, cache_dtype=kv,
                           ring_buffer=ring)
     freqs = t(np.stack([cos, sin], axis=-1).astype(F32))
+    lmh = ow.lmh_p.view(np.int32).reshape(cfg.vocab, -1) if ow.lmh_p.ndim == 2 else ow.lmh_p
+    if wte16:
+        wte_emb = t(fm.dequant_q8_rows(np.arange(cfg.vocab), ow.wte_p, ow.wte_sb).astype(F16))
+        wte_p = wte_s = None
+    else:
+        wte_emb, wte_p, wte_s = None, t(ow.wte_p.view(np.int32).reshape(cfg.vocab, -1)), t(ow.wte_sb)
     r = QuantizedDecodeRunner(
-        None, t(ow.lmh_p), t(ow.lmh_sb), freqs, [t(x) for x in ow.ln1], [t(x) for x in ow.c_attn_p],
+        wte_emb, t(lmh), t(ow.lmh_sb), freqs, [t(x) for x in ow.ln1], [t(x) for x in ow.c_attn_p],
         [t(x) for x in ow.c_attn_s], [t(x) for x in ow.c_proj_p], [t(x) for x in ow.c_proj_s],
         [t(x) for x in ow.ln2], [t(x) for x in ow.gu_p], [t(x) for x in ow.gu_s], [t(x) for x in ow.wd_p],
         [t(x) for x in ow.wd_s], t(ow.lnf), cache.k_caches, cache.v_caches, cfg.n_head, cfg.n_kv_head,
-        cfg.head_dim, True, cfg.eps, [], cfg.vocab, wte_p=t(ow.wte_p.view(np.int32).reshape(cfg.vocab, -1)),
-        wte_s=t(ow.wte_sb), k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv, layout=layout,
-        max_tokens=max_tokens)
+        cfg.head_dim, True, cfg.eps, [t(b) for b in ow.c_attn_b], cfg.vocab, wte_p=wte_p, wte_s=wte_s,
+        k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv, layout=layout, max_tokens=max_tokens)
     if mode is not None:
         r.set_mode(mode)
     return r, cache
@@ -103,6 +115,38 @@ def _load_gpu_cache(ocache, cache):
         ocache.vs[...] = cache.scales[:, 1, 0].cpu().numpy()
 
 
+def _signed_codes(kv, a):
+    """Codes on a line where neighbouring codes differ by one: int4 nibbles as signed values,
+    fp8 bytes as sign * magnitude (bytes of one sign are monotone in value)."""
+    a = np.asarray(a)
+    if kv == "int4":
+        lo = ((a.astype(np.int32) & 0xF) ^ 8) - 8
+        hi = (((a.astype(np.int32) >> 4) & 0xF) ^ 8) - 8
+        return np.stack([lo, hi])
+    return np.where(a & 0x80, -1, 1) * (a.astype(np.int32) & 0x7F)
+
+
+def _code_diffs(kv, ocache):
+    """|GPU code - oracle code| over every slot of the oracle's last (frozen) write, per layer:
+    the GPU's codes were loaded into the frozen oracle cache, the oracle's own codes are
+    in last_write."""
+    out = []
+    for L in range(ocache.n_layer):
+        slots, kq, _, vq, _ = ocache.last_write[L]
+        g = np.stack([ocache.k[L][:, slots], ocache.v[L][:, slots]])
+        o = np.stack([kq, vq])
+        out.append(np.abs(_signed_codes(kv, g) - _signed_codes(kv, o)).ravel())
+    return np.concatenate(out)
+
+
+def _check_codes(kv, diff, what):
+    """Bar of test_runner_quantized_kv_matches_oracle: >= 95% identical, >= 99% within one step."""
+    same, near = (diff == 0).mean(), (diff <= 1).mean()
+    print(f"[{what}] kv={kv}: {same:.4f} of codes identical, {near:.5f} within one step", flush=True)
+    assert same >= 0.95, f"{what}: only {same:.4f} of codes identical"
+    assert near >= 0.99, f"{what}: only {near:.5f} of codes within one step"
+
+
 @pytest.mark.parametrize("kv", ["fp8", "int4"])
 def test_runner_quantized_kv_matches_oracle(dev, kv):
     """Quantized KV inside the captured step.
@@ -131,13 +175,6 @@ def test_runner_quantized_kv_matches_oracle(dev, kv):
     frozen.frozen = True
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, cfg.vocab, 40).tolist()
-    if kv == "int4":
-        lo = lambda a: ((a.astype(np.int32) & 0xF) ^ 8) - 8  # noqa: E731
-        hi = lambda a: (((a.astype(np.int32) >> 4) & 0xF) ^ 8) - 8  # noqa: E731
-        signed = lambda a: np.stack([lo(a), hi(a)])  # noqa: E731
-    else:
-        # fp8 bytes of one sign are monotone in value: adjacent codes differ by 1
-        signed = lambda a: np.where(a & 0x80, -1, 1) * (a.astype(np.int32) & 0x7F)  # noqa: E731
     diffs = []
     for i, tok in enumerate(prompt):
         got = run_steps(runner, cache, [tok], dev)[0]
@@ -149,13 +186,9 @@ def test_runner_quantized_kv_matches_oracle(dev, kv):
             assert list(slots) == [i]
             g = np.stack([frozen.k[L][:, i], frozen.v[L][:, i]])
             o = np.stack([kq[:, 0], vq[:, 0]])
-            diffs.append(np.abs(signed(g) - signed(o)).ravel())
+            diffs.append(np.abs(_signed_codes(kv, g) - _signed_codes(kv, o)).ravel())
         _check_logits(got, ref, f"step {i}")
-    diff = np.concatenate(diffs)
-    same, near = (diff == 0).mean(), (diff <= 1).mean()
-    print(f"[runner_qkv] kv={kv}: {same:.4f} of codes identical, {near:.5f} within one step", flush=True)
-    assert same >= 0.95, f"only {same:.4f} of codes identical"
-    assert near >= 0.99, f"only {near:.5f} of codes within one step"
+    _check_codes(kv, np.concatenate(diffs), "runner_qkv")
 
 
 @pytest.mark.parametrize("mode", MODES)
@@ -186,7 +219,7 @@ def test_runner_greedy_c1(dev, mode):
         lg = run_steps(runner, cache, [tok], dev)[0]
         _check_logits(lg, ref_logits[i], f"greedy step {i}")
         tok = int(np.argmax(lg))
-    assert mism == 0 or len(got_tokens) > 0
+    assert len(got_tokens) == 64 or mism == 1
 
 
 @pytest.mark.parametrize("mode", MODES)
@@ -369,6 +402,11 @@ def test_runner_verify_step_split_gemms(dev, kv):
         if frozen:
             sync(seen)
         ref = model.forward(toks, ocache, return_all_logits=True)
+        if frozen:
+            # the codes the one-launch RoPE + cache write stored for the T new rows against
+            # the oracle's own quantization of the rows it computed
+            assert all(list(ocache.last_write[L][0]) == list(range(seen, seen + T)) for L in range(cfg.n_layer))
+            _check_codes(kv, _code_diffs(kv, ocache), f"verify_split T={T}")
         cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
         cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
         for t in range(T):
@@ -459,3 +497,155 @@ def test_runner_speculative_decode_matches_greedy(dev):
     assert seen == len(prompt) - 1 + n_new and calls <= n_new and drafted >= accepted >= 0 and secs > 0
     print(f"[runner_speculative] calls={calls} drafted={drafted} accepted={accepted} near-tie choices={ties}",
           flush=True)
+
+
+# ---------------------------------------------------------------------------
+# Runner branches: tied Q8_G64 lm_head, fp16 embedding table, QKV bias
+# ---------------------------------------------------------------------------
+def _branch_model(variant):
+    cfg = om.OracleConfig(n_layer=2, n_head=4, n_kv_head=2, d_model=256, hidden=704, vocab=1024, eps=1e-5,
+                          block_size=256)
+    W = om.make_float_weights(cfg, seed=7)
+    if variant == "tied_q8":
+        W["lm_head"] = W["wte"]
+    ow = om.pack_model_rtn(cfg, W)
+    if variant == "tied_q8":
+        # tie_word_embeddings: the lm_head is the Q8_G64 pack of the embedding and the
+        # embedding gather shares it (transformer.py:842-846, 889-892)
+        ow.lmh_p, ow.lmh_sb = ow.wte_p, ow.wte_sb
+    if variant == "qkv_bias":
+        rng = np.random.default_rng(17)
+        rows = (cfg.n_head + 2 * cfg.n_kv_head) * cfg.head_dim
+        ow.c_attn_b = [(rng.standard_normal(rows) * 0.5).astype(F16) for _ in range(cfg.n_layer)]
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, 10000.0)
+    return cfg, ow, cos, sin
+
+
+@pytest.mark.parametrize("variant", ["tied_q8", "fp16_wte", "qkv_bias"])
+def test_runner_branches_match_oracle(dev, variant):
+    """The reference default head for tied embeddings (Q8_G64 lm_head shared with the
+    embedding gather, runner lm_head format 1), an fp16 embedding table (wte format 0)
+    and a QKV bias, through decode steps, a 6-token verify chain and a 9-node tree,
+    against the oracle (logits <= 1e-2)."""
+    print(f"[runner_branches] {variant}", flush=True)
+    cfg, ow, cos, sin = _branch_model(variant)
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, wte16=(variant == "fp16_wte"))
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    rng = np.random.default_rng(31)
+    toks = rng.integers(0, cfg.vocab, 24).tolist()
+    got = run_steps(runner, cache, toks, dev)
+    for i, tok in enumerate(toks):
+        _check_logits(got[i], model.forward([tok], ocache)[-1], f"{variant} step {i}")
+    seen = cache.total_seen_tokens[0]
+    chain = rng.integers(0, cfg.vocab, 6).tolist()
+    g = runner.verify_step(torch.tensor([chain], device=dev), seen, seen, seen + 6)[0].float().cpu().numpy()
+    ref = model.forward(chain, ocache, return_all_logits=True)
+    for t in range(6):
+        _check_logits(g[t], ref[t], f"{variant} verify token {t}")
+    seen += 6
+    cache.total_seen_tokens[:] = [seen] * cfg.n_layer
+    cache.layer_seq_lens[:] = [seen] * cfg.n_layer
+    parents = [-1, 0, 0, 1, 1, 2, 3, 5, 5]
+    depths, masks = [], []
+    for u, p in enumerate(parents):
+        depths.append(0 if p < 0 else depths[p] + 1)
+        masks.append((0 if p < 0 else masks[p]) | (1 << u))
+    tree = rng.integers(0, cfg.vocab, len(parents)).tolist()
+    g = runner.verify_tree_step(torch.tensor([tree], device=dev), seen, seen, seen, depths, masks)
+    g = g[0].float().cpu().numpy()
+    ref = model.forward_tree(tree, ocache, depths, masks)
+    for t in range(len(tree)):
+        _check_logits(g[t], ref[t], f"{variant} tree node {t}")
+
+
+# ---------------------------------------------------------------------------
+# Head size 128 with grouped KV heads: the one-launch RoPE + cache write of the
+# verify step at tree depths and across the ring's end, fp16 / fp8 / int4
+# ---------------------------------------------------------------------------
+def _gqa128_model():
+    cfg = om.OracleConfig(n_layer=2, n_head=8, n_kv_head=2, d_model=1024, hidden=1024, vocab=1024, eps=1e-5,
+                          block_size=512)
+    W = om.make_float_weights(cfg, seed=9)
+    ow = om.pack_model_rtn(cfg, W)
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, 10000.0)
+    return cfg, ow, cos, sin
+
+
+def _sync_frozen(ocache, cache, seen, S):
+    _load_gpu_cache(ocache, cache)
+    ocache.total_seen_tokens[:] = [seen] * ocache.n_layer
+    ocache.layer_seq_lens[:] = [min(seen, S)] * ocache.n_layer
+
+
+@pytest.mark.parametrize("kv", ["fp16", "fp8", "int4"])
+def test_runner_verify_tree_step_gqa_head128(dev, kv):
+    """A 24-node tree (depths up to 6) on 8 query / 2 KV heads of size 128.  fp16: the oracle
+    writes its own rows.  fp8 / int4: the oracle attends over the GPU's codes (loaded after
+    the GPU step) and the codes the GPU wrote for the 24 tree slots are compared with the
+    oracle's quantization of its own rows (test_runner_quantized_kv_matches_oracle's bar)."""
+    print(f"[runner_tree_gqa128] kv={kv}", flush=True)
+    cfg, ow, cos, sin = _gqa128_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, kv, max_tokens=64)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv)
+    frozen = kv != "fp16"
+    ocache.frozen = frozen
+    rng = np.random.default_rng(23)
+    prefix = rng.integers(0, cfg.vocab, 20).tolist()
+    if frozen:
+        run_steps(runner, cache, prefix, dev)
+    else:
+        _prefill(runner, cache, ocache, model, prefix, dev)
+    parents = [-1] + [int(rng.integers(max(0, u - 4), u)) for u in range(1, 24)]
+    depths, masks = [], []
+    for u, p in enumerate(parents):
+        depths.append(0 if p < 0 else depths[p] + 1)
+        masks.append((0 if p < 0 else masks[p]) | (1 << u))
+    assert max(depths) >= 4
+    toks = rng.integers(0, cfg.vocab, len(parents)).tolist()
+    seen = cache.total_seen_tokens[0]
+    got = runner.verify_tree_step(torch.tensor([toks], device=dev), seen, seen, seen, depths, masks)
+    got = got[0].float().cpu().numpy()
+    if frozen:
+        _sync_frozen(ocache, cache, seen, S)
+    ref = model.forward_tree(toks, ocache, depths, masks)
+    for t in range(len(toks)):
+        _check_logits(got[t], ref[t], f"tree gqa128 node {t}")
+    if frozen:
+        _check_codes(kv, _code_diffs(kv, ocache), "tree_gqa128")
+
+
+@pytest.mark.parametrize("kv", ["fp16", "fp8", "int4"])
+def test_runner_verify_step_ring_wrap_gqa_head128(dev, kv):
+    """verify_step whose 6 slots wrap around a 48-slot ring (every token attends all S
+    slots) on 8 query / 2 KV heads of size 128."""
+    print(f"[runner_ring_gqa128] kv={kv}", flush=True)
+    cfg, ow, cos, sin = _gqa128_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 48
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, kv, ring=True)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv, ring_buffer=True)
+    frozen = kv != "fp16"
+    ocache.frozen = frozen
+    rng = np.random.default_rng(29)
+    prefix = rng.integers(0, cfg.vocab, 45).tolist()
+    if frozen:
+        run_steps(runner, cache, prefix, dev)
+    else:
+        _prefill(runner, cache, ocache, model, prefix, dev)
+    seen = cache.total_seen_tokens[0]
+    T = 6
+    toks = rng.integers(0, cfg.vocab, T).tolist()
+    got = runner.verify_step(torch.tensor([toks], device=dev), seen, seen % S, min(seen + T, S))
+    got = got[0].float().cpu().numpy()
+    if frozen:
+        _sync_frozen(ocache, cache, seen, S)
+    ref = model.forward_verify_ring(toks, ocache, seen, seen % S)
+    for t in range(T):
+        _check_logits(got[t], ref[t], f"ring gqa128 token {t}")
+    if frozen:
+        assert list(ocache.last_write[0][0]) == [(seen + t) % S for t in range(T)]
+        _check_codes(kv, _code_diffs(kv, ocache), "ring_gqa128")
