@@ -13,6 +13,7 @@
 // every key/value byte is read exactly once per workgroup.  Softmax is online
 // in the exp2 domain with fp32 state; partial (m, l, o) per split are merged by
 // a second kernel (or written directly when there is a single split).
+#include <mutex>
 #include <type_traits>
 
 #include "kernels.h"
@@ -1449,6 +1450,76 @@ extern "C" int axm_gqa_flash_decode(const void* q, const void* k_cache, const vo
                                (float*)workspace, (hipStream_t)stream);
   if (rc) return rc;
   AXM_LAUNCH_CHECK("gqa_flash_decode");
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation flash decode: the split partials live in `scratch`, a file-scope
+// device array (one copy per GPU).  Its device address is resolved once per
+// device with hipGetSymbolAddress (the array's name in host code is only a
+// host-side stand-in) and that address is what the kernels receive.  Every
+// split writes its partial row before the reduce reads it, so nothing in the
+// array has to start at zero.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[AXM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kScratchMaxDevices] = {};
+
+// Device address of the current device's scratch array (resolved on first use).
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchMaxDevices) {
+    (void)hipGetLastError();
+    axm_set_error("gqa_flash_decode_noalloc: no current device (or device index >= %d)", kScratchMaxDevices);
+    return -5;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      axm_set_error("gqa_flash_decode_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      return -5;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int axm_gqa_flash_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                            const void* k_scales, const void* v_scales, int kv_dtype, void* out,
+                                            int B, int n_head, int n_kv_head, int head_dim, int max_seq_len,
+                                            int active_len, int num_splits, void* stream) {
+  KvView kv{(void*)k_cache, (void*)v_cache, (f16*)k_scales, (f16*)v_scales, kv_dtype, B, n_kv_head, max_seq_len,
+            head_dim};
+  if (int rc = check_kv(kv, "gqa_flash_decode_noalloc")) return rc;
+  AXM_CHECK_ARG(q && out, -1, "gqa_flash_decode_noalloc: null q/out");
+  AXM_CHECK_ARG(n_head % n_kv_head == 0 && n_head / n_kv_head <= 64, -1,
+                "gqa_flash_decode_noalloc: n_head=%d not a multiple of n_kv_head=%d", n_head, n_kv_head);
+  AXM_CHECK_ARG(active_len >= 1 && active_len <= max_seq_len, -1,
+                "gqa_flash_decode_noalloc: active_len=%d out of [1, %d]", active_len, max_seq_len);
+  if (num_splits <= 0) num_splits = attn_choose_splits(B, n_kv_head, active_len);
+  AXM_CHECK_ARG(num_splits <= 1024, -1, "gqa_flash_decode_noalloc: num_splits=%d too large", num_splits);
+  const size_t need = attn_workspace_bytes(B, n_head, head_dim, num_splits);
+  AXM_CHECK_ARG(need <= (size_t)AXM_NOALLOC_SCRATCH_BYTES, -1,
+                "gqa_flash_decode_noalloc: %zu bytes of split partials (B=%d, %d heads of %d, %d splits) exceed "
+                "the fixed %u-byte scratch array",
+                need, B, n_head, head_dim, num_splits, (unsigned)AXM_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_address(&ws)) return rc;
+  }
+  int rc = launch_flash_decode((const f16*)q, kv, (f16*)out, n_head, active_len, nullptr, num_splits, (float*)ws,
+                               (hipStream_t)stream);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("gqa_flash_decode_noalloc");
   return 0;
 }
 

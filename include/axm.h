@@ -179,6 +179,20 @@ int axm_gqa_flash_decode(const void* q, const void* k_cache, const void* v_cache
                          int head_dim, int max_seq_len, int active_len, int num_splits, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* No-allocation variant of axm_gqa_flash_decode.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split-KV partials go to a fixed device array inside the library (one per GPU,
+ * AXM_NOALLOC_SCRATCH_BYTES, held until the process ends) instead of a caller
+ * workspace; a call whose partials would exceed it returns -1 with an error
+ * message, and the function itself calls no hipMalloc / hipFree.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads) race.  Same arguments, splits and results as axm_gqa_flash_decode. */
+#define AXM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int axm_gqa_flash_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, const void* k_scales,
+                                 const void* v_scales, int kv_dtype, void* out, int B, int n_head, int n_kv_head,
+                                 int head_dim, int max_seq_len, int active_len, int num_splits, void* stream);
+
 /* Key splits the tree-verification attention picks for num_splits <= 0 (T nodes,
  * n_keys = prefix_len + T); the split heuristic of gqa_tree_verify_*_mps
  * (mps_kernels.mm:1508-1631) re-derived for 64-row matrix-core workgroups. */
