@@ -72,7 +72,7 @@ _SIGNATURES = {
         [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
          c_int, c_int, c_int, c_int, c_int, c_void_p],
     ),
-    "axm_attention_num_splits": (c_int, [c_int, c_int, c_int]),
+    "axm_attention_num_splits": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "axm_attention_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "axm_tree_attention_num_splits": (c_int, [c_int, c_int, c_int, c_int]),
     "axm_gqa_flash_decode": (

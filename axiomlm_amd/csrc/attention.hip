@@ -857,6 +857,24 @@ int attn_choose_splits(int B, int Hkv, int active_len) {
   return splits;
 }
 
+int attn_flash_splits(int B, int Hq, int Hkv, int hd, int kv_dtype, int active_len) {
+  const int n_rep = Hkv > 0 ? Hq / Hkv : 0;
+  if (!(n_rep >= 2 && n_rep <= 16 && (hd == 64 || hd == 128))) return attn_choose_splits(B, Hkv, active_len);
+  // Matrix-core decode (4-wave workgroups, 32-key blocks).  Measured on the C3
+  // shape (batch 8, 32 query / 8 KV heads of 128, 1k-32k keys): fastest at
+  // about two workgroups per CU for int4 / fp16 caches and one per CU for fp8
+  // (whose two-block prefetch holds more registers); every split keeps >= 128
+  // keys, one 32-key block per wave.
+  const int rows = B * Hkv;
+  const int target = (kv_dtype == AXM_KV_FP8 ? 1 : 2) * axm_num_cus();
+  int splits = (target + rows - 1) / rows;
+  const int by_len = (active_len + 127) / 128;
+  if (splits > by_len) splits = by_len;
+  if (splits > 64) splits = 64;
+  if (splits < 1) splits = 1;
+  return splits;
+}
+
 int attn_parts_splits(int B, int Hkv, int active_len) {
   // Split partials merged by the consumer cost no reduce launch, so the split
   // count aims at one workgroup per CU (measured on 32 heads x 128: eight
@@ -1425,8 +1443,10 @@ extern "C" size_t axm_attention_workspace_bytes(int B, int n_query_rows_per_batc
   return attn_workspace_bytes(B, n_query_rows_per_batch, head_dim, n_splits);
 }
 
-extern "C" int axm_attention_num_splits(int B, int n_kv_head, int active_len) {
-  return attn_choose_splits(B, n_kv_head, active_len);
+extern "C" int axm_attention_num_splits(int B, int n_head, int n_kv_head, int head_dim, int kv_dtype,
+                                        int active_len) {
+  if (B < 1 || n_head < 1 || n_kv_head < 1 || head_dim < 1 || active_len < 1) return 1;
+  return attn_flash_splits(B, n_head, n_kv_head, head_dim, kv_dtype, active_len);
 }
 
 extern "C" int axm_gqa_flash_decode(const void* q, const void* k_cache, const void* v_cache, const void* k_scales,
@@ -1441,7 +1461,7 @@ extern "C" int axm_gqa_flash_decode(const void* q, const void* k_cache, const vo
                 "gqa_flash_decode: n_head=%d not a multiple of n_kv_head=%d", n_head, n_kv_head);
   AXM_CHECK_ARG(active_len >= 1 && active_len <= max_seq_len, -1, "gqa_flash_decode: active_len=%d out of [1, %d]",
                 active_len, max_seq_len);
-  if (num_splits <= 0) num_splits = attn_choose_splits(B, n_kv_head, active_len);
+  if (num_splits <= 0) num_splits = attn_flash_splits(B, n_head, n_kv_head, head_dim, kv_dtype, active_len);
   AXM_CHECK_ARG(num_splits <= 1024, -1, "gqa_flash_decode: num_splits=%d too large", num_splits);
   const size_t need = attn_workspace_bytes(B, n_head, head_dim, num_splits);
   AXM_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace), -1,
@@ -1505,7 +1525,7 @@ extern "C" int axm_gqa_flash_decode_noalloc(const void* q, const void* k_cache, 
                 "gqa_flash_decode_noalloc: n_head=%d not a multiple of n_kv_head=%d", n_head, n_kv_head);
   AXM_CHECK_ARG(active_len >= 1 && active_len <= max_seq_len, -1,
                 "gqa_flash_decode_noalloc: active_len=%d out of [1, %d]", active_len, max_seq_len);
-  if (num_splits <= 0) num_splits = attn_choose_splits(B, n_kv_head, active_len);
+  if (num_splits <= 0) num_splits = attn_flash_splits(B, n_head, n_kv_head, head_dim, kv_dtype, active_len);
   AXM_CHECK_ARG(num_splits <= 1024, -1, "gqa_flash_decode_noalloc: num_splits=%d too large", num_splits);
   const size_t need = attn_workspace_bytes(B, n_head, head_dim, num_splits);
   AXM_CHECK_ARG(need <= (size_t)AXM_NOALLOC_SCRATCH_BYTES, -1,

@@ -53,6 +53,9 @@ int launch_rope_kv_write(const KvView& kv, const f16* qkv, int Hq, int T, const 
 // attn_workspace_bytes(); active_len_dev overrides active_len when non-null.
 size_t attn_workspace_bytes(int B, int Hq, int hd, int n_splits);
 int attn_choose_splits(int B, int Hkv, int active_len);
+// Split count of launch_flash_decode for the attention kernel it picks (matrix-core
+// form for 2-16 query heads per KV head and head size 64 / 128).
+int attn_flash_splits(int B, int Hq, int Hkv, int hd, int kv_dtype, int active_len);
 int launch_flash_decode(const f16* q, const KvView& kv, f16* out, int Hq, int active_len, const int* active_len_dev,
                         int n_splits, float* ws, hipStream_t s);
 

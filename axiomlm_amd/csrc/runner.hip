@@ -630,7 +630,7 @@ struct axm_runner {
         rc = launch_tree_attention(q, kv, attn_y, d.n_head, T, prefix, write_pos, (const uint64_t*)tree_mask, splits, ws,
                                    s);
       } else {
-        const int splits = attn_choose_splits(1, d.n_kv_head, d.max_seq_len);
+        const int splits = attn_flash_splits(1, d.n_head, d.n_kv_head, d.head_dim, d.kv_dtype, d.max_seq_len);
         for (int t = 0; t < T && rc == 0; ++t)
           rc = launch_flash_decode(q + (size_t)t * q_dim, kv, attn_y + (size_t)t * q_dim, d.n_head, d.max_seq_len,
                                    nullptr, splits, ws, s);

@@ -189,8 +189,8 @@ def gqa_flash_decode_mps(
     n_head = q.numel() // (B * head_dim)
     if code and (k_scales is None or v_scales is None):
         raise ValueError("quantized KV cache needs k_scales and v_scales")
-    splits = int(num_splits) if num_splits and num_splits > 0 else _lib.lib().axm_attention_num_splits(B, Hkv,
-                                                                                                        int(active_len))
+    splits = int(num_splits) if num_splits and num_splits > 0 else _lib.lib().axm_attention_num_splits(
+        B, n_head, Hkv, head_dim, code, int(active_len))
     ws_bytes = _lib.lib().axm_attention_workspace_bytes(B, n_head, head_dim, splits)
     ws = torch.empty(max(1, ws_bytes), dtype=torch.uint8, device=q.device) if ws_bytes else None
     qc = q.to(torch.float16).contiguous()

@@ -10,9 +10,10 @@ whole-step hipGraph (the argmax of step t feeds step t+1 on the device).
 
 Printed JSON line: value = tokens/s; roofline = the runner's fused RMSNorm +
 gate/up GEMV + SwiGLU kernel (tile16 matrix-core layout; the largest per-launch
-weight stream, 50.7 MB) timed live with HIP events on its stream; cpu_baseline = the numpy oracle (the reference's CPU
-fallback: dequantize every weight, then matmul) on a bounded sample of the same
-step, extrapolated to tokens/s.
+weight stream, 50.7 MB) timed live with HIP events on its stream; cpu_baseline = the
+reference's CPU path restated with torch on the host cores (dequantize every weight
+on every call, then F.linear in fp16) on a bounded sample of the same step,
+extrapolated to tokens/s, plus C1 end to end and a C2 layer on the CPU.
 """
 
 from __future__ import annotations
@@ -183,54 +184,99 @@ def gate_up_traffic():
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+def _cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(layers, lnf, c, budget_s=20.0):
-    """Oracle (reference CPU fallback semantics) on a bounded sample: whole decode-step layers of
-    the 7B shape at context CTX0, repeated until ~budget_s, extrapolated to 32 layers + lm_head."""
+    """The reference's CPU path restated with torch on the host cores (oracle/torch_cpu.py:
+    quantized linears dequantize the MARLIN codes to fp16 on every call, then F.linear in
+    fp16, as quant.py:656-661 does), torch.set_num_threads = every core this process may use.
+
+    value: 7B-shape tokens/s from whole decoder layers (T = 1, fp16 cache of CTX0 tokens) run
+    for about budget_s, extrapolated to 32 layers + lm_head (by weight bytes).  Also: C1 end
+    to end (32-token prompt as one prefill, then 64 greedy steps) and one C2 layer at
+    M = 1, 4, 16 tokens."""
     import numpy as np
+    import torch
 
-    from oracle import formats as fm
     from oracle import model as om
+    from oracle import torch_cpu as tc
 
-    L1 = 1
-    pk = {k: [t.cpu().numpy() for t in v[:L1]] for k, v in layers.items()}
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
     d, H, hd = c["d"], c["hidden"], c["hd"]
-    rng = np.random.default_rng(0)
-    kc = rng.standard_normal((c["n_kv_head"], CTX0, hd)).astype(np.float16)
-    vc = rng.standard_normal((c["n_kv_head"], CTX0, hd)).astype(np.float16)
-    x = rng.standard_normal((1, d)).astype(np.float16)
-    qd = c["n_head"] * hd
-    n_layers_done = 0
+    cfg7 = om.OracleConfig(n_layer=1, n_head=c["n_head"], n_kv_head=c["n_kv_head"], d_model=d, hidden=H,
+                           vocab=c["vocab"], eps=1e-5, block_size=CTX0 + 64)
+    cos, sin = om.rope_tables(hd, CTX0 + 64)
+    lay = [{"ln1": layers["ln1"][0], "ln2": layers["ln2"][0], "qkv_p": layers["qkv_p"][0],
+            "qkv_s": layers["qkv_s"][0], "o_p": layers["o_p"][0], "o_s": layers["o_s"][0],
+            "gu_p": layers["gu_p"][0], "gu_s": layers["gu_s"][0], "dn_p": layers["dn_p"][0],
+            "dn_s": layers["dn_s"][0]}]
+    m = tc.TorchCpuModel.from_tensors(cfg7, lay, lnf, lay[0]["qkv_p"], lay[0]["qkv_s"], lay[0]["qkv_p"],
+                                      lay[0]["qkv_s"], cos, sin)
+    gen = torch.Generator().manual_seed(0)
+
+    def fresh_cache():
+        cache = m.new_cache(CTX0 + 32)
+        cache["k"][:, :, :, :CTX0] = torch.randn(cache["k"][:, :, :, :CTX0].shape, generator=gen).half()
+        cache["v"][:, :, :, :CTX0] = torch.randn(cache["v"][:, :, :, :CTX0].shape, generator=gen).half()
+        cache["seen"] = CTX0
+        return cache
+
+    x = torch.randn(1, 1, d, generator=gen).half()
+    n_done = 0
     t0 = time.perf_counter()
-    while True:
-        i = 0
-        h1 = om.rmsnorm_fp16(x, pk["ln1"][i], 1e-5)
-        qkv = fm.qmv_q4_marlin(h1, pk["qkv_p"][i], pk["qkv_s"][i], qd * 3)
-        q = qkv[:, :qd].reshape(1, c["n_head"], hd).transpose(1, 0, 2)
-        y = om.sdpa_fp16(q, kc, vc).transpose(1, 0, 2).reshape(1, qd)
-        x = (x.astype(np.float32) + fm.qmv_q4_marlin(y, pk["o_p"][i], pk["o_s"][i], d).astype(np.float32)).astype(
-            np.float16)
-        h2 = om.rmsnorm_fp16(x, pk["ln2"][i], 1e-5)
-        gu = fm.qmv_q4_marlin(h2, pk["gu_p"][i], pk["gu_s"][i], 2 * H).astype(np.float32)
-        sw = ((gu[:, :H] / (1 + np.exp(-gu[:, :H]))).astype(np.float16).astype(np.float32) * gu[:, H:]).astype(
-            np.float16)
-        x = (x.astype(np.float32) + fm.qmv_q4_marlin(sw, pk["dn_p"][i], pk["dn_s"][i], d).astype(np.float32)).astype(
-            np.float16)
-        n_layers_done += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    per_layer = (time.perf_counter() - t0) / n_layers_done
-    # lm_head (Q4, 32000 x 4096) costs ~ vocab/(qkv+o+gu+dn rows) of a layer: scale by bytes
+    with torch.no_grad():
+        while True:
+            cache = fresh_cache()
+            x = m.layer(0, x, cache, CTX0)
+            n_done += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        per_layer = (time.perf_counter() - t0) / n_done
+        c2 = {}
+        for M in (1, 4, 16):
+            cache = fresh_cache()
+            xm = torch.randn(1, M, d, generator=gen).half()
+            t1 = time.perf_counter()
+            m.layer(0, xm, cache, CTX0)
+            c2[str(M)] = round((time.perf_counter() - t1) * 1e6, 1)
+        # C1 end to end (BASELINE configs[0]; MLP 688 zero-padded to 704 for the group-64 packer)
+        c1 = om.OracleConfig(n_layer=4, n_head=4, n_kv_head=4, d_model=256, hidden=704, vocab=1024, eps=1e-5,
+                             block_size=256)
+        c1m = tc.TorchCpuModel(c1, om.pack_model_rtn(c1, om.make_float_weights(c1, seed=0)),
+                               *om.rope_tables(c1.head_dim, c1.block_size))
+        prompt = np.random.default_rng(0).integers(0, c1.vocab, 32).tolist()
+        cache = c1m.new_cache(128)
+        t1 = time.perf_counter()
+        tok = int(torch.argmax(c1m.forward(prompt, cache)[-1].float()))
+        t2 = time.perf_counter()
+        for _ in range(64):
+            tok = int(torch.argmax(c1m.forward([tok], cache)[-1].float()))
+        t3 = time.perf_counter()
     lm_frac = q4_bytes(c["vocab"], d) / layer_weight_bytes(c)
     per_token = per_layer * (c["n_layer"] + lm_frac)
-    threads = len(os.sched_getaffinity(0))
     return {
         "value": 1.0 / per_token,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{n_layers_done} x one 7B-shape decoder layer (Q4 dequantize-per-call + fp32 GEMV, "
-                   f"SDPA over {CTX0} fp16 KV, numpy BLAS on up to {threads} threads) in {per_layer * n_layers_done:.1f}"
-                   f" s, extrapolated to 32 layers + lm_head"),
+        "sample": (f"{n_done} x one 7B-shape decoder layer (torch CPU: MARLIN Q4 dequantized to fp16 every call, "
+                   f"then F.linear; SDPA over {CTX0} fp16 keys) in {per_layer * n_done:.1f} s, extrapolated to "
+                   f"32 layers + lm_head"),
+        "cpu_model": _cpu_model_name(),
+        "torch": torch.__version__,
+        "c1_end_to_end": {"prefill_32_ms": round((t2 - t1) * 1e3, 2),
+                          "decode_tokens_per_s": round(64 / (t3 - t2), 2)},
+        "c2_layer_us": c2,
     }
 
 

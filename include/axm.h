@@ -172,7 +172,7 @@ int axm_rope_kv_cache_write(void* qkv, int T, const void* freqs, int rope_len, i
  * (axm_attention_num_splits).  workspace >= axm_attention_workspace_bytes().
  * Replaces gqa_flash_decode{,_fp8,_int4}_mps (mps_kernels.mm:1399-1506, 1672-1906,
  * 2040-2120; Python entry axiomlm/kernels/ops.py:552-654). */
-int axm_attention_num_splits(int B, int n_kv_head, int active_len);
+int axm_attention_num_splits(int B, int n_head, int n_kv_head, int head_dim, int kv_dtype, int active_len);
 size_t axm_attention_workspace_bytes(int B, int n_query_rows_per_batch, int head_dim, int n_splits);
 int axm_gqa_flash_decode(const void* q, const void* k_cache, const void* v_cache, const void* k_scales,
                          const void* v_scales, int kv_dtype, void* out, int B, int n_head, int n_kv_head,

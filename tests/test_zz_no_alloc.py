@@ -48,7 +48,7 @@ def test_noalloc_flash_decode_matches_workspace_entry_point(dev, kind):
         print(f"[noalloc] kind={kind} B={B} Hq={Hq} Hkv={Hkv} hd={hd} L={L}", flush=True)
         kc, vc, ks, vs = _cache(kind, B, Hkv, S, hd, g, dev)
         q = torch.randn(B, Hq, hd, generator=g, device=dev).half()
-        splits = lib.axm_attention_num_splits(B, Hkv, L)
+        splits = lib.axm_attention_num_splits(B, Hq, Hkv, hd, code, L)
         if splits < 2:
             splits = 4
         need = lib.axm_attention_workspace_bytes(B, Hq, hd, splits)
