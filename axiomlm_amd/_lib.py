@@ -31,21 +31,27 @@ _SIGNATURES = {
     ),
     "axm_tile16_bytes": (c_size_t, [c_int, c_int, c_int]),
     "axm_repack_q4_marlin_tile16": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
-    "axm_qmv_q4_tile16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "axm_qmv_q4_tile16": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]
+    ),
+    "axm_repack_q4_marlin_g128_tile16": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "axm_pack_q4_marlin_rtn_g128": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "axm_dequantize_q4_marlin_g128": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "axm_compact_tree_kv": (
         c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int), c_int, c_void_p]
     ),
     "axm_qmv_ternary": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "axm_qmv_q2_k": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "axm_qmv_q4_tile16_swiglu": (
-        c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]
+        c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]
     ),
     "axm_qmm_q4_tile16_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "axm_qmm_q4_tile16": (
-        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p],
     ),
     "axm_qmm_q4_tile16_swiglu": (
-        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]
     ),
     "axm_dequantize_q4_marlin": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "axm_pack_q4_marlin_rtn": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
@@ -129,7 +135,7 @@ class RunnerDesc(ctypes.Structure):
         ("down_w", ctypes.POINTER(c_void_p)), ("down_sb", ctypes.POINTER(c_void_p)),
         ("k_cache", ctypes.POINTER(c_void_p)), ("v_cache", ctypes.POINTER(c_void_p)),
         ("k_scales", ctypes.POINTER(c_void_p)), ("v_scales", ctypes.POINTER(c_void_p)),
-        ("max_tokens", c_int), ("layout", c_int),
+        ("max_tokens", c_int), ("layout", c_int), ("group_size", c_int),
     ]
 
 

@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(kThreads) q4m_gemv_kernel(Q4GemvArgs a) {
 // quant.py:597-634.
 // ---------------------------------------------------------------------------
 __global__ void q4m_dequant_kernel(const uint32_t* __restrict__ w, const f16x2* __restrict__ sb,
-                                   f16* __restrict__ out, int n_tiles, int KG, int N) {
+                                   f16* __restrict__ out, int n_tiles, int KG, int N, int g_shift) {
   // One thread per (tile, g, ref lane); writes 16 values.
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const long total = (long)n_tiles * KG * 32;
@@ -405,7 +405,8 @@ __global__ void q4m_dequant_kernel(const uint32_t* __restrict__ w, const f16x2* 
     for (int half = 0; half < 2; ++half) {
       const int row = tile * 8 + c0 + half;
       if (row >= N) continue;
-      const f16x2 s_b = sb[((size_t)tile * KG + g) * 8 + c0 + half];
+      // (scale, bias) of group g >> g_shift: g_shift 1 for one pair per 128 columns
+      const f16x2 s_b = sb[((size_t)tile * (KG >> g_shift) + (g >> g_shift)) * 8 + c0 + half];
       const float sc = h2f(s_b.x), bi = h2f(s_b.y);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -421,21 +422,26 @@ __global__ void q4m_dequant_kernel(const uint32_t* __restrict__ w, const f16x2* 
 // One 64-thread block per (tile, group).  SRC_FP16 selects torch's fp16 op
 // semantics for (max - min) and the /15 (each rounded to fp16).
 // ---------------------------------------------------------------------------
-template <bool SRC_FP16>
-__global__ void __launch_bounds__(64) q4m_pack_rtn_kernel(const void* __restrict__ wsrc, int N, int K,
+// One block per (8-row tile, GS-column group), GS = 64 (the reference layout) or
+// 128 (the group-128 variant: same code layout per 64-column block, one
+// (scale, bias) per 128 columns in sb [N/8][K/GS][8]).  Thread t holds row t / (GS/8)
+// of the tile and the 8-column slice t % (GS/8).
+template <bool SRC_FP16, int GS>
+__global__ void __launch_bounds__(GS) q4m_pack_rtn_kernel(const void* __restrict__ wsrc, int N, int K,
                                                           uint32_t* __restrict__ w_out, f16x2* __restrict__ sb_out) {
-  const int KG = K / 64;
+  constexpr int SL = GS / 8;  // slices per row
+  const int KG = K / GS;
   const int tile = blockIdx.x / KG;
   const int g = blockIdx.x % KG;
   const int t = threadIdx.x;
-  const int c = t >> 3;     // row within tile
-  const int sub = t & 7;    // 8-element slice
+  const int c = t / SL;     // row within tile
+  const int sub = t % SL;   // 8-element slice
   const int row = tile * 8 + c;
-  __shared__ uint8_t qs[8][64];
+  __shared__ uint8_t qs[8][GS];
   float vals[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int k = 64 * g + 8 * sub + i;
+    const int k = GS * g + 8 * sub + i;
     if (row < N) {
       vals[i] = SRC_FP16 ? h2f(reinterpret_cast<const f16*>(wsrc)[(size_t)row * K + k])
                          : reinterpret_cast<const float*>(wsrc)[(size_t)row * K + k];
@@ -450,7 +456,7 @@ __global__ void __launch_bounds__(64) q4m_pack_rtn_kernel(const void* __restrict
     mx = fmaxf(mx, vals[i]);
   }
 #pragma unroll
-  for (int o = 1; o < 8; o <<= 1) {
+  for (int o = 1; o < SL; o <<= 1) {
     mn = fminf(mn, __shfl_xor(mn, o, 64));
     mx = fmaxf(mx, __shfl_xor(mx, o, 64));
   }
@@ -475,20 +481,24 @@ __global__ void __launch_bounds__(64) q4m_pack_rtn_kernel(const void* __restrict
   }
   if (sub == 0) sb_out[((size_t)tile * KG + g) * 8 + c] = f16x2{sc_h, bi_h};
   __syncthreads();
-  if (t < 32) {
-    const int l = t;
+  // One 32-lane set per 64-column block of the group.
+  if (t < 32 * (GS / 64)) {
+    const int l = t & 31;
+    const int blk = t >> 5;
     const int r = ((l & 16) >> 2) | ((l & 6) >> 1);
     const int c0 = ((l & 8) >> 1) | ((l & 1) << 1);
+    const int KG64 = K / 64;
+    const int g64 = g * (GS / 64) + blk;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       uint32_t word = 0;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int kk = 32 * j + 8 * s + r;
+        const int kk = 64 * blk + 32 * j + 8 * s + r;
         word |= (uint32_t)qs[c0][kk] << (4 * s);
         word |= (uint32_t)qs[c0 + 1][kk] << (16 + 4 * s);
       }
-      w_out[(((size_t)tile * KG + g) * 32 + l) * 2 + j] = word;
+      w_out[(((size_t)tile * KG64 + g64) * 32 + l) * 2 + j] = word;
     }
   }
 }
@@ -728,8 +738,20 @@ extern "C" int axm_dequantize_q4_marlin(const void* w_marlin, const void* sb_mar
   const int n_tiles = (N + 7) / 8, KG = K / 64;
   const long total = (long)n_tiles * KG * 32;
   hipLaunchKernelGGL(q4m_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint32_t*)w_marlin, (const f16x2*)sb_marlin, (f16*)out, n_tiles, KG, N);
+                     (const uint32_t*)w_marlin, (const f16x2*)sb_marlin, (f16*)out, n_tiles, KG, N, 0);
   AXM_LAUNCH_CHECK("dequantize_q4_marlin");
+  return 0;
+}
+
+extern "C" int axm_dequantize_q4_marlin_g128(const void* w_marlin, const void* sb128, void* out, int K, int N,
+                                             void* stream) {
+  AXM_CHECK_ARG(w_marlin && sb128 && out, -1, "dequantize_q4_marlin_g128: null pointer");
+  AXM_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0, -1, "dequantize_q4_marlin_g128: bad shape K=%d N=%d", K, N);
+  const int n_tiles = (N + 7) / 8, KG = K / 64;
+  const long total = (long)n_tiles * KG * 32;
+  hipLaunchKernelGGL(q4m_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint32_t*)w_marlin, (const f16x2*)sb128, (f16*)out, n_tiles, KG, N, 1);
+  AXM_LAUNCH_CHECK("dequantize_q4_marlin_g128");
   return 0;
 }
 
@@ -740,12 +762,27 @@ extern "C" int axm_pack_q4_marlin_rtn(const void* w, int src_is_fp16, int N, int
   const int n_tiles = (N + 7) / 8, KG = K / 64;
   const unsigned blocks = (unsigned)n_tiles * KG;
   if (src_is_fp16)
-    hipLaunchKernelGGL(q4m_pack_rtn_kernel<true>, dim3(blocks), dim3(64), 0, (hipStream_t)stream, w, N, K,
+    hipLaunchKernelGGL((q4m_pack_rtn_kernel<true, 64>), dim3(blocks), dim3(64), 0, (hipStream_t)stream, w, N, K,
                        (uint32_t*)w_marlin, (f16x2*)sb_marlin);
   else
-    hipLaunchKernelGGL(q4m_pack_rtn_kernel<false>, dim3(blocks), dim3(64), 0, (hipStream_t)stream, w, N, K,
+    hipLaunchKernelGGL((q4m_pack_rtn_kernel<false, 64>), dim3(blocks), dim3(64), 0, (hipStream_t)stream, w, N, K,
                        (uint32_t*)w_marlin, (f16x2*)sb_marlin);
   AXM_LAUNCH_CHECK("pack_q4_marlin_rtn");
+  return 0;
+}
+
+extern "C" int axm_pack_q4_marlin_rtn_g128(const void* w, int src_is_fp16, int N, int K, void* w_marlin,
+                                           void* sb128, void* stream) {
+  AXM_CHECK_ARG(w && w_marlin && sb128, -1, "pack_q4_marlin_g128: null pointer");
+  AXM_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0, -1, "pack_q4_marlin_g128: K=%d must be a multiple of 128", K);
+  const unsigned blocks = (unsigned)((N + 7) / 8) * (K / 128);
+  if (src_is_fp16)
+    hipLaunchKernelGGL((q4m_pack_rtn_kernel<true, 128>), dim3(blocks), dim3(128), 0, (hipStream_t)stream, w, N, K,
+                       (uint32_t*)w_marlin, (f16x2*)sb128);
+  else
+    hipLaunchKernelGGL((q4m_pack_rtn_kernel<false, 128>), dim3(blocks), dim3(128), 0, (hipStream_t)stream, w, N, K,
+                       (uint32_t*)w_marlin, (f16x2*)sb128);
+  AXM_LAUNCH_CHECK("pack_q4_marlin_rtn_g128");
   return 0;
 }
 

@@ -7,7 +7,8 @@ struct T16Args {
   const f16* x;        // [M][ldx] activations
   int ldx;
   const u32x4* w16;    // [N16][KB][64] x 16 B
-  const u32x2* sb16;   // [N16][KB][16] x 8 B (two groups of (scale, bias))
+  const u32x2* sb16;   // [N16][KB][16] x 8 B (two groups of (scale, bias)); g128: x 4 B (one)
+  int g128;            // one (scale, bias) per 128 columns (group-128 packs)
   int K, KB, N;        // N = valid output rows
   int N_rows_alloc;    // rows the w16 / sb16 arrays were packed for (2 H for gate/up)
   size_t w16_bytes, sb16_bytes;  // set by t16_gemv_launch (buffer bounds)
@@ -66,7 +67,9 @@ size_t t16_smem_bytes(int M, int NT, int K);
 void t16_prepare_attributes();
 // Picks split / grid (a.split is overwritten); M in [1, 4].
 int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s);
-int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16, hipStream_t s);
+// g128: sb_marlin holds one (scale, bias) per 128 columns ([N/8][K/128][8]).
+int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16, hipStream_t s,
+               int g128);
 // Multi-token GEMM over the same tile16 weights for M in [1, 64] tokens (one to
 // four 16-row MFMA A tiles): every weight chunk is streamed once for all M
 // tokens.  Activations must be normalized already (a.ln_w == nullptr); epi is
@@ -79,4 +82,4 @@ constexpr int kTile16GemmMaxSplits = 16;
 size_t t16_gemm_ws_bytes(int K, int n_units, int NT);
 int t16_gemm_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipStream_t s);
 size_t t16_weight_bytes(int N, int K);
-size_t t16_sb_bytes(int N, int K);
+size_t t16_sb_bytes(int N, int K, int g128);

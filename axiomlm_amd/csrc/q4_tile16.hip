@@ -36,8 +36,11 @@ __device__ __forceinline__ int marlin_lane_of(int r, int c0) {
 }
 
 // One thread per (tile16, kb, lane): the four words of that lane.
+// g128: sbm holds one (scale, bias) per 128 columns ([N/8][K/128][8]) and sb16
+// one per (row, kb) ([N16][KB][16 rows]); otherwise two per kb as above.
 __global__ void repack_tile16_kernel(const uint32_t* __restrict__ wm, const f16x2* __restrict__ sbm, int N_pad8,
-                                     int K, uint32_t* __restrict__ w16, f16x2* __restrict__ sb16, int N16, int KB) {
+                                     int K, uint32_t* __restrict__ w16, f16x2* __restrict__ sb16, int N16, int KB,
+                                     int g128) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)N16 * KB * 64) return;
   const int l = (int)(idx & 63);
@@ -65,7 +68,11 @@ __global__ void repack_tile16_kernel(const uint32_t* __restrict__ wm, const f16x
     }
     w16[idx * 4 + c] = word;
   }
-  if (l < 16) {
+  if (l < 16 && g128) {
+    f16x2 v = f16x2{f16(0), f16(0)};
+    if (row < N_pad8 && kb < KB) v = sbm[((size_t)(row >> 3) * KB + kb) * 8 + (row & 7)];
+    sb16[((size_t)t16 * KB + kb) * 16 + l] = v;
+  } else if (l < 16) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int g = 2 * kb + h;
@@ -370,11 +377,14 @@ constexpr int kT16WaveDepth = 8;      // chunk register slots per wave in kT16Wa
 constexpr int kT16WavePre = 4;        // chunks issued before the activation staging
 constexpr int kT16WaveMaxChunks = 16;  // chunks per wave kT16Wave handles
 
-template <int M, int NT, int EPI, int P, int MODE>
+// G128: one (scale, bias) word per row and chunk (group-128 packs) instead of two;
+// it is applied to both 64-column halves of the chunk.
+template <int M, int NT, int EPI, int P, int MODE, bool G128>
 __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
   constexpr bool ONE = MODE != kT16Loop;
   constexpr bool SBW = MODE == kT16Wave;
-  constexpr int QS = SBW ? kT16WaveMaxChunks / 8 : 1;  // 16-byte scale loads per lane and tile (kT16Wave)
+  constexpr int VPC = G128 ? 4 : 8;  // 16-byte scale vectors per chunk and tile
+  constexpr int QS = SBW ? kT16WaveMaxChunks * VPC / 64 : 1;  // 16-byte scale loads per lane and tile (kT16Wave)
   constexpr int NJ = SBW ? kT16WaveMaxChunks : P;        // unrolled chunk slots per pass
   extern __shared__ __align__(16) unsigned char smem[];
   f16* xs = reinterpret_cast<f16*>(smem);                                   // [M][KB*128]
@@ -417,9 +427,14 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
     for (int t = 0; t < NT; ++t) {
       const int base = (unit + t * a.pair_offset) * a.KB + kb0 + ci;
       const int wo = ok ? (base * 64 + lane) * 16 : kOOB;
-      const int so = ok ? (base * 16 + (lane & 15)) * 8 : kOOB;
+      const int so = ok ? (base * 16 + (lane & 15)) * (G128 ? 4 : 8) : kOOB;
       wr[j][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
-      if (!SBW) sr[j][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+      if (!SBW && G128) {
+        const uint32_t v = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0));
+        sr[j][t] = u32x2{v, v};
+      } else if (!SBW) {
+        sr[j][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+      }
     }
   };
 
@@ -435,8 +450,9 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
   else
     t16_load_x<M>(a, xr);
   // kT16Wave: the wave's (scale, bias) run; 16-byte vector v holds chunk v / 8,
-  // rows 2 (v % 8) and 2 (v % 8) + 1.  Issued before the weight loads so that
-  // storing it to LDS waits only for itself.
+  // rows 2 (v % 8) and 2 (v % 8) + 1 (G128: chunk v / 4, rows 4 (v % 4) ..
+  // 4 (v % 4) + 3).  Issued before the weight loads so that storing it to LDS
+  // waits only for itself.
   u32x4 sbv[NT][QS];
   u32x2* my_sb = sbw + (size_t)wave * NT * per * 16;
   if (SBW) {
@@ -445,8 +461,8 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
 #pragma unroll
       for (int q = 0; q < QS; ++q) {
         const int v = q * 64 + lane;
-        const bool ok = unit < a.n_units && v < my * 8;
-        const int bo = ok ? (((unit + t * a.pair_offset) * a.KB + kb0) * 8 + v) * 16 : kOOB;
+        const bool ok = unit < a.n_units && v < my * VPC;
+        const int bo = ok ? (((unit + t * a.pair_offset) * a.KB + kb0) * VPC + v) * 16 : kOOB;
         sbv[t][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, bo, 0, 0));
       }
   }
@@ -463,7 +479,7 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
 #pragma unroll
       for (int q = 0; q < QS; ++q) {
         const int v = q * 64 + lane;
-        if (v < my * 8) *reinterpret_cast<u32x4*>(my_sb + (size_t)t * per * 16 + 2 * v) = sbv[t][q];
+        if (v < my * VPC) *reinterpret_cast<u32x4*>(my_sb + (size_t)t * per * 16 + 2 * v) = sbv[t][q];
       }
   }
   if (from_parts) t16_merge_parts<M>(a, pp, xr);
@@ -508,7 +524,13 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
             cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (size_t)tok * 2 * a.KB + 2 * kb);
           }
         }
-        if (SBW) {
+        if (SBW && G128) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const uint32_t v = reinterpret_cast<const uint32_t*>(my_sb + (size_t)t * per * 16)[ci * 16 + (lane & 15)];
+            sr[j][t] = u32x2{v, v};
+          }
+        } else if (SBW) {
 #pragma unroll
           for (int t = 0; t < NT; ++t) sr[j][t] = my_sb[(size_t)t * per * 16 + ci * 16 + (lane & 15)];
         }
@@ -578,7 +600,10 @@ struct T16Depth {
 
 template <int M, int NT, int EPI, int P, int MODE>
 void t16_set_attr_mode() {
-  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE>,
+  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE, false>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+    (void)hipGetLastError();
+  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE, true>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
     (void)hipGetLastError();
 }
@@ -590,15 +615,23 @@ void t16_set_attr() {
   t16_set_attr_mode<M, NT, EPI, kT16WaveDepth, kT16Wave>();
 }
 
-template <int M, int NT, int EPI>
-int t16_launch_one(const T16Args& a, int mode, int grid, size_t smem, hipStream_t s) {
+template <int M, int NT, int EPI, bool G128>
+void t16_launch_g(const T16Args& a, int mode, int grid, size_t smem, hipStream_t s) {
   const dim3 g(grid), b(kT16Threads);
   if (mode == kT16Wave)
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, kT16WaveDepth, kT16Wave>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, kT16WaveDepth, kT16Wave, G128>), g, b, smem, s, a);
   else if (mode == kT16OnePass)
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16OnePass>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16OnePass, G128>), g, b, smem, s, a);
   else
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16Loop>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16Loop, G128>), g, b, smem, s, a);
+}
+
+template <int M, int NT, int EPI>
+int t16_launch_one(const T16Args& a, int mode, int grid, size_t smem, hipStream_t s) {
+  if (a.g128)
+    t16_launch_g<M, NT, EPI, true>(a, mode, grid, smem, s);
+  else
+    t16_launch_g<M, NT, EPI, false>(a, mode, grid, smem, s);
   return 0;
 }
 
@@ -650,7 +683,7 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   while (S < kT16Waves && a.n_units * S < 8 * cus && a.KB >= 4 * S) S *= 2;
   a.split = S;
   a.w16_bytes = t16_weight_bytes(a.N_rows_alloc, a.K);
-  a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K);
+  a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K, a.g128);
   a.unpack[0] = 0x000F000Fu;
   a.unpack[1] = 0x00F000F0u;
   a.unpack[2] = 0x64006400u;
@@ -689,40 +722,54 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   return -2;
 }
 
-int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16, hipStream_t s) {
+int t16_repack(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16, hipStream_t s,
+               int g128) {
   const int n_tiles8 = (N + 7) / 8;
   const int N16 = (N + 15) / 16;
   const int KB = (K + 127) / 128;
   const long total = (long)N16 * KB * 64;
   hipLaunchKernelGGL(repack_tile16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                      (const uint32_t*)w_marlin, (const f16x2*)sb_marlin, n_tiles8 * 8, K, (uint32_t*)w16,
-                     (f16x2*)sb16, N16, KB);
+                     (f16x2*)sb16, N16, KB, g128);
   return 0;
 }
 
 size_t t16_weight_bytes(int N, int K) { return (size_t)((N + 15) / 16) * ((K + 127) / 128) * 64 * 16; }
-size_t t16_sb_bytes(int N, int K) { return (size_t)((N + 15) / 16) * ((K + 127) / 128) * 16 * 8; }
+size_t t16_sb_bytes(int N, int K, int g128) {
+  return (size_t)((N + 15) / 16) * ((K + 127) / 128) * 16 * (g128 ? 4 : 8);
+}
 
 // ---------------------------------------------------------------------------
 // C ABI: repack + GEMV on the tile16 layout (the runner uses the same code).
 // ---------------------------------------------------------------------------
 extern "C" size_t axm_tile16_bytes(int N, int K, int which) {
-  return which == 0 ? t16_weight_bytes(N, K) : t16_sb_bytes(N, K);
+  return which == 0 ? t16_weight_bytes(N, K) : t16_sb_bytes(N, K, which == 2);
 }
 
 extern "C" int axm_repack_q4_marlin_tile16(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16,
                                            void* sb16, void* stream) {
   AXM_CHECK_ARG(w_marlin && sb_marlin && w16 && sb16, -1, "repack_tile16: null pointer");
   AXM_CHECK_ARG(N > 0 && K > 0 && K % 64 == 0, -1, "repack_tile16: bad shape N=%d K=%d", N, K);
-  t16_repack(w_marlin, sb_marlin, N, K, w16, sb16, (hipStream_t)stream);
+  t16_repack(w_marlin, sb_marlin, N, K, w16, sb16, (hipStream_t)stream, 0);
   AXM_LAUNCH_CHECK("repack_tile16");
   return 0;
 }
 
+extern "C" int axm_repack_q4_marlin_g128_tile16(const void* w_marlin, const void* sb128, int N, int K, void* w16,
+                                                void* sb16, void* stream) {
+  AXM_CHECK_ARG(w_marlin && sb128 && w16 && sb16, -1, "repack_g128_tile16: null pointer");
+  AXM_CHECK_ARG(N > 0 && K > 0 && K % 128 == 0, -1, "repack_g128_tile16: bad shape N=%d K=%d", N, K);
+  t16_repack(w_marlin, sb128, N, K, w16, sb16, (hipStream_t)stream, 1);
+  AXM_LAUNCH_CHECK("repack_g128_tile16");
+  return 0;
+}
+
 extern "C" int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M,
-                                 int K, int N, void* stream) {
+                                 int K, int N, int group_size, void* stream) {
   AXM_CHECK_ARG(x && w16 && sb16 && y, -1, "qmv_q4_tile16: null pointer");
   AXM_CHECK_ARG(K > 0 && K % 64 == 0 && N > 0 && M >= 1, -1, "qmv_q4_tile16: bad shape M=%d K=%d N=%d", M, K, N);
+  AXM_CHECK_ARG(group_size == 64 || (group_size == 128 && K % 128 == 0), -1,
+                "qmv_q4_tile16: group_size %d (64, or 128 with K %% 128 == 0)", group_size);
   for (int m0 = 0; m0 < M; m0 += 4) {
     const int mc = (M - m0) < 4 ? (M - m0) : 4;
     T16Args a{};
@@ -730,6 +777,7 @@ extern "C" int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb1
     a.ldx = K;
     a.w16 = (const u32x4*)w16;
     a.sb16 = (const u32x2*)sb16;
+    a.g128 = group_size == 128;
     a.K = K;
     a.KB = (K + 127) / 128;
     a.N = N;
@@ -746,15 +794,19 @@ extern "C" int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb1
 }
 
 extern "C" int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const void* gu16,
-                                        const void* gusb16, void* y, int M, int K, int H, void* stream) {
+                                        const void* gusb16, void* y, int M, int K, int H, int group_size,
+                                        void* stream) {
   AXM_CHECK_ARG(x && gu16 && gusb16 && y, -1, "qmv_q4_tile16_swiglu: null pointer");
   AXM_CHECK_ARG(K > 0 && K % 64 == 0 && H > 0 && H % 16 == 0 && M >= 1 && M <= 4, -1,
                 "qmv_q4_tile16_swiglu: bad shape M=%d K=%d H=%d (H %% 16 == 0, M <= 4)", M, K, H);
+  AXM_CHECK_ARG(group_size == 64 || (group_size == 128 && K % 128 == 0), -1,
+                "qmv_q4_tile16_swiglu: group_size %d (64, or 128 with K %% 128 == 0)", group_size);
   T16Args a{};
   a.x = (const f16*)x;
   a.ldx = K;
   a.w16 = (const u32x4*)gu16;
   a.sb16 = (const u32x2*)gusb16;
+  a.g128 = group_size == 128;
   a.K = K;
   a.KB = (K + 127) / 128;
   a.N = H;

@@ -118,7 +118,9 @@ __device__ __forceinline__ void t16g_store(const T16Args& a, int tok, int row, f
 // of the reference's multi-token kernel) and the MFMAs accumulate the dot
 // products directly, so a token tile costs its four A reads and four MFMAs and
 // no per-tile vector math.
-template <int NT, int EPI, int MB, int RC, bool DQ>
+// G128: one (scale, bias) word per row and chunk (group-128 packs), applied to
+// both 64-column halves.
+template <int NT, int EPI, int MB, int RC, bool DQ, bool G128>
 __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   using G = GemmShape<MB, RC>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -151,9 +153,14 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
       const bool ok = unit + (kPair ? 0 : t) < a.n_units && kl < kbN;
       const int base = (unit + t * tstride) * a.KB + kbA + kl;
       const int wo = ok ? (base * 64 + lane) * 16 : kGOOB;
-      const int so = ok ? (base * 16 + (lane & 15)) * 8 : kGOOB;
+      const int so = ok ? (base * 16 + (lane & 15)) * (G128 ? 4 : 8) : kGOOB;
       wr[c][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
-      sr[c][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+      if (G128) {
+        const uint32_t v = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0));
+        sr[c][t] = u32x2{v, v};
+      } else {
+        sr[c][t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+      }
     }
   };
   // Activations of range r: thread tid stages vector svi = tid % VPR of token
@@ -412,17 +419,25 @@ bool post_norm_fusable(const T16Args& a) {
   return a.N % 4 == 0 && a.N <= 4 * kRnThreads * kRnVec && a.ldr % 4 == 0 && (al & 7) == 0;
 }
 
-template <int NT, int EPI, int MB, int RC, bool DQ>
-void t16g_launch_shape(const T16Args& a, dim3 grid, hipStream_t s) {
+template <int NT, int EPI, int MB, int RC, bool DQ, bool G128>
+void t16g_launch_group(const T16Args& a, dim3 grid, hipStream_t s) {
   using G = GemmShape<MB, RC>;
   static bool set = false;
   if (!set) {
     set = true;
-    if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI, MB, RC, DQ>,
+    if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI, MB, RC, DQ, G128>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)G::smem) != hipSuccess)
       (void)hipGetLastError();
   }
-  hipLaunchKernelGGL((t16g_kernel<NT, EPI, MB, RC, DQ>), grid, dim3(kGThreads), G::smem, s, a);
+  hipLaunchKernelGGL((t16g_kernel<NT, EPI, MB, RC, DQ, G128>), grid, dim3(kGThreads), G::smem, s, a);
+}
+
+template <int NT, int EPI, int MB, int RC, bool DQ>
+void t16g_launch_shape(const T16Args& a, dim3 grid, hipStream_t s) {
+  if (a.g128)
+    t16g_launch_group<NT, EPI, MB, RC, DQ, true>(a, grid, s);
+  else
+    t16g_launch_group<NT, EPI, MB, RC, DQ, false>(a, grid, s);
 }
 
 // The (MB, RC, DQ, units per wave) shapes here are the ones gemm_cfg returns.
@@ -482,7 +497,7 @@ int t16_gemm_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipSt
   a.part_ws = ws;
   a.part_cols = a.n_units * gemm_cols_per_unit(epi);
   a.w16_bytes = t16_weight_bytes(a.N_rows_alloc, a.K);
-  a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K);
+  a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K, a.g128);
   a.unpack[0] = 0x000F000Fu;
   a.unpack[1] = 0x00F000F0u;
   a.unpack[2] = 0x64006400u;
@@ -537,7 +552,7 @@ extern "C" size_t axm_qmm_q4_tile16_workspace_bytes(int K, int N, int swiglu) {
 }
 
 static int qmm_tile16_rows(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
-                           int N, int epi, void* ws, size_t ws_bytes, hipStream_t s) {
+                           int N, int group_size, int epi, void* ws, size_t ws_bytes, hipStream_t s) {
   for (int m0 = 0; m0 < M; m0 += kTile16GemmMaxTokens) {
     const int mc = (M - m0) < kTile16GemmMaxTokens ? (M - m0) : kTile16GemmMaxTokens;
     T16Args a{};
@@ -545,6 +560,7 @@ static int qmm_tile16_rows(const void* x, const void* w16, const void* sb16, con
     a.ldx = K;
     a.w16 = (const u32x4*)w16;
     a.sb16 = (const u32x2*)sb16;
+    a.g128 = group_size == 128;
     a.K = K;
     a.N = N;
     a.n_units = (N + 15) / 16;
@@ -564,22 +580,28 @@ static int qmm_tile16_rows(const void* x, const void* w16, const void* sb16, con
 }
 
 extern "C" int axm_qmm_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M,
-                                 int K, int N, void* workspace, size_t workspace_bytes, void* stream) {
+                                 int K, int N, int group_size, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
   AXM_CHECK_ARG(x && w16 && sb16 && y, -1, "qmm_q4_tile16: null pointer");
   AXM_CHECK_ARG(K > 0 && K % 64 == 0 && N > 0 && M >= 1, -1, "qmm_q4_tile16: bad shape M=%d K=%d N=%d", M, K, N);
-  const int rc = qmm_tile16_rows(x, w16, sb16, bias, y, M, K, N, Q4_EPI_STORE, workspace, workspace_bytes,
-                                 (hipStream_t)stream);
+  AXM_CHECK_ARG(group_size == 64 || (group_size == 128 && K % 128 == 0), -1,
+                "qmm_q4_tile16: group_size %d (64, or 128 with K %% 128 == 0)", group_size);
+  const int rc = qmm_tile16_rows(x, w16, sb16, bias, y, M, K, N, group_size, Q4_EPI_STORE, workspace,
+                                 workspace_bytes, (hipStream_t)stream);
   if (rc) return rc;
   AXM_LAUNCH_CHECK("qmm_q4_tile16");
   return 0;
 }
 
 extern "C" int axm_qmm_q4_tile16_swiglu(const void* x_normed, const void* gu16, const void* gusb16, void* y, int M,
-                                        int K, int H, void* workspace, size_t workspace_bytes, void* stream) {
+                                        int K, int H, int group_size, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
   AXM_CHECK_ARG(x_normed && gu16 && gusb16 && y, -1, "qmm_q4_tile16_swiglu: null pointer");
   AXM_CHECK_ARG(K > 0 && K % 64 == 0 && H > 0 && H % 16 == 0 && M >= 1, -1,
                 "qmm_q4_tile16_swiglu: bad shape M=%d K=%d H=%d (H %% 16 == 0)", M, K, H);
-  const int rc = qmm_tile16_rows(x_normed, gu16, gusb16, nullptr, y, M, K, H, Q4_EPI_SWIGLU, workspace,
+  AXM_CHECK_ARG(group_size == 64 || (group_size == 128 && K % 128 == 0), -1,
+                "qmm_q4_tile16_swiglu: group_size %d (64, or 128 with K %% 128 == 0)", group_size);
+  const int rc = qmm_tile16_rows(x_normed, gu16, gusb16, nullptr, y, M, K, H, group_size, Q4_EPI_SWIGLU, workspace,
                                  workspace_bytes, (hipStream_t)stream);
   if (rc) return rc;
   AXM_LAUNCH_CHECK("qmm_q4_tile16_swiglu");

@@ -165,6 +165,7 @@ struct Mat {
   void* w16 = nullptr;
   void* sb16 = nullptr;
   int N = 0, K = 0;
+  int g128 = 0;  // one (scale, bias) per 128 columns (tile16 copy only)
 };
 
 // Prologue / epilogue settings shared by both GEMV paths.
@@ -237,6 +238,7 @@ static int run_gemv(const Mat& m, int epi, int out_rows, const GemvCall& c, int 
     fill_common(a, c, m.K, out_rows);
     a.w16 = (const u32x4*)m.w16;
     a.sb16 = (const u32x2*)m.sb16;
+    a.g128 = m.g128;
     a.KB = (m.K + 127) / 128;
     a.N_rows_alloc = m.N;
     a.n_units = (out_rows + 15) / 16;
@@ -322,6 +324,7 @@ struct axm_runner {
   void setup_persistent() {
     if (!kPersistEnabled) return;
     if (m_qkv.empty() || m_qkv[0].w16 == nullptr || d.kv_dtype != AXM_KV_FP16 || d.lm_head_format != 0 ||
+        d.group_size == 128 ||
         m_lmh.w16 == nullptr)
       return;
     if (persist_check(d.d_model, d.hidden_dim, d.n_head, d.head_dim, d.vocab_size, &p_grid, &p_smem) != 0) return;
@@ -555,6 +558,7 @@ struct axm_runner {
         a.ldx = c.ldx;
         a.w16 = (const u32x4*)m.w16;
         a.sb16 = (const u32x2*)m.sb16;
+        a.g128 = m.g128;
         a.K = m.K;
         a.KB = (m.K + 127) / 128;
         a.N = out_rows;
@@ -689,12 +693,13 @@ struct axm_runner {
 
   // Re-tile one matrix for the matrix-core GEMV (runner-owned copy).
   int make_tile16(Mat& m) {
-    const size_t wb = t16_weight_bytes(m.N, m.K), sbb = t16_sb_bytes(m.N, m.K);
+    m.g128 = d.group_size == 128;
+    const size_t wb = t16_weight_bytes(m.N, m.K), sbb = t16_sb_bytes(m.N, m.K, d.group_size == 128);
     if (hipMalloc(&m.w16, wb) != hipSuccess) return -4;
     owned.push_back(m.w16);
     if (hipMalloc(&m.sb16, sbb) != hipSuccess) return -4;
     owned.push_back(m.sb16);
-    return t16_repack(m.w, m.sb, m.N, m.K, m.w16, m.sb16, nullptr);
+    return t16_repack(m.w, m.sb, m.N, m.K, m.w16, m.sb16, nullptr, d.group_size == 128);
   }
 };
 
@@ -720,6 +725,13 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
                 "runner_create: quantized KV cache needs scale arrays");
   AXM_CHECK_ARG(d.lm_head_format == 0 || d.lm_head_format == 1, -1, "runner_create: bad lm_head format");
   AXM_CHECK_ARG(d.lm_head_format == 1 || d.lm_head_sb, -1, "runner_create: lm_head scales missing");
+  AXM_CHECK_ARG(d.group_size == 0 || d.group_size == 64 || d.group_size == 128, -1,
+                "runner_create: group_size %d must be 64 or 128", d.group_size);
+  AXM_CHECK_ARG(d.group_size != 128 ||
+                    (d.layout != 1 && d.d_model % 128 == 0 && d.hidden_dim % 128 == 0 &&
+                     (d.n_head * d.head_dim) % 128 == 0 && d.hidden_dim % 16 == 0 && d.hidden_dim <= kTile16MaxK &&
+                     d.d_model <= kTile16MaxK && d.n_head * d.head_dim <= kTile16MaxK),
+                -1, "runner_create: group-128 weights need the tile16 layout and K %% 128 == 0 for every matrix");
 
   axm_runner* r = new axm_runner();
   r->d = d;

@@ -63,18 +63,30 @@ def pack_linear_q4_marlin(
     col_importance: torch.Tensor | None = None,
     grid_steps: int = 13,
     min_shrink: float = 0.72,
+    group_size: int = 64,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """(N, K) -> w_marlin int32 (ceil(N/8), K/64, 32, 2), sb_marlin fp16 (ceil(N/8), K/64, 8, 2).
 
     clip_search=False and no importance: round-to-nearest (quant.py:482-494);
-    otherwise the importance-weighted MSE clip search (quant.py:495-571)."""
+    otherwise the importance-weighted MSE clip search (quant.py:495-571).
+    group_size=128 (this build's extension, round to nearest only): the same code
+    layout with one (scale, bias) per 128 columns, sb fp16 (ceil(N/8), K/128, 8, 2)."""
+    if group_size not in (64, 128):
+        raise ValueError(f"pack_linear_q4_marlin: group_size must be 64 or 128, got {group_size}")
+    if group_size == 128 and (clip_search or col_importance is not None):
+        raise ValueError("pack_linear_q4_marlin: group_size=128 packs by round to nearest (clip_search=False)")
     src, dev, N, K = _gpu_src(weight, "pack_linear_q4_marlin")
+    if K % group_size != 0:
+        raise AssertionError(f"K ({K}) must be an exact multiple of group size {group_size}")
     nt, KG = (N + 7) // 8, K // 64
     w_m = torch.empty((nt, KG, 32, 2), dtype=torch.int32, device=dev)
-    sb_m = torch.empty((nt, KG, 8, 2), dtype=torch.float16, device=dev)
+    sb_m = torch.empty((nt, K // group_size, 8, 2), dtype=torch.float16, device=dev)
     s = _lib.stream_of(dev)
     is16 = int(src.dtype == torch.float16)
-    if not clip_search and col_importance is None:
+    if group_size == 128:
+        _lib.check(_lib.lib().axm_pack_q4_marlin_rtn_g128(_lib.ptr(src), is16, N, K, _lib.ptr(w_m), _lib.ptr(sb_m),
+                                                          s), "pack_linear_q4_marlin")
+    elif not clip_search and col_importance is None:
         _lib.check(_lib.lib().axm_pack_q4_marlin_rtn(_lib.ptr(src), is16, N, K, _lib.ptr(w_m), _lib.ptr(sb_m), s),
                    "pack_linear_q4_marlin")
     else:
@@ -95,17 +107,28 @@ def pack_linear_q4_marlin(
     return w_m, sb_m
 
 
+def marlin_group_size(w_marlin, sb_marlin) -> int:
+    """64 (reference layout) or 128 (one (scale, bias) per 128 columns), from the packed shapes."""
+    KG64, KGs = int(w_marlin.shape[1]), int(sb_marlin.shape[1])
+    if KGs == KG64:
+        return 64
+    if 2 * KGs == KG64:
+        return 128
+    raise ValueError(f"MARLIN scales cover {KGs} groups for {KG64} 64-column blocks")
+
+
 def dequantize_q4_marlin(w_marlin, sb_marlin, K: int, out_features: int | None = None) -> torch.Tensor:
-    """Packed MARLIN -> fp16 (N, K), quant.py:597-634."""
+    """Packed MARLIN -> fp16 (N, K), quant.py:597-634 (group 64 or, from the scale shape, 128)."""
     _lib.require_gpu(w_marlin, "dequantize_q4_marlin")
     nt, KG = int(w_marlin.shape[0]), int(w_marlin.shape[1])
     if KG * 64 != K:
         raise AssertionError(f"Expected K={KG * 64}, got {K}")
     N = nt * 8
     out = torch.empty((N, K), dtype=torch.float16, device=w_marlin.device)
-    _lib.check(_lib.lib().axm_dequantize_q4_marlin(_lib.ptr(w_marlin.contiguous()), _lib.ptr(sb_marlin.contiguous()),
-                                                   _lib.ptr(out), K, N, _lib.stream_of(w_marlin.device)),
-               "dequantize_q4_marlin")
+    fn = (_lib.lib().axm_dequantize_q4_marlin_g128 if marlin_group_size(w_marlin, sb_marlin) == 128
+          else _lib.lib().axm_dequantize_q4_marlin)
+    _lib.check(fn(_lib.ptr(w_marlin.contiguous()), _lib.ptr(sb_marlin.contiguous()), _lib.ptr(out), K, N,
+                  _lib.stream_of(w_marlin.device)), "dequantize_q4_marlin")
     if out_features is not None and out_features < N:
         out = out[:out_features]
     return out
@@ -124,6 +147,9 @@ def qmv_q4_marlin(x, w_marlin, sb_marlin, out_features: int | None = None, bias=
     N = nt * 8 if (out_features is None or out_features < 0) else int(out_features)
     if N > nt * 8:
         raise RuntimeError(f"qmv_q4_marlin: out_features={N} exceeds packed rows {nt * 8}")
+    if marlin_group_size(w_marlin, sb_marlin) != 64:
+        raise RuntimeError("qmv_q4_marlin: group-128 packs run on the tile16 copy (repack_q4_marlin_tile16, "
+                           "qmv_q4_tile16)")
     xc = x.contiguous()
     y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
     b = None
@@ -143,15 +169,28 @@ def qmm_q4_marlin(x, w_marlin, sb_marlin, out_features: int | None = None, bias=
 
 def repack_q4_marlin_tile16(w_marlin, sb_marlin, N: int, K: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Bit-exact re-tiling of a MARLIN matrix for the matrix-core GEMV (the layout
-    the decode runner streams); returns (w16 int32, sb16 fp16) flat buffers."""
+    the decode runner streams); returns (w16 int32, sb16 fp16) flat buffers.  A
+    group-128 pack keeps one (scale, bias) per row and 128 columns (half the sb16)."""
     _lib.require_gpu(w_marlin, "repack_q4_marlin_tile16")
     L = _lib.lib()
+    g128 = marlin_group_size(w_marlin, sb_marlin) == 128
     w16 = torch.empty(L.axm_tile16_bytes(N, K, 0) // 4, dtype=torch.int32, device=w_marlin.device)
-    sb16 = torch.empty(L.axm_tile16_bytes(N, K, 1) // 2, dtype=torch.float16, device=w_marlin.device)
-    _lib.check(L.axm_repack_q4_marlin_tile16(_lib.ptr(w_marlin.contiguous()), _lib.ptr(sb_marlin.contiguous()), N, K,
-                                             _lib.ptr(w16), _lib.ptr(sb16), _lib.stream_of(w_marlin.device)),
-               "repack_q4_marlin_tile16")
+    sb16 = torch.empty(L.axm_tile16_bytes(N, K, 2 if g128 else 1) // 2, dtype=torch.float16, device=w_marlin.device)
+    fn = L.axm_repack_q4_marlin_g128_tile16 if g128 else L.axm_repack_q4_marlin_tile16
+    _lib.check(fn(_lib.ptr(w_marlin.contiguous()), _lib.ptr(sb_marlin.contiguous()), N, K, _lib.ptr(w16),
+                  _lib.ptr(sb16), _lib.stream_of(w_marlin.device)), "repack_q4_marlin_tile16")
     return w16, sb16
+
+
+def tile16_group_size(sb16, N_rows: int, K: int) -> int:
+    """64 or 128, from the size of a tile16 scale buffer made for N_rows x K."""
+    L = _lib.lib()
+    nbytes = sb16.numel() * sb16.element_size()
+    if nbytes == L.axm_tile16_bytes(N_rows, K, 1):
+        return 64
+    if nbytes == L.axm_tile16_bytes(N_rows, K, 2):
+        return 128
+    raise ValueError(f"tile16 scales of {nbytes} bytes match neither group size for {N_rows} x {K}")
 
 
 def _qmm_workspace(K: int, N: int, swiglu: bool, device):
@@ -169,14 +208,15 @@ def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
     y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
     b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
     xc = x.contiguous()
+    gs = tile16_group_size(sb16, N, K)
     if M <= 4:
         _lib.check(_lib.lib().axm_qmv_q4_tile16(_lib.ptr(xc), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b),
-                                                _lib.ptr(y), M, K, N, _lib.stream_of(x.device)),
+                                                _lib.ptr(y), M, K, N, gs, _lib.stream_of(x.device)),
                    "qmv_q4_tile16")
         return y
     ws, n = _qmm_workspace(K, N, False, x.device)
     _lib.check(_lib.lib().axm_qmm_q4_tile16(_lib.ptr(xc), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b), _lib.ptr(y),
-                                            M, K, N, _lib.ptr(ws), n, _lib.stream_of(x.device)),
+                                            M, K, N, gs, _lib.ptr(ws), n, _lib.stream_of(x.device)),
                "qmm_q4_tile16")
     return y
 
@@ -186,7 +226,7 @@ def qmm_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
     return qmv_q4_tile16(x, w16, sb16, out_features, bias)
 
 
-def _swiglu_call(fn, name, x, ln_w, eps, w, sb, H):
+def _swiglu_call(fn, name, x, ln_w, eps, w, sb, H, group_size=None):
     _lib.require_gpu(x, name)
     K = x.size(-1)
     M = x.numel() // K
@@ -194,8 +234,9 @@ def _swiglu_call(fn, name, x, ln_w, eps, w, sb, H):
         raise RuntimeError(f"{name}: x must be float16 with 1..4 rows")
     y = torch.empty((*x.shape[:-1], int(H)), dtype=torch.float16, device=x.device)
     lw = None if ln_w is None else ln_w.to(device=x.device, dtype=torch.float16).contiguous()
+    extra = () if group_size is None else (int(group_size),)
     _lib.check(fn(_lib.ptr(x.contiguous()), _lib.ptr(lw), float(eps), _lib.ptr(w.contiguous()),
-                  _lib.ptr(sb.contiguous()), _lib.ptr(y), M, K, int(H), _lib.stream_of(x.device)), name)
+                  _lib.ptr(sb.contiguous()), _lib.ptr(y), M, K, int(H), *extra, _lib.stream_of(x.device)), name)
     return y
 
 
@@ -210,9 +251,10 @@ def qmv_q4_tile16_swiglu(x, ln_w, eps: float, gu16, gusb16, H: int) -> torch.Ten
     more than 4 rows are normalized first and go through the multi-token GEMM."""
     K = x.size(-1)
     M = x.numel() // K
+    gs = tile16_group_size(gusb16, 2 * int(H), K)
     if M <= 4:
         return _swiglu_call(_lib.lib().axm_qmv_q4_tile16_swiglu, "qmv_q4_tile16_swiglu", x, ln_w, eps, gu16, gusb16,
-                            H)
+                            H, gs)
     from .ops import fused_rmsnorm
 
     _lib.require_gpu(x, "qmv_q4_tile16_swiglu")
@@ -222,7 +264,7 @@ def qmv_q4_tile16_swiglu(x, ln_w, eps: float, gu16, gusb16, H: int) -> torch.Ten
     y = torch.empty((*x.shape[:-1], int(H)), dtype=torch.float16, device=x.device)
     ws, n = _qmm_workspace(K, int(H), True, x.device)
     _lib.check(_lib.lib().axm_qmm_q4_tile16_swiglu(_lib.ptr(xn), _lib.ptr(gu16.contiguous()),
-                                                   _lib.ptr(gusb16.contiguous()), _lib.ptr(y), M, K, int(H),
+                                                   _lib.ptr(gusb16.contiguous()), _lib.ptr(y), M, K, int(H), gs,
                                                    _lib.ptr(ws), n, _lib.stream_of(x.device)),
                "qmm_q4_tile16_swiglu")
     return y

@@ -85,7 +85,8 @@ class QuantizedDecodeRunner:
             vocab_sz = wte.shape[0] if lmh_fmt == 0 else lmh_packed.shape[0]
         self.vocab_size = int(vocab_sz)
         self.d_model = int(n_h * hd)
-        self.hidden_dim = int(w_down_s[0].shape[1] * 64)
+        # 64-column code blocks of w_down (its scales hold K / 128 groups in a group-128 pack)
+        self.hidden_dim = int(w_down_p[0].shape[1] * 64)
         kv_code = KV_CODES[kv_dtype]
         self.kv_dtype = kv_dtype
         self.max_seq_len = int(k_cs[0].shape[-2])
@@ -124,6 +125,18 @@ class QuantizedDecodeRunner:
         d.k_cache, d.v_cache = cv(a[11], P), cv(a[12], P)
         d.k_scales, d.v_scales = (cv(a[13], P), cv(a[14], P)) if kv_code else (None, None)
         d.max_tokens = int(max_tokens)
+        # group 64 (reference) or 128, from the packed scales; one size for every Q4 matrix
+        from .kernels.quant import marlin_group_size
+
+        packs = list(c_attn_p) + list(c_proj_p) + list(gate_up_p) + list(w_down_p)
+        scales = list(c_attn_s) + list(c_proj_s) + list(gate_up_s) + list(w_down_s)
+        groups = {marlin_group_size(p, s) for p, s in zip(packs, scales)}
+        if lmh_fmt == 0:
+            groups.add(marlin_group_size(lmh_packed, lmh_sb))
+        if len(groups) != 1:
+            raise RuntimeError(f"QuantizedDecodeRunner: mixed MARLIN group sizes {sorted(groups)}")
+        self.group_size = groups.pop()
+        d.group_size = self.group_size
         if layout not in ("tile16", "marlin"):
             raise ValueError(f"layout must be 'tile16' or 'marlin', got {layout!r}")
         d.layout = 0 if layout == "tile16" else 1

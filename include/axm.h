@@ -44,17 +44,28 @@ int axm_qmv_q4_marlin_swiglu(const void* x, const void* ln_w, float eps, const v
 /* Matrix-core ("tile16") copy of a MARLIN matrix, the layout the decode runner
  * streams: w16 u32 [ceil(N/16)][ceil(K/128)][64][4], sb16 [ceil(N/16)][ceil(K/128)][16][2]
  * (scale, bias).  The re-tiling is bit-exact (same codes, scales and biases).
- * axm_tile16_bytes(N, K, 0) / (N, K, 1) give the two buffer sizes. */
+ * axm_tile16_bytes(N, K, 0) / (N, K, 1) give the two buffer sizes; (N, K, 2) the
+ * scale buffer of a group-128 copy (one (scale, bias) per row and kb: [N16][KB][16]). */
 size_t axm_tile16_bytes(int N, int K, int which);
 int axm_repack_q4_marlin_tile16(const void* w_marlin, const void* sb_marlin, int N, int K, void* w16, void* sb16,
                                 void* stream);
-/* y = x W^T (+ bias) on the tile16 copy, MFMA 16x16x32 f16 with fp32 accumulation. */
+/* Group-128 variant (no counterpart in the reference, whose MARLIN groups are 64
+ * columns): the same 64-column code layout with one (scale, bias) per 128 columns,
+ * sb128 fp16 [N/8][K/128][8][2] (0.53125 bytes per weight).  RTN packer (the rule of
+ * quant.py:483-494 over 128 columns), fp16 dequantization, and the re-tiling. */
+int axm_pack_q4_marlin_rtn_g128(const void* w, int src_is_fp16, int N, int K, void* w_marlin, void* sb128,
+                                void* stream);
+int axm_dequantize_q4_marlin_g128(const void* w_marlin, const void* sb128, void* out, int K, int N, void* stream);
+int axm_repack_q4_marlin_g128_tile16(const void* w_marlin, const void* sb128, int N, int K, void* w16, void* sb16,
+                                     void* stream);
+/* y = x W^T (+ bias) on the tile16 copy, MFMA 16x16x32 f16 with fp32 accumulation.
+ * group_size: 64, or 128 for a group-128 copy (K % 128 == 0), on every tile16 entry. */
 int axm_qmv_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
-                      int N, void* stream);
+                      int N, int group_size, void* stream);
 /* axm_qmv_q4_marlin_swiglu on the tile16 copy of the packed [W_gate; W_up] (2 H rows,
  * H % 16 == 0): the runner's MLP-input launch (transformer.py:1178-1189). */
 int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const void* gu16, const void* gusb16,
-                             void* y, int M, int K, int H, void* stream);
+                             void* y, int M, int K, int H, int group_size, void* stream);
 /* Multi-token GEMM on the tile16 copy: y[M][N] = x @ W^T (+ bias) with every weight
  * chunk streamed once per 64 tokens (the M > 8 path of qmm_q4_marlin_mps: kernels
  * qmm_q4_marlin_m8_apple_kernel / qmm_q4_marlin_apple_kernel, metal_kernels.metal:
@@ -65,11 +76,11 @@ int axm_qmv_q4_tile16_swiglu(const void* x, const void* ln_w, float eps, const v
  * (axm_qmm_q4_tile16_workspace_bytes: enough for any M, 0 when no split is used). */
 size_t axm_qmm_q4_tile16_workspace_bytes(int K, int N, int swiglu);
 int axm_qmm_q4_tile16(const void* x, const void* w16, const void* sb16, const void* bias, void* y, int M, int K,
-                      int N, void* workspace, size_t workspace_bytes, void* stream);
+                      int N, int group_size, void* workspace, size_t workspace_bytes, void* stream);
 /* silu(g) * u over the tile16 [W_gate; W_up] copy for M tokens whose activations are
  * already RMS-normalized (the multi-token MLP input, transformer.py:1178-1189). */
 int axm_qmm_q4_tile16_swiglu(const void* x_normed, const void* gu16, const void* gusb16, void* y, int M, int K,
-                             int H, void* workspace, size_t workspace_bytes, void* stream);
+                             int H, int group_size, void* workspace, size_t workspace_bytes, void* stream);
 /* Row-major fp16 [N][K] dequantization (axiomlm/kernels/quant.py:597-634). */
 int axm_dequantize_q4_marlin(const void* w_marlin, const void* sb_marlin, void* out, int K, int N, void* stream);
 /* Round-to-nearest packer, clip_search=False (axiomlm/kernels/quant.py:447-494, 573-593).
@@ -247,6 +258,8 @@ typedef struct axm_runner_desc {
   void* const* v_scales;
   int max_tokens; /* capacity of the multi-token (verify) paths, <= 64 */
   int layout;     /* 0: re-tile weights for the matrix cores (default); 1: stream the reference layout */
+  int group_size; /* MARLIN Q4 packs (layers and a Q4 lm_head): 64 (reference), or 128 (tile16 layout only);
+                     0 means 64 */
 } axm_runner_desc;
 
 typedef struct axm_runner* axm_runner_t;

@@ -186,6 +186,34 @@ def _marlin_group_order():
 _MARLIN_ORDER = _marlin_group_order()
 
 
+def pack_linear_q4_marlin_g128(weight: np.ndarray):
+    """MARLIN Q4 with one (scale, bias) per 128 columns (this build's group-128 variant of
+    quant.py:447-594; round to nearest): the codes keep the group-64 lane interleave of every
+    64-column block, the scales become sb_marlin [N/8][K/128][8][2].  The reference has no
+    group-128 packer; scale and bias follow its RTN rule (quant.py:483-494) over 128 columns."""
+    N, K = weight.shape
+    assert K % 128 == 0
+    nt = (N + 7) // 8
+    Np = nt * 8
+    w = np.zeros((Np, K), dtype=weight.dtype)
+    w[:N] = weight
+    wg = w.reshape(Np, K // 128, 128)
+    scale, bias = _rtn_scale_bias(wg, weight.dtype == F16)
+    q = _codes(wg.astype(F32), scale, bias, 15.0).reshape(Np, K // 64, 64)
+    wm, _ = interleave_marlin(q, np.zeros((Np, K // 64, 1), F32), np.zeros((Np, K // 64, 1), F32))
+    sb = np.stack([scale[..., 0], bias[..., 0]], axis=-1).astype(F16)  # (Np, K/128, 2)
+    return wm, np.ascontiguousarray(sb.reshape(nt, 8, K // 128, 2).transpose(0, 2, 1, 3))
+
+
+def dequantize_q4_marlin_g128(w_marlin: np.ndarray, sb128: np.ndarray, K: int, out_features: int | None = None):
+    """fp16 [N, K] = fp16(q * scale + bias) with the (scale, bias) of column k's 128-group."""
+    nt = w_marlin.shape[0]
+    q = unpack_marlin_codes(w_marlin).astype(F32).reshape(nt * 8, K // 128, 128)
+    sb = sb128.transpose(0, 2, 1, 3).reshape(nt * 8, K // 128, 2).astype(F32)
+    w = (q * sb[..., 0:1] + sb[..., 1:2]).reshape(nt * 8, K).astype(F16)
+    return w[:out_features] if out_features is not None and out_features < w.shape[0] else w
+
+
 def unpack_marlin_codes(w_marlin: np.ndarray):
     """Inverse interleave: codes [N_pad, K] (uint8), quant.py:597-625."""
     nt, KG, _, _ = w_marlin.shape

@@ -278,7 +278,9 @@ def _dequantized(wp, wsb, K, out_features):
     hit = _DEQ_MEMO.get(key)
     if hit is not None and hit[0] is wp and hit[1] is wsb:
         return hit[2]
-    if wp.ndim == 4:
+    if wp.ndim == 4 and wsb.shape[1] * 2 == wp.shape[1]:
+        w = fm.dequantize_q4_marlin_g128(wp, wsb, K, out_features)
+    elif wp.ndim == 4:
         w = fm.dequantize_q4_marlin(wp, wsb, K, out_features)
     else:
         w = fm.dequantize_q8_g64(wp, wsb, K)
@@ -484,12 +486,15 @@ def pack_model(cfg: OracleConfig, W, mode: str = "q4") -> OracleWeights:
     Q8_G64 embedding, MARLIN Q4 lm_head and layer matrices (gate|up rows stacked,
     :959-963).  mode "q4" = MSE clip search with the reference importance vectors
     (|ln_f| for lm_head, |ln_1| for c_attn, |ln_2| for gate|up, row-norm product of
-    w_gate and w_up for w_down, none for c_proj; :876-948); "q4_rtn" = round to nearest."""
+    w_gate and w_up for w_down, none for c_proj; :876-948); "q4_rtn" = round to nearest;
+    "q4_g128" = round to nearest with one (scale, bias) per 128 columns."""
     mse = mode == "q4"
-    if mode not in ("q4", "q4_rtn"):
+    if mode not in ("q4", "q4_rtn", "q4_g128"):
         raise ValueError(f"unsupported mode {mode!r}")
 
     def pack(w, imp):
+        if mode == "q4_g128":  # this build's group-128 variant (round to nearest)
+            return fm.pack_linear_q4_marlin_g128(w)
         return fm.pack_linear_q4_marlin(w, clip_search=mse, col_importance=imp if mse else None)
 
     a = lambda v: np.abs(v.astype(F32))  # noqa: E731

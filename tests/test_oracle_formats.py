@@ -228,3 +228,49 @@ def test_kv_zero_group_gives_nan_codes():
     t = torch.zeros(1, 64, dtype=torch.float16)
     s_t = torch.clamp(t.abs().amax(dim=-1, keepdim=True) / 448.0, min=1e-8).to(torch.float16)
     assert float(s_t) == 0.0
+
+
+# ---------------------------------------------------------------------------
+# MARLIN Q4 group 128 (the build's variant: group-64 code layout, one scale per 128)
+# ---------------------------------------------------------------------------
+def test_g128_equals_g64_with_shared_pair_scales():
+    # Duplicating each 128-group's (scale, bias) over its two 64-groups gives a group-64 pack
+    # that must dequantize bit for bit like the group-128 one (the scale of column k is the
+    # one of group k // 128, not k // 64).
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((24, 384)) * 0.03).astype(F16)
+    wm, sb128 = fm.pack_linear_q4_marlin_g128(w)
+    assert wm.shape == (3, 6, 32, 2) and sb128.shape == (3, 3, 8, 2)
+    sb64 = np.repeat(sb128, 2, axis=1)
+    a = fm.dequantize_q4_marlin_g128(wm, sb128, 384)
+    b = fm.dequantize_q4_marlin(wm, sb64, 384)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    # a matrix whose 64-groups already share (min, max) per 128 packs to the same codes in G64
+    w2 = w.copy().reshape(24, 3, 2, 64)
+    w2[:, :, :, 0] = w2.reshape(24, 3, 128).min(-1)[:, :, None]
+    w2[:, :, :, 1] = w2.reshape(24, 3, 128).max(-1)[:, :, None]
+    w2 = w2.reshape(24, 384)
+    g64m, g64s = fm.pack_linear_q4_marlin(w2, clip_search=False)
+    g128m, g128s = fm.pack_linear_q4_marlin_g128(w2)
+    assert np.array_equal(g64m, g128m)
+    assert np.array_equal(g64s.view(np.uint16), np.repeat(g128s, 2, axis=1).view(np.uint16))
+
+
+def test_g128_rtn_closed_form_and_nearest_codes():
+    rng = np.random.default_rng(13)
+    w = (rng.standard_normal((8, 128)) * 0.05).astype(np.float32)
+    wm, sb = fm.pack_linear_q4_marlin_g128(w)
+    mn, mx = w.min(-1), w.max(-1)
+    assert np.array_equal(sb[0, 0, :, 0], ((mx - mn) / np.float32(15.0)).astype(F16))
+    assert np.array_equal(sb[0, 0, :, 1], mn.astype(F16))
+    codes = fm.unpack_marlin_codes(wm)[:8].astype(np.int64)
+    s = sb[0, 0, :, 0].astype(F32)[:, None]
+    b = sb[0, 0, :, 1].astype(F32)[:, None]
+    t = (w - b) / s
+    best = np.abs(t[..., None] - np.arange(16)).argmin(-1)
+    ok = (np.abs(t % 1.0 - 0.5) > 1e-4) & (t > -0.5) & (t < 15.5)
+    assert np.array_equal(codes[ok], best[ok])
+    # bytes per weight: 4-bit codes + one fp16 scale and bias per 128
+    N, K = 4096, 4096
+    assert (wm.nbytes / w.size, sb.nbytes / w.size) == (0.5, 4 / 128)
+    assert (N * K // 2 + N * K // 128 * 4) / (N * K) == 0.53125
