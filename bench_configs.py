@@ -11,7 +11,11 @@ per case, each against the HBM roofline (8 TB/s) with its algorithmic bytes:
   c4  BitNet ternary and affine 2-bit GEMVs at the FFN shapes (4096 -> 11008,
       11008 -> 4096), batch 1
   c5  speculative tree verification, 7B shape, FP8 KV, prefix 2048, a 64-node
-      tree (depth 6, branching 4,4,2,2,1,1): one runner.verify_tree_step
+      tree (depth 6, branching 4,4,2,2,1,1): one runner.verify_tree_step; the
+      128-step greedy-acceptance loop (verify, greedy walk, KV compaction) with
+      seeded random drafts and with drafts that follow the model's own greedy
+      continuation along the first-child chain; this runner's t(N) latency
+      profile and the Sequoia tree it selects
 
 Kernels are timed from a captured HIP graph of back-to-back calls (no host
 launch gaps), rotating over enough weight / cache copies that the stream does
@@ -184,7 +188,8 @@ def run_c5(dev):
 
     c = bench.CFG_7B
     d, H, L, hd = c["d"], c["hidden"], c["n_layer"], c["hd"]
-    prefix, S, T = 2048, 2048 + 128, 64
+    prefix, T, loop_steps = 2048, 64, 128
+    S = prefix + loop_steps * 7 + T + 64  # room for 7 tokens per loop step
     g = torch.Generator(device=dev)
     g.manual_seed(0)
 
@@ -251,6 +256,71 @@ def run_c5(dev):
     _line("C5", f"verify_tree_step T={T} prefix={prefix} fp8 KV", us, w_bytes + kv_bytes,
           {"mfma_frac_f16": round(flops / (us * 1e-6) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4),
            "tree_nodes_per_s": round(T / (us * 1e-6), 1), "host_wall_us": round(wall * 1e6, 1)})
+    _c5_loops(runner, cache, tree, prefix, loop_steps, c["vocab"], dev, g)
+
+
+def _loop_line(case, T, r, cont):
+    n_tok = len(r["tokens"])
+    match = sum(int(a == b) for a, b in zip(r["tokens"], cont))
+    print(json.dumps({"config": "C5", "case": case, "tree_nodes": T, "steps": r["model_calls"], "tokens": n_tok,
+                      "mean_accepted_per_step": round(sum(r["accepted"]) / len(r["accepted"]), 3),
+                      "ms_per_step": round(r["seconds"] * 1e3 / r["model_calls"], 3),
+                      "tokens_per_s": round(n_tok / r["seconds"], 1),
+                      "tokens_equal_to_reference_continuation": f"{match}/{n_tok}"}), flush=True)
+
+
+def _c5_loops(runner, cache, tree, prefix, n_steps, vocab, dev, g):
+    """The 128-step tree loop of medusa.py:278-363 (greedy acceptance) on the C5 model, then
+    the runner's t(N) profile and the Sequoia tree chosen with it."""
+    import torch
+
+    from axiomlm_amd.sequoia import SequoiaDPOptimizer, measure_tree_latency
+    from axiomlm_amd.speculative import tree_decode_greedy
+
+    T = tree["num_nodes"]
+    chain = []
+    u = 0
+    while tree["children"][u]:
+        u = tree["children"][u][0]
+        chain.append(u)
+    root = int(torch.randint(0, vocab, (1,), generator=g, device=dev))
+    rng = torch.Generator().manual_seed(1)
+
+    def reset():
+        cache.total_seen_tokens[:] = [prefix] * cache.n_layer
+        cache.layer_seq_lens[:] = [prefix] * cache.n_layer
+
+    def random_draft(step, last, seen):
+        return torch.randint(0, vocab, (T - 1,), generator=rng).tolist()
+
+    # Random drafts are never accepted, so this run emits the model's greedy continuation
+    # one token per step, computed by the same verify path as the loop below.
+    reset()
+    tree_decode_greedy(runner, cache, root, tree, random_draft, 2)  # warm-up
+    reset()
+    n_ref = n_steps * (len(chain) + 1)
+    r = tree_decode_greedy(runner, cache, root, tree, random_draft, n_ref)
+    cont = r["tokens"]  # cont[i] = greedy token at position prefix + 1 + i
+    _loop_line(f"{n_ref}-step tree loop, seeded random drafts", T, r, cont)
+
+    def chain_draft(step, last, seen):
+        nodes = torch.randint(0, vocab, (T,), generator=rng).tolist()
+        for k, node in enumerate(chain, start=1):
+            i = seen - prefix + k - 1
+            nodes[node] = cont[i] if i < len(cont) else 0
+        return nodes[1:]
+
+    reset()
+    r = tree_decode_greedy(runner, cache, root, tree, chain_draft, n_steps)
+    _loop_line(f"{n_steps}-step tree loop, drafts = the greedy continuation on the first-child chain", T, r, cont)
+    reset()
+    prof = measure_tree_latency(runner, cache, budgets=(2, 4, 8, 16, 24, 32, 48, 64))
+    opt = SequoiaDPOptimizer(num_heads=6, max_branches=4, max_budget=64, latency_profile=prof)
+    res = opt.solve_optimal_tree()
+    print(json.dumps({"config": "C5", "case": "t(N) = verify_tree_step(N) / step, 7B Q4 FP8 prefix 2048",
+                      "t_of_N": prof, "sequoia_N": res.optimal_N, "sequoia_depth": res.max_depth,
+                      "sequoia_expected_tokens": res.expected_accepted_tokens,
+                      "sequoia_speedup": res.speedup}), flush=True)
 
 
 def main() -> None:

@@ -499,6 +499,54 @@ def test_runner_speculative_decode_matches_greedy(dev):
           flush=True)
 
 
+def test_sequoia_tree_loop_matches_greedy(dev):
+    """The tree loop (verify, greedy walk, compaction) over a Sequoia-sized tree: drafts on the
+    tree's first-child chain follow the oracle's greedy continuation (so nodes are accepted),
+    the other nodes are random; every emitted token must be the oracle's greedy choice given
+    the tokens before it, up to near-ties within the logit tolerance."""
+    from axiomlm_amd.sequoia import SequoiaDPOptimizer
+    from axiomlm_amd.speculative import tree_decode_greedy
+
+    print("[sequoia_tree_loop]", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S)
+    tree = SequoiaDPOptimizer(num_heads=4, max_branches=4, max_budget=24).solve_fixed_budget(24).compiled_tree
+    T = tree["num_nodes"]
+    chain, u = [], 0
+    while tree["children"][u]:
+        u = tree["children"][u][0]
+        chain.append(u)
+    rng = np.random.default_rng(15)
+    prompt = rng.integers(0, cfg.vocab, 16).tolist()
+    run_steps(runner, cache, prompt[:-1], dev)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    lg = model.forward(prompt, ocache)[-1]
+    cont = []  # oracle greedy tokens at positions 16, 17, ...
+    for _ in range(60):
+        cont.append(int(np.argmax(lg)))
+        lg = model.forward([cont[-1]], ocache)[-1]
+    p0 = len(prompt)
+
+    def draft(step, last, seen):
+        nodes = rng.integers(0, cfg.vocab, T).tolist()
+        for k, node in enumerate(chain, start=1):
+            i = seen + k - p0
+            nodes[node] = cont[i] if 0 <= i < len(cont) else 0
+        return nodes[1:]
+
+    r = tree_decode_greedy(runner, cache, prompt[-1], tree, draft, n_steps=8)
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
+    lg = model.forward(prompt, ocache)[-1].astype(F32)
+    for i, tk in enumerate(r["tokens"]):
+        assert lg[tk] >= lg.max() - 2 * TOL, f"token {i}: {tk} scores {lg[tk]}, greedy max {lg.max()}"
+        lg = model.forward([tk], ocache)[-1].astype(F32)
+    assert cache.total_seen_tokens[0] == p0 - 1 + len(r["tokens"])
+    assert sum(r["accepted"]) > 0 and r["model_calls"] == 8
+    print(f"[sequoia_tree_loop] T={T} tokens={len(r['tokens'])} accepted={r['accepted']}", flush=True)
+
+
 # ---------------------------------------------------------------------------
 # Runner branches: tied Q8_G64 lm_head, fp16 embedding table, QKV bias
 # ---------------------------------------------------------------------------
