@@ -42,6 +42,9 @@ _SIGNATURES = {
     ),
     "axm_qmv_ternary": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "axm_qmv_q2_k": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "axm_pack_q2_k_gguf": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "axm_dequantize_q2_k_gguf": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "axm_qmv_q2_k_gguf": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "axm_qmv_q4_tile16_swiglu": (
         c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]
     ),

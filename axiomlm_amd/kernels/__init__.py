@@ -24,10 +24,12 @@ from .quant import (  # noqa: F401
     compute_quantization_metrics,
     dequant_q8_rows,
     dequantize_q2_k,
+    dequantize_q2_k_gguf,
     dequantize_q4_marlin,
     dequantize_q8_g64,
     dequantize_ternary,
     pack_linear_q2_k,
+    pack_linear_q2_k_gguf,
     pack_linear_q4_marlin,
     pack_linear_q8_g64,
     pack_linear_ternary,
@@ -40,6 +42,7 @@ from .quant import (  # noqa: F401
     qmv_ternary,
     qmm_ternary,
     qmv_q2_k,
+    qmv_q2_k_gguf,
     qmm_q2_k,
     qmv_q4_tile16_swiglu,
     qmv_q4_marlin_swiglu,

@@ -409,6 +409,58 @@ def qmm_q2_k(x, w_packed, scales_biases, bias=None) -> torch.Tensor:
     return qmv_q2_k(x, w_packed, scales_biases, bias)
 
 
+# ---------------------------------------------------------------------------
+# GGUF Q2_K super-blocks (ggml block_q2_K; no counterpart in the reference)
+# ---------------------------------------------------------------------------
+Q2K_GGUF_BLOCK_BYTES = 84
+
+
+def pack_linear_q2_k_gguf(weight: torch.Tensor) -> torch.Tensor:
+    """(N, K) fp16/fp32, K % 256 == 0 -> uint8 (N, K/256, 84) GGUF Q2_K blocks (round to nearest)."""
+    src, dev, N, K = _gpu_src(weight, "pack_linear_q2_k_gguf")
+    if K % 256:
+        raise RuntimeError(f"pack_linear_q2_k_gguf: K={K} is not a multiple of 256")
+    blocks = torch.empty((N, K // 256, Q2K_GGUF_BLOCK_BYTES), dtype=torch.uint8, device=dev)
+    _lib.check(_lib.lib().axm_pack_q2_k_gguf(_lib.ptr(src), int(src.dtype == torch.float16), N, K, _lib.ptr(blocks),
+                                             _lib.stream_of(dev)),
+               "pack_linear_q2_k_gguf")
+    return blocks.to(weight.device) if weight.device.type != "cuda" else blocks
+
+
+def _q2k_shape(blocks, name):
+    if blocks.dtype != torch.uint8 or blocks.dim() != 3 or blocks.shape[2] != Q2K_GGUF_BLOCK_BYTES:
+        raise RuntimeError(f"{name}: blocks must be uint8 (N, K/256, 84)")
+    return int(blocks.shape[0]), int(blocks.shape[1]) * 256
+
+
+def dequantize_q2_k_gguf(blocks) -> torch.Tensor:
+    """GGUF Q2_K blocks -> fp16 (N, K): d * (sc & 15) * q - dmin * (sc >> 4) in fp32."""
+    _lib.require_gpu(blocks, "dequantize_q2_k_gguf")
+    N, K = _q2k_shape(blocks, "dequantize_q2_k_gguf")
+    out = torch.empty((N, K), dtype=torch.float16, device=blocks.device)
+    _lib.check(_lib.lib().axm_dequantize_q2_k_gguf(_lib.ptr(blocks.contiguous()), N, K, _lib.ptr(out),
+                                                   _lib.stream_of(blocks.device)),
+               "dequantize_q2_k_gguf")
+    return out
+
+
+def qmv_q2_k_gguf(x, blocks, bias=None) -> torch.Tensor:
+    """y = x @ W^T (+ bias) on GGUF Q2_K blocks; x fp16 (..., K), any number of rows."""
+    _lib.require_gpu(x, "qmv_q2_k_gguf")
+    if x.dtype != torch.float16:
+        raise RuntimeError("qmv_q2_k_gguf: x must be float16")
+    N, K = _q2k_shape(blocks, "qmv_q2_k_gguf")
+    if x.size(-1) != K:
+        raise RuntimeError(f"qmv_q2_k_gguf: x has K={x.size(-1)}, blocks hold K={K}")
+    M = x.numel() // K
+    y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
+    b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
+    _lib.check(_lib.lib().axm_qmv_q2_k_gguf(_lib.ptr(x.contiguous()), _lib.ptr(blocks.contiguous()), _lib.ptr(b),
+                                            _lib.ptr(y), M, K, N, _lib.stream_of(x.device)),
+               "qmv_q2_k_gguf")
+    return y
+
+
 def compute_quantization_metrics(orig, dequant, quant_bytes: int | None = None) -> dict:
     """SQNR / cosine / MSE / L_inf / compression ratio (quant.py:855-893)."""
     o = orig.flatten().float()

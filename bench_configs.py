@@ -8,8 +8,8 @@ per case, each against the HBM roofline (8 TB/s) with its algorithmic bytes:
       down; MARLIN Q4 G64 re-tiled for the matrix cores) at M = 1, 4, 16 tokens
   c3  split-K decode attention, B 8, 32 query / 8 KV heads, hd 128, INT4 and FP8
       KV at 1k / 8k / 32k keys, and the 4096-slot ring buffer after 10k tokens
-  c4  BitNet ternary and affine 2-bit GEMVs at the FFN shapes (4096 -> 11008,
-      11008 -> 4096), batch 1
+  c4  BitNet ternary, affine 2-bit and GGUF Q2_K GEMVs at the FFN shapes
+      (4096 -> 11008, 11008 -> 4096), batch 1 (GGUF also 4 tokens)
   c5  speculative tree verification, 7B shape, FP8 KV, prefix 2048, a 64-node
       tree (depth 6, branching 4,4,2,2,1,1): one runner.verify_tree_step; the
       128-step greedy-acceptance loop (verify, greedy walk, KV compaction) with
@@ -176,6 +176,21 @@ def run_c4(dev):
             _line("C4", f"{fmt} {K}->{N} M=1", us, wb + (K + N) * 2, {"weight_copies": n_copies})
             del packs
             torch.cuda.empty_cache()
+    from axiomlm_amd.kernels import pack_linear_q2_k_gguf, qmv_q2_k_gguf
+
+    for N, K in ((11008, 4096), (4096, 11008)):
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+        blocks = pack_linear_q2_k_gguf(w)
+        del w
+        wb = blocks.numel()  # 84 bytes per 256 weights
+        n_copies = max(2, COLD_POOL_BYTES // wb + 1)
+        pool = [blocks.clone() for _ in range(n_copies)]
+        for M in (1, 4):
+            x = torch.randn(M, K, generator=g, device=dev).half()
+            us = _graph_time_us(lambda i: qmv_q2_k_gguf(x, pool[i % n_copies]), 2 * n_copies)
+            _line("C4", f"GGUF Q2_K {K}->{N} M={M}", us, wb + M * (K + N) * 2, {"weight_copies": n_copies})
+        del pool, blocks
+        torch.cuda.empty_cache()
 
 
 def run_c5(dev):

@@ -120,6 +120,21 @@ int axm_qmv_ternary(const void* x, const void* w_packed, const void* scales, con
 int axm_qmv_q2_k(const void* x, const void* w_packed, const void* scales_biases, const void* bias, void* y, int M,
                  int K, int N, void* stream);
 
+/* ---- GGUF Q2_K super-blocks (ggml block_q2_K, QK_K = 256) ----------------
+ * No counterpart in the reference's kernels (its "Q2_K" is the affine group-64
+ * format above); this is the GGUF layout the C4 configuration names, read as
+ * stored: blocks uint8 [N][K/256][84] = scales[16] (4-bit scale | 4-bit min << 4
+ * per 16 elements), qs[64] (element 128h + 32j + l at bits 2j of qs[32h + l]),
+ * d, dmin fp16; w = d * (sc & 15) * q - dmin * (sc >> 4).  K % 256 == 0.
+ * Packer: round to nearest (per-sub-block min/max, 4-bit scale and min codes
+ * against fp16 super-block maxima), not ggml's iterative scale search. */
+int axm_pack_q2_k_gguf(const void* w, int src_is_fp16, int N, int K, void* blocks, void* stream);
+/* blocks -> fp16 [N][K], fp32 arithmetic, one rounding. */
+int axm_dequantize_q2_k_gguf(const void* blocks, int N, int K, void* out, void* stream);
+/* y = x W^T (+ bias), x fp16 [M][K], y fp16 [M][N], fp32 accumulation; K <= 16384. */
+int axm_qmv_q2_k_gguf(const void* x, const void* blocks, const void* bias, void* y, int M, int K, int N,
+                      void* stream);
+
 /* ---- norms / activations / argmax ---------------------------------------- */
 /* rmsnorm_infer_mps (mps_kernels.mm:247-266; math of axiomlm/models/modules.py:41-43). */
 int axm_rmsnorm(const void* x, const void* w, void* y, int rows, int D, float eps, void* stream);

@@ -24,6 +24,11 @@ Pinning (see tests/test_oracle_*.py):
     round / clamp / int8 cast (quant.py:789-803) on exact .5 ties, all-zero
     (NaN-code) groups, subnormal groups and every fp16 quotient in [-8.5, 8.5]
     (tests/test_oracle_model.py).
+  * GGUF Q2_K (ggml block_q2_K; not in the reference's code, not vendored, no
+    gguf library here): the decoder against a hand-assembled block and an
+    element-by-element loop over the published formula, lattice round trips,
+    0.328125 B/w.  The encoder is this build's round-to-nearest: parity
+    unpinned against ggml's quantize_row_q2_K (iterative scale search).
 """
 
 from __future__ import annotations
@@ -374,6 +379,75 @@ def dequantize_q2_k(packed: np.ndarray, sb: np.ndarray, K: int | None = None):
     # q.to(fp16) * sc + bi: two fp16 roundings (torch fp16 ops)
     t = _h(q * sb[..., 0:1].astype(F32))
     return _h(t + sb[..., 1:2].astype(F32)).reshape(N, K).astype(F16)
+
+
+# ---------------------------------------------------------------------------
+# GGUF Q2_K super-blocks: ggml's block_q2_K (QK_K = 256, 84 bytes) and its
+# published decoder dequantize_row_q2_K (llama.cpp ggml-quants.c); the format is
+# not part of the reference's code (its "Q2_K" above is affine group-64).
+# ---------------------------------------------------------------------------
+Q2K_BLOCK_BYTES = 84  # scales[16] | qs[64] | d fp16 | dmin fp16
+
+
+def q2k_element_maps():
+    """For element e of a block: (qs byte index, bit shift, sub-block index):
+    e = 128h + 32j + l -> qs[32h + l] >> 2j, sub-block e // 16."""
+    e = np.arange(256)
+    h, j, l = e // 128, (e // 32) % 4, e % 32
+    return 32 * h + l, 2 * j, e // 16
+
+
+def pack_q2_k_gguf(weight: np.ndarray) -> np.ndarray:
+    """(N, K) -> uint8 (N, K/256, 84), round to nearest (this build's encoder): per
+    16-element sub-block m = min(0, min w), scale = (max w - m) / 3; d = fp16(max
+    scale / 15), dmin = fp16(max(-m) / 15); 4-bit codes rint(scale / d), rint(-m / dmin)
+    clamped to [0, 15]; 2-bit codes rint((w + dmin mc) / (d sc)) clamped to [0, 3]
+    (0 where d sc == 0).  fp32, one rounding per operation, rint = half to even."""
+    N, K = weight.shape
+    assert K % 256 == 0
+    NB = K // 256
+    w = weight.astype(F32).reshape(N, NB, 16, 16)
+    mn = np.minimum(w.min(-1), F32(0))
+    mx = w.max(-1)
+    sub_scale = ((mx - mn).astype(F32) / F32(3)).astype(F32)
+    sub_min = (-mn).astype(F32)
+    d = (sub_scale.max(-1) / F32(15)).astype(F32).astype(F16).astype(F32)  # (N, NB)
+    dmin = (sub_min.max(-1) / F32(15)).astype(F32).astype(F16).astype(F32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        sc = np.where(d[..., None] > 0, np.clip(np.rint(sub_scale / d[..., None]), 0, 15), 0).astype(F32)
+        mc = np.where(dmin[..., None] > 0, np.clip(np.rint(sub_min / dmin[..., None]), 0, 15), 0).astype(F32)
+        dl = (d[..., None] * sc).astype(F32)
+        dm = (dmin[..., None] * mc).astype(F32)
+        num = (w + dm[..., None]).astype(F32)
+        q = np.where(dl[..., None] > 0, np.clip(np.rint(num / dl[..., None]), 0, 3), 0).astype(np.uint8)
+    q = q.reshape(N, NB, 256)
+    byte_idx, shift, _ = q2k_element_maps()
+    qs = np.zeros((N, NB, 64), np.uint8)
+    for e in range(256):
+        qs[:, :, byte_idx[e]] |= (q[:, :, e] << shift[e]).astype(np.uint8)
+    out = np.zeros((N, NB, Q2K_BLOCK_BYTES), np.uint8)
+    out[:, :, :16] = (sc.astype(np.uint8) | (mc.astype(np.uint8) << 4))
+    out[:, :, 16:80] = qs
+    out[:, :, 80:82] = d.astype(F16).view(np.uint8).reshape(N, NB, 2)
+    out[:, :, 82:84] = dmin.astype(F16).view(np.uint8).reshape(N, NB, 2)
+    return out
+
+
+def dequantize_q2_k_gguf(blocks: np.ndarray, out_dtype=F16) -> np.ndarray:
+    """uint8 (N, K/256, 84) -> (N, K): w = d * (sc & 15) * q - dmin * (sc >> 4) in fp32
+    (dl = d * scale and ml = dmin * min first, as the published decoder forms them),
+    rounded once to out_dtype."""
+    N, NB, _ = blocks.shape
+    byte_idx, shift, sub = q2k_element_maps()
+    qs = blocks[:, :, 16:80]
+    q = ((qs[:, :, byte_idx] >> shift) & 3).astype(F32)  # (N, NB, 256)
+    scb = blocks[:, :, :16][:, :, sub]
+    d = blocks[:, :, 80:82].copy().view(F16).astype(F32)  # (N, NB, 1)
+    dmin = blocks[:, :, 82:84].copy().view(F16).astype(F32)
+    dl = (d * (scb & 15).astype(F32)).astype(F32)
+    ml = (dmin * (scb >> 4).astype(F32)).astype(F32)
+    w = ((dl * q).astype(F32) - ml).astype(F32)
+    return w.reshape(N, NB * 256).astype(out_dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -274,3 +274,112 @@ def test_g128_rtn_closed_form_and_nearest_codes():
     N, K = 4096, 4096
     assert (wm.nbytes / w.size, sb.nbytes / w.size) == (0.5, 4 / 128)
     assert (N * K // 2 + N * K // 128 * 4) / (N * K) == 0.53125
+
+
+# ---------------------------------------------------------------------------
+# GGUF Q2_K super-blocks (ggml block_q2_K)
+# ---------------------------------------------------------------------------
+def _published_q2k_decode(block: bytes) -> list:
+    """ggml's dequantize_row_q2_K for one block, written as its nested loops: two
+    halves of 128 elements, each reading 32 qs bytes at shifts 0, 2, 4, 6, sixteen
+    elements per scale byte."""
+    sc, qs = block[:16], block[16:80]
+    d = float(np.frombuffer(block[80:82], np.float16)[0])
+    dmin = float(np.frombuffer(block[82:84], np.float16)[0])
+    out, is_ = [], 0
+    for n in (0, 128):
+        q = qs[n // 4:n // 4 + 32]
+        for shift in (0, 2, 4, 6):
+            for half in (0, 16):
+                s = sc[is_]
+                is_ += 1
+                dl, ml = np.float32(d) * np.float32(s & 0xF), np.float32(dmin) * np.float32(s >> 4)
+                for l in range(16):
+                    out.append(np.float32(dl * np.float32((q[half + l] >> shift) & 3)) - ml)
+    return out
+
+
+def test_q2k_decoder_matches_published_loop_on_a_hand_assembled_block():
+    rng = np.random.default_rng(7)
+    blk = bytearray(84)
+    blk[:16] = bytes((s % 16) | (((7 * s + 3) % 16) << 4) for s in range(16))
+    blk[16:80] = rng.integers(0, 256, 64, dtype=np.uint8).tobytes()
+    blk[80:82] = np.float16(0.0371).tobytes()
+    blk[82:84] = np.float16(0.0113).tobytes()
+    want = np.array(_published_q2k_decode(bytes(blk)), np.float32)
+    got = fm.dequantize_q2_k_gguf(np.frombuffer(bytes(blk), np.uint8).reshape(1, 1, 84), np.float32)[0]
+    assert np.array_equal(got, want)
+    # element 0 is bits 0-1 of qs[0] with scale byte 0; element 37 = 32 * 1 + 5 is bits 2-3 of qs[5]
+    # with scale byte 2; element 200 = 128 + 32 * 2 + 8 is bits 4-5 of qs[40] with scale byte 12
+    d16, m16 = np.float32(np.float16(0.0371)), np.float32(np.float16(0.0113))
+    for e, byte, shift, s in ((0, 0, 0, 0), (37, 5, 2, 2), (200, 40, 4, 12)):
+        q = (blk[16 + byte] >> shift) & 3
+        val = np.float32(d16 * np.float32(blk[s] & 15)) * np.float32(q) - np.float32(m16 * np.float32(blk[s] >> 4))
+        assert got[e] == val, e
+
+
+def test_q2k_element_map_planted_mistake_is_caught():
+    """A decoder that swaps the roles of j and l (element 128h + 4l + j) differs from the
+    published loop on a random block."""
+    rng = np.random.default_rng(8)
+    blk = np.zeros(84, np.uint8)
+    blk[:16] = rng.integers(0, 256, 16)
+    blk[16:80] = rng.integers(0, 256, 64)
+    blk[80:82] = np.frombuffer(np.float16(0.05).tobytes(), np.uint8)
+    want = np.array(_published_q2k_decode(blk.tobytes()), np.float32)
+    e = np.arange(256)
+    wrong_q = (blk[16 + 32 * (e // 128) + (e % 128) // 4] >> (2 * (e % 4))) & 3
+    wrong = np.float32(0.05) * (blk[:16][e // 16] & 15).astype(np.float32) * wrong_q
+    assert not np.allclose(wrong.astype(np.float32), want)
+
+
+def _q2k_lattice(rng, N, NB):
+    """Weights that sit exactly on a Q2_K lattice the encoder must reproduce: every block has
+    a sub-block with scale code 15 and one with min code 15, every sub-block holds codes 0 and 3."""
+    d = rng.uniform(2.0 ** -8, 2.0 ** -7, (N, NB)).astype(F16).astype(F32)
+    dmin = rng.uniform(2.0 ** -8, 2.0 ** -7, (N, NB)).astype(F16).astype(F32)
+    sc = rng.integers(1, 16, (N, NB, 16))
+    mc = rng.integers(0, 16, (N, NB, 16))
+    sc[..., 0] = 15
+    mc[..., 1] = 15
+    q = rng.integers(0, 4, (N, NB, 16, 16))
+    q[..., 0] = 0
+    q[..., 1] = 3
+    w = (d[..., None, None] * sc[..., None] * q - (dmin[..., None] * mc)[..., None]).astype(F32)
+    return w.reshape(N, NB * 256), d, dmin, sc, mc, q
+
+
+def test_q2k_lattice_round_trip_and_bytes_per_weight():
+    rng = np.random.default_rng(9)
+    w, d, dmin, sc, mc, q = _q2k_lattice(rng, 6, 3)
+    blocks = fm.pack_q2_k_gguf(w)
+    assert blocks.shape == (6, 3, 84) and blocks.nbytes / w.size == 0.328125
+    assert np.array_equal(blocks[..., 80:82].copy().view(F16)[..., 0].astype(F32), d)
+    assert np.array_equal(blocks[..., 82:84].copy().view(F16)[..., 0].astype(F32), dmin)
+    assert np.array_equal(blocks[..., :16], (sc | (mc << 4)).astype(np.uint8))
+    assert np.array_equal(fm.dequantize_q2_k_gguf(blocks, F32), w)
+    # the C4 shapes: 11008 x 4096 and 4096 x 11008 hold 14,794,752 bytes each
+    assert 11008 * (4096 // 256) * 84 == 4096 * (11008 // 256) * 84 == 14794752
+
+
+def test_q2k_rtn_codes_are_nearest_with_the_quantized_scales():
+    rng = np.random.default_rng(10)
+    w = (rng.standard_normal((4, 512)) * 0.02).astype(F16)
+    blocks = fm.pack_q2_k_gguf(w)
+    deq = fm.dequantize_q2_k_gguf(blocks, F32).reshape(4, 2, 16, 16)
+    scb = blocks[..., :16]
+    d = blocks[..., 80:82].copy().view(F16).astype(F32)
+    dmin = blocks[..., 82:84].copy().view(F16).astype(F32)
+    dl = d * (scb & 15)
+    ml = dmin * (scb >> 4)
+    # every weight decodes to a lattice point of its sub-block no farther than any other code's
+    lattice = dl[..., None] * np.arange(4, dtype=F32) - ml[..., None]  # (4, 2, 16, 4)
+    err = np.abs(w.astype(F32).reshape(4, 2, 16, 16)[..., None] - lattice[..., None, :])
+    best = err.min(-1)
+    got = np.abs(w.astype(F32).reshape(4, 2, 16, 16) - deq)
+    assert np.all(got <= best + 1e-6)
+    # the super-block scales are the fp16 maxima over sub-blocks / 15
+    wr = w.astype(F32).reshape(4, 2, 16, 16)
+    mn = np.minimum(wr.min(-1), 0)
+    assert np.array_equal(d[..., 0], (((wr.max(-1) - mn) / F32(3)).astype(F32).max(-1) / F32(15)).astype(F16)
+                          .astype(F32))
