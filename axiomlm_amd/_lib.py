@@ -139,6 +139,7 @@ class RunnerDesc(ctypes.Structure):
         ("k_cache", ctypes.POINTER(c_void_p)), ("v_cache", ctypes.POINTER(c_void_p)),
         ("k_scales", ctypes.POINTER(c_void_p)), ("v_scales", ctypes.POINTER(c_void_p)),
         ("max_tokens", c_int), ("layout", c_int), ("group_size", c_int),
+        ("qkv_format", c_int), ("o_format", c_int), ("gu_format", c_int), ("down_format", c_int),
     ]
 
 

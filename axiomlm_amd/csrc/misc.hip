@@ -284,6 +284,18 @@ int launch_add_rmsnorm(f16* x, const f16* r, const f16* w, f16* y, int rows, int
     hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, r, w, y, D, eps);
   return 0;
 }
+namespace {
+// x[i] = fp16(x[i] + y[i]): the residual add of a projection computed apart from its GEMV.
+__global__ void resid_add_kernel(f16* __restrict__ x, const f16* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = f2h(add_rn(h2f(x[i]), h2f(y[i])));
+}
+}  // namespace
+
+int launch_resid_add(f16* x, const f16* y, long n, hipStream_t s) {
+  hipLaunchKernelGGL(resid_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+  return 0;
+}
 int launch_swiglu(const f16* gu, f16* y, int rows, int H, hipStream_t s) {
   const long n = (long)rows * H;
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gu, y, rows, H);
@@ -306,8 +318,11 @@ int launch_embed_q8(const uint8_t* wq, const f16* sb, const int64_t* tokens, con
 
 int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
                    const f16* ln_w, float eps, hipStream_t s) {
-  for (int m0 = 0; m0 < M; m0 += 4) {
-    const int mc = (M - m0) < 4 ? (M - m0) : 4;
+  // Up to four rows per launch, fewer when their fp32 staging would not fit in LDS.
+  int rows_max = 4;
+  while (rows_max > 1 && (size_t)rows_max * K * sizeof(float) > 150 * 1024) --rows_max;
+  for (int m0 = 0; m0 < M; m0 += rows_max) {
+    const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
     const size_t smem = (size_t)mc * K * sizeof(float);
     if (smem > 150 * 1024) {
       axm_set_error("q8 gemv: K=%d too large for LDS staging", K);

@@ -166,6 +166,7 @@ struct Mat {
   void* sb16 = nullptr;
   int N = 0, K = 0;
   int g128 = 0;  // one (scale, bias) per 128 columns (tile16 copy only)
+  int fmt = 0;   // 0: MARLIN Q4 (w int32 [N/8][K/64][32][2]); 1: Q8_G64 (w uint8 [N][K], sb fp16 [N][K/64][2])
 };
 
 // Prologue / epilogue settings shared by both GEMV paths.
@@ -277,6 +278,7 @@ struct axm_runner {
   f16* logits = nullptr;
   f16* norm = nullptr;
   f16* qkvbuf = nullptr;                 // [T][qkv_dim] (multi-token paths)
+  f16* q8tmp = nullptr;                  // [T][max(D, 2H)] outputs of Q8_G64 GEMVs before their epilogue
   int* tree_pos = nullptr;               // [kMaxVerify]
   unsigned long long* tree_mask = nullptr;  // [kMaxVerify]
   float* ws = nullptr;
@@ -308,7 +310,7 @@ struct axm_runner {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
     void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys, parts_o,
-                    qkvbuf, tree_pos, tree_mask, p_layers, p_bar, p_head_cnt, p_tok_next, p_err};
+                    qkvbuf, q8tmp, tree_pos, tree_mask, p_layers, p_bar, p_head_cnt, p_tok_next, p_err};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     if (p_err_host) (void)hipHostFree(p_err_host);
@@ -324,7 +326,7 @@ struct axm_runner {
   void setup_persistent() {
     if (!kPersistEnabled) return;
     if (m_qkv.empty() || m_qkv[0].w16 == nullptr || d.kv_dtype != AXM_KV_FP16 || d.lm_head_format != 0 ||
-        d.group_size == 128 ||
+        d.group_size == 128 || d.qkv_format != 0 || d.o_format != 0 || d.gu_format != 0 || d.down_format != 0 ||
         m_lmh.w16 == nullptr)
       return;
     if (persist_check(d.d_model, d.hidden_dim, d.n_head, d.head_dim, d.vocab_size, &p_grid, &p_smem) != 0) return;
@@ -469,10 +471,21 @@ struct axm_runner {
         a.kv_stride_h = d.head_dim;
         a.max_seq = 1;
       }
-      int rc = run_gemv(m_qkv[i], Q4_EPI_QKV_ROPE, qkv_dim, a, 1, s);
-      if (rc) return rc;
-      if (d.kv_dtype != AXM_KV_FP16)
+      int rc = 0;
+      if (m_qkv[i].fmt == 1) {
+        // Q8_G64 QKV: GEMV (+ bias) into qkvbuf, RoPE of q / k into q / kvst, then the slot write.
+        rc = launch_q8_gemv(x, (const uint8_t*)m_qkv[i].w, (const f16*)m_qkv[i].sb, a.bias, qkvbuf, 1, D, qkv_dim,
+                            a.ln_w, d.eps, s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, 1), dim3(256), 0, s, qkvbuf, q_dim,
+                           kv_dim, d.head_dim, d.freqs, params + P_ROPE, q, kvst);
         launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
+      } else {
+        rc = run_gemv(m_qkv[i], Q4_EPI_QKV_ROPE, qkv_dim, a, 1, s);
+        if (rc) return rc;
+        if (d.kv_dtype != AXM_KV_FP16)
+          launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
+      }
       // 2. attention over slots [0, active_len); with parts_ok the split
       // partials are merged while the O projection stages its activations.
       const bool merge_in_o = parts_ok && n_splits > 1;
@@ -494,7 +507,7 @@ struct axm_runner {
         o.n_parts = n_splits;
         o.parts_hd = d.head_dim;
       }
-      rc = run_gemv(m_o[i], Q4_EPI_RESID, D, o, 1, s);
+      rc = gemv(m_o[i], Q4_EPI_RESID, D, o, 1, s);
       if (rc) return rc;
       // 4. gate/up with RMSNorm prologue and SwiGLU epilogue.
       GemvCall g{};
@@ -505,7 +518,7 @@ struct axm_runner {
       g.ln_w = (const f16*)ln2[i];
       g.eps = d.eps;
       g.pair_rows = H;
-      rc = run_gemv(m_gu[i], Q4_EPI_SWIGLU, H, g, 1, s);
+      rc = gemv(m_gu[i], Q4_EPI_SWIGLU, H, g, 1, s);
       if (rc) return rc;
       // 5. down projection, residual add.
       GemvCall dn{};
@@ -513,7 +526,7 @@ struct axm_runner {
       dn.ldx = H;
       dn.resid = x;
       dn.ldr = D;
-      rc = run_gemv(m_dn[i], Q4_EPI_RESID, D, dn, 1, s);
+      rc = gemv(m_dn[i], Q4_EPI_RESID, D, dn, 1, s);
       if (rc) return rc;
     }
     // Final RMSNorm + lm_head (+ per-tile greedy argmax keys).
@@ -536,6 +549,57 @@ struct axm_runner {
       if (rc) return rc;
     }
     return 0;
+  }
+
+  // A Q8_G64 matrix: the Q8 GEMV (RMSNorm prologue, bias) followed by the
+  // epilogue as separate launches with the rounding of the fused epilogues
+  // (residual add in fp16, silu(fp16 g) * fp16 u).  Activation and output rows
+  // are contiguous ([M][K] in, [M][N] out), as every caller lays them out.
+  int run_q8(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
+    if (c.x_parts != nullptr || c.argmax_keys != nullptr || epi == Q4_EPI_QKV_ROPE || c.ldx != m.K) {
+      axm_set_error("runner: unsupported call on a Q8_G64 matrix (epilogue %d)", epi);
+      return -2;
+    }
+    const uint8_t* w = (const uint8_t*)m.w;
+    const f16* sb = (const f16*)m.sb;
+    const f16* xin = c.x;
+    const f16* ln = c.ln_w;
+    if (c.x_norm_out != nullptr && ln != nullptr) {
+      launch_rmsnorm(c.x, ln, c.x_norm_out, M, m.K, c.eps, s);
+      xin = c.x_norm_out;
+      ln = nullptr;
+    }
+    int rc = 0;
+    if (epi == Q4_EPI_STORE) {
+      if (c.ldy != out_rows) {
+        axm_set_error("runner: a Q8 store needs contiguous output rows");
+        return -2;
+      }
+      return launch_q8_gemv(xin, w, sb, c.bias, c.y, M, m.K, out_rows, ln, c.eps, s);
+    }
+    if (epi == Q4_EPI_SWIGLU) {
+      if (c.ldy != out_rows) {
+        axm_set_error("runner: a Q8 SwiGLU needs contiguous output rows");
+        return -2;
+      }
+      rc = launch_q8_gemv(xin, w, sb, nullptr, q8tmp, M, m.K, 2 * out_rows, ln, c.eps, s);
+      if (rc) return rc;
+      return launch_swiglu(q8tmp, c.y, M, out_rows, s);
+    }
+    // Q4_EPI_RESID
+    if (c.ldr != out_rows) {
+      axm_set_error("runner: a Q8 residual needs contiguous rows");
+      return -2;
+    }
+    rc = launch_q8_gemv(xin, w, sb, nullptr, q8tmp, M, m.K, out_rows, ln, c.eps, s);
+    if (rc) return rc;
+    launch_resid_add(c.resid, q8tmp, (long)M * out_rows, s);
+    if (c.post_ln_w != nullptr) launch_rmsnorm(c.resid, c.post_ln_w, c.post_norm_out, M, out_rows, c.eps, s);
+    return 0;
+  }
+
+  int gemv(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
+    return m.fmt == 1 ? run_q8(m, epi, out_rows, c, M, s) : run_gemv(m, epi, out_rows, c, M, s);
   }
 
   // GEMV over T token rows in launches of at most 4 rows.
@@ -585,7 +649,9 @@ struct axm_runner {
       if (c.y) cc.y = c.y + (size_t)t0 * c.ldy;
       if (c.resid) cc.resid = c.resid + (size_t)t0 * c.ldr;
       if (c.x_norm_out) cc.x_norm_out = c.x_norm_out + (size_t)t0 * c.ldx;
-      const int rc = run_gemv(m, epi, out_rows, cc, mc, s);
+      GemvCall cq = cc;
+      if (m.fmt == 1) cq.post_ln_w = nullptr;  // normalized once below
+      const int rc = gemv(m, epi, out_rows, cq, mc, s);
       if (rc) return rc;
     }
     if (c.post_ln_w != nullptr) return launch_rmsnorm(c.resid, c.post_ln_w, c.post_norm_out, T, out_rows, c.eps, s);
@@ -727,6 +793,10 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
   AXM_CHECK_ARG(d.lm_head_format == 1 || d.lm_head_sb, -1, "runner_create: lm_head scales missing");
   AXM_CHECK_ARG(d.group_size == 0 || d.group_size == 64 || d.group_size == 128, -1,
                 "runner_create: group_size %d must be 64 or 128", d.group_size);
+  for (int f : {d.qkv_format, d.o_format, d.gu_format, d.down_format})
+    AXM_CHECK_ARG(f == 0 || f == 1, -1, "runner_create: layer matrix format %d must be 0 (MARLIN Q4) or 1 (Q8_G64)", f);
+  AXM_CHECK_ARG(d.qkv_format == 0 || (d.n_head + 2 * d.n_kv_head) * d.head_dim % 8 == 0, -1,
+                "runner_create: a Q8_G64 QKV needs q, k and v rows in multiples of 8");
   AXM_CHECK_ARG(d.group_size != 128 ||
                     (d.layout != 1 && d.d_model % 128 == 0 && d.hidden_dim % 128 == 0 &&
                      (d.n_head * d.head_dim) % 128 == 0 && d.hidden_dim % 16 == 0 && d.hidden_dim <= kTile16MaxK &&
@@ -767,10 +837,10 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
   {
     const int qkv_rows = (d.n_head + 2 * d.n_kv_head) * d.head_dim;
     for (int i = 0; i < L; ++i) {
-      r->m_qkv.push_back(Mat{r->qkv_w[i], r->qkv_sb[i], nullptr, nullptr, qkv_rows, d.d_model});
-      r->m_o.push_back(Mat{r->o_w[i], r->o_sb[i], nullptr, nullptr, d.d_model, d.n_head * d.head_dim});
-      r->m_gu.push_back(Mat{r->gu_w[i], r->gu_sb[i], nullptr, nullptr, 2 * d.hidden_dim, d.d_model});
-      r->m_dn.push_back(Mat{r->dn_w[i], r->dn_sb[i], nullptr, nullptr, d.d_model, d.hidden_dim});
+      r->m_qkv.push_back(Mat{r->qkv_w[i], r->qkv_sb[i], nullptr, nullptr, qkv_rows, d.d_model, 0, d.qkv_format});
+      r->m_o.push_back(Mat{r->o_w[i], r->o_sb[i], nullptr, nullptr, d.d_model, d.n_head * d.head_dim, 0, d.o_format});
+      r->m_gu.push_back(Mat{r->gu_w[i], r->gu_sb[i], nullptr, nullptr, 2 * d.hidden_dim, d.d_model, 0, d.gu_format});
+      r->m_dn.push_back(Mat{r->dn_w[i], r->dn_sb[i], nullptr, nullptr, d.d_model, d.hidden_dim, 0, d.down_format});
     }
     r->m_lmh = Mat{d.lm_head_w, d.lm_head_sb, nullptr, nullptr, d.vocab_size, d.d_model};
     // The gate/up pair shares a tile16 boundary when H % 16 == 0, and the tile16
@@ -781,10 +851,9 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
     if (t16) {
       int rc = 0;
       for (int i = 0; i < L && rc == 0; ++i) {
-        rc = rc ? rc : r->make_tile16(r->m_qkv[i]);
-        rc = rc ? rc : r->make_tile16(r->m_o[i]);
-        rc = rc ? rc : r->make_tile16(r->m_gu[i]);
-        rc = rc ? rc : r->make_tile16(r->m_dn[i]);
+        // Q8_G64 matrices keep the reference layout (the Q8 GEMV streams it).
+        for (Mat* m : {&r->m_qkv[i], &r->m_o[i], &r->m_gu[i], &r->m_dn[i]})
+          if (m->fmt == 0) rc = rc ? rc : r->make_tile16(*m);
       }
       if (rc == 0 && d.lm_head_format == 0) rc = r->make_tile16(r->m_lmh);
       if (rc != 0 || hipDeviceSynchronize() != hipSuccess) {
@@ -824,6 +893,7 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
       {(void**)&r->parts_o, attn_parts_bytes(1, d.n_head, d.head_dim)},
       {(void**)&r->argmax_keys, (size_t)((d.vocab_size + 7) / 8) * sizeof(unsigned long long)},
       {(void**)&r->qkvbuf, (size_t)T * r->qkv_dim * sizeof(f16)},
+      {(void**)&r->q8tmp, (size_t)T * (2 * d.hidden_dim > d.d_model ? 2 * d.hidden_dim : d.d_model) * sizeof(f16)},
       {(void**)&r->tree_pos, kMaxVerify * sizeof(int)},
       {(void**)&r->tree_mask, kMaxVerify * sizeof(unsigned long long)},
   };

@@ -10,8 +10,10 @@ Constructor arguments and methods follow the reference pybind class
                           k_scales=None, v_scales=None, kv_dtype="fp16")
 
 Formats are detected from the packed tensors as the reference does
-(mps_kernels.mm:3055-3068, 3149-3157): a 4-D lm_head is MARLIN Q4, a 2-D int32
-one is Q8_G64; a 2-D int32 ``wte_p`` selects the Q8 embedding gather.  The
+(mps_kernels.mm:3055-3068, 3149-3157): a 4-D pack is MARLIN Q4, a 2-D int32 one
+(K/4 words per row) is Q8_G64 -- per kind of layer matrix and for the lm_head,
+which covers the modes "q4", "q4_rtn", "q4_k_m" (Q8 w_down and lm_head) and "q8";
+a 2-D int32 ``wte_p`` selects the Q8 embedding gather.  The
 keyword arguments after ``wte_s`` are this build's additions: quantized (FP8 /
 INT4) KV caches inside the captured step, and ``layout`` -- "tile16" (default)
 re-tiles every MARLIN matrix once, bit-exactly, for the matrix-core GEMV;
@@ -45,14 +47,32 @@ def _p(t):
     return None if t is None or (isinstance(t, torch.Tensor) and t.numel() == 0) else t.data_ptr()
 
 
+def _packed_k(p) -> int:
+    """Input width of a packed matrix: MARLIN Q4 int32 [N/8][K/64][32][2], or Q8_G64 codes as
+    int32 [N][K/4] (the reference packer's view) or uint8 [N][K]."""
+    if p.dim() == 4:
+        return int(p.shape[1]) * 64
+    if p.dim() == 2:
+        return int(p.shape[1]) * (4 if p.element_size() == 4 else 1)
+    raise RuntimeError(f"QuantizedDecodeRunner: unsupported packed weight of shape {tuple(p.shape)}")
+
+
+def _matrix_format(p, K: int, name: str) -> int:
+    """0 for MARLIN Q4, 1 for Q8_G64 (the shape test of mps_kernels.mm:3055-3068)."""
+    if p.dim() == 4 and _packed_k(p) == K:
+        return 0
+    if p.dim() == 2 and _packed_k(p) == K:
+        return 1
+    raise RuntimeError(f"QuantizedDecodeRunner: the {name} pack of shape {tuple(p.shape)} is neither MARLIN Q4 nor "
+                       f"Q8_G64 for K={K} (the legacy Q4_G64 layout of mode 'q4_legacy' is not on this runner)")
+
+
 class QuantizedDecodeRunner:
     def __init__(self, wte_emb, lmh_packed, lmh_sb, freqs_r, ln1_ws, c_attn_p, c_attn_s, c_proj_p, c_proj_s,
                  ln2_ws, gate_up_p, gate_up_s, w_down_p, w_down_s, lnf_w, k_cs, v_cs, n_h, n_kvh, hd, use_q4,
                  epsilon, c_attn_bs=(), vocab_sz=-1, wte_p=None, wte_s=None, k_scales=None, v_scales=None,
                  kv_dtype="fp16", max_tokens: int = 32, layout: str = "tile16"):
         L = len(ln1_ws)
-        if not use_q4 or c_attn_p[0].dim() != 4:
-            raise RuntimeError("QuantizedDecodeRunner on MI355X supports MARLIN Q4 layer weights")
         dev = lmh_packed.device
         _lib.require_gpu(lmh_packed, "QuantizedDecodeRunner")
         h16 = lambda t: t.to(device=dev, dtype=torch.float16).contiguous()  # noqa: E731
@@ -85,8 +105,10 @@ class QuantizedDecodeRunner:
             vocab_sz = wte.shape[0] if lmh_fmt == 0 else lmh_packed.shape[0]
         self.vocab_size = int(vocab_sz)
         self.d_model = int(n_h * hd)
-        # 64-column code blocks of w_down (its scales hold K / 128 groups in a group-128 pack)
-        self.hidden_dim = int(w_down_p[0].shape[1] * 64)
+        # MLP width from the gate|up rows (MARLIN packs hold N/8 tiles of 8 rows; Q8_G64 one
+        # row per output); w_down's packed input width is checked against it below
+        gu0 = gate_up_p[0]
+        self.hidden_dim = int(gu0.shape[0]) * (8 if gu0.dim() == 4 else 1) // 2
         kv_code = KV_CODES[kv_dtype]
         self.kv_dtype = kv_dtype
         self.max_seq_len = int(k_cs[0].shape[-2])
@@ -128,14 +150,28 @@ class QuantizedDecodeRunner:
         # group 64 (reference) or 128, from the packed scales; one size for every Q4 matrix
         from .kernels.quant import marlin_group_size
 
-        packs = list(c_attn_p) + list(c_proj_p) + list(gate_up_p) + list(w_down_p)
-        scales = list(c_attn_s) + list(c_proj_s) + list(gate_up_s) + list(w_down_s)
+        # per kind of layer matrix: MARLIN Q4 (4-D pack) or Q8_G64 (2-D), as the reference runner
+        # dispatches on the packed shape (mps_kernels.mm:3055-3068); one format per kind
+        fmts = []
+        for name, ps, K in (("c_attn", c_attn_p, self.d_model), ("c_proj", c_proj_p, self.d_model),
+                            ("gate_up", gate_up_p, self.d_model), ("w_down", w_down_p, self.hidden_dim)):
+            kinds = {_matrix_format(p, K, name) for p in ps}
+            if len(kinds) != 1:
+                raise RuntimeError(f"QuantizedDecodeRunner: {name} packs mix MARLIN Q4 and Q8_G64 layers")
+            fmts.append(kinds.pop())
+        d.qkv_format, d.o_format, d.gu_format, d.down_format = fmts
+        self.layer_formats = tuple("q8_g64" if f else "q4_marlin" for f in fmts)
+        packs, scales = [], []
+        for f, ps, ss in zip(fmts, (c_attn_p, c_proj_p, gate_up_p, w_down_p), (c_attn_s, c_proj_s, gate_up_s, w_down_s)):
+            if f == 0:
+                packs += list(ps)
+                scales += list(ss)
         groups = {marlin_group_size(p, s) for p, s in zip(packs, scales)}
         if lmh_fmt == 0:
             groups.add(marlin_group_size(lmh_packed, lmh_sb))
-        if len(groups) != 1:
+        if len(groups) > 1:
             raise RuntimeError(f"QuantizedDecodeRunner: mixed MARLIN group sizes {sorted(groups)}")
-        self.group_size = groups.pop()
+        self.group_size = groups.pop() if groups else 64
         d.group_size = self.group_size
         if layout not in ("tile16", "marlin"):
             raise ValueError(f"layout must be 'tile16' or 'marlin', got {layout!r}")

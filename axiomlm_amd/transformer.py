@@ -109,8 +109,12 @@ class Transformer:
 
     # -- transformer.py:276-320 ---------------------------------------------
     def quantize(self, mode: str | None = "q4", lm_head_q8: bool | None = None) -> "Transformer":
-        if mode not in (None, "q4", "q4_rtn"):
-            raise ValueError(f"quant mode {mode!r} is not on the MI355X decode path (q4, q4_rtn)")
+        """Modes of the quantized decode runner (transformer.py:282-289): "q4" (MARLIN Q4 with the
+        importance-weighted MSE clip search), "q4_rtn" (round to nearest), "q4_k_m" ("q4" with
+        Q8_G64 w_down and lm_head), "q8" (Q8_G64 everywhere).  The reference's "q4_legacy",
+        "q2_k" and "ternary" modes do not run through its decode runner and are not modes here."""
+        if mode not in (None, "q4", "q4_rtn", "q4_k_m", "q8"):
+            raise ValueError(f"quant mode {mode!r} is not on the MI355X decode path (q4, q4_rtn, q4_k_m, q8)")
         self._quant_mode = mode
         self._lm_head_q8 = lm_head_q8
         self._quant_weights_cache = None
@@ -128,12 +132,16 @@ class Transformer:
         if self._quant_mode is None:
             raise RuntimeError("call quantize() first")
         c = self.config
-        mse = self._quant_mode == "q4"
-        use_q8_lm = bool(self._lm_head_q8) if self._lm_head_q8 is not None else bool(c.tie_word_embeddings)
+        mode = self._quant_mode
+        mse = mode in ("q4", "q4_k_m")
+        # transformer.py:840-847: Q8 lm_head for q4_k_m / q8 or tied embeddings unless overridden
+        use_q8_lm = (bool(self._lm_head_q8) if self._lm_head_q8 is not None
+                     else (mode in ("q4_k_m", "q8") or bool(c.tie_word_embeddings)))
+        use_q8_down = mode in ("q4_k_m", "q8")
 
         def pack(w, imp=None, q8=False):
             w = w.to(self.device)
-            if q8:
+            if q8 or mode == "q8":
                 return pack_linear_q8_g64(w)
             if not mse:
                 return pack_linear_q4_marlin(w, clip_search=False)
@@ -165,8 +173,8 @@ class Transformer:
             p, s = pack(torch.cat([wg, wu], dim=0), ln2)
             q["gu_p"].append(p)
             q["gu_s"].append(s)
-            imp_sw = (wg.float().norm(dim=1) * wu.float().norm(dim=1)) if mse else None
-            p, s = pack(self.w[pre + "mlp.w_down.weight"], imp_sw)
+            imp_sw = (wg.float().norm(dim=1) * wu.float().norm(dim=1)) if (mse and not use_q8_down) else None
+            p, s = pack(self.w[pre + "mlp.w_down.weight"], imp_sw, use_q8_down)
             q["wd_p"].append(p)
             q["wd_s"].append(s)
         self._quant_weights_cache = q
@@ -190,7 +198,8 @@ class Transformer:
         self._runner = QuantizedDecodeRunner(
             None, qw["lmh_p"], qw["lmh_sb"], self.freqs_real.to(self.device), ln1, qw["c_attn_p"], qw["c_attn_s"],
             qw["c_proj_p"], qw["c_proj_s"], ln2, qw["gu_p"], qw["gu_s"], qw["wd_p"], qw["wd_s"], lnf,
-            cache0.k_caches, cache0.v_caches, c.n_head, c.kv_heads, c.head_dim, True, c.rms_norm_eps, biases,
+            cache0.k_caches, cache0.v_caches, c.n_head, c.kv_heads, c.head_dim, self._quant_mode != "q8",
+            c.rms_norm_eps, biases,
             c.vocab_size, wte_p=qw["wte_p"], wte_s=qw["wte_sb"], k_scales=cache0.k_scales, v_scales=cache0.v_scales,
             kv_dtype=cache0.cache_dtype, max_tokens=64)
         self._runner_key = key

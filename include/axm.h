@@ -275,6 +275,11 @@ typedef struct axm_runner_desc {
   int layout;     /* 0: re-tile weights for the matrix cores (default); 1: stream the reference layout */
   int group_size; /* MARLIN Q4 packs (layers and a Q4 lm_head): 64 (reference), or 128 (tile16 layout only);
                      0 means 64 */
+  /* Format of each kind of layer matrix, as the reference runner dispatches it from the
+   * packed shape (mps_kernels.mm:3055-3068): 0 = MARLIN Q4 (4-D pack), 1 = Q8_G64 (uint8
+   * [N][K], sb fp16 [N][K/64][2]).  Mode "q4_k_m" packs down as Q8, mode "q8" every matrix
+   * (transformer.py:840-847, 897-903). */
+  int qkv_format, o_format, gu_format, down_format;
 } axm_runner_desc;
 
 typedef struct axm_runner* axm_runner_t;

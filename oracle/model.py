@@ -487,19 +487,24 @@ def pack_model(cfg: OracleConfig, W, mode: str = "q4") -> OracleWeights:
     :959-963).  mode "q4" = MSE clip search with the reference importance vectors
     (|ln_f| for lm_head, |ln_1| for c_attn, |ln_2| for gate|up, row-norm product of
     w_gate and w_up for w_down, none for c_proj; :876-948); "q4_rtn" = round to nearest;
-    "q4_g128" = round to nearest with one (scale, bias) per 128 columns."""
-    mse = mode == "q4"
-    if mode not in ("q4", "q4_rtn", "q4_g128"):
+    "q4_k_m" = "q4" with Q8_G64 w_down and lm_head (:840-847; no importance vector for
+    w_down, :931-941); "q8" = every matrix Q8_G64; "q4_g128" = round to nearest with one
+    (scale, bias) per 128 columns (this build's variant).  Q8_G64 packs are uint8 [N][K]."""
+    if mode not in ("q4", "q4_rtn", "q4_g128", "q4_k_m", "q8"):
         raise ValueError(f"unsupported mode {mode!r}")
+    mse = mode in ("q4", "q4_k_m")
+    q8_down = mode in ("q4_k_m", "q8")
 
-    def pack(w, imp):
+    def pack(w, imp, q8=False):
+        if q8 or mode == "q8":
+            return fm.pack_linear_q8_g64(w)
         if mode == "q4_g128":  # this build's group-128 variant (round to nearest)
             return fm.pack_linear_q4_marlin_g128(w)
         return fm.pack_linear_q4_marlin(w, clip_search=mse, col_importance=imp if mse else None)
 
     a = lambda v: np.abs(v.astype(F32))  # noqa: E731
     wte_p, wte_sb = fm.pack_linear_q8_g64(W["wte"])
-    lmh_p, lmh_sb = pack(W["lm_head"], a(W["lnf"]))
+    lmh_p, lmh_sb = pack(W["lm_head"], a(W["lnf"]), q8=mode in ("q4_k_m", "q8"))
     ow = OracleWeights(wte_p, wte_sb, lmh_p, lmh_sb, [], [], W["lnf"], [], [], [], [], [], [], [], [])
     for L in W["layers"]:
         ow.ln1.append(L["ln1"])
@@ -514,7 +519,7 @@ def pack_model(cfg: OracleConfig, W, mode: str = "q4") -> OracleWeights:
         ow.gu_p.append(p)
         ow.gu_s.append(s)
         imp_sw = (np.linalg.norm(L["w_gate"].astype(F32), axis=1) * np.linalg.norm(L["w_up"].astype(F32), axis=1))
-        p, s = pack(L["w_down"], imp_sw)
+        p, s = pack(L["w_down"], imp_sw, q8=q8_down)
         ow.wd_p.append(p)
         ow.wd_s.append(s)
     return ow

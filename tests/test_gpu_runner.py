@@ -39,10 +39,12 @@ def build_runner(cfg, ow, cos, sin, dev, S, kv="fp16", ring=False, layout="tile1
         wte_p = wte_s = None
     else:
         wte_emb, wte_p, wte_s = None, t(ow.wte_p.view(np.int32).reshape(cfg.vocab, -1)), t(ow.wte_sb)
+    # 2-D (Q8_G64) layer packs go in as the reference packer's int32 [N, K/4] view
+    pk = lambda x: t(x.view(np.int32).reshape(x.shape[0], -1) if x.ndim == 2 else x)  # noqa: E731
     r = QuantizedDecodeRunner(
-        wte_emb, t(lmh), t(ow.lmh_sb), freqs, [t(x) for x in ow.ln1], [t(x) for x in ow.c_attn_p],
-        [t(x) for x in ow.c_attn_s], [t(x) for x in ow.c_proj_p], [t(x) for x in ow.c_proj_s],
-        [t(x) for x in ow.ln2], [t(x) for x in ow.gu_p], [t(x) for x in ow.gu_s], [t(x) for x in ow.wd_p],
+        wte_emb, t(lmh), t(ow.lmh_sb), freqs, [t(x) for x in ow.ln1], [pk(x) for x in ow.c_attn_p],
+        [t(x) for x in ow.c_attn_s], [pk(x) for x in ow.c_proj_p], [t(x) for x in ow.c_proj_s],
+        [t(x) for x in ow.ln2], [pk(x) for x in ow.gu_p], [t(x) for x in ow.gu_s], [pk(x) for x in ow.wd_p],
         [t(x) for x in ow.wd_s], t(ow.lnf), cache.k_caches, cache.v_caches, cfg.n_head, cfg.n_kv_head,
         cfg.head_dim, True, cfg.eps, [t(b) for b in ow.c_attn_b], cfg.vocab, wte_p=wte_p, wte_s=wte_s,
         k_scales=cache.k_scales, v_scales=cache.v_scales, kv_dtype=kv, layout=layout, max_tokens=max_tokens)
@@ -697,3 +699,54 @@ def test_runner_verify_step_ring_wrap_gqa_head128(dev, kv):
     if frozen:
         assert list(ocache.last_write[0][0]) == [(seen + t) % S for t in range(T)]
         _check_codes(kv, _code_diffs(kv, ocache), "ring_gqa128")
+
+
+# ---------------------------------------------------------------------------
+# Sibling modes: q4_k_m (Q8_G64 w_down and lm_head) and q8 (Q8_G64 everywhere)
+# ---------------------------------------------------------------------------
+MODE_FORMATS = {"q4_k_m": ("q4_marlin", "q4_marlin", "q4_marlin", "q8_g64"), "q8": ("q8_g64",) * 4}
+
+
+@pytest.mark.parametrize("mode,kv", [("q4_k_m", "fp16"), ("q8", "fp16"), ("q4_k_m", "fp8"), ("q8", "int4")])
+def test_runner_modes_match_oracle(dev, mode, kv):
+    """Modes "q4_k_m" and "q8" (transformer.py:840-847, the runner's per-matrix format
+    dispatch of mps_kernels.mm:3055-3068): 12 decode steps through the captured graph, then
+    verify chains of 3 tokens (decode GEMV rows) and 9 tokens (the multi-token path), each
+    against the oracle, logits <= 1e-2.  Quantized caches are loaded from the GPU into a
+    frozen oracle cache before each comparison, as in test_runner_quantized_kv_matches_oracle."""
+    print(f"[runner_modes] mode={mode} kv={kv}", flush=True)
+    cfg = om.OracleConfig(n_layer=3, n_head=4, n_kv_head=2, d_model=256, hidden=704, vocab=1024, eps=1e-5,
+                          block_size=256)
+    ow = om.pack_model(cfg, om.make_float_weights(cfg, seed=6), mode)
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size)
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, kv)
+    assert runner.layer_formats == MODE_FORMATS[mode]
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv)
+    ocache.frozen = kv != "fp16"
+    rng = np.random.default_rng(16)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, 12).tolist()):
+        got = run_steps(runner, cache, [tok], dev)[0]
+        if ocache.frozen:
+            _load_gpu_cache(ocache, cache)
+        _check_logits(got, model.forward([tok], ocache)[-1], f"{mode} step {i}")
+    for T in (3, 9):
+        seen = cache.total_seen_tokens[0]
+        chain = rng.integers(0, cfg.vocab, T).tolist()
+        g = runner.verify_step(torch.tensor([chain], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
+        if ocache.frozen:
+            _load_gpu_cache(ocache, cache)
+        ref = model.forward(chain, ocache, return_all_logits=True)
+        cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
+        cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
+        for t in range(T):
+            _check_logits(g[t], ref[t], f"{mode} verify T={T} token {t}")
+
+
+def test_runner_rejects_legacy_q4_g64(dev):
+    """The reference's A/B layout Q4_G64 ("q4_legacy") is not on this runner: a clear error."""
+    cfg, ow, cos, sin = c1_model()
+    ow.wd_p = [np.zeros((cfg.d_model, cfg.hidden // 2), np.uint8) for _ in ow.wd_p]
+    with pytest.raises(RuntimeError, match="neither MARLIN Q4 nor Q8_G64"):
+        build_runner(cfg, ow, cos, sin, dev, 32)

@@ -181,3 +181,49 @@ def test_tree_verify_chain_matches_reference(dev):
     assert cache.total_seen_tokens == [35] * cfg.n_layer
     lg = m.forward(torch.tensor([[nodes[3]]], device=dev), kv_caches=cache)[0]
     _check(lg[0, 0].float().cpu().numpy(), ref[35], "after compaction")
+
+
+@pytest.mark.parametrize("mode", ["q4_k_m", "q8"])
+def test_quantize_modes_decode_against_oracle(dev, mode):
+    """quantize("q4_k_m") packs w_down and lm_head as Q8_G64 and the rest as MSE-clipped MARLIN
+    Q4; quantize("q8") packs every matrix Q8_G64 (transformer.py:840-847).  The Q8 packs are
+    byte-identical to the oracle's packer; forward() token by token matches the oracle model
+    running on the packs the GPU produced (logits <= 1e-2)."""
+    from oracle import formats as fm
+
+    print(f"[transformer_modes] {mode}", flush=True)
+    m, cfg = _model(dev)
+    m.quantize(mode)
+    qw = m._ensure_quant_weights()
+    from c1_golden import c1_config
+
+    c = c1_config()
+    W = om.make_float_weights(c, seed=0)
+
+    def host(p):  # Q8 packs as uint8 [N][K] like the oracle's; MARLIN packs unchanged
+        a = p.cpu().numpy()
+        return a.view(np.uint8).reshape(a.shape[0], -1) if a.ndim == 2 else a
+
+    def q8_same(p, s, w):
+        wp, wsb = fm.pack_linear_q8_g64(w)
+        return np.array_equal(host(p), wp) and np.array_equal(s.cpu().numpy().view(np.uint16), wsb.view(np.uint16))
+
+    assert qw["lmh_p"].dim() == 2 and q8_same(qw["lmh_p"], qw["lmh_sb"], W["lm_head"])
+    for i, lw in enumerate(W["layers"]):
+        assert qw["wd_p"][i].dim() == 2 and q8_same(qw["wd_p"][i], qw["wd_s"][i], lw["w_down"])
+        assert (qw["c_attn_p"][i].dim() == 2) == (mode == "q8")
+    ow = om.OracleWeights(host(qw["wte_p"]), qw["wte_sb"].cpu().numpy(), host(qw["lmh_p"]),
+                          qw["lmh_sb"].cpu().numpy(), [lw["ln1"] for lw in W["layers"]],
+                          [lw["ln2"] for lw in W["layers"]], W["lnf"],
+                          [host(p) for p in qw["c_attn_p"]], [s.cpu().numpy() for s in qw["c_attn_s"]],
+                          [host(p) for p in qw["c_proj_p"]], [s.cpu().numpy() for s in qw["c_proj_s"]],
+                          [host(p) for p in qw["gu_p"]], [s.cpu().numpy() for s in qw["gu_s"]],
+                          [host(p) for p in qw["wd_p"]], [s.cpu().numpy() for s in qw["wd_s"]])
+    cos, sin = om.rope_tables(c.head_dim, c.block_size)
+    model = om.OracleModel(c, ow, cos, sin)
+    cache = _cache(cfg, dev)
+    ocache = om.OracleKVCache(128, c.n_layer, c.n_kv_head, c.head_dim)
+    rng = np.random.default_rng(21)
+    for i, tok in enumerate(rng.integers(0, c.vocab, 10).tolist()):
+        got = m.forward(torch.tensor([[tok]], device=dev), kv_caches=cache)[0][0, -1].float().cpu().numpy()
+        _check(got, model.forward([tok], ocache)[-1], f"{mode} token {i}")

@@ -68,8 +68,11 @@ def test_quantize_modes_and_tied_head():
     sd = {"transformer.wte.weight": torch.zeros(128, 64, dtype=torch.float16)}
     m = Transformer(c, sd, device="cpu")
     assert m.w["lm_head.weight"] is m.w["transformer.wte.weight"]  # tied by default
-    with pytest.raises(ValueError):
-        m.quantize("q8")
+    for mode in ("q4", "q4_rtn", "q4_k_m", "q8", None):
+        m.quantize(mode)
+    for mode in ("q4_legacy", "q2_k", "ternary", "int4"):  # not modes of the decode runner
+        with pytest.raises(ValueError):
+            m.quantize(mode)
     m.quantize("q4_rtn")
     with pytest.raises(RuntimeError):
         Transformer(c, sd, device="cpu").forward(torch.zeros(1, 1, dtype=torch.long), kv_caches=None)
