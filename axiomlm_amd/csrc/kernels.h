@@ -23,6 +23,8 @@ int launch_embed_q8(const uint8_t* wq, const f16* sb, const int64_t* tokens, con
 
 // ---- Q8_G64 GEMV (affine 8-bit, group 64), optional fused fp16 RMSNorm -------
 int launch_resid_add(f16* x, const f16* y, long n, hipStream_t s);
+int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
+                    float eps, hipStream_t s);
 int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
                    const f16* ln_w, float eps, hipStream_t s);
 

@@ -267,7 +267,97 @@ __global__ void __launch_bounds__(kQ8Threads)
   }
 }
 
+// fp16 GEMV (the dense layers of the fp16 decode runner):  y[n] = sum_k w[n][k] x[k].
+// Activations (optionally RMS-normalized with the fp16 op order of the quantized
+// paths) are staged in LDS as fp16 pairs; one wave per output row per iteration,
+// each lane streaming 16 bytes (8 weights) per step into v_dot2_f32_f16 with fp32
+// accumulation.
+__global__ void __launch_bounds__(kQ8Threads)
+    f16_gemv_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f16* __restrict__ bias,
+                    f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w, float eps) {
+  extern __shared__ __align__(16) f16 xh[];  // [M][K]
+  __shared__ float red[4];
+  for (int mi = 0; mi < M; ++mi) {
+    const f16* xr = x + (size_t)mi * K;
+    float rinv = 1.f;
+    if (ln_w != nullptr) {
+      float s = 0.f;
+      for (int k = threadIdx.x; k < K; k += kQ8Threads) {
+        const float v = h2f(xr[k]);
+        s += h2f(f2h(v * v));
+      }
+      rinv = rms_inv_fp16(block_sum_256(s, red), K, eps);
+    }
+    for (int k = threadIdx.x; k < K; k += kQ8Threads) {
+      f16 h = xr[k];
+      if (ln_w != nullptr) h = f2h(h2f(f2h(h2f(h) * rinv)) * h2f(ln_w[k]));
+      xh[(size_t)mi * K + k] = h;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n_waves_total = gridDim.x * (kQ8Threads / 64);
+  for (int n = blockIdx.x * (kQ8Threads / 64) + wave; n < N; n += n_waves_total) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const f16* wr = w + (size_t)n * K;
+    for (int k0 = lane * 8; k0 < K; k0 += 64 * 8) {
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + k0);
+      for (int mi = 0; mi < M && mi < 4; ++mi) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xh + (size_t)mi * K + k0);
+        float d = acc[mi];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_fdot2(as_h2(xv[c]), as_h2(wv[c]), d, false);
+        acc[mi] = d;
+      }
+    }
+    for (int mi = 0; mi < M && mi < 4; ++mi) {
+      const float v = wave_sum(acc[mi]);
+      if (lane == 0) {
+        f16 h = f2h(v);
+        if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[n]));
+        y[(size_t)mi * N + n] = h;
+      }
+    }
+  }
+}
+
 }  // namespace
+
+int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
+                    float eps, hipStream_t s) {
+  if (K % 8 != 0) {
+    axm_set_error("f16 gemv: K=%d must be a multiple of 8", K);
+    return -2;
+  }
+  int rows_max = 4;
+  while (rows_max > 1 && (size_t)rows_max * K * sizeof(f16) > 150 * 1024) --rows_max;
+  if ((size_t)K * sizeof(f16) > 150 * 1024) {
+    axm_set_error("f16 gemv: K=%d too large for LDS staging", K);
+    return -2;
+  }
+  for (int m0 = 0; m0 < M; m0 += rows_max) {
+    const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
+    const size_t smem = (size_t)mc * K * sizeof(f16);
+    static size_t attr_bytes = 0;
+    if (smem > 48 * 1024 && smem > attr_bytes) {
+      if (hipFuncSetAttribute((const void*)f16_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
+          hipSuccess) {
+        (void)hipGetLastError();
+        axm_set_error("f16 gemv: cannot reserve %zu bytes of LDS", smem);
+        return -2;
+      }
+      attr_bytes = smem;
+    }
+    const int rows_per_block = kQ8Threads / 64;
+    int grid = (N + rows_per_block - 1) / rows_per_block;
+    const int cap = axm_num_cus() * 8;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(f16_gemv_kernel, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, bias,
+                       y + (size_t)m0 * N, mc, K, N, ln_w, eps);
+  }
+  return 0;
+}
 
 int launch_rmsnorm(const f16* x, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s) {
   if (norm_vec_ok(x, x, w, y, D))

@@ -166,7 +166,8 @@ struct Mat {
   void* sb16 = nullptr;
   int N = 0, K = 0;
   int g128 = 0;  // one (scale, bias) per 128 columns (tile16 copy only)
-  int fmt = 0;   // 0: MARLIN Q4 (w int32 [N/8][K/64][32][2]); 1: Q8_G64 (w uint8 [N][K], sb fp16 [N][K/64][2])
+  int fmt = 0;   // 0: MARLIN Q4 (w int32 [N/8][K/64][32][2]); 1: Q8_G64 (w uint8 [N][K], sb fp16 [N][K/64][2]);
+                 // 2: fp16 (w fp16 [N][K], no sb)
 };
 
 // Prologue / epilogue settings shared by both GEMV paths.
@@ -472,10 +473,9 @@ struct axm_runner {
         a.max_seq = 1;
       }
       int rc = 0;
-      if (m_qkv[i].fmt == 1) {
-        // Q8_G64 QKV: GEMV (+ bias) into qkvbuf, RoPE of q / k into q / kvst, then the slot write.
-        rc = launch_q8_gemv(x, (const uint8_t*)m_qkv[i].w, (const f16*)m_qkv[i].sb, a.bias, qkvbuf, 1, D, qkv_dim,
-                            a.ln_w, d.eps, s);
+      if (m_qkv[i].fmt != 0) {
+        // Q8_G64 / fp16 QKV: GEMV (+ bias) into qkvbuf, RoPE of q / k into q / kvst, then the slot write.
+        rc = dense_gemv(m_qkv[i], x, a.bias, qkvbuf, 1, qkv_dim, a.ln_w, d.eps, s);
         if (rc) return rc;
         hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, 1), dim3(256), 0, s, qkvbuf, q_dim,
                            kv_dim, d.head_dim, d.freqs, params + P_ROPE, q, kvst);
@@ -544,24 +544,37 @@ struct axm_runner {
       if (rc) return rc;
     } else {
       launch_rmsnorm(x, (const f16*)d.lnf_w, norm, 1, D, d.eps, s);
-      int rc = launch_q8_gemv(norm, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, 1, D,
-                              d.vocab_size, nullptr, 0.f, s);
+      int rc = lm_head_dense(norm, 1, s);
       if (rc) return rc;
     }
     return 0;
   }
 
-  // A Q8_G64 matrix: the Q8 GEMV (RMSNorm prologue, bias) followed by the
+  // Q8_G64 (format 1) or fp16 (format 2) lm_head over T normalized rows into logits.
+  int lm_head_dense(const f16* xn, int T, hipStream_t s) {
+    if (d.lm_head_format == 2)
+      return launch_f16_gemv(xn, (const f16*)d.lm_head_w, nullptr, logits, T, d.d_model, d.vocab_size, nullptr, 0.f,
+                             s);
+    return launch_q8_gemv(xn, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, T, d.d_model,
+                          d.vocab_size, nullptr, 0.f, s);
+  }
+
+  // The GEMV of a Q8_G64 (fmt 1) or fp16 (fmt 2) matrix, [M][K] -> [M][N] rows.
+  static int dense_gemv(const Mat& m, const f16* x, const f16* bias, f16* y, int M, int N, const f16* ln,
+                        float eps, hipStream_t s) {
+    if (m.fmt == 2) return launch_f16_gemv(x, (const f16*)m.w, bias, y, M, m.K, N, ln, eps, s);
+    return launch_q8_gemv(x, (const uint8_t*)m.w, (const f16*)m.sb, bias, y, M, m.K, N, ln, eps, s);
+  }
+
+  // A Q8_G64 or fp16 matrix: its GEMV (RMSNorm prologue, bias) followed by the
   // epilogue as separate launches with the rounding of the fused epilogues
   // (residual add in fp16, silu(fp16 g) * fp16 u).  Activation and output rows
   // are contiguous ([M][K] in, [M][N] out), as every caller lays them out.
-  int run_q8(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
+  int run_dense(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
     if (c.x_parts != nullptr || c.argmax_keys != nullptr || epi == Q4_EPI_QKV_ROPE || c.ldx != m.K) {
-      axm_set_error("runner: unsupported call on a Q8_G64 matrix (epilogue %d)", epi);
+      axm_set_error("runner: unsupported call on a Q8_G64 / fp16 matrix (epilogue %d)", epi);
       return -2;
     }
-    const uint8_t* w = (const uint8_t*)m.w;
-    const f16* sb = (const f16*)m.sb;
     const f16* xin = c.x;
     const f16* ln = c.ln_w;
     if (c.x_norm_out != nullptr && ln != nullptr) {
@@ -575,14 +588,14 @@ struct axm_runner {
         axm_set_error("runner: a Q8 store needs contiguous output rows");
         return -2;
       }
-      return launch_q8_gemv(xin, w, sb, c.bias, c.y, M, m.K, out_rows, ln, c.eps, s);
+      return dense_gemv(m, xin, c.bias, c.y, M, out_rows, ln, c.eps, s);
     }
     if (epi == Q4_EPI_SWIGLU) {
       if (c.ldy != out_rows) {
         axm_set_error("runner: a Q8 SwiGLU needs contiguous output rows");
         return -2;
       }
-      rc = launch_q8_gemv(xin, w, sb, nullptr, q8tmp, M, m.K, 2 * out_rows, ln, c.eps, s);
+      rc = dense_gemv(m, xin, nullptr, q8tmp, M, 2 * out_rows, ln, c.eps, s);
       if (rc) return rc;
       return launch_swiglu(q8tmp, c.y, M, out_rows, s);
     }
@@ -591,7 +604,7 @@ struct axm_runner {
       axm_set_error("runner: a Q8 residual needs contiguous rows");
       return -2;
     }
-    rc = launch_q8_gemv(xin, w, sb, nullptr, q8tmp, M, m.K, out_rows, ln, c.eps, s);
+    rc = dense_gemv(m, xin, nullptr, q8tmp, M, out_rows, ln, c.eps, s);
     if (rc) return rc;
     launch_resid_add(c.resid, q8tmp, (long)M * out_rows, s);
     if (c.post_ln_w != nullptr) launch_rmsnorm(c.resid, c.post_ln_w, c.post_norm_out, M, out_rows, c.eps, s);
@@ -599,7 +612,7 @@ struct axm_runner {
   }
 
   int gemv(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
-    return m.fmt == 1 ? run_q8(m, epi, out_rows, c, M, s) : run_gemv(m, epi, out_rows, c, M, s);
+    return m.fmt != 0 ? run_dense(m, epi, out_rows, c, M, s) : run_gemv(m, epi, out_rows, c, M, s);
   }
 
   // GEMV over T token rows in launches of at most 4 rows.
@@ -650,7 +663,7 @@ struct axm_runner {
       if (c.resid) cc.resid = c.resid + (size_t)t0 * c.ldr;
       if (c.x_norm_out) cc.x_norm_out = c.x_norm_out + (size_t)t0 * c.ldx;
       GemvCall cq = cc;
-      if (m.fmt == 1) cq.post_ln_w = nullptr;  // normalized once below
+      if (m.fmt != 0) cq.post_ln_w = nullptr;  // normalized once below
       const int rc = gemv(m, epi, out_rows, cq, mc, s);
       if (rc) return rc;
     }
@@ -753,8 +766,7 @@ struct axm_runner {
       return gemv_rows(m_lmh, Q4_EPI_STORE, d.vocab_size, l, T, s);
     }
     if (!post) launch_rmsnorm(x, (const f16*)d.lnf_w, norm, T, D, d.eps, s);
-    return launch_q8_gemv(norm, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, T, D,
-                          d.vocab_size, nullptr, 0.f, s);
+    return lm_head_dense(norm, T, s);
   }
 
   // Re-tile one matrix for the matrix-core GEMV (runner-owned copy).
@@ -789,12 +801,13 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
                 -1, "runner_create: null per-layer array");
   AXM_CHECK_ARG(d.kv_dtype == AXM_KV_FP16 || (d.k_scales && d.v_scales), -1,
                 "runner_create: quantized KV cache needs scale arrays");
-  AXM_CHECK_ARG(d.lm_head_format == 0 || d.lm_head_format == 1, -1, "runner_create: bad lm_head format");
-  AXM_CHECK_ARG(d.lm_head_format == 1 || d.lm_head_sb, -1, "runner_create: lm_head scales missing");
+  AXM_CHECK_ARG(d.lm_head_format >= 0 && d.lm_head_format <= 2, -1, "runner_create: bad lm_head format");
+  AXM_CHECK_ARG(d.lm_head_format == 2 || d.lm_head_sb, -1, "runner_create: lm_head scales missing");
   AXM_CHECK_ARG(d.group_size == 0 || d.group_size == 64 || d.group_size == 128, -1,
                 "runner_create: group_size %d must be 64 or 128", d.group_size);
   for (int f : {d.qkv_format, d.o_format, d.gu_format, d.down_format})
-    AXM_CHECK_ARG(f == 0 || f == 1, -1, "runner_create: layer matrix format %d must be 0 (MARLIN Q4) or 1 (Q8_G64)", f);
+    AXM_CHECK_ARG(f >= 0 && f <= 2, -1,
+                  "runner_create: layer matrix format %d must be 0 (MARLIN Q4), 1 (Q8_G64) or 2 (fp16)", f);
   AXM_CHECK_ARG(d.qkv_format == 0 || (d.n_head + 2 * d.n_kv_head) * d.head_dim % 8 == 0, -1,
                 "runner_create: a Q8_G64 QKV needs q, k and v rows in multiples of 8");
   AXM_CHECK_ARG(d.group_size != 128 ||
@@ -815,10 +828,12 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
     }
     return true;
   };
+  // fp16 matrices (format 2) have no scale arrays
   bool ok = copy(d.ln1_w, r->ln1, false) && copy(d.ln2_w, r->ln2, false) && copy(d.qkv_w, r->qkv_w, false) &&
-            copy(d.qkv_sb, r->qkv_sb, false) && copy(d.qkv_bias, r->qkv_b, true) && copy(d.o_w, r->o_w, false) &&
-            copy(d.o_sb, r->o_sb, false) && copy(d.gu_w, r->gu_w, false) && copy(d.gu_sb, r->gu_sb, false) &&
-            copy(d.down_w, r->dn_w, false) && copy(d.down_sb, r->dn_sb, false);
+            copy(d.qkv_sb, r->qkv_sb, d.qkv_format == 2) && copy(d.qkv_bias, r->qkv_b, true) &&
+            copy(d.o_w, r->o_w, false) && copy(d.o_sb, r->o_sb, d.o_format == 2) && copy(d.gu_w, r->gu_w, false) &&
+            copy(d.gu_sb, r->gu_sb, d.gu_format == 2) && copy(d.down_w, r->dn_w, false) &&
+            copy(d.down_sb, r->dn_sb, d.down_format == 2);
   if (!ok) {
     delete r;
     axm_set_error("runner_create: a per-layer weight pointer is null");
@@ -1140,7 +1155,7 @@ extern "C" int axm_runner_speculative_decode(axm_runner_t r, const int64_t* init
   const axm_runner_desc& d = r->d;
   AXM_CHECK_ARG(1 + max_spec_tokens <= d.max_tokens, -1, "speculative_decode: max_spec_tokens + 1 exceeds max_tokens %d",
                 d.max_tokens);
-  AXM_CHECK_ARG(d.lm_head_format == 0 || d.lm_head_format == 1, -1, "speculative_decode: bad lm_head");
+  AXM_CHECK_ARG(d.lm_head_format >= 0 && d.lm_head_format <= 2, -1, "speculative_decode: bad lm_head");
   hipStream_t s = (hipStream_t)stream;
   std::vector<int64_t> gen(initial_tokens, initial_tokens + n_initial);
   const int64_t target = (int64_t)n_initial + max_new_tokens;

@@ -7,7 +7,7 @@ paged_cache.py:407-430).  ``load_rocm_module()`` returns an object with the
 attribute names and argument order of the reference's pybind module
 (mps_kernels.mm:4300-4641) for every operation of the decode path, each one
 calling a ``torch.ops.axiomlm`` custom operator (``axiomlm_amd.torch_ops``)
-or, for the runner, ``QuantizedDecodeRunner``.
+or, for the runners, ``QuantizedDecodeRunner`` and the fp16 ``DecodeRunner``.
 
 Names of the reference module that belong to training (backward kernels,
 cross entropy, flash attention forward), to the fp16 ``MPSDecodeRunner`` or to
@@ -24,7 +24,7 @@ def _build():
     import torch
 
     from . import torch_ops  # noqa: F401  (registers torch.ops.axiomlm)
-    from .runner import QuantizedDecodeRunner
+    from .runner import DecodeRunner, QuantizedDecodeRunner
 
     A = torch.ops.axiomlm
 
@@ -151,7 +151,8 @@ def _build():
         return A.argmax_rows(last).view(1, 1)
 
     names = {k: v for k, v in locals().items() if k.endswith("_mps")}
-    return types.SimpleNamespace(MPSQuantizedDecodeRunner=QuantizedDecodeRunner, **names)
+    return types.SimpleNamespace(MPSQuantizedDecodeRunner=QuantizedDecodeRunner, MPSDecodeRunner=DecodeRunner,
+                                 **names)
 
 
 def load_rocm_module(require_device: bool = True):

@@ -58,10 +58,13 @@ def _packed_k(p) -> int:
 
 
 def _matrix_format(p, K: int, name: str) -> int:
-    """0 for MARLIN Q4, 1 for Q8_G64 (the shape test of mps_kernels.mm:3055-3068)."""
+    """0 for MARLIN Q4, 1 for Q8_G64 (the shape test of mps_kernels.mm:3055-3068), 2 for an
+    fp16 [N][K] matrix (the fp16 runner's weights)."""
+    if p.dim() == 2 and p.dtype == torch.float16 and int(p.shape[1]) == K:
+        return 2
     if p.dim() == 4 and _packed_k(p) == K:
         return 0
-    if p.dim() == 2 and _packed_k(p) == K:
+    if p.dim() == 2 and p.dtype != torch.float16 and _packed_k(p) == K:
         return 1
     raise RuntimeError(f"QuantizedDecodeRunner: the {name} pack of shape {tuple(p.shape)} is neither MARLIN Q4 nor "
                        f"Q8_G64 for K={K} (the legacy Q4_G64 layout of mode 'q4_legacy' is not on this runner)")
@@ -88,7 +91,7 @@ class QuantizedDecodeRunner:
         lnf = keep(h16(lnf_w))
         freqs = keep(freqs_r.to(device=dev, dtype=torch.float32).contiguous())
         mats = [c_attn_p, c_attn_s, c_proj_p, c_proj_s, gate_up_p, gate_up_s, w_down_p, w_down_s]
-        mats = [[keep(t.contiguous()) for t in m] for m in mats]
+        mats = [[keep(t.contiguous()) if t is not None else None for t in m] for m in mats]
         biases = [keep(h16(b)) if (b is not None and b.numel() > 0) else None for b in (c_attn_bs or [])]
         biases = biases + [None] * (L - len(biases))
 
@@ -98,9 +101,9 @@ class QuantizedDecodeRunner:
             wte_fmt, wte, wte_sb = 1, keep(wte_emb.contiguous()), keep(lmh_sb.contiguous())
         else:
             wte_fmt, wte, wte_sb = 0, keep(h16(wte_emb)), None
-        lmh_fmt = 0 if lmh_packed.dim() == 4 else 1
+        lmh_fmt = 0 if lmh_packed.dim() == 4 else (2 if lmh_packed.dtype == torch.float16 else 1)
         lmh = keep(lmh_packed.contiguous())
-        lmh_s = keep(lmh_sb.contiguous())
+        lmh_s = keep(lmh_sb.contiguous()) if lmh_sb is not None else None
         if vocab_sz is None or vocab_sz <= 0:
             vocab_sz = wte.shape[0] if lmh_fmt == 0 else lmh_packed.shape[0]
         self.vocab_size = int(vocab_sz)
@@ -160,7 +163,7 @@ class QuantizedDecodeRunner:
                 raise RuntimeError(f"QuantizedDecodeRunner: {name} packs mix MARLIN Q4 and Q8_G64 layers")
             fmts.append(kinds.pop())
         d.qkv_format, d.o_format, d.gu_format, d.down_format = fmts
-        self.layer_formats = tuple("q8_g64" if f else "q4_marlin" for f in fmts)
+        self.layer_formats = tuple(("q4_marlin", "q8_g64", "fp16")[f] for f in fmts)
         packs, scales = [], []
         for f, ps, ss in zip(fmts, (c_attn_p, c_proj_p, gate_up_p, w_down_p), (c_attn_s, c_proj_s, gate_up_s, w_down_s)):
             if f == 0:
@@ -323,3 +326,28 @@ class _RawBuffer:
             }
 
         return torch.as_tensor(_Cai(), device=device)
+
+
+class DecodeRunner(QuantizedDecodeRunner):
+    """The reference's fp16 decode runner ``MPSDecodeRunner`` (mps_kernels.mm:2304-2980, binding
+    :4328-4373) on MI355X:
+
+        DecodeRunner(wte_w, freqs_r, ln1_ws, c_attn_ws, c_proj_ws, ln2_ws, gate_up_ws, w_down_ws,
+                     lnf_w, k_cs, v_cs, n_h, n_kvh, hd, epsilon, lm_head_w=None, c_attn_bs=[])
+
+    fp16 [N][K] weights (gate_up rows [W_gate; W_up]); the lm_head defaults to the embedding
+    table (tied), and the vocabulary is its row count.  The same native runner as the
+    quantized class with every matrix in the fp16 format (an HBM-bound fp16 GEMV), so the
+    methods are the same: step, verify_step, verify_tree_step, speculative_decode,
+    get_last_norm.  Keyword arguments after c_attn_bs are this build's (max_tokens, kv_dtype
+    and layout of the quantized class)."""
+
+    def __init__(self, wte_w, freqs_r, ln1_ws, c_attn_ws, c_proj_ws, ln2_ws, gate_up_ws, w_down_ws, lnf_w, k_cs,
+                 v_cs, n_h, n_kvh, hd, epsilon, lm_head_w=None, c_attn_bs=(), **kw):
+        L = len(ln1_ws)
+        lm = wte_w if lm_head_w is None or lm_head_w.numel() == 0 else lm_head_w
+        h16 = lambda ts: [t.to(torch.float16).contiguous() for t in ts]  # noqa: E731
+        none = [None] * L
+        super().__init__(wte_w.to(torch.float16), lm.to(torch.float16).contiguous(), None, freqs_r, ln1_ws,
+                         h16(c_attn_ws), none, h16(c_proj_ws), none, ln2_ws, h16(gate_up_ws), none, h16(w_down_ws),
+                         none, lnf_w, k_cs, v_cs, n_h, n_kvh, hd, False, epsilon, c_attn_bs, int(lm.shape[0]), **kw)

@@ -30,7 +30,7 @@ import torch
 
 from .cache import StaticKVCache
 from .kernels import pack_linear_q4_marlin, pack_linear_q8_g64
-from .runner import QuantizedDecodeRunner
+from .runner import DecodeRunner, QuantizedDecodeRunner
 
 
 @dataclass
@@ -188,6 +188,10 @@ class Transformer:
         key = (id(cache0), cache0.k_caches[0].data_ptr(), self._quant_mode, self._lm_head_q8)
         if self._runner is not None and self._runner_key == key:
             return self._runner
+        if self._quant_mode is None:
+            self._runner = self._fp16_runner(cache0)
+            self._runner_key = key
+            return self._runner
         qw = self._ensure_quant_weights()
         c = self.config
         h16 = lambda t: t.to(self.device, torch.float16).contiguous()  # noqa: E731
@@ -204,6 +208,24 @@ class Transformer:
             kv_dtype=cache0.cache_dtype, max_tokens=64)
         self._runner_key = key
         return self._runner
+
+    def _fp16_runner(self, cache0: StaticKVCache) -> DecodeRunner:
+        """The unquantized model on the fp16 runner (transformer.py:1310-1380, MPSDecodeRunner):
+        fp16 weights as given, gate|up stacked [W_gate; W_up]."""
+        c = self.config
+        h16 = lambda name: self.w[name].to(self.device, torch.float16).contiguous()  # noqa: E731
+        pre = [f"transformer.h.{i}." for i in range(c.n_layer)]
+        bias = [self.w.get(p + "attn.c_attn.bias") for p in pre]
+        return DecodeRunner(
+            h16("transformer.wte.weight"), self.freqs_real.to(self.device), [h16(p + "ln_1.weight") for p in pre],
+            [h16(p + "attn.c_attn.weight") for p in pre], [h16(p + "attn.c_proj.weight") for p in pre],
+            [h16(p + "ln_2.weight") for p in pre],
+            [torch.cat([h16(p + "mlp.w_gate.weight"), h16(p + "mlp.w_up.weight")], dim=0) for p in pre],
+            [h16(p + "mlp.w_down.weight") for p in pre], h16("transformer.ln_f.weight"), cache0.k_caches,
+            cache0.v_caches, c.n_head, c.kv_heads, c.head_dim, c.rms_norm_eps, lm_head_w=h16("lm_head.weight"),
+            c_attn_bs=[b.to(self.device, torch.float16) if b is not None else torch.empty(0, device=self.device)
+                       for b in bias],
+            k_scales=cache0.k_scales, v_scales=cache0.v_scales, kv_dtype=cache0.cache_dtype, max_tokens=64)
 
     def _positions(self, cache0: StaticKVCache, T: int):
         seen = cache0.total_seen_tokens[0]

@@ -250,7 +250,7 @@ typedef struct axm_runner_desc {
   int wte_format;     /* 0: fp16 table [V][d]; 1: Q8_G64 (uint8 [V][d] + sb [V][d/64][2]) */
   const void* wte;
   const void* wte_sb;
-  int lm_head_format; /* 0: MARLIN Q4; 1: Q8_G64 */
+  int lm_head_format; /* 0: MARLIN Q4; 1: Q8_G64; 2: fp16 [V][d] (no scales) */
   const void* lm_head_w;
   const void* lm_head_sb;
   const float* freqs; /* [rope_len][head_dim/2][2] (cos, sin) */
@@ -277,8 +277,9 @@ typedef struct axm_runner_desc {
                      0 means 64 */
   /* Format of each kind of layer matrix, as the reference runner dispatches it from the
    * packed shape (mps_kernels.mm:3055-3068): 0 = MARLIN Q4 (4-D pack), 1 = Q8_G64 (uint8
-   * [N][K], sb fp16 [N][K/64][2]).  Mode "q4_k_m" packs down as Q8, mode "q8" every matrix
-   * (transformer.py:840-847, 897-903). */
+   * [N][K], sb fp16 [N][K/64][2]), 2 = fp16 [N][K] without scales (the weights of the
+   * reference's fp16 runner MPSDecodeRunner, mps_kernels.mm:2304-2980).  Mode "q4_k_m" packs
+   * down as Q8, mode "q8" every matrix (transformer.py:840-847, 897-903). */
   int qkv_format, o_format, gu_format, down_format;
 } axm_runner_desc;
 

@@ -278,7 +278,9 @@ def _dequantized(wp, wsb, K, out_features):
     hit = _DEQ_MEMO.get(key)
     if hit is not None and hit[0] is wp and hit[1] is wsb:
         return hit[2]
-    if wp.ndim == 4 and wsb.shape[1] * 2 == wp.shape[1]:
+    if wsb is None:  # fp16 weights (the fp16 runner's layers)
+        w = wp.astype(F16)
+    elif wp.ndim == 4 and wsb.shape[1] * 2 == wp.shape[1]:
         w = fm.dequantize_q4_marlin_g128(wp, wsb, K, out_features)
     elif wp.ndim == 4:
         w = fm.dequantize_q4_marlin(wp, wsb, K, out_features)
@@ -308,6 +310,12 @@ class OracleModel:
         self.cos = cos
         self.sin = sin
 
+    def _embed(self, idx):
+        """Token rows: the Q8_G64 gather (quant.py:132-163), or an fp16 table (the fp16 model)."""
+        if self.w.wte_sb is None:
+            return self.w.wte_p[idx].astype(F16)
+        return fm.dequant_q8_rows(idx, self.w.wte_p, self.w.wte_sb).astype(F16)
+
     # -- transformer.py:1036-1200 ------------------------------------------
     def forward(self, idx, cache: OracleKVCache | None = None, return_all_logits=False, return_norm=False):
         c = self.cfg
@@ -316,7 +324,7 @@ class OracleModel:
         hd = c.head_dim
         qd, kvd = c.n_head * hd, c.n_kv_head * hd
         n_rep = c.n_head // c.n_kv_head
-        x = fm.dequant_q8_rows(idx, self.w.wte_p, self.w.wte_sb).astype(F16)  # [T, d]
+        x = self._embed(idx)  # [T, d]
         for i in range(c.n_layer):
             start = cache.total_seen_tokens[i] if cache is not None else 0
             h1 = rmsnorm_fp16(x, self.w.ln1[i], c.eps)
@@ -375,7 +383,7 @@ class OracleModel:
                     attn_mask[u, seen + j] = True
         pos = np.array([(rope_pos + int(d)) % self.cos.shape[0] for d in depths])
         cs, sn = self.cos[pos], self.sin[pos]
-        x = fm.dequant_q8_rows(idx, self.w.wte_p, self.w.wte_sb).astype(F16)
+        x = self._embed(idx)
         for i in range(c.n_layer):
             h1 = rmsnorm_fp16(x, self.w.ln1[i], c.eps)
             b_i = self.w.c_attn_b[i] if self.w.c_attn_b else None
@@ -412,7 +420,7 @@ class OracleModel:
         pos = np.array([(start_pos + t) % self.cos.shape[0] for t in range(T)])
         cs, sn = self.cos[pos], self.sin[pos]
         slots = np.array([(write_pos + t) % S for t in range(T)])
-        x = fm.dequant_q8_rows(idx, self.w.wte_p, self.w.wte_sb).astype(F16)
+        x = self._embed(idx)
         for i in range(c.n_layer):
             h1 = rmsnorm_fp16(x, self.w.ln1[i], c.eps)
             b_i = self.w.c_attn_b[i] if self.w.c_attn_b else None
@@ -522,6 +530,22 @@ def pack_model(cfg: OracleConfig, W, mode: str = "q4") -> OracleWeights:
         p, s = pack(L["w_down"], imp_sw, q8=q8_down)
         ow.wd_p.append(p)
         ow.wd_s.append(s)
+    return ow
+
+
+def fp16_model(cfg: OracleConfig, W) -> OracleWeights:
+    """The unquantized fp16 model the reference's fp16 runner executes: every matrix fp16
+    [N][K] (gate|up rows stacked), an fp16 embedding table; scale arrays are None."""
+    h = lambda a: np.ascontiguousarray(a.astype(F16))  # noqa: E731
+    ow = OracleWeights(h(W["wte"]), None, h(W["lm_head"]), None, [], [], W["lnf"], [], [], [], [], [], [], [], [])
+    for L in W["layers"]:
+        ow.ln1.append(L["ln1"])
+        ow.ln2.append(L["ln2"])
+        for dst, w in ((ow.c_attn_p, L["c_attn"]), (ow.c_proj_p, L["c_proj"]),
+                       (ow.gu_p, np.concatenate([L["w_gate"], L["w_up"]], axis=0)), (ow.wd_p, L["w_down"])):
+            dst.append(h(w))
+        for dst in (ow.c_attn_s, ow.c_proj_s, ow.gu_s, ow.wd_s):
+            dst.append(None)
     return ow
 
 

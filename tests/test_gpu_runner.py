@@ -750,3 +750,69 @@ def test_runner_rejects_legacy_q4_g64(dev):
     ow.wd_p = [np.zeros((cfg.d_model, cfg.hidden // 2), np.uint8) for _ in ow.wd_p]
     with pytest.raises(RuntimeError, match="neither MARLIN Q4 nor Q8_G64"):
         build_runner(cfg, ow, cos, sin, dev, 32)
+
+
+# ---------------------------------------------------------------------------
+# The fp16 runner (MPSDecodeRunner): every matrix fp16 [N][K]
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("kv,bias", [("fp16", False), ("fp16", True), ("fp8", False)])
+def test_fp16_runner_matches_oracle(dev, kv, bias):
+    """DecodeRunner with the reference MPSDecodeRunner signature (mps_kernels.mm:4328-4373) over
+    fp16 weights (GQA 4 / 2 heads, optional QKV bias): 12 decode steps, verify chains of 3 and 9
+    tokens and a 9-node tree against the oracle on the same fp16 weights, logits <= 1e-2
+    (quantized caches loaded into a frozen oracle cache, as for the quantized runner)."""
+    from axiomlm_amd.cache import StaticKVCache
+    from axiomlm_amd.runner import DecodeRunner
+
+    print(f"[fp16_runner] kv={kv} bias={bias}", flush=True)
+    cfg = om.OracleConfig(n_layer=3, n_head=4, n_kv_head=2, d_model=256, hidden=704, vocab=1024, eps=1e-5,
+                          block_size=256)
+    W = om.make_float_weights(cfg, seed=7)
+    ow = om.fp16_model(cfg, W)
+    if bias:
+        rng_b = np.random.default_rng(1)
+        qkv_rows = (cfg.n_head + 2 * cfg.n_kv_head) * cfg.head_dim
+        ow.c_attn_b = [(rng_b.standard_normal(qkv_rows) * 0.1).astype(F16) for _ in range(cfg.n_layer)]
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size)
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    cache = StaticKVCache(1, S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, device=dev, cache_dtype=kv)
+    runner = DecodeRunner(t(ow.wte_p), t(np.stack([cos, sin], axis=-1).astype(F32)), [t(x) for x in ow.ln1],
+                          [t(x) for x in ow.c_attn_p], [t(x) for x in ow.c_proj_p], [t(x) for x in ow.ln2],
+                          [t(x) for x in ow.gu_p], [t(x) for x in ow.wd_p], t(ow.lnf), cache.k_caches, cache.v_caches,
+                          cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.eps, lm_head_w=t(ow.lmh_p),
+                          c_attn_bs=[t(b) for b in ow.c_attn_b], k_scales=cache.k_scales, v_scales=cache.v_scales,
+                          kv_dtype=kv)
+    assert runner.layer_formats == ("fp16",) * 4 and runner.vocab_size == cfg.vocab
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, kv)
+    ocache.frozen = kv != "fp16"
+    rng = np.random.default_rng(17)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, 12).tolist()):
+        got = run_steps(runner, cache, [tok], dev)[0]
+        if ocache.frozen:
+            _load_gpu_cache(ocache, cache)
+        _check_logits(got, model.forward([tok], ocache)[-1], f"fp16 step {i}")
+    for T in (3, 9):
+        seen = cache.total_seen_tokens[0]
+        chain = rng.integers(0, cfg.vocab, T).tolist()
+        g = runner.verify_step(torch.tensor([chain], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
+        if ocache.frozen:
+            _load_gpu_cache(ocache, cache)
+        ref = model.forward(chain, ocache, return_all_logits=True)
+        cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
+        cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
+        for tt in range(T):
+            _check_logits(g[tt], ref[tt], f"fp16 verify T={T} token {tt}")
+    if kv == "fp16":
+        seen = cache.total_seen_tokens[0]
+        parents = [-1, 0, 0, 1, 1, 2, 3, 5, 5]
+        depths, masks = [], []
+        for u, p in enumerate(parents):
+            depths.append(0 if p < 0 else depths[p] + 1)
+            masks.append((0 if p < 0 else masks[p]) | (1 << u))
+        tree = rng.integers(0, cfg.vocab, len(parents)).tolist()
+        g = runner.verify_tree_step(torch.tensor([tree], device=dev), seen, seen, seen, depths, masks)[0].float()
+        ref = model.forward_tree(tree, ocache, depths, masks)
+        for u in range(len(tree)):
+            _check_logits(g[u].cpu().numpy(), ref[u], f"fp16 tree node {u}")

@@ -227,3 +227,26 @@ def test_quantize_modes_decode_against_oracle(dev, mode):
     for i, tok in enumerate(rng.integers(0, c.vocab, 10).tolist()):
         got = m.forward(torch.tensor([[tok]], device=dev), kv_caches=cache)[0][0, -1].float().cpu().numpy()
         _check(got, model.forward([tok], ocache)[-1], f"{mode} token {i}")
+
+
+def test_unquantized_model_runs_on_the_fp16_runner(dev):
+    """quantize(None) (the unquantized model) decodes through the fp16 runner
+    (transformer.py:1310-1380) and matches the oracle on the same fp16 weights."""
+    from c1_golden import c1_config
+
+    from axiomlm_amd.runner import DecodeRunner
+
+    print("[transformer_fp16]", flush=True)
+    m, cfg = _model(dev)
+    m.quantize(None)
+    c = c1_config()
+    W = om.make_float_weights(c, seed=0)
+    cos, sin = om.rope_tables(c.head_dim, c.block_size)
+    model = om.OracleModel(c, om.fp16_model(c, W), cos, sin)
+    cache = _cache(cfg, dev)
+    ocache = om.OracleKVCache(128, c.n_layer, c.n_kv_head, c.head_dim)
+    rng = np.random.default_rng(22)
+    for i, tok in enumerate(rng.integers(0, c.vocab, 10).tolist()):
+        got = m.forward(torch.tensor([[tok]], device=dev), kv_caches=cache)[0][0, -1].float().cpu().numpy()
+        _check(got, model.forward([tok], ocache)[-1], f"fp16 token {i}")
+    assert isinstance(m.get_decode_runner(cache), DecodeRunner)

@@ -95,6 +95,17 @@ def test_runner_class_signature(mod):
         assert callable(getattr(mod.MPSQuantizedDecodeRunner, meth))
 
 
+def test_fp16_runner_class_signature(mod):
+    params = list(inspect.signature(mod.MPSDecodeRunner.__init__).parameters)[1:]
+    # MPSDecodeRunner's constructor (mps_kernels.mm:4328-4373): 15 positional arguments, then
+    # lm_head_w and c_attn_bs
+    assert params[:17] == ["wte_w", "freqs_r", "ln1_ws", "c_attn_ws", "c_proj_ws", "ln2_ws", "gate_up_ws",
+                           "w_down_ws", "lnf_w", "k_cs", "v_cs", "n_h", "n_kvh", "hd", "epsilon", "lm_head_w",
+                           "c_attn_bs"]
+    for meth in ("step", "verify_step", "verify_tree_step", "speculative_decode", "get_last_norm"):
+        assert callable(getattr(mod.MPSDecodeRunner, meth))
+
+
 def test_no_device_means_no_module():
     from axiomlm_amd.rocm_module import load_rocm_module
 
