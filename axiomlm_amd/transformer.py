@@ -108,17 +108,40 @@ class Transformer:
         self._runner_key = None
 
     # -- transformer.py:276-320 ---------------------------------------------
-    def quantize(self, mode: str | None = "q4", lm_head_q8: bool | None = None) -> "Transformer":
+    def quantize(self, mode: str | None = "q4", lm_head_q8: bool | None = None,
+                 release_fp16: bool = False) -> "Transformer":
         """Modes of the quantized decode runner (transformer.py:282-289): "q4" (MARLIN Q4 with the
         importance-weighted MSE clip search), "q4_rtn" (round to nearest), "q4_k_m" ("q4" with
-        Q8_G64 w_down and lm_head), "q8" (Q8_G64 everywhere).  The reference's "q4_legacy",
-        "q2_k" and "ternary" modes do not run through its decode runner and are not modes here."""
+        Q8_G64 w_down and lm_head), "q8" (Q8_G64 everywhere); None runs the fp16 weights on the
+        fp16 runner.  The reference's "q4_legacy", "q2_k" and "ternary" modes do not run through
+        its decode runner and are not modes here.
+
+        release_fp16 (transformer.py:321-351): pack now, then drop the fp16 copies of every
+        packed matrix (layer projections, lm_head, embedding table), keeping only the packs and
+        the norms; the model cannot be unquantized or repacked in another mode afterwards."""
         if mode not in (None, "q4", "q4_rtn", "q4_k_m", "q8"):
             raise ValueError(f"quant mode {mode!r} is not on the MI355X decode path (q4, q4_rtn, q4_k_m, q8)")
+        if getattr(self, "_fp16_released", False) and (mode, lm_head_q8) != (self._quant_mode, self._lm_head_q8):
+            raise RuntimeError("the fp16 weights were released by quantize(..., release_fp16=True); the model cannot "
+                               "be unquantized or packed in another mode")
+        if not getattr(self, "_fp16_released", False):
+            self._quant_weights_cache = None
+            self._runner = None
         self._quant_mode = mode
         self._lm_head_q8 = lm_head_q8
-        self._quant_weights_cache = None
-        self._runner = None
+        if release_fp16 and mode is not None:
+            self._ensure_quant_weights()
+            names = ["lm_head.weight", "transformer.wte.weight"]
+            for i in range(self.config.n_layer):
+                pre = f"transformer.h.{i}."
+                names += [pre + n for n in ("attn.c_attn.weight", "attn.c_proj.weight", "mlp.w_gate.weight",
+                                            "mlp.w_up.weight", "mlp.w_down.weight")]
+            for n in names:
+                if n in self.w:
+                    self.w[n] = torch.empty(0, dtype=torch.float16, device=self.w[n].device)
+            self._fp16_released = True
+            if self.device.type == "cuda":
+                torch.cuda.empty_cache()
         return self
 
     def _t(self, name: str) -> torch.Tensor:

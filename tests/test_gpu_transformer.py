@@ -183,6 +183,30 @@ def test_tree_verify_chain_matches_reference(dev):
     _check(lg[0, 0].float().cpu().numpy(), ref[35], "after compaction")
 
 
+def _host(p):
+    """A pack on the host: Q8 packs as uint8 [N][K] like the oracle's; MARLIN packs unchanged."""
+    a = p.cpu().numpy()
+    return a.view(np.uint8).reshape(a.shape[0], -1) if a.ndim == 2 else a
+
+
+def _oracle_on_packs(m, c):
+    """The oracle model over the packs the GPU produced for Transformer m (and its fp16 norms)."""
+    qw = m._ensure_quant_weights()
+    h = lambda k: m.w[k].to(torch.float16).cpu().numpy()  # noqa: E731
+    L = c.n_layer
+    bias = [b.cpu().numpy() if b is not None else None for b in qw["c_attn_b"]]
+    ow = om.OracleWeights(_host(qw["wte_p"]), qw["wte_sb"].cpu().numpy(), _host(qw["lmh_p"]),
+                          qw["lmh_sb"].cpu().numpy(), [h(f"transformer.h.{i}.ln_1.weight") for i in range(L)],
+                          [h(f"transformer.h.{i}.ln_2.weight") for i in range(L)], h("transformer.ln_f.weight"),
+                          [_host(p) for p in qw["c_attn_p"]], [s.cpu().numpy() for s in qw["c_attn_s"]],
+                          [_host(p) for p in qw["c_proj_p"]], [s.cpu().numpy() for s in qw["c_proj_s"]],
+                          [_host(p) for p in qw["gu_p"]], [s.cpu().numpy() for s in qw["gu_s"]],
+                          [_host(p) for p in qw["wd_p"]], [s.cpu().numpy() for s in qw["wd_s"]],
+                          [] if all(b is None for b in bias) else bias)
+    cos, sin = om.rope_tables(c.head_dim, c.block_size, m.config.rope_theta)
+    return om.OracleModel(c, ow, cos, sin)
+
+
 @pytest.mark.parametrize("mode", ["q4_k_m", "q8"])
 def test_quantize_modes_decode_against_oracle(dev, mode):
     """quantize("q4_k_m") packs w_down and lm_head as Q8_G64 and the rest as MSE-clipped MARLIN
@@ -200,27 +224,15 @@ def test_quantize_modes_decode_against_oracle(dev, mode):
     c = c1_config()
     W = om.make_float_weights(c, seed=0)
 
-    def host(p):  # Q8 packs as uint8 [N][K] like the oracle's; MARLIN packs unchanged
-        a = p.cpu().numpy()
-        return a.view(np.uint8).reshape(a.shape[0], -1) if a.ndim == 2 else a
-
     def q8_same(p, s, w):
         wp, wsb = fm.pack_linear_q8_g64(w)
-        return np.array_equal(host(p), wp) and np.array_equal(s.cpu().numpy().view(np.uint16), wsb.view(np.uint16))
+        return np.array_equal(_host(p), wp) and np.array_equal(s.cpu().numpy().view(np.uint16), wsb.view(np.uint16))
 
     assert qw["lmh_p"].dim() == 2 and q8_same(qw["lmh_p"], qw["lmh_sb"], W["lm_head"])
     for i, lw in enumerate(W["layers"]):
         assert qw["wd_p"][i].dim() == 2 and q8_same(qw["wd_p"][i], qw["wd_s"][i], lw["w_down"])
         assert (qw["c_attn_p"][i].dim() == 2) == (mode == "q8")
-    ow = om.OracleWeights(host(qw["wte_p"]), qw["wte_sb"].cpu().numpy(), host(qw["lmh_p"]),
-                          qw["lmh_sb"].cpu().numpy(), [lw["ln1"] for lw in W["layers"]],
-                          [lw["ln2"] for lw in W["layers"]], W["lnf"],
-                          [host(p) for p in qw["c_attn_p"]], [s.cpu().numpy() for s in qw["c_attn_s"]],
-                          [host(p) for p in qw["c_proj_p"]], [s.cpu().numpy() for s in qw["c_proj_s"]],
-                          [host(p) for p in qw["gu_p"]], [s.cpu().numpy() for s in qw["gu_s"]],
-                          [host(p) for p in qw["wd_p"]], [s.cpu().numpy() for s in qw["wd_s"]])
-    cos, sin = om.rope_tables(c.head_dim, c.block_size)
-    model = om.OracleModel(c, ow, cos, sin)
+    model = _oracle_on_packs(m, c)
     cache = _cache(cfg, dev)
     ocache = om.OracleKVCache(128, c.n_layer, c.n_kv_head, c.head_dim)
     rng = np.random.default_rng(21)
@@ -250,3 +262,39 @@ def test_unquantized_model_runs_on_the_fp16_runner(dev):
         got = m.forward(torch.tensor([[tok]], device=dev), kv_caches=cache)[0][0, -1].float().cpu().numpy()
         _check(got, model.forward([tok], ocache)[-1], f"fp16 token {i}")
     assert isinstance(m.get_decode_runner(cache), DecodeRunner)
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen2"])
+def test_hf_checkpoint_runs_on_the_gpu_runners(dev, tmp_path, family):
+    """A HuggingFace safetensors checkpoint (tiny random-init Llama / Qwen2 written by
+    transformers, head size 64) imported with load_hf_safetensors: on the fp16 runner its
+    logits match HuggingFace's own forward; quantized ("q4_rtn", then release_fp16) it still
+    decodes, with the fp16 copies of the packed matrices gone."""
+    from test_hf_import import tiny_hf_checkpoint
+
+    from axiomlm_amd.hf_import import load_hf_safetensors
+
+    print(f"[hf_gpu] {family}", flush=True)
+    path, hf = tiny_hf_checkpoint(tmp_path, family, False, hidden=256, inter=512)
+    m = load_hf_safetensors(path, device=dev).quantize(None)
+    ids = [5, 77, 200, 3, 141, 9, 64, 250]
+    with torch.no_grad():
+        want = hf(torch.tensor([ids])).logits[0].float().numpy()
+    cache = _cache(m.config, dev)
+    got = np.stack([m.forward(torch.tensor([[t]], device=dev), kv_caches=cache)[0][0, -1].float().cpu().numpy()
+                    for t in ids])
+    err = float(np.abs(got - want).max())
+    assert err <= 2e-2 * max(1.0, float(np.abs(want).max())), err
+    m.quantize("q4_rtn", release_fp16=True)
+    assert m.w["transformer.h.0.attn.c_attn.weight"].numel() == 0 and m.w["lm_head.weight"].numel() == 0
+    with pytest.raises(RuntimeError):
+        m.quantize(None)
+    c = m.config
+    oracle = _oracle_on_packs(m, om.OracleConfig(n_layer=c.n_layer, n_head=c.n_head, n_kv_head=c.kv_heads,
+                                                 d_model=c.n_embd, hidden=c.hidden, vocab=c.vocab_size,
+                                                 eps=c.rms_norm_eps, block_size=c.block_size))
+    cache = _cache(m.config, dev)
+    ocache = om.OracleKVCache(128, c.n_layer, c.kv_heads, c.head_dim)
+    for i, t in enumerate(ids):
+        q = m.forward(torch.tensor([[t]], device=dev), kv_caches=cache)[0][0, -1].float().cpu().numpy()
+        _check(q, oracle.forward([t], ocache)[-1], f"{family} q4_rtn token {i}")
