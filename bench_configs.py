@@ -193,7 +193,7 @@ def run_c4(dev):
         torch.cuda.empty_cache()
 
 
-def run_c5(dev):
+def run_c5(dev, quick=False):
     import torch
 
     from axiomlm_amd.cache import StaticKVCache
@@ -271,7 +271,8 @@ def run_c5(dev):
     _line("C5", f"verify_tree_step T={T} prefix={prefix} fp8 KV", us, w_bytes + kv_bytes,
           {"mfma_frac_f16": round(flops / (us * 1e-6) / 1e12 / MFMA_PEAK_F16_TFLOPS, 4),
            "tree_nodes_per_s": round(T / (us * 1e-6), 1), "host_wall_us": round(wall * 1e6, 1)})
-    _c5_loops(runner, cache, tree, prefix, loop_steps, c["vocab"], dev, g)
+    if not quick:
+        _c5_loops(runner, cache, tree, prefix, loop_steps, c["vocab"], dev, g)
 
 
 def _loop_line(case, T, r, cont):
@@ -341,6 +342,8 @@ def _c5_loops(runner, cache, tree, prefix, n_steps, vocab, dev, g):
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("configs", nargs="*", default=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--quick", action="store_true",
+                    help="c5: time the single verify step only (short runs under counter collection)")
     args = ap.parse_args()
     import torch
 
@@ -350,7 +353,7 @@ def main() -> None:
         if name not in runs:
             sys.exit(f"unknown config {name!r}; choose from {sorted(runs)}")
         print(f"[bench_configs] {name}", file=sys.stderr, flush=True)
-        runs[name](dev)
+        runs[name](dev, quick=args.quick) if name == "c5" else runs[name](dev)
         torch.cuda.empty_cache()
 
 
