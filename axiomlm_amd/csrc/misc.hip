@@ -197,75 +197,7 @@ __global__ void embed_q8_kernel(const uint8_t* __restrict__ wq, const f16* __res
 }
 
 // ---------------------------------------------------------------------------
-// Q8_G64 GEMV:  y[n] = sum_g scale*(sum q*x) + bias*(sum x)   (quant.py:72-129)
-// One wave per output row per iteration; each lane streams 16 bytes (16 codes
-// of one group quarter).  Activations (optionally RMS-normalized) are staged
-// in LDS as fp32.
-// ---------------------------------------------------------------------------
 constexpr int kQ8Threads = 256;
-
-__global__ void __launch_bounds__(kQ8Threads)
-    q8_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ sb,
-                   const f16* __restrict__ bias, f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w,
-                   float eps) {
-  extern __shared__ __align__(16) float xs[];  // [M][K]
-  __shared__ float red[4];
-  for (int mi = 0; mi < M; ++mi) {
-    const f16* xr = x + (size_t)mi * K;
-    float rinv = 1.f;
-    if (ln_w != nullptr) {
-      float s = 0.f;
-      for (int k = threadIdx.x; k < K; k += kQ8Threads) {
-        float v = h2f(xr[k]);
-        s += h2f(f2h(v * v));
-      }
-      rinv = rms_inv_fp16(block_sum_256(s, red), K, eps);
-    }
-    for (int k = threadIdx.x; k < K; k += kQ8Threads) {
-      f16 h = xr[k];
-      if (ln_w != nullptr) h = f2h(h2f(f2h(h2f(h) * rinv)) * h2f(ln_w[k]));
-      xs[(size_t)mi * K + k] = h2f(h);
-    }
-  }
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int G = K / 64;
-  const int n_waves_total = gridDim.x * (kQ8Threads / 64);
-  for (int n = blockIdx.x * (kQ8Threads / 64) + wave; n < N; n += n_waves_total) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    const uint8_t* wr = w + (size_t)n * K;
-    const f16* sbr = sb + (size_t)n * G * 2;
-    for (int k0 = lane * 16; k0 < K; k0 += 64 * 16) {
-      const u32x4 q4 = *reinterpret_cast<const u32x4*>(wr + k0);
-      const int g = k0 >> 6;
-      const float sc = h2f(sbr[2 * g]), bi = h2f(sbr[2 * g + 1]);
-      for (int mi = 0; mi < M && mi < 4; ++mi) {
-        const float* xk = xs + (size_t)mi * K + k0;
-        float d = 0.f, xsum = 0.f;
-#pragma unroll
-        for (int wi = 0; wi < 4; ++wi) {
-          const uint32_t word = q4[wi];
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const float xv = xk[wi * 4 + b];
-            d = __builtin_fmaf((float)((word >> (8 * b)) & 0xFFu), xv, d);
-            xsum += xv;
-          }
-        }
-        acc[mi] = __builtin_fmaf(sc, d, __builtin_fmaf(bi, xsum, acc[mi]));
-      }
-    }
-    for (int mi = 0; mi < M && mi < 4; ++mi) {
-      const float v = wave_sum(acc[mi]);
-      if (lane == 0) {
-        f16 h = f2h(v);
-        if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[n]));
-        y[(size_t)mi * N + n] = h;
-      }
-    }
-  }
-}
 
 // fp16 GEMV (the dense layers of the fp16 decode runner):  y[n] = sum_k w[n][k] x[k].
 // Activations (optionally RMS-normalized with the fp16 op order of the quantized
@@ -406,39 +338,6 @@ int launch_embed_q8(const uint8_t* wq, const f16* sb, const int64_t* tokens, con
   return 0;
 }
 
-int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
-                   const f16* ln_w, float eps, hipStream_t s) {
-  // Up to four rows per launch, fewer when their fp32 staging would not fit in LDS.
-  int rows_max = 4;
-  while (rows_max > 1 && (size_t)rows_max * K * sizeof(float) > 150 * 1024) --rows_max;
-  for (int m0 = 0; m0 < M; m0 += rows_max) {
-    const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
-    const size_t smem = (size_t)mc * K * sizeof(float);
-    if (smem > 150 * 1024) {
-      axm_set_error("q8 gemv: K=%d too large for LDS staging", K);
-      return -2;
-    }
-    static size_t attr_bytes = 0;
-    if (smem > 48 * 1024 && smem > attr_bytes) {
-      // Raise the dynamic-LDS limit to what this launch needs (the kernel also
-      // has a few bytes of static LDS, so the full 160 KiB cannot be requested).
-      if (hipFuncSetAttribute((const void*)q8_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
-          hipSuccess) {
-        (void)hipGetLastError();
-        axm_set_error("q8 gemv: cannot reserve %zu bytes of LDS", smem);
-        return -2;
-      }
-      attr_bytes = smem;
-    }
-    const int rows_per_block = kQ8Threads / 64;
-    int grid = (N + rows_per_block - 1) / rows_per_block;
-    const int cap = axm_num_cus() * 8;
-    if (grid > cap) grid = cap;
-    hipLaunchKernelGGL(q8_gemv_kernel, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, sb, bias,
-                       y + (size_t)m0 * N, mc, K, N, ln_w, eps);
-  }
-  return 0;
-}
 
 // ---------------------------------------------------------------------------
 // C ABI wrappers.

@@ -307,15 +307,16 @@ def dequant_q8_rows(indices, w_packed, scales_biases) -> torch.Tensor:
     return out.view(*indices.shape, K)
 
 
-def qmv_q8_g64(x, w_packed, scales_biases) -> torch.Tensor:
-    """y = x @ W^T with Q8_G64 weights (quant.py:201-218)."""
+def qmv_q8_g64(x, w_packed, scales_biases, bias=None) -> torch.Tensor:
+    """y = x @ W^T (+ bias, this build's addition) with Q8_G64 weights (quant.py:201-218)."""
     _lib.require_gpu(x, "qmv_q8_g64")
     K = x.size(-1)
     M = x.numel() // K
     N = w_packed.shape[0]
     y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
+    b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
     _lib.check(_lib.lib().axm_qmv_q8_g64(_lib.ptr(x.contiguous()), _lib.ptr(w_packed.contiguous()),
-                                         _lib.ptr(scales_biases.contiguous()), None, _lib.ptr(y), M, K, N,
+                                         _lib.ptr(scales_biases.contiguous()), _lib.ptr(b), _lib.ptr(y), M, K, N,
                                          _lib.stream_of(x.device)),
                "qmv_q8_g64")
     return y

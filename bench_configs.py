@@ -16,6 +16,7 @@ per case, each against the HBM roofline (8 TB/s) with its algorithmic bytes:
       seeded random drafts and with drafts that follow the model's own greedy
       continuation along the first-child chain; this runner's t(N) latency
       profile and the Sequoia tree it selects
+  modes  the 7B decode step with q4_k_m, q8 and fp16 weights (the runner's other formats)
 
 Kernels are timed from a captured HIP graph of back-to-back calls (no host
 launch gaps), rotating over enough weight / cache copies that the stream does
@@ -339,6 +340,92 @@ def _c5_loops(runner, cache, tree, prefix, n_steps, vocab, dev, g):
                       "sequoia_speedup": res.speedup}), flush=True)
 
 
+def run_modes(dev):
+    """The 7B decode step in the runner's other weight formats: "q4_k_m" (MARLIN Q4 with Q8_G64
+    w_down and lm_head), "q8" (Q8_G64 everywhere) and the fp16 runner (every matrix fp16),
+    fp16 KV cache, context 128; tokens fed from device memory (no greedy feedback, which
+    needs the MARLIN lm_head)."""
+    import torch
+
+    from axiomlm_amd.cache import StaticKVCache
+    from axiomlm_amd.kernels import pack_linear_q4_marlin, pack_linear_q8_g64
+    from axiomlm_amd.runner import DecodeRunner, QuantizedDecodeRunner
+
+    c = bench.CFG_7B
+    d, H, L, hd, V = c["d"], c["hidden"], c["n_layer"], c["hd"], c["vocab"]
+    qkv_rows = (c["n_head"] + 2 * c["n_kv_head"]) * hd
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    fr = torch.outer(torch.arange(bench.MAX_SEQ * 4, dtype=torch.float32), inv)
+    freqs = torch.stack([fr.cos(), fr.sin()], dim=-1).to(dev)
+    shapes = {"qkv": (qkv_rows, d), "o": (d, d), "gu": (2 * H, d), "dn": (d, H)}
+    bpw = {"q4": 0.5625, "q8": 1.0625, "fp16": 2.0}
+    for mode in ("q4_k_m", "q8", "fp16"):
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+
+        def randn(*shape, std=0.02):
+            return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std).to(torch.float16)
+
+        def fmt_of(kind):
+            if mode == "fp16":
+                return "fp16"
+            return "q8" if (mode == "q8" or kind in ("dn", "lm")) else "q4"
+
+        def pack(kind, rows, k):
+            w = randn(rows, k)
+            f = fmt_of(kind)
+            if f == "fp16":
+                return w, None
+            return pack_linear_q8_g64(w) if f == "q8" else pack_linear_q4_marlin(w, clip_search=False)
+
+        lay = {k: [] for k in ("ln1", "ln2", "qkv", "o", "gu", "dn")}
+        for _ in range(L):
+            lay["ln1"].append((1 + randn(d, std=0.1).float()).half())
+            lay["ln2"].append((1 + randn(d, std=0.1).float()).half())
+            for k, (n, kk) in shapes.items():
+                lay[k].append(pack(k, n, kk))
+        lnf = (1 + randn(d, std=0.1).float()).half()
+        cache = StaticKVCache(1, bench.MAX_SEQ, L, c["n_kv_head"], hd, device=dev)
+        cache.cache.normal_(generator=g)
+        P = lambda k: [p for p, _ in lay[k]]  # noqa: E731
+        S = lambda k: [s for _, s in lay[k]]  # noqa: E731
+        if mode == "fp16":
+            wte = randn(V, d)
+            runner = DecodeRunner(wte, freqs, lay["ln1"], P("qkv"), P("o"), lay["ln2"], P("gu"), P("dn"), lnf,
+                                  cache.k_caches, cache.v_caches, c["n_head"], c["n_kv_head"], hd, 1e-5,
+                                  lm_head_w=randn(V, d))
+        else:
+            lmh_p, lmh_s = pack("lm", V, d)
+            wte_p, wte_s = pack_linear_q8_g64(randn(V, d))
+            runner = QuantizedDecodeRunner(None, lmh_p, lmh_s, freqs, lay["ln1"], P("qkv"), S("qkv"), P("o"), S("o"),
+                                           lay["ln2"], P("gu"), S("gu"), P("dn"), S("dn"), lnf, cache.k_caches,
+                                           cache.v_caches, c["n_head"], c["n_kv_head"], hd, mode != "q8", 1e-5, [],
+                                           V, wte_p=wte_p, wte_s=wte_s)
+        tok = torch.zeros((1, 1), dtype=torch.int64, device=dev)
+        pos = bench.CTX0
+        for i in range(10):
+            runner.step(tok, pos + i, pos + i, pos + i + 1)
+        torch.cuda.synchronize()
+        steps = 100
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            p = pos + 10 + i
+            runner.step(tok, p, p, p + 1)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        w_bytes = sum(L * n * kk * bpw[fmt_of(k)] for k, (n, kk) in shapes.items()) + V * d * bpw[fmt_of("lm")]
+        active = pos + 10 + steps // 2
+        b = w_bytes + L * 2 * c["n_kv_head"] * active * hd * 2
+        print(json.dumps({"config": "modes", "case": f"7B decode, {mode} weights ({runner.layer_formats})",
+                          "ms_per_token": round(ms, 4), "tokens_per_s": round(1000.0 / ms, 1),
+                          "algorithmic_bytes_per_token": int(b),
+                          "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
+        del runner, cache, lay
+        torch.cuda.empty_cache()
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("configs", nargs="*", default=["c2", "c3", "c4", "c5"])
@@ -348,7 +435,7 @@ def main() -> None:
     import torch
 
     dev = torch.device("cuda", 0)
-    runs = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}
+    runs = {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5, "modes": run_modes}
     for name in args.configs:
         if name not in runs:
             sys.exit(f"unknown config {name!r}; choose from {sorted(runs)}")

@@ -374,6 +374,28 @@ def test_q8_qmv_matches_oracle(dev):
     assert (np.abs(got - ref) / (1 + np.abs(ref))).max() <= 2e-3
 
 
+@pytest.mark.parametrize("M,N_,K,bias", [(1, 32000, 4096, False), (1, 4096, 11008, False), (3, 12288, 4096, True),
+                                         (4, 4096, 11008, False), (5, 2048, 4096, True), (2, 77, 640, True),
+                                         (1, 1, 64, False)])
+def test_q8_qmv_shapes_match_oracle(dev, M, N_, K, bias):
+    """The Q8_G64 GEMV at the 7B lm_head / down / QKV shapes (one, two and four rows per
+    wave), several tokens, a bias and ragged sizes, against the oracle's dequantize-then-
+    matmul (fp16 weights, as the reference CPU path rounds them), 2e-3 relative."""
+    from axiomlm_amd.kernels import qmv_q8_g64
+
+    print(f"[q8_qmv] M={M} N={N_} K={K} bias={bias}", flush=True)
+    rng = np.random.default_rng(N_ + K + M)
+    w = (rng.standard_normal((N_, K)) * 0.02).astype(F16)
+    x = rng.standard_normal((M, K)).astype(F16)
+    b = (rng.standard_normal(N_) * 0.1).astype(F16) if bias else None
+    p, sb = fm.pack_linear_q8_g64(w)
+    ref = fm.linear_fp16(x, fm.dequantize_q8_g64(p, sb, K), b).astype(F32)
+    got = N(qmv_q8_g64(T(x, dev), T(p.view(np.int32).reshape(N_, K // 4), dev), T(sb, dev),
+                       None if b is None else T(b, dev))).astype(F32)
+    err = np.abs(got - ref)
+    assert np.all(err <= 2e-3 * np.maximum(1.0, np.abs(ref))), float(err.max())
+
+
 @pytest.mark.parametrize("src", [F16, F32])
 def test_ternary_and_q2_pack_bit_exact(dev, src):
     from axiomlm_amd.kernels import pack_linear_q2_k, pack_linear_ternary
