@@ -41,9 +41,18 @@ HIP_FLAGS = [
 ]
 
 
+# Per-file code generation options.  attention.hip: MFMA accumulators in VGPRs
+# (with them in AGPRs the compiler copied every output accumulator out and back
+# on each key block of the decode kernel).
+FILE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "-c", src, "-o", obj]
+    extra = FILE_FLAGS.get(os.path.basename(src), [])
+    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, *extra, "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

@@ -391,9 +391,60 @@ __device__ __forceinline__ KvRaw8 kv_fetch8(const KvHead& h, int slot, int hd, i
     f.sc = __builtin_amdgcn_raw_buffer_load_b16(h.scales, ok ? (slot * (hd / 64) + e0 / 64) * 2 : kOff, 0, 0);
   return f;
 }
+// Position e of an f16x8 from kv_half8 holds element kv_dim_of<KVT>(e) of the chunk:
+// the int4 form delivers the even elements 0, 2, 4, 6, then the odd ones.
+template <int KVT>
+__device__ __forceinline__ constexpr int kv_dim_of(int e) {
+  return KVT == AXM_KV_INT4 ? ((e & 3) << 1) | (e >> 2) : e;
+}
+
+// Eight consecutive query elements in the order kv_half8 delivers the chunk's
+// elements (the MFMA k index then pairs each query element with its key element).
+template <int KVT>
+__device__ __forceinline__ f16x8 kv_order8(f16x8 v) {
+  f16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = v[kv_dim_of<KVT>(e)];
+  return r;
+}
+
 template <int KVT>
 __device__ __forceinline__ f16x8 kv_half8(const KvRaw8& f) {
   if (KVT == AXM_KV_FP16) return __builtin_bit_cast(f16x8, f.r);
+  if (KVT == AXM_KV_INT4) {
+    // u = nibble ^ 8 = q + 8 in [0, 15].  The even nibbles (one per byte of lo) and
+    // the odd ones (hi) become, by one byte permute per pair with the exponent byte
+    // 0x64, the exact halves 1024 + u; minus 1032 gives q exactly, and one fp16
+    // multiply by the scale rounds q * scale once (the fp32 product of a 4-bit
+    // integer and an fp16 scale is exact, so this equals fp16(float(q) * scale)).
+    const uint32_t u = f.r.x ^ 0x88888888u;
+    const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+    const f16 sc = u16_as_h((uint16_t)f.sc);
+    const f16x2 s2 = {sc, sc};
+    const f16x2 off = {(f16)1032.f, (f16)1032.f};
+    const uint32_t pr[4] = {__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u),
+                            __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u),
+                            __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u),
+                            __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)};
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = as_u32((as_h2(pr[i]) - off) * s2);
+    return __builtin_bit_cast(f16x8, o);
+  }
+  if (KVT == AXM_KV_FP8) {
+    // Two E4M3FN codes -> two fp16 per conversion (scale 1.0: every finite code is
+    // an exact fp16), then one fp16 multiply rounds code * scale once, as the fp32
+    // product (exact: 4 x 11 significant bits) rounded to fp16 does.
+    const f16 sc = u16_as_h((uint16_t)f.sc);
+    const f16x2 s2 = {sc, sc};
+    u32x4 o;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      o[2 * w] = as_u32(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(f.r[w], 1.0f, false) * s2);
+      o[2 * w + 1] = as_u32(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(f.r[w], 1.0f, true) * s2);
+    }
+    return __builtin_bit_cast(f16x8, o);
+  }
   float x[8];
   kv8_convert<KVT, true>(f.r, h2f(u16_as_h((uint16_t)f.sc)), x);
   f16x8 h;
@@ -1055,7 +1106,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
     for (int c = 0; c < KSTEPS; ++c) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) qa[c][i] = f16(0);
-      if (r < R) qa[c] = *reinterpret_cast<const f16x8*>(p.q + (size_t)grow(r) * HD + 32 * c + 8 * lq);
+      if (r < R) qa[c] = kv_order8<KVT>(*reinterpret_cast<const f16x8*>(p.q + (size_t)grow(r) * HD + 32 * c + 8 * lq));
     }
   }
   // D-tile rows of this lane: row0 + 4 lq + v.
@@ -1093,7 +1144,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
       if (j < kVec) {
         const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vt[vt_at(e0 + e, kk)] = vv[i][e];
+        for (int e = 0; e < 8; ++e) vt[vt_at(e0 + kv_dim_of<KVT>(e), kk)] = vv[i][e];
       }
     }
     // S = Q K^T for the block's two 16-key halves.
@@ -1213,26 +1264,29 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
 
   // A wave's key blocks are fetched DEPTH ahead into DEPTH register buffers;
   // keys at or past k_end read zeros, so every fetch is issued unconditionally.
-  // Two ahead pays for the fp8 cache (C3 shape, 32k keys: 187 -> 163 us); the
-  // int4 and fp16 forms keep one, where the second buffer's registers cost more
-  // occupancy than it gains (int4, 32k keys: 144 -> 172 us with two).
+  // Two ahead pays for the fp8 cache (C3 shape, 32k keys: 187 -> 163 us).  The
+  // int4 form gains nothing from a second buffer (32k keys: 108 -> 110 us, 1k
+  // keys 12.7 -> 13.5 us), and for fp16 it takes hd 128 past 256 VGPRs, i.e. from
+  // two waves per SIMD to one.
   constexpr int DEPTH = KVT == AXM_KV_FP8 ? 2 : 1;
   KvRaw8 kraw[DEPTH][2][KSTEPS], vraw[DEPTH][kVPL];
-  const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, p.kv.S, HD);
-  const KvHead vh = kv_head<KVT>(p.kv.v, p.kv.vs, head_row0, p.kv.S, HD);
+  // The key / value descriptors end at the split's last key, so fetches past it
+  // read zeros without a per-chunk select.
+  const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, k_end, HD);
+  const KvHead vh = kv_head<KVT>(p.kv.v, p.kv.vs, head_row0, k_end, HD);
   auto fetch = [&](int kb0, auto bc) {
     constexpr int bf = decltype(bc)::value;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int key = kb0 + 16 * h + l16;
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) kraw[bf][h][c] = kv_fetch8<KVT>(kh, key, HD, 32 * c + 8 * lq, key < k_end);
+      for (int c = 0; c < KSTEPS; ++c) kraw[bf][h][c] = kv_fetch8<KVT>(kh, key, HD, 32 * c + 8 * lq, true);
     }
 #pragma unroll
     for (int i = 0; i < kVPL; ++i) {
       const int j = i * 64 + lane;
       const int key = kb0 + j / (HD / 8), e0 = 8 * (j % (HD / 8));
-      vraw[bf][i] = kv_fetch8<KVT>(vh, key, HD, e0, key < k_end);
+      vraw[bf][i] = kv_fetch8<KVT>(vh, key, HD, e0, true);
     }
   };
   using B0 = std::integral_constant<int, 0>;
@@ -1247,7 +1301,7 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   for (int c = 0; c < KSTEPS; ++c) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) qa[c][i] = f16(0);
-    if (l16 < R) qa[c] = *reinterpret_cast<const f16x8*>(p.q + (qrow0 + l16) * HD + 32 * c + 8 * lq);
+    if (l16 < R) qa[c] = kv_order8<KVT>(*reinterpret_cast<const f16x8*>(p.q + (qrow0 + l16) * HD + 32 * c + 8 * lq));
   }
   bool row_ok[4];
   float m[4], l[4];
@@ -1276,7 +1330,7 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
       const int j = i * 64 + lane;
       const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[wave][vt_at(e0 + e, kk)] = vv[i][e];
+      for (int e = 0; e < 8; ++e) vt[wave][vt_at(e0 + kv_dim_of<KVT>(e), kk)] = vv[i][e];
     }
     f32x4 sc[2];
 #pragma unroll
@@ -1285,6 +1339,7 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
 #pragma unroll
       for (int c = 0; c < KSTEPS; ++c) sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf[h][c], sc[h], 0, 0, 0);
     }
+    float alpha[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float s2[2];
@@ -1294,16 +1349,22 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
         s2[h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
       }
       const float m_new = fmaxf(m[v], row16_max(fmaxf(s2[0], s2[1])));
-      const float alpha = fast_exp2(m[v] - m_new);
+      alpha[v] = fast_exp2(m[v] - m_new);
       float pr[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) pr[h] = s2[h] == kNegBig ? 0.f : fast_exp2(s2[h] - m_new);
-      l[v] = l[v] * alpha + row16_sum(pr[0] + pr[1]);
+      l[v] = l[v] * alpha[v] + row16_sum(pr[0] + pr[1]);
       m[v] = m_new;
 #pragma unroll
-      for (int d = 0; d < DT; ++d) o[d][v] *= alpha;
-#pragma unroll
       for (int h = 0; h < 2; ++h) pt[wave][pt_at(4 * lq + v, 16 * h + l16)] = f2h(pr[h]);
+    }
+    // Rescale the output accumulators only when some row's running max moved
+    // (alpha == 1 exactly otherwise, so skipping the multiply changes nothing).
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f)) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[d][v] *= alpha[v];
     }
     // The wave reads back its own LDS writes: DS operations of one wave complete
     // in order, and the reads below wait for them.

@@ -534,6 +534,45 @@ def test_flash_decode_split_invariance(dev):
         assert np.abs(o - outs[0]).max() <= 2e-3  # test_phase3_task32_fused_attention.py:304-367
 
 
+@pytest.mark.parametrize("kind", ["fp8", "int4"])
+@pytest.mark.parametrize("hd", [64, 128])
+def test_mfma_decode_single_key_returns_dequantized_value_bit_exact(dev, kind, hd):
+    """Over one key the softmax weight is exactly 1, so the grouped-query MFMA decode
+    kernel returns the value row as its key/value conversion produced it: this pins
+    that conversion (every finite FP8 code, every int4 nibble, scales whose products
+    are fp16 subnormals or near the fp16 maximum, negative scales) bit for bit against
+    the reference dequantizers (quant.py:760-768, 843-852)."""
+    from axiomlm_amd.kernels import gqa_flash_decode_mps
+
+    print(f"[single_key_dequant] kv={kind} hd={hd}", flush=True)
+    rng = np.random.default_rng(11 + hd)
+    B, Hkv, n_rep, S = 4, 4, 2, 8
+    Hq = Hkv * n_rep
+    G = hd // 64
+    if kind == "fp8":
+        finite = np.array([c for c in range(256) if c & 0x7F != 0x7F], dtype=np.uint8)
+        codes = np.resize(rng.permutation(np.tile(finite, 16)), (B, Hkv, S, hd)).astype(np.uint8)
+    else:
+        codes = rng.integers(0, 256, (B, Hkv, S, hd // 2), dtype=np.uint8)
+    # Scales: ordinary, tiny (subnormal fp16 products), large (products near 65504 for
+    # fp8's 448 / int4's 8), negative.
+    pool = np.array([0.0123, 0.5, 1.0, 3.75, 2.0 ** -14, 2.0 ** -20, 6.1e-5, 100.0, 146.0, -0.75, 7000.0],
+                    dtype=np.float64)
+    if kind == "fp8":
+        pool = pool[np.abs(pool) * 448 < 65504]
+    scales = rng.choice(pool, (B, Hkv, S, G)).astype(F16)
+    other = rng.standard_normal((B, Hkv, S, hd)).astype(F16)
+    qf = fm.quantize_kv_fp8_single if kind == "fp8" else fm.quantize_kv_int4_single
+    kq, ks = qf(other)  # keys: any finite codes (one key, its weight is 1 whatever the score)
+    deq = fm.dequantize_kv_fp8 if kind == "fp8" else fm.dequantize_kv_int4
+    want = deq(codes, scales)[:, :, 0]  # [B, Hkv, hd]
+    q = (0.1 * rng.standard_normal((B, Hq, 1, hd))).astype(F16)
+    got = N(gqa_flash_decode_mps(T(q, dev), T(kq, dev), T(codes, dev), 1, 0, T(ks, dev), T(scales, dev), kind))
+    want_q = np.repeat(want, n_rep, axis=1)[:, :, None, :].astype(F32)
+    # Exact equality of values (the fp32 accumulation turns a -0 value into +0).
+    assert np.array_equal(got.astype(F32), want_q)
+
+
 def _tree_masks(depths, parents):
     masks = []
     for u, p in enumerate(parents):
