@@ -1065,7 +1065,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   auto grow = [&](int r) {  // global query row (node * Hq + query head) of row r < R
     return (r / p.n_rep) * p.Hq + kvh * p.n_rep + (r % p.n_rep);
   };
-  auto slot_of = [&](int key) { return key < prefix ? key : (p.write_pos + (key - prefix)) % p.kv.S; };
+  // Tree key t sits in slot (write_pos + t) % S; the launch guarantees T <= S (and
+  // write_pos < S), so one conditional subtraction wraps it.  Selects only: a
+  // branch here split the loop body and cost the key buffers their registers.
+  auto slot_of = [&](int key) {
+    const int w = p.write_pos + (key - prefix);
+    const int wrapped = w >= p.kv.S ? w - p.kv.S : w;
+    return key < prefix ? key : wrapped;
+  };
 
   // Key / value fetches of one block into register buffer b (two blocks are in
   // flight): this lane's K B-operand fragments (keys kb0 + 16 h + l16, dims
@@ -1094,10 +1101,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  // The first two blocks' keys and values are requested before the query rows.
-  fetch(k_begin, B0{});
-  fetch(k_begin + kTreeKeys, B1{});
-
   // A operand: query row row0 + l16, dims 32 c + 8 lq .. +7.
   f16x8 qa[KSTEPS];
   {
@@ -1124,6 +1127,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   }
 #pragma unroll
   for (int d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The first two blocks' keys and values are requested after the query rows and
+  // masks: loads complete in order, so the loop's waits for a key block then also
+  // cover them (requested last, they made every iteration wait for all loads).
+  fetch(k_begin, B0{});
+  fetch(k_begin + kTreeKeys, B1{});
 
   // One key block from register buffer b, whose registers then take the block
   // two ahead.
@@ -1136,12 +1144,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
       for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(kraw[b][h][c]);
 #pragma unroll
     for (int i = 0; i < kVPT; ++i) vv[i] = kv_half8<KVT>(vraw[b][i]);
+    // The refill is not scheduled above the conversions: the old and new contents of
+    // buffer b then never overlap and keep the same registers across iterations
+    // (otherwise the loop head copied the new ones, waiting for every load).
+    __builtin_amdgcn_sched_barrier(0);
     fetch(kb0 + 2 * kTreeKeys, bc);
     // Stage V transposed: vector j covers key kb0 + j / (HD/8), dims 8 (j % (HD/8)).
 #pragma unroll
     for (int i = 0; i < kVPT; ++i) {
       const int j = i * 256 + threadIdx.x;
-      if (j < kVec) {
+      if (kVec % 256 == 0 || j < kVec) {
         const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
 #pragma unroll
         for (int e = 0; e < 8; ++e) vt[vt_at(e0 + kv_dim_of<KVT>(e), kk)] = vv[i][e];
@@ -1156,27 +1168,33 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
       for (int c = 0; c < KSTEPS; ++c) sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf[h][c], sc[h], 0, 0, 0);
     }
     // Mask, scale, online softmax per D-tile row; P to the wave's LDS tile.
+    float alpha[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float s[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int key = kb0 + 16 * h + l16;
-        bool vis = row_ok[v] && key < k_end;
-        if (key >= prefix) vis = vis && ((mask[v] >> (key - prefix)) & 1ull);
+        const bool in_tree = ((mask[v] >> ((key - prefix) & 63)) & 1ull) != 0;
+        const bool vis = row_ok[v] && key < k_end && (key < prefix || in_tree);
         s[h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
       }
       const float m_new = fmaxf(m[v], row16_max(fmaxf(s[0], s[1])));
-      const float alpha = fast_exp2(m[v] - m_new);
+      alpha[v] = fast_exp2(m[v] - m_new);
       float pr[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) pr[h] = s[h] == kNegBig ? 0.f : fast_exp2(s[h] - m_new);
-      l[v] = l[v] * alpha + row16_sum(pr[0] + pr[1]);
+      l[v] = l[v] * alpha[v] + row16_sum(pr[0] + pr[1]);
       m[v] = m_new;
 #pragma unroll
-      for (int d = 0; d < DT; ++d) o[d][v] *= alpha;
-#pragma unroll
       for (int h = 0; h < 2; ++h) pt[wave][pt_at(4 * lq + v, 16 * h + l16)] = f2h(pr[h]);
+    }
+    // Rescale only when some row's running max moved (alpha == 1 exactly otherwise).
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f)) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[d][v] *= alpha[v];
     }
     __syncthreads();  // V staged by every wave; P tiles written
     // O += P V: A = P[row l16][keys 8 lq ..], B = V^T[dim 16 d + l16][keys 8 lq ..].
@@ -1188,10 +1206,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
     }
     __syncthreads();  // before the next block overwrites vt / pt
   };
-  for (int kb0 = k_begin; kb0 < k_end; kb0 += 2 * kTreeKeys) {
+  // Both blocks of an iteration run unconditionally and an odd last block is peeled
+  // off: with a conditional second block the two register buffers reach the loop
+  // head from two paths, and the compiler copied the freshly requested ones there,
+  // waiting for every load in flight on each iteration.
+  int kb0 = k_begin;
+  for (; kb0 + kTreeKeys < k_end; kb0 += 2 * kTreeKeys) {
     block(kb0, B0{});
-    if (kb0 + kTreeKeys < k_end) block(kb0 + kTreeKeys, B1{});
+    block(kb0 + kTreeKeys, B1{});
   }
+  if (kb0 < k_end) block(kb0, B0{});
 
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
@@ -1250,7 +1274,7 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   auto vt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 3) & 3)) << 3) + (key & 7); };
   auto pt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 2) & 3)) << 3) + (key & 7); };
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, lq = lane >> 4;
   const int b = blockIdx.x / p.kv.Hkv, kvh = blockIdx.x % p.kv.Hkv;
   const int R = p.n_rep;
@@ -1293,8 +1317,6 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   using B1 = std::integral_constant<int, 1>;
   constexpr int kStride = 4 * kTreeKeys;  // the four waves interleave their blocks
   const int kb_first = k_begin + kTreeKeys * wave;
-  fetch(kb_first, B0{});
-  if constexpr (DEPTH == 2) fetch(kb_first + kStride, B1{});
 
   f16x8 qa[KSTEPS];
 #pragma unroll
@@ -1314,6 +1336,11 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   }
 #pragma unroll
   for (int d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The first key blocks are requested after the query rows: loads complete in
+  // order, so the loop's waits for a key block also cover the query loads
+  // (requested last, they made every iteration wait for all loads in flight).
+  fetch(kb_first, B0{});
+  if constexpr (DEPTH == 2) fetch(kb_first + kStride, B1{});
 
   auto block = [&](int kb0, auto bc) {
     constexpr int bf = decltype(bc)::value;
@@ -1375,11 +1402,19 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
     }
   };
-  for (int kb0 = kb_first; kb0 < k_end; kb0 += DEPTH * kStride) {
-    block(kb0, B0{});
-    if constexpr (DEPTH == 2) {
-      if (kb0 + kStride < k_end) block(kb0 + kStride, B1{});
+  // With two buffers both blocks of an iteration run unconditionally and an odd
+  // last block is peeled off, so each buffer keeps its registers across iterations
+  // (a conditional second block made the compiler copy the buffers at the loop
+  // head, waiting for every load in flight).
+  int kb0 = kb_first;
+  if constexpr (DEPTH == 2) {
+    for (; kb0 + kStride < k_end; kb0 += 2 * kStride) {
+      block(kb0, B0{});
+      block(kb0 + kStride, B1{});
     }
+    if (kb0 < k_end) block(kb0, B0{});
+  } else {
+    for (; kb0 < k_end; kb0 += kStride) block(kb0, B0{});
   }
 
   // Merge the four waves' (m, l, o) per query row.
@@ -1469,7 +1504,7 @@ int launch_tree_attention(const f16* q, const KvView& kv, f16* out, int Hq, int 
   p.scale_log2 = kLog2e / sqrtf((float)kv.hd);
   const int rows = T * p.n_rep;
   int rc;
-  if (kv.B == 1 && (kv.hd == 64 || kv.hd == 128)) {
+  if (kv.B == 1 && (kv.hd == 64 || kv.hd == 128) && T <= kv.S) {
     const dim3 grid(kv.Hkv, (rows + kTreeRows - 1) / kTreeRows, n_splits);
     rc = kv.hd == 128 ? launch_tree_mfma<128>(p, grid, s) : launch_tree_mfma<64>(p, grid, s);
   } else {
