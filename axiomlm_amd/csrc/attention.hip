@@ -1289,9 +1289,9 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   // A wave's key blocks are fetched DEPTH ahead into DEPTH register buffers;
   // keys at or past k_end read zeros, so every fetch is issued unconditionally.
   // Two ahead pays for the fp8 cache (C3 shape, 32k keys: 187 -> 163 us).  The
-  // int4 form gains nothing from a second buffer (32k keys: 108 -> 110 us, 1k
-  // keys 12.7 -> 13.5 us), and for fp16 it takes hd 128 past 256 VGPRs, i.e. from
-  // two waves per SIMD to one.
+  // int4 form is slower with a second buffer (32k keys 102 -> 106 us, the ring of
+  // 4096 slots 21.4 -> 23.5 us), and for fp16 it takes hd 128 past 256 VGPRs, i.e.
+  // from two waves per SIMD to one.
   constexpr int DEPTH = KVT == AXM_KV_FP8 ? 2 : 1;
   KvRaw8 kraw[DEPTH][2][KSTEPS], vraw[DEPTH][kVPL];
   // The key / value descriptors end at the split's last key, so fetches past it
