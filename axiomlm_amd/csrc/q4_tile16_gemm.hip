@@ -252,18 +252,24 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
             const f16x8 bi = {sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y, sb.y};
             B[t][q] = __builtin_elementwise_fma(unpack_word(wr[c][t][q], U) - magic, sc, bi);
           }
+        // Every A fragment of the chunk is read from LDS first, then the MFMAs run
+        // k-step by k-step across the token tiles: consecutive MFMAs accumulate
+        // into different tiles instead of waiting on each other, and none waits on
+        // an LDS read issued just before it.
+        f16x8 A[MB][4];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
           const f16* xk = xa + (size_t)16 * mb * G::XROW + c * 128;
-          f16x8 A[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) A[q] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * q));
+          for (int q = 0; q < 4; ++q) A[mb][q] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * q));
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[q], B[t][q], acc[t][mb], 0, 0, 0);
-        }
+            for (int mb = 0; mb < MB; ++mb)
+              acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb][q], B[t][q], acc[t][mb], 0, 0, 0);
       } else if (c < n_here) {
         // The chunk's B fragments are unpacked once for all token tiles.
         f16x8 B[NT][4];
