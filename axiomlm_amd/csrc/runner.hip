@@ -28,6 +28,9 @@
 namespace {
 
 enum { P_TOKEN = 0, P_ROPE = 1, P_WRITE = 2, P_ACTIVE = 3, P_COUNT = 4 };
+// Token rows from which a multi-token step (verify / prompt chunk) runs the
+// multi-token GEMM instead of the decode GEMV per group of up to four rows.
+constexpr int kGemmMinTokens = 3;
 // Byte offset inside the parameter block of the int64 token id used by the
 // current step.
 constexpr int kTokenOffset = 72;
@@ -615,9 +618,10 @@ struct axm_runner {
     return m.fmt != 0 ? run_dense(m, epi, out_rows, c, M, s) : run_gemv(m, epi, out_rows, c, M, s);
   }
 
-  // GEMV over T token rows in launches of at most 4 rows.
+  // GEMV over T token rows in launches of at most 4 rows, or the multi-token GEMM
+  // from kGemmMinTokens rows on.
   int gemv_rows(const Mat& m, int epi, int out_rows, GemvCall c, int T, hipStream_t s) {
-    if (m.w16 != nullptr && T > 4 && c.argmax_keys == nullptr && c.q_dim == 0 &&
+    if (m.w16 != nullptr && T >= kGemmMinTokens && c.argmax_keys == nullptr && c.q_dim == 0 &&
         (epi == Q4_EPI_STORE || epi == Q4_EPI_RESID || epi == Q4_EPI_SWIGLU)) {
       // Multi-token GEMM: up to 64 tokens per weight pass, activations normalized first
       // (into x_norm_out when the caller wants them, else into the norm scratch).
@@ -681,8 +685,8 @@ struct axm_runner {
     // Multi-token GEMMs take normalized activations: there the residual GEMMs
     // (O, down) also write the RMSNorm of the rows they update into `norm` for
     // the next GEMM (fused into their split reduce), instead of a norm launch
-    // per normed GEMM.  Up to 4 tokens keep the GEMVs' fused norm prologue.
-    const bool post = T > 4;
+    // per normed GEMM.  Fewer tokens keep the GEMVs' fused norm prologue.
+    const bool post = T >= kGemmMinTokens;
     if (d.wte_format == 0)
       launch_embed_f16((const f16*)d.wte, idx_dev, nullptr, x, T, D, d.vocab_size, s);
     else

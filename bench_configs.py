@@ -331,7 +331,7 @@ def _c5_loops(runner, cache, tree, prefix, n_steps, vocab, dev, g):
     r = tree_decode_greedy(runner, cache, root, tree, chain_draft, n_steps)
     _loop_line(f"{n_steps}-step tree loop, drafts = the greedy continuation on the first-child chain", T, r, cont)
     reset()
-    prof = measure_tree_latency(runner, cache, budgets=(2, 4, 8, 16, 24, 32, 48, 64))
+    prof = measure_tree_latency(runner, cache, budgets=(2, 3, 4, 6, 8, 16, 24, 32, 48, 64))
     opt = SequoiaDPOptimizer(num_heads=6, max_branches=4, max_budget=64, latency_profile=prof)
     res = opt.solve_optimal_tree()
     print(json.dumps({"config": "C5", "case": "t(N) = verify_tree_step(N) / step, 7B Q4 FP8 prefix 2048",
