@@ -349,7 +349,8 @@ def test_runner_verify_step_chain(dev):
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
     rng = np.random.default_rng(11)
     _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 10).tolist(), dev)
-    for T in (5, 17):
+    # 2 tokens run the decode GEMV per row group, 3 and more the multi-token GEMM.
+    for T in (2, 3, 4, 5, 17):
         seen = cache.total_seen_tokens[0]
         toks = rng.integers(0, cfg.vocab, T).tolist()
         got = runner.verify_step(torch.tensor([toks], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
