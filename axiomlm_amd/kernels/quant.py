@@ -198,9 +198,15 @@ def _qmm_workspace(K: int, N: int, swiglu: bool, device):
     return (torch.empty(n, dtype=torch.uint8, device=device) if n else None), n
 
 
+# Rows from which the tile16 entry points run the multi-token GEMM instead of the decode
+# GEMV (the runner's verify steps switch at the same count).
+TILE16_GEMM_MIN_ROWS = 3
+
+
 def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
     """y = x @ W^T (+ bias) on a tile16 copy made by :func:`repack_q4_marlin_tile16`: the
-    decode GEMV for up to 4 rows, the multi-token GEMM (16 rows per weight pass) beyond."""
+    decode GEMV for one or two rows, the multi-token GEMM (up to 64 rows per weight pass)
+    from three."""
     _lib.require_gpu(x, "qmv_q4_tile16")
     K = x.size(-1)
     M = x.numel() // K
@@ -209,7 +215,7 @@ def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
     b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
     xc = x.contiguous()
     gs = tile16_group_size(sb16, N, K)
-    if M <= 4:
+    if M < TILE16_GEMM_MIN_ROWS:
         _lib.check(_lib.lib().axm_qmv_q4_tile16(_lib.ptr(xc), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b),
                                                 _lib.ptr(y), M, K, N, gs, _lib.stream_of(x.device)),
                    "qmv_q4_tile16")
@@ -248,11 +254,11 @@ def qmv_q4_marlin_swiglu(x, ln_w, eps: float, gu_w, gu_sb, H: int) -> torch.Tens
 
 def qmv_q4_tile16_swiglu(x, ln_w, eps: float, gu16, gusb16, H: int) -> torch.Tensor:
     """:func:`qmv_q4_marlin_swiglu` on the tile16 copy of the packed [W_gate; W_up] (H % 16 == 0);
-    more than 4 rows are normalized first and go through the multi-token GEMM."""
+    from three rows on they are normalized first and go through the multi-token GEMM."""
     K = x.size(-1)
     M = x.numel() // K
     gs = tile16_group_size(gusb16, 2 * int(H), K)
-    if M <= 4:
+    if M < TILE16_GEMM_MIN_ROWS:
         return _swiglu_call(_lib.lib().axm_qmv_q4_tile16_swiglu, "qmv_q4_tile16_swiglu", x, ln_w, eps, gu16, gusb16,
                             H, gs)
     from .ops import fused_rmsnorm
