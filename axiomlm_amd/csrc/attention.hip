@@ -793,8 +793,48 @@ __global__ void attn_reduce_kernel(const float* __restrict__ ws, f16* __restrict
   out[(size_t)row * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
 }
 
+// Up to kReduceRegSplits splits: every thread requests the (m, l) of all splits
+// and its output element of each at once, one round of loads with no barrier,
+// and sums in split order.
+constexpr int kReduceRegSplits = 16;
+__global__ void attn_reduce_reg_kernel(const float* __restrict__ ws, f16* __restrict__ out, int n_splits, int hd) {
+  const int row = blockIdx.x;
+  const int e = threadIdx.x;
+  if (e >= hd) return;
+  const size_t st = 2 + hd;
+  const float* base = ws + (size_t)row * n_splits * st;
+  float mv[kReduceRegSplits], lv[kReduceRegSplits], ov[kReduceRegSplits];
+#pragma unroll
+  for (int sp = 0; sp < kReduceRegSplits; ++sp) {
+    // Splits past n_splits load the last one (always in range) and are masked.
+    const bool in = sp < n_splits;
+    const float* src = base + (size_t)min(sp, n_splits - 1) * st;
+    const float m0 = src[0], l0 = src[1], o0 = src[2 + e];
+    mv[sp] = in ? m0 : kNegBig;
+    lv[sp] = in ? l0 : 0.f;
+    ov[sp] = in ? o0 : 0.f;
+  }
+  float mm = kNegBig;
+#pragma unroll
+  for (int sp = 0; sp < kReduceRegSplits; ++sp) mm = fmaxf(mm, mv[sp]);
+  float ll = 0.f, oo = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < kReduceRegSplits; ++sp) {
+    if (sp < n_splits) {
+      const float a = exp2f(mv[sp] - mm);
+      ll += lv[sp] * a;
+      oo += ov[sp] * a;
+    }
+  }
+  out[(size_t)row * hd + e] = f2h(ll > 0.f ? oo / ll : 0.f);
+}
+
 void launch_attn_reduce(const float* ws, f16* out, int rows, int n_splits, int hd, hipStream_t s) {
   const int threads = ((hd > 64 ? hd : 64) + 63) / 64 * 64;
+  if (n_splits <= kReduceRegSplits) {
+    hipLaunchKernelGGL(attn_reduce_reg_kernel, dim3(rows), dim3(threads), 0, s, ws, out, n_splits, hd);
+    return;
+  }
   hipLaunchKernelGGL(attn_reduce_kernel, dim3(rows), dim3(threads), (n_splits + 1) * sizeof(float), s, ws, out,
                      n_splits, hd);
 }
@@ -1033,6 +1073,24 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 constexpr int kTreeKeys = 32;    // keys per block (the k extent of one P V MFMA)
+
+// LDS tiles of the matrix-core attention kernels, 32 keys per row.
+// vt [dim][key]: V staged transposed.  A staging write covers 16 dims spaced 8
+// apart and 4 (8 for hd 64) consecutive keys; an operand read covers 16
+// consecutive dims, 8 keys each.  Rows r and r + 8 sit on opposite halves of the
+// banks (row r ^ bit 3 of r) and the 8-key groups are XOR-swizzled by bits 1-2 and
+// 4-5 of the dim, so both spread over all banks (the former swizzle by bits 3-4
+// only put a write's 64 lanes on 8 banks).
+// pt [row][key]: P, written 4 rows x 16 keys at a time, read 8 keys per row
+// (2-way at most either way).
+__device__ __forceinline__ int vt_index(int row, int key) {
+  const int prow = row ^ ((row >> 3) & 1);
+  const int swz = ((row >> 1) ^ (row >> 4)) & 3;
+  return prow * kTreeKeys + (((key >> 3) ^ swz) << 3) + (key & 7);
+}
+__device__ __forceinline__ int pt_index(int row, int key) {
+  return row * kTreeKeys + (((key >> 3) ^ ((row >> 2) & 3)) << 3) + (key & 7);
+}
 constexpr int kTreeRows = 64;    // query rows per workgroup (four waves of 16)
 
 template <int KVT, int HD>
@@ -1047,8 +1105,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   // 16-byte operand read still covers whole units of one contiguous 1 KB tile.
   __shared__ __align__(16) f16 vt[HD * kTreeKeys];
   __shared__ __align__(16) f16 pt[4][16 * kTreeKeys];
-  auto vt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 3) & 3)) << 3) + (key & 7); };
-  auto pt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 2) & 3)) << 3) + (key & 7); };
+  auto vt_at = vt_index;
+  auto pt_at = pt_index;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
@@ -1271,8 +1329,8 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   __shared__ __align__(16) f16 vt[4][HD * kTreeKeys];
   __shared__ __align__(16) f16 pt[4][16 * kTreeKeys];
   __shared__ float mrg[4][16][2 + HD];
-  auto vt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 3) & 3)) << 3) + (key & 7); };
-  auto pt_at = [](int row, int key) { return row * kTreeKeys + (((key >> 3) ^ ((row >> 2) & 3)) << 3) + (key & 7); };
+  auto vt_at = vt_index;
+  auto pt_at = pt_index;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, lq = lane >> 4;

@@ -6,7 +6,9 @@
 // Both store uint8 [N][K/4], element 4b+j of a row at bits 2j of byte b, and one
 // (scale) or (scale, bias) fp16 entry per row and 64-column group.
 //
-// Mapping: 4 waves per workgroup, kRows rows per wave; lane l handles groups
+// Mapping: 4 waves per workgroup, ROWS rows per wave (four when the grid still
+// holds two workgroups per CU, else two: fewer workgroups re-stage the activation
+// row); lane l handles groups
 // g = l, l + 64, ... (ITERS of them, K <= ITERS * 4096).  One 16-byte load per
 // (row, group) brings all 64 codes of the group; a lane requests the codes and
 // scales of all its groups before the workgroup stages the activations, so the
@@ -26,7 +28,6 @@
 namespace {
 
 constexpr int kLbThreads = 256;
-constexpr int kLbRows = 2;  // rows per wave
 
 __device__ __forceinline__ uint32_t ternary_to_offset(uint32_t w) {
   const uint32_t lo = w & 0x55555555u;
@@ -43,7 +44,7 @@ __device__ __forceinline__ f16x2 code_pair(uint32_t w, int p) {
 
 // xs: [M][K] fp16, each 16-column block stored as pairs (k, k+8), k = 0..7.
 // gs: [M][K/64] fp32 group sums of x.
-template <int FMT, int M, int ITERS>
+template <int FMT, int M, int ITERS, int kLbRows>
 __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __restrict__ x, int K, int N,
                                                                 const uint8_t* __restrict__ w,
                                                                 const f16* __restrict__ s, const f16* __restrict__ bias,
@@ -180,26 +181,34 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
   }
 }
 
-template <int FMT, int M, int ITERS>
-int lowbit_launch_iters(const f16* x, int K, int N, const uint8_t* w, const f16* s, const f16* bias, f16* y,
-                        hipStream_t st) {
+template <int FMT, int M, int ITERS, int ROWS>
+int lowbit_launch_rows(const f16* x, int K, int N, const uint8_t* w, const f16* s, const f16* bias, f16* y,
+                       hipStream_t st) {
   const size_t smem = (size_t)M * K * sizeof(f16) + (size_t)M * (K / 64) * sizeof(float);
   if (smem > 160 * 1024) {
     axm_set_error("lowbit gemv: K=%d needs %zu B of LDS", K, smem);
     return -2;
   }
   if (smem > 64 * 1024 &&
-      hipFuncSetAttribute((const void*)lowbit_gemv_kernel<FMT, M, ITERS>,
+      hipFuncSetAttribute((const void*)lowbit_gemv_kernel<FMT, M, ITERS, ROWS>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess) {
     (void)hipGetLastError();
     axm_set_error("lowbit gemv: cannot reserve %zu B of LDS", smem);
     return -2;
   }
-  const int rows_per_block = (kLbThreads / 64) * kLbRows;
+  const int rows_per_block = (kLbThreads / 64) * ROWS;
   const int grid = (N + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((lowbit_gemv_kernel<FMT, M, ITERS>), dim3(grid), dim3(kLbThreads), smem, st, x, K, N, w, s,
-                     bias, y);
+  hipLaunchKernelGGL((lowbit_gemv_kernel<FMT, M, ITERS, ROWS>), dim3(grid), dim3(kLbThreads), smem, st, x, K, N, w,
+                     s, bias, y);
   return 0;
+}
+
+template <int FMT, int M, int ITERS>
+int lowbit_launch_iters(const f16* x, int K, int N, const uint8_t* w, const f16* s, const f16* bias, f16* y,
+                        hipStream_t st) {
+  const int wg4 = (N + 4 * (kLbThreads / 64) - 1) / (4 * (kLbThreads / 64));
+  if (wg4 >= 2 * axm_num_cus()) return lowbit_launch_rows<FMT, M, ITERS, 4>(x, K, N, w, s, bias, y, st);
+  return lowbit_launch_rows<FMT, M, ITERS, 2>(x, K, N, w, s, bias, y, st);
 }
 
 // Groups per lane: K / 64 groups over 64 lanes, up to 8 (K <= 32768).
