@@ -1,21 +1,24 @@
 """Benchmark: Q4 7B-shape batch-1 decode on one MI355X.
 
 Workload (BASELINE.json metric "Q4 7B-shape decode tok/s (bs=1, 1 GPU); achieved
-HBM GB/s as % of peak"): a Llama-7B-shape decoder (32 layers, d 4096, 32 heads x
-128, SwiGLU 11008, vocab 32000) with random-init N(0, 0.02) weights packed to
-MARLIN Q4 (group 64, fp16 scale + bias, round-to-nearest), a Q8_G64 embedding
-table, an fp16 KV cache of 4096 slots whose first CTX0 slots hold synthetic
-N(0,1) context.  One step = one greedy decode token through the captured
-whole-step hipGraph (the argmax of step t feeds step t+1 on the device).
+HBM GB/s as % of peak", on the configuration it names: Q4 MARLIN-interleaved
+weights of group 128 with fp16 scales): a Llama-7B-shape decoder (32 layers,
+d 4096, 32 heads x 128, SwiGLU 11008, vocab 32000) with random-init N(0, 0.02)
+weights packed to MARLIN Q4 group 128 (one fp16 scale + bias per 128 columns,
+round-to-nearest), a Q8_G64 embedding table, an fp16 KV cache of 4096 slots whose
+first CTX0 slots hold synthetic N(0,1) context.  One step = one greedy decode token
+through the captured whole-step hipGraph (the argmax of step t feeds step t+1 on
+the device).
 
 Printed JSON line: value = tokens/s; roofline = the runner's fused RMSNorm +
 gate/up GEMV + SwiGLU kernel (tile16 matrix-core layout; the largest per-launch
-weight stream, 50.7 MB) timed live with HIP events on its stream; cpu_baseline = the
-reference's CPU path restated with torch on the host cores (dequantize every weight
-on every call, then F.linear in fp16) on a bounded sample of the same step,
-extrapolated to tokens/s, plus C1 end to end and a C2 layer on the CPU;
-group128_decode = the same decode with group-128 weights (one scale + bias per 128
-columns: 0.53 instead of 0.56 bytes per weight), reported beside the headline.
+weight stream, 47.6 MB at group 128) timed live with HIP events on its stream;
+cpu_baseline = the reference's CPU path restated with torch on the host cores
+(dequantize every weight on every call, then F.linear in fp16) on a bounded sample
+of the same step, extrapolated to tokens/s, plus C1 end to end and a C2 layer on the
+CPU (group-64 packs: the reference's CPU dequantizer has no other group size);
+group64_decode = the same decode with the reference's own group-64 packs (0.56
+instead of 0.53 bytes per weight), reported beside the headline.
 """
 
 from __future__ import annotations
@@ -34,6 +37,7 @@ HBM_PEAK_GBS = 8000.0
 CFG_7B = dict(n_layer=32, d=4096, n_head=32, n_kv_head=32, hd=128, hidden=11008, vocab=32000)
 CTX0 = 128
 MAX_SEQ = 4096
+HEADLINE_GROUP = 128  # BASELINE configs[1] / north_star: MARLIN Q4, group 128, fp16 scales
 def q4_bytes(n_rows: int, k: int, group: int = 64) -> int:
     """MARLIN Q4 bytes: group/2 bytes of nibbles + an fp16 (scale, bias) pair per group."""
     return ((n_rows + 7) // 8) * 8 * (k // group) * (group // 2 + 4)
@@ -134,11 +138,11 @@ def time_decode(runner, cache, steps, warmup, dev, ctx0=CTX0):
     return ms, wall, pos0
 
 
-def time_gate_up_kernel(layers, c, dev, reps=200, n_copies=8):
+def time_gate_up_kernel(layers, c, dev, reps=200, n_copies=8, group=HEADLINE_GROUP):
     """Average duration of the runner's fused RMSNorm + gate/up + SwiGLU launch (tile16
     matrix-core GEMV, 7B shape), timed with HIP events recorded on the stream it is
-    launched on.  Launches rotate over n_copies layers' weights (8 x 50.7 MB) so the
-    stream does not sit in the 256 MB last-level cache."""
+    launched on.  Launches rotate over n_copies layers' weights (8 x 47.6 MB at group
+    128) so the stream does not sit in the 256 MB last-level cache."""
     import torch
 
     from axiomlm_amd import _lib
@@ -155,7 +159,7 @@ def time_gate_up_kernel(layers, c, dev, reps=200, n_copies=8):
         li = i % n_copies
         w16, sb16 = copies[li]
         rc = _lib.lib().axm_qmv_q4_tile16_swiglu(_lib.ptr(x), _lib.ptr(layers["ln2"][li]), 1e-5, _lib.ptr(w16),
-                                                 _lib.ptr(sb16), _lib.ptr(y), 1, d, H, 64, stream)
+                                                 _lib.ptr(sb16), _lib.ptr(y), 1, d, H, group, stream)
         _lib.check(rc, "qmv_q4_tile16_swiglu")
 
     for i in range(10):
@@ -168,16 +172,17 @@ def time_gate_up_kernel(layers, c, dev, reps=200, n_copies=8):
     e1.record(s)
     torch.cuda.synchronize()
     avg_us = e0.elapsed_time(e1) * 1000.0 / reps
-    bytes_per_launch = q4_bytes(2 * H, d) + d * 2 + d * 2 + H * 2  # weights + x + ln_w + y
+    bytes_per_launch = q4_bytes(2 * H, d, group) + d * 2 + d * 2 + H * 2  # weights + x + ln_w + y
     del copies
     return avg_us, bytes_per_launch
 
 
-def gate_up_traffic():
+def gate_up_traffic(group=HEADLINE_GROUP):
     """HBM bytes per gate/up launch measured with rocprofv3 FETCH_SIZE and WRITE_SIZE counters
-    (profiles/gate_up_traffic.json, written from two counter runs and a copy-kernel
-    calibration; the summary beside it gives the commands).  None when absent."""
-    path = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
+    (profiles/gate_up_g128_traffic.json for group 128, gate_up_traffic.json for group 64,
+    written from two counter runs and a copy-kernel calibration; the summary beside each
+    gives the commands).  None when absent."""
+    path = os.path.join(ROOT, "profiles", "gate_up_g128_traffic.json" if group == 128 else "gate_up_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -269,7 +274,8 @@ def cpu_baseline(layers, lnf, c, budget_s=20.0):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{n_done} x one 7B-shape decoder layer (torch CPU: MARLIN Q4 dequantized to fp16 every call, "
+        "sample": (f"{n_done} x one 7B-shape decoder layer (torch CPU: MARLIN Q4 group-64 packs, the reference "
+                   f"CPU dequantizer's only group size, dequantized to fp16 every call, "
                    f"then F.linear; SDPA over {CTX0} fp16 keys) in {per_layer * n_done:.1f} s, extrapolated to "
                    f"32 layers + lm_head"),
         "cpu_model": _cpu_model_name(),
@@ -286,7 +292,10 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-g128", action="store_true", help="skip the group-128 decode line")
+    ap.add_argument("--group", type=int, choices=(64, 128), default=HEADLINE_GROUP,
+                    help="MARLIN group size of the headline decode and the gate/up roofline (default %(default)s)")
+    ap.add_argument("--no-other-group", action="store_true",
+                    help="skip the decode line of the other group size")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--context", type=int, default=CTX0,
                     help="tokens of synthetic context before the first timed step (default %(default)s)")
@@ -317,42 +326,49 @@ def main():
         print(json.dumps({"copy_calibration_bytes_per_copy": n}), flush=True)
         return
     c = CFG_7B
+    G = args.group
+    other = 64 if G == 128 else 128
     t_build = time.perf_counter()
-    runner, cache, layers, lnf = build_model(c, dev)
+    runner, cache, layers, lnf = build_model(c, dev, group_size=G)
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t_build
     print(f"[bench] model built and packed in {t_build:.1f} s", file=sys.stderr, flush=True)
     if args.kernel_only:
-        avg_us, bpl = time_gate_up_kernel(layers, c, dev, reps=20)
+        avg_us, bpl = time_gate_up_kernel(layers, c, dev, reps=20, group=G)
         print(json.dumps({"gate_up_avg_launch_us": round(avg_us, 3), "bytes_per_launch": bpl}), flush=True)
         return
     ms, wall, pos0 = time_decode(runner, cache, args.steps, args.warmup, dev, args.context)
     ms_per_step = ms / args.steps
     tok_s = 1000.0 / ms_per_step
     mean_active = pos0 + (args.steps + 1) / 2.0
-    bytes_tok = step_bytes(c, int(round(mean_active)))
+    bytes_tok = step_bytes(c, int(round(mean_active)), G)
     gbs = bytes_tok / (ms_per_step * 1e-3) / 1e9
     print(f"[bench] decode {ms_per_step:.3f} ms/token, {tok_s:.1f} tok/s, {gbs:.0f} GB/s step-level", file=sys.stderr,
           flush=True)
-    avg_us, bpl = time_gate_up_kernel(layers, c, dev)
+    avg_us, bpl = time_gate_up_kernel(layers, c, dev, group=G)
     ach = bpl / (avg_us * 1e-6) / 1e9
     print(f"[bench] gate/up kernel {avg_us:.2f} us, {ach:.0f} GB/s", file=sys.stderr, flush=True)
     cpu = None
-    if not args.no_cpu_baseline:
+    second = None
+    # The CPU baseline runs on group-64 packs (the reference's CPU dequantizer's format).
+    if G == 64 and not args.no_cpu_baseline:
         cpu = cpu_baseline(layers, lnf, c, args.cpu_budget)
-    g128 = None
-    if not args.no_g128:
+    if not args.no_other_group or (other == 64 and not args.no_cpu_baseline):
         del runner, cache, layers, lnf
         torch.cuda.empty_cache()
-        runner, cache, _, _ = build_model(c, dev, group_size=128)
-        ms128, _, p128 = time_decode(runner, cache, args.steps, args.warmup, dev, args.context)
-        ms128 /= args.steps
-        b128 = step_bytes(c, int(round(p128 + (args.steps + 1) / 2.0)), 128)
-        g128 = {"weights": "MARLIN Q4 group 128 (one fp16 scale+bias per 128 columns), RTN",
-                "tokens_per_s": round(1000.0 / ms128, 2), "ms_per_step": round(ms128, 4),
-                "algorithmic_bytes_per_token": b128,
-                "step_hbm_frac_of_peak": round(b128 / (ms128 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        print(f"[bench] group-128 decode {ms128:.3f} ms/token", file=sys.stderr, flush=True)
+        runner, cache, layers, lnf = build_model(c, dev, group_size=other)
+        if not args.no_other_group:
+            ms2, _, p2 = time_decode(runner, cache, args.steps, args.warmup, dev, args.context)
+            ms2 /= args.steps
+            b2 = step_bytes(c, int(round(p2 + (args.steps + 1) / 2.0)), other)
+            second = {"weights": (f"MARLIN Q4 group {other}" + (" (the reference's pack format)" if other == 64 else "")
+                                  + ", RTN"),
+                      "tokens_per_s": round(1000.0 / ms2, 2), "ms_per_step": round(ms2, 4),
+                      "algorithmic_bytes_per_token": b2,
+                      "step_hbm_frac_of_peak": round(b2 / (ms2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            print(f"[bench] group-{other} decode {ms2:.3f} ms/token", file=sys.stderr, flush=True)
+        if other == 64 and not args.no_cpu_baseline:
+            cpu = cpu_baseline(layers, lnf, c, args.cpu_budget)
     line = {
         "metric": "Q4 7B-shape decode tok/s (bs=1, 1 GPU); achieved HBM GB/s as % of peak",
         "value": round(tok_s, 2),
@@ -369,25 +385,26 @@ def main():
         "config": {
             "workload": "Llama-7B-shape quantized decode step, batch 1 (BASELINE configs[1] shapes, full 32-layer model)",
             "layers": c["n_layer"], "d_model": c["d"], "heads": c["n_head"], "head_dim": c["hd"],
-            "mlp_hidden": c["hidden"], "vocab": c["vocab"], "weights": "MARLIN Q4 group 64 (fp16 scale+bias), RTN",
+            "mlp_hidden": c["hidden"], "vocab": c["vocab"], "weights": f"MARLIN Q4 group {G} (fp16 scale+bias), RTN",
             "embedding": "Q8_G64", "kv_cache": f"fp16, {MAX_SEQ} slots, context {pos0}..{pos0 + args.steps}",
             "algorithmic_bytes_per_token": bytes_tok,
             "step_hbm_gbs": round(gbs, 1),
             "step_hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": "t16_gemv_kernel<1,2,2,8,2> (fused RMSNorm + gate/up Q4 GEMV on matrix cores + SwiGLU, 22016x4096)",
+            "kernel": (f"t16_gemv_kernel<1,2,2,8,2,{'true' if G == 128 else 'false'}> (fused RMSNorm + gate/up Q4 "
+                       f"G{G} GEMV on matrix cores + SwiGLU, 22016x4096)"),
             "bound": "hbm",
             "achieved": round(ach, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": gate_up_traffic(),
+            "traffic": gate_up_traffic(G),
             "avg_launch_us": round(avg_us, 3),
             "algorithmic_bytes_per_launch": bpl,
         },
         "cpu_baseline": cpu,
-        "group128_decode": g128,
+        f"group{other}_decode": second,
     }
     print(json.dumps(line), flush=True)
 
