@@ -1093,6 +1093,42 @@ __device__ __forceinline__ int pt_index(int row, int key) {
 }
 constexpr int kTreeRows = 64;    // query rows per workgroup (four waves of 16)
 
+// Online softmax of one 32-key block for the wave's 16-row D tile: lane (l16, lq)
+// holds the scaled scores s[v][h] of row 4 lq + v, key 16 h + l16 (kNegBig when
+// masked), and the row's running max m[v] (the same in the row's 16 lanes), a
+// per-lane partial l[v] of the row's weight sum and the output accumulators o.
+// The running max moves only when some score of the wave exceeds it by more
+// than kMaxSlack (grows, tested with one ballot); otherwise the weights
+// exp2(s - m) stay below 2^kMaxSlack with no row reduction, and only the
+// rescaling path takes the row maxima.  The caller sums l over each row's 16
+// lanes once after the last block.  The quotient o / l does not depend on m; the
+// fp16 weights P keep their relative precision up to 2^kMaxSlack.
+constexpr float kMaxSlack = 8.f;
+template <int DT>
+__device__ __forceinline__ void softmax_block(const float (&s)[4][2], bool grows, float (&m)[4], float (&l)[4],
+                                              f32x4 (&o)[DT], f16* pt, int lq, int l16) {
+  if (__builtin_amdgcn_ballot_w64(grows)) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float m_new = fmaxf(m[v], row16_max(fmaxf(s[v][0], s[v][1])));
+      const float alpha = fast_exp2(m[v] - m_new);
+      m[v] = m_new;
+      l[v] *= alpha;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) o[d][v] *= alpha;
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float pr[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) pr[h] = s[v][h] == kNegBig ? 0.f : fast_exp2(s[v][h] - m[v]);
+    l[v] += pr[0] + pr[1];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) pt[pt_index(4 * lq + v, 16 * h + l16)] = f2h(pr[h]);
+  }
+}
+
 template <int KVT, int HD>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) tree_mfma_kernel(AttnParams p) {
   constexpr int KSTEPS = HD / 32;  // MFMA k-steps over the head dimension
@@ -1225,35 +1261,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
 #pragma unroll
       for (int c = 0; c < KSTEPS; ++c) sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf[h][c], sc[h], 0, 0, 0);
     }
-    // Mask, scale, online softmax per D-tile row; P to the wave's LDS tile.
-    float alpha[4];
+    // Mask and scale; online softmax per D-tile row; P to the wave's LDS tile.
+    float s2[4][2];
+    bool grows = false;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float s[2];
+    for (int v = 0; v < 4; ++v)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int key = kb0 + 16 * h + l16;
         const bool in_tree = ((mask[v] >> ((key - prefix) & 63)) & 1ull) != 0;
         const bool vis = row_ok[v] && key < k_end && (key < prefix || in_tree);
-        s[h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
+        s2[v][h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
+        grows |= s2[v][h] > m[v] + kMaxSlack;
       }
-      const float m_new = fmaxf(m[v], row16_max(fmaxf(s[0], s[1])));
-      alpha[v] = fast_exp2(m[v] - m_new);
-      float pr[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) pr[h] = s[h] == kNegBig ? 0.f : fast_exp2(s[h] - m_new);
-      l[v] = l[v] * alpha[v] + row16_sum(pr[0] + pr[1]);
-      m[v] = m_new;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) pt[wave][pt_at(4 * lq + v, 16 * h + l16)] = f2h(pr[h]);
-    }
-    // Rescale only when some row's running max moved (alpha == 1 exactly otherwise).
-    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f)) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int d = 0; d < DT; ++d) o[d][v] *= alpha[v];
-    }
+    softmax_block(s2, grows, m, l, o, pt[wave], lq, l16);
     __syncthreads();  // V staged by every wave; P tiles written
     // O += P V: A = P[row l16][keys 8 lq ..], B = V^T[dim 16 d + l16][keys 8 lq ..].
     const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][pt_at(l16, 8 * lq)]);
@@ -1275,6 +1296,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   }
   if (kb0 < k_end) block(kb0, B0{});
 
+#pragma unroll
+  for (int v = 0; v < 4; ++v) l[v] = row16_sum(l[v]);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     if (!row_ok[v]) continue;
@@ -1424,33 +1447,17 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
 #pragma unroll
       for (int c = 0; c < KSTEPS; ++c) sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kf[h][c], sc[h], 0, 0, 0);
     }
-    float alpha[4];
+    float s2[4][2];
+    bool grows = false;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float s2[2];
+    for (int v = 0; v < 4; ++v)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const bool vis = row_ok[v] && kb0 + 16 * h + l16 < k_end;
-        s2[h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
+        s2[v][h] = vis ? sc[h][v] * p.scale_log2 : kNegBig;
+        grows |= s2[v][h] > m[v] + kMaxSlack;
       }
-      const float m_new = fmaxf(m[v], row16_max(fmaxf(s2[0], s2[1])));
-      alpha[v] = fast_exp2(m[v] - m_new);
-      float pr[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) pr[h] = s2[h] == kNegBig ? 0.f : fast_exp2(s2[h] - m_new);
-      l[v] = l[v] * alpha[v] + row16_sum(pr[0] + pr[1]);
-      m[v] = m_new;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) pt[wave][pt_at(4 * lq + v, 16 * h + l16)] = f2h(pr[h]);
-    }
-    // Rescale the output accumulators only when some row's running max moved
-    // (alpha == 1 exactly otherwise, so skipping the multiply changes nothing).
-    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f)) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int d = 0; d < DT; ++d) o[d][v] *= alpha[v];
-    }
+    softmax_block(s2, grows, m, l, o, pt[wave], lq, l16);
     // The wave reads back its own LDS writes: DS operations of one wave complete
     // in order, and the reads below wait for them.
     const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][pt_at(l16, 8 * lq)]);
@@ -1476,6 +1483,8 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   }
 
   // Merge the four waves' (m, l, o) per query row.
+#pragma unroll
+  for (int v = 0; v < 4; ++v) l[v] = row16_sum(l[v]);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int row = 4 * lq + v;
