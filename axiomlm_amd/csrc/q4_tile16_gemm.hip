@@ -4,10 +4,7 @@
 // The decode GEMV (q4_tile16.hip) fills only 1..4 of the 16 token rows of the
 // v_mfma_f32_16x16x32_f16 A operand; here MB tiles of 16 token rows each carry
 // tokens, so every weight chunk (16 rows x 128 k, 1 KB) is read from HBM once
-// for up to 16 MB tokens and its nibble unpack (the B operand) is shared by all
-// of them.  Per chunk and token tile a wave issues the same four MFMAs as the
-// GEMV and applies (scale, bias) of the two 64-groups to the four tokens its
-// lanes hold in the D tile.
+// for up to 16 MB tokens and dequantized once (the B operand) for all of them.
 //
 // A wave owns one unit for the workgroup's K split, so the eight waves of a
 // workgroup cover 128 output rows and share one staged copy of the activations
@@ -28,29 +25,28 @@ constexpr int kGOOB = 0x7FFFFFF0;
 
 // Shapes of one instantiation: MB token tiles (16 MB tokens per weight pass)
 // and RC chunks (128 k) per staged activation range.  Staged rows are padded by
-// 16 bytes (activations) and 16 bytes (group sums) so that the A-operand reads
-// of 16 token rows (and the group-sum reads of the four rows a lane holds) do
-// not all fall into the same LDS banks.
+// 16 bytes so that the A-operand reads of 16 token rows do not all fall into the
+// same LDS banks.
 template <int MB, int RC>
 struct GemmShape {
   static constexpr int TOK = 16 * MB;
   static constexpr int XROW = RC * 128 + 8;             // halves per staged activation row
-  static constexpr int CROW = 2 * RC + 2;               // (corr, sum) pairs per staged row
   static constexpr size_t XS = (size_t)TOK * XROW;      // halves per buffer
-  static constexpr size_t CX = (size_t)TOK * CROW;      // pairs per buffer
   static constexpr int VPR = 16 * RC;                   // 8-element vectors per token row and range
   static constexpr int RPP = kGThreads / VPR;           // token rows staged per pass of the workgroup
   static constexpr int PER = TOK / RPP;                 // vectors staged per thread
-  static constexpr size_t smem = 2 * (XS * sizeof(f16) + CX * sizeof(f32x2));
+  static constexpr size_t smem = 2 * XS * sizeof(f16);
   static_assert(RPP * VPR == kGThreads && PER * RPP == TOK, "staging map");
   static_assert(smem <= 160 * 1024, "LDS");
 };
 
-// The three instantiations by tokens per launch: 16 tokens stage 8 chunks per
-// range (an 8-deep weight ring) and keep the GEMV's arithmetic; 32 and 64
-// tokens stage 4 (LDS holds two 64-token ranges of 4 chunks, 143 KB, and the
-// shorter ring bounds the SwiGLU form's registers) and dequantize each chunk
-// once for all of their token tiles (DQ).
+// The instantiations by tokens per launch: one, two or four 16-token tiles per
+// weight pass, each with 4-chunk activation ranges (LDS holds two 64-token ranges,
+// 133 KB) and every chunk dequantized once for all of its token tiles.  Up to 16
+// tokens once kept the GEMV's arithmetic instead (raw magic-exponent nibbles into
+// the MFMA, per-group corrections from staged activation sums, 8-chunk ranges):
+// the dequantized form is faster there too (7B layer at 4 tokens 69.2 -> 62.2 us,
+// at 16 tokens 72.3 -> 63.7 us).
 // upw = units per wave of the store epilogue at 64 tokens: two adjacent units
 // share each A fragment read from LDS, as the gate / up pair of the SwiGLU form
 // always does.  Measured in the 7B verify step it sped up the QKV and lm_head
@@ -60,7 +56,7 @@ struct GemmCfg {
   int mb, rc, upw;
 };
 GemmCfg gemm_cfg(int M) {
-  if (M <= 16) return {1, 8, 1};
+  if (M <= 16) return {1, 4, 1};
   if (M <= 32) return {2, 4, 1};
   return {4, 4, 2};
 }
@@ -110,22 +106,15 @@ __device__ __forceinline__ void t16g_store(const T16Args& a, int tok, int row, f
 // register slots that range r's chunks free, so the weight stream does not stop
 // at range boundaries.
 //
-// DQ selects how (scale, bias) enter.  DQ = false (the GEMV's arithmetic): the
-// MFMAs take the raw magic-exponent fp16 nibbles, and per 64-group and token
-// the corrections sum_x(magic) and bias * sum_x come from group sums staged
-// with the activations.  DQ = true: every weight is dequantized once per chunk
-// to fp16 q * scale + bias (one rounding, the "dequantize to half, then MMA"
-// of the reference's multi-token kernel) and the MFMAs accumulate the dot
-// products directly, so a token tile costs its four A reads and four MFMAs and
-// no per-tile vector math.
-// G128: one (scale, bias) word per row and chunk (group-128 packs), applied to
-// both 64-column halves.
-template <int NT, int EPI, int MB, int RC, bool DQ, bool G128>
+// Every weight is dequantized once per chunk to fp16 q * scale + bias (one
+// rounding, the "dequantize to half, then MMA" of the reference's multi-token
+// kernel) and the MFMAs accumulate the dot products directly, so a token tile
+// costs its four A reads and four MFMAs and no per-tile vector math.
+template <int NT, int EPI, int MB, int RC, bool G128>
 __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   using G = GemmShape<MB, RC>;
   extern __shared__ __align__(16) unsigned char smem[];
   f16* xs0 = reinterpret_cast<f16*>(smem);                     // [2][TOK][XROW]
-  f32x2* cx0 = reinterpret_cast<f32x2*>(xs0 + 2 * G::XS);      // [2][TOK][CROW]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -188,24 +177,9 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
   };
   auto stage_store = [&](int buf) {
     f16* xs = xs0 + buf * G::XS;
-    f32x2* cx = cx0 + buf * G::CX;
 #pragma unroll
-    for (int i = 0; i < G::PER; ++i) {
-      const int tok = stok + G::RPP * i, vi = svi;
-      float corr = 0.f, sum = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8 * !DQ; ++e) {
-        const float f = h2f(xv[i][e]);
-        sum += f;
-        corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
-      }
-      *reinterpret_cast<f16x8*>(xs + (size_t)tok * G::XROW + 8 * vi) = xv[i];
-      if (!DQ) {
-        corr = group_sum<8>(corr);
-        sum = group_sum<8>(sum);
-        if ((tid & 7) == 0) cx[tok * G::CROW + (vi >> 3)] = f32x2{corr, sum};
-      }
-    }
+    for (int i = 0; i < G::PER; ++i)
+      *reinterpret_cast<f16x8*>(xs + (size_t)(stok + G::RPP * i) * G::XROW + 8 * svi) = xv[i];
   };
 
   // Weights of range 0 first, then its activations (both one latency away).
@@ -228,7 +202,6 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
     const bool more = r + 1 < n_ranges;
     if (more) stage_load(r + 1);
     const f16* xs = xs0 + (r & 1) * G::XS;
-    const f32x2* cx = cx0 + (r & 1) * G::CX;
     // A operand: token 16 mb + lane % 16 (rows past M are zeros), k sub-block lane / 16.
     const f16* xa = xs + (size_t)(lane & 15) * G::XROW + 8 * kq;
     // Only the last range of a split can be partial (uniform across the
@@ -237,7 +210,7 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
     const int n_here = min(RC, kbN - r * RC);
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
-      if (c < n_here && DQ) {
+      if (c < n_here) {
         // Word q of a lane holds 8 k of group q / 2; its unpacked elements are
         // 1024 + n or 64 + n (pattern of unpack_word), subtracted exactly.
         const f16x8 magic = {(f16)1024.f, (f16)1024.f, (f16)64.f, (f16)64.f,
@@ -270,45 +243,6 @@ __global__ void __launch_bounds__(kGThreads) t16g_kernel(T16Args a) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
               acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb][q], B[t][q], acc[t][mb], 0, 0, 0);
-      } else if (c < n_here) {
-        // The chunk's B fragments are unpacked once for all token tiles.
-        f16x8 B[NT][4];
-        f16x2 sb[NT][2];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) B[t][q] = unpack_word(wr[c][t][q], U);
-          sb[t][0] = as_h2(sr[c][t][0]);
-          sb[t][1] = as_h2(sr[c][t][1]);
-        }
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const f16* xk = xa + (size_t)16 * mb * G::XROW + c * 128;
-          f16x8 A[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) A[q] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xk + 32 * q));
-          f32x4 cxv[4];
-#pragma unroll
-          for (int vi = 0; vi < 4; ++vi)
-            cxv[vi] = *reinterpret_cast<const f32x4*>(cx + (16 * mb + 4 * kq + vi) * G::CROW + 2 * c);
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-            f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[t][0], z4, 0, 0, 0);
-            f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], B[t][2], z4, 0, 0, 0);
-            d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], B[t][1], d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], B[t][3], d1, 0, 0, 0);
-#pragma unroll
-            for (int vi = 0; vi < 4; ++vi) {
-              float x = acc[t][mb][vi];
-              x = __builtin_fmaf(h2f(sb[t][0].x), d0[vi] - cxv[vi][0], x);
-              x = __builtin_fmaf(h2f(sb[t][0].y), cxv[vi][1], x);
-              x = __builtin_fmaf(h2f(sb[t][1].x), d1[vi] - cxv[vi][2], x);
-              x = __builtin_fmaf(h2f(sb[t][1].y), cxv[vi][3], x);
-              acc[t][mb][vi] = x;
-            }
-          }
-        }
       }
       load(r + 1, c);
     }
@@ -425,39 +359,39 @@ bool post_norm_fusable(const T16Args& a) {
   return a.N % 4 == 0 && a.N <= 4 * kRnThreads * kRnVec && a.ldr % 4 == 0 && (al & 7) == 0;
 }
 
-template <int NT, int EPI, int MB, int RC, bool DQ, bool G128>
+template <int NT, int EPI, int MB, int RC, bool G128>
 void t16g_launch_group(const T16Args& a, dim3 grid, hipStream_t s) {
   using G = GemmShape<MB, RC>;
   static bool set = false;
   if (!set) {
     set = true;
-    if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI, MB, RC, DQ, G128>,
+    if (hipFuncSetAttribute((const void*)t16g_kernel<NT, EPI, MB, RC, G128>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)G::smem) != hipSuccess)
       (void)hipGetLastError();
   }
-  hipLaunchKernelGGL((t16g_kernel<NT, EPI, MB, RC, DQ, G128>), grid, dim3(kGThreads), G::smem, s, a);
+  hipLaunchKernelGGL((t16g_kernel<NT, EPI, MB, RC, G128>), grid, dim3(kGThreads), G::smem, s, a);
 }
 
-template <int NT, int EPI, int MB, int RC, bool DQ>
+template <int NT, int EPI, int MB, int RC>
 void t16g_launch_shape(const T16Args& a, dim3 grid, hipStream_t s) {
   if (a.g128)
-    t16g_launch_group<NT, EPI, MB, RC, DQ, true>(a, grid, s);
+    t16g_launch_group<NT, EPI, MB, RC, true>(a, grid, s);
   else
-    t16g_launch_group<NT, EPI, MB, RC, DQ, false>(a, grid, s);
+    t16g_launch_group<NT, EPI, MB, RC, false>(a, grid, s);
 }
 
-// The (MB, RC, DQ, units per wave) shapes here are the ones gemm_cfg returns.
+// The (MB, RC, units per wave) shapes here are the ones gemm_cfg returns.
 template <int EPI>
 void t16g_launch_epi(const T16Args& a, GemmCfg cfg, dim3 grid, hipStream_t s) {
   constexpr int P = EPI == Q4_EPI_SWIGLU ? 2 : 1;  // tiles per unit
   if (cfg.mb == 1)
-    t16g_launch_shape<P, EPI, 1, 8, false>(a, grid, s);
+    t16g_launch_shape<P, EPI, 1, 4>(a, grid, s);
   else if (cfg.mb == 2)
-    t16g_launch_shape<P, EPI, 2, 4, true>(a, grid, s);
+    t16g_launch_shape<P, EPI, 2, 4>(a, grid, s);
   else if (gemm_upw(EPI, cfg) == 1)
-    t16g_launch_shape<P, EPI, 4, 4, true>(a, grid, s);
+    t16g_launch_shape<P, EPI, 4, 4>(a, grid, s);
   else
-    t16g_launch_shape<2, EPI, 4, 4, true>(a, grid, s);
+    t16g_launch_shape<2, EPI, 4, 4>(a, grid, s);
 }
 
 size_t gemm_ws_bytes_cfg(int KB, int n_units, int epi, GemmCfg cfg) {
