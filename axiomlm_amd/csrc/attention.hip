@@ -391,6 +391,53 @@ __device__ __forceinline__ KvRaw8 kv_fetch8(const KvHead& h, int slot, int hd, i
     f.sc = __builtin_amdgcn_raw_buffer_load_b16(h.scales, ok ? (slot * (hd / 64) + e0 / 64) * 2 : kOff, 0, 0);
   return f;
 }
+// NC consecutive 8-element chunks [e0, e0 + 8 NC) of a cache row (all inside one
+// 64-element scale group) in as few loads as their bytes allow (int4 with NC 4:
+// one 16-byte load and one scale load instead of four of each).
+template <int KVT, int NC>
+struct KvRun {
+  static constexpr int kDw8 = KVT == AXM_KV_FP16 ? 4 : (KVT == AXM_KV_FP8 ? 2 : 1);  // dwords per chunk
+  static constexpr int kDw = NC * kDw8;
+  uint32_t w[kDw];
+  uint32_t sc;  // fp16 bits in the low half
+  __device__ __forceinline__ KvRaw8 chunk(int c) const {
+    KvRaw8 f;
+    f.r = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int d = 0; d < kDw8; ++d) f.r[d] = w[c * kDw8 + d];
+    f.sc = sc;
+    return f;
+  }
+};
+template <int KVT, int NC>
+__device__ __forceinline__ KvRun<KVT, NC> kv_fetch_run(const KvHead& h, int slot, int hd, int e0, bool ok = true) {
+  using Run = KvRun<KVT, NC>;
+  constexpr int kOff = 0x7FFFFFF0;
+  const int eb = KVT == AXM_KV_FP16 ? 2 * e0 : (KVT == AXM_KV_FP8 ? e0 : e0 / 2);
+  const int off = ok ? slot * kv_row_bytes<KVT>(hd) + eb : kOff;
+  Run r;
+  if constexpr (Run::kDw % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < Run::kDw / 4; ++i) {
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(h.codes, off + 16 * i, 0, 0));
+      r.w[4 * i + 0] = v.x;
+      r.w[4 * i + 1] = v.y;
+      r.w[4 * i + 2] = v.z;
+      r.w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (Run::kDw == 2) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(h.codes, off, 0, 0));
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else {
+    r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(h.codes, off, 0, 0);
+  }
+  r.sc = 0u;
+  if (KVT != AXM_KV_FP16)
+    r.sc = __builtin_amdgcn_raw_buffer_load_b16(h.scales, ok ? (slot * (hd / 64) + e0 / 64) * 2 : kOff, 0, 0);
+  return r;
+}
+
 // Position e of an f16x8 from kv_half8 holds element kv_dim_of<KVT>(e) of the chunk:
 // the int4 form delivers the even elements 0, 2, 4, 6, then the odd ones.
 template <int KVT>
@@ -1134,7 +1181,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   constexpr int KSTEPS = HD / 32;  // MFMA k-steps over the head dimension
   constexpr int DT = HD / 16;      // 16-wide output dimension tiles
   constexpr int kVec = kTreeKeys * HD / 8;        // 8-element V vectors per key block
-  constexpr int kVPT = (kVec + 255) / 256;        // of them per thread
   // V block, dim-major, and per wave the P tile of its 16 rows.  Both store
   // row r's 8-key unit u at unit u ^ swz(r), so that the transposing 2-byte
   // writes of rows 8 (V) or 4 (P) apart fall in different banks, while a
@@ -1169,11 +1215,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   };
 
   // Key / value fetches of one block into register buffer b (two blocks are in
-  // flight): this lane's K B-operand fragments (keys kb0 + 16 h + l16, dims
-  // 32 c + 8 lq) and this thread's V vectors.  Keys at or past k_end read zeros
-  // (out-of-range offsets), so every fetch is issued unconditionally and the
-  // compiler counts the loads in flight exactly.
-  KvRaw8 kraw[2][2][KSTEPS], vraw[2][kVPT];
+  // flight), each a run of consecutive chunks of one cache row: this lane's K
+  // B-operand fragments (keys kb0 + 16 h + l16, dims [HD/4 lq, HD/4 (lq + 1)), of
+  // which k-step c takes dims HD/4 lq + 8 c (+ 0..7), the query using the same dim
+  // order) and this thread's V run (kVRun chunks, key threadIdx / kRunsPerKey).  Keys
+  // at or past k_end read zeros (out-of-range offsets), so every fetch is issued
+  // unconditionally and the compiler counts the loads in flight exactly.
+  constexpr int kVRun = kVec / 256;          // V chunks per thread
+  constexpr int kRunsPerKey = HD / 8 / kVRun;
+  static_assert(kVec % 256 == 0, "one V run per thread");
+  KvRun<KVT, KSTEPS> krun[2][2];
+  KvRun<KVT, kVRun> vrun[2];
   const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, p.kv.S, HD);
   const KvHead vh = kv_head<KVT>(p.kv.v, p.kv.vs, head_row0, p.kv.S, HD);
   auto fetch = [&](int kb0, auto bc) {
@@ -1181,21 +1233,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int key = kb0 + 16 * h + l16;
-      const int slot = slot_of(key);
-#pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) kraw[b][h][c] = kv_fetch8<KVT>(kh, slot, HD, 32 * c + 8 * lq, key < k_end);
+      krun[b][h] = kv_fetch_run<KVT, KSTEPS>(kh, slot_of(key), HD, (HD / 4) * lq, key < k_end);
     }
-#pragma unroll
-    for (int i = 0; i < kVPT; ++i) {
-      const int j = i * 256 + threadIdx.x;
-      const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
-      const int key = kb0 + kk;
-      vraw[b][i] = kv_fetch8<KVT>(vh, slot_of(key), HD, e0, j < kVec && key < k_end);
-    }
+    const int key = kb0 + threadIdx.x / kRunsPerKey;
+    vrun[b] = kv_fetch_run<KVT, kVRun>(vh, slot_of(key), HD, 8 * kVRun * (threadIdx.x % kRunsPerKey), key < k_end);
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  // A operand: query row row0 + l16, dims 32 c + 8 lq .. +7.
+  // A operand: query row row0 + l16, dims HD/4 lq + 8 c .. +7.
   f16x8 qa[KSTEPS];
   {
     const int r = row0 + l16;
@@ -1203,7 +1248,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
     for (int c = 0; c < KSTEPS; ++c) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) qa[c][i] = f16(0);
-      if (r < R) qa[c] = kv_order8<KVT>(*reinterpret_cast<const f16x8*>(p.q + (size_t)grow(r) * HD + 32 * c + 8 * lq));
+      if (r < R)
+        qa[c] = kv_order8<KVT>(*reinterpret_cast<const f16x8*>(p.q + (size_t)grow(r) * HD + (HD / 4) * lq + 8 * c));
     }
   }
   // D-tile rows of this lane: row0 + 4 lq + v.
@@ -1231,27 +1277,26 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   // two ahead.
   auto block = [&](int kb0, auto bc) {
     constexpr int b = decltype(bc)::value;
-    f16x8 kf[2][KSTEPS], vv[kVPT];
+    f16x8 kf[2][KSTEPS], vv[kVRun];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(kraw[b][h][c]);
+      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(krun[b][h].chunk(c));
 #pragma unroll
-    for (int i = 0; i < kVPT; ++i) vv[i] = kv_half8<KVT>(vraw[b][i]);
+    for (int c = 0; c < kVRun; ++c) vv[c] = kv_half8<KVT>(vrun[b].chunk(c));
     // The refill is not scheduled above the conversions: the old and new contents of
     // buffer b then never overlap and keep the same registers across iterations
     // (otherwise the loop head copied the new ones, waiting for every load).
     __builtin_amdgcn_sched_barrier(0);
     fetch(kb0 + 2 * kTreeKeys, bc);
-    // Stage V transposed: vector j covers key kb0 + j / (HD/8), dims 8 (j % (HD/8)).
+    // Stage V transposed: this thread's run covers key kb0 + tid / kRunsPerKey,
+    // dims 8 kVRun (tid % kRunsPerKey) onwards.
+    {
+      const int kk = threadIdx.x / kRunsPerKey, e0 = 8 * kVRun * (threadIdx.x % kRunsPerKey);
 #pragma unroll
-    for (int i = 0; i < kVPT; ++i) {
-      const int j = i * 256 + threadIdx.x;
-      if (kVec % 256 == 0 || j < kVec) {
-        const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
+      for (int c = 0; c < kVRun; ++c)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vt[vt_at(e0 + kv_dim_of<KVT>(e), kk)] = vv[i][e];
-      }
+        for (int e = 0; e < 8; ++e) vt[vt_at(e0 + 8 * c + kv_dim_of<KVT>(e), kk)] = vv[c][e];
     }
     // S = Q K^T for the block's two 16-key halves.
     f32x4 sc[2];
@@ -1374,7 +1419,13 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   // 4096 slots 21.4 -> 23.5 us), and for fp16 it takes hd 128 past 256 VGPRs, i.e.
   // from two waves per SIMD to one.
   constexpr int DEPTH = KVT == AXM_KV_FP8 ? 2 : 1;
-  KvRaw8 kraw[DEPTH][2][KSTEPS], vraw[DEPTH][kVPL];
+  // A lane fetches runs of KSTEPS chunks (a quarter of a row, HD / 4 elements): the
+  // keys of a half-block as dims [HD/4 lq, HD/4 (lq + 1)) of key l16, so k-step c
+  // pairs dims HD/4 lq + 8 c (+ 0..7) with the same dims of the query (the MFMA's
+  // k order is a permutation of the head dims, the same for both operands); the
+  // values as runs j = i 64 + lane, key j / 4, dims HD/4 (j % 4).
+  constexpr int kRuns = kVPL / KSTEPS;  // value runs per lane and block
+  KvRun<KVT, KSTEPS> krun[DEPTH][2], vrun[DEPTH][kRuns];
   // The key / value descriptors end at the split's last key, so fetches past it
   // read zeros without a per-chunk select.
   const KvHead kh = kv_head<KVT>(p.kv.k, p.kv.ks, head_row0, k_end, HD);
@@ -1382,16 +1433,11 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   auto fetch = [&](int kb0, auto bc) {
     constexpr int bf = decltype(bc)::value;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int key = kb0 + 16 * h + l16;
+    for (int h = 0; h < 2; ++h) krun[bf][h] = kv_fetch_run<KVT, KSTEPS>(kh, kb0 + 16 * h + l16, HD, (HD / 4) * lq);
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) kraw[bf][h][c] = kv_fetch8<KVT>(kh, key, HD, 32 * c + 8 * lq, true);
-    }
-#pragma unroll
-    for (int i = 0; i < kVPL; ++i) {
+    for (int i = 0; i < kRuns; ++i) {
       const int j = i * 64 + lane;
-      const int key = kb0 + j / (HD / 8), e0 = 8 * (j % (HD / 8));
-      vraw[bf][i] = kv_fetch8<KVT>(vh, key, HD, e0, true);
+      vrun[bf][i] = kv_fetch_run<KVT, KSTEPS>(vh, kb0 + j / 4, HD, (HD / 4) * (j % 4));
     }
   };
   using B0 = std::integral_constant<int, 0>;
@@ -1404,7 +1450,8 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   for (int c = 0; c < KSTEPS; ++c) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) qa[c][i] = f16(0);
-    if (l16 < R) qa[c] = kv_order8<KVT>(*reinterpret_cast<const f16x8*>(p.q + (qrow0 + l16) * HD + 32 * c + 8 * lq));
+    if (l16 < R)
+      qa[c] = kv_order8<KVT>(*reinterpret_cast<const f16x8*>(p.q + (qrow0 + l16) * HD + (HD / 4) * lq + 8 * c));
   }
   bool row_ok[4];
   float m[4], l[4];
@@ -1425,20 +1472,24 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
 
   auto block = [&](int kb0, auto bc) {
     constexpr int bf = decltype(bc)::value;
-    f16x8 kf[2][KSTEPS], vv[kVPL];
+    f16x8 kf[2][KSTEPS], vv[kRuns][KSTEPS];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(kraw[bf][h][c]);
+      for (int c = 0; c < KSTEPS; ++c) kf[h][c] = kv_half8<KVT>(krun[bf][h].chunk(c));
 #pragma unroll
-    for (int i = 0; i < kVPL; ++i) vv[i] = kv_half8<KVT>(vraw[bf][i]);
+    for (int i = 0; i < kRuns; ++i)
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) vv[i][c] = kv_half8<KVT>(vrun[bf][i].chunk(c));
     fetch(kb0 + DEPTH * kStride, bc);
 #pragma unroll
-    for (int i = 0; i < kVPL; ++i) {
+    for (int i = 0; i < kRuns; ++i) {
       const int j = i * 64 + lane;
-      const int kk = j / (HD / 8), e0 = 8 * (j % (HD / 8));
+      const int kk = j / 4, e0 = (HD / 4) * (j % 4);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[wave][vt_at(e0 + kv_dim_of<KVT>(e), kk)] = vv[i][e];
+      for (int c = 0; c < KSTEPS; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[wave][vt_at(e0 + 8 * c + kv_dim_of<KVT>(e), kk)] = vv[i][c][e];
     }
     f32x4 sc[2];
 #pragma unroll
