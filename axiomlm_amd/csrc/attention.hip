@@ -1415,9 +1415,9 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   // A wave's key blocks are fetched DEPTH ahead into DEPTH register buffers;
   // keys at or past k_end read zeros, so every fetch is issued unconditionally.
   // Two ahead pays for the fp8 cache (C3 shape, 32k keys: 187 -> 163 us).  The
-  // int4 form is slower with a second buffer (32k keys 102 -> 106 us, the ring of
-  // 4096 slots 21.4 -> 23.5 us), and for fp16 it takes hd 128 past 256 VGPRs, i.e.
-  // from two waves per SIMD to one.
+  // int4 form is slower with a second buffer (with one-load runs: 32k keys 86.9 ->
+  // 92.8 us, the ring of 4096 slots 17.9 -> 19.3 us), and for fp16 it takes hd 128
+  // past 256 VGPRs, i.e. from two waves per SIMD to one.
   constexpr int DEPTH = KVT == AXM_KV_FP8 ? 2 : 1;
   // A lane fetches runs of KSTEPS chunks (a quarter of a row, HD / 4 elements): the
   // keys of a half-block as dims [HD/4 lq, HD/4 (lq + 1)) of key l16, so k-step c
