@@ -56,8 +56,21 @@ __global__ void __launch_bounds__(256) set_params_kernel(int* params, const int6
   __shared__ unsigned long long red[4];
   int64_t tok = 0;
   if (idx_dev == nullptr && tok_host < 0) {
+    // Sixteen keys per thread and pass, all requested before any is compared
+    // (keys past n_keys read 0, below every real key).
+    constexpr int kPerThread = 16;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)keys, (short)0, n_keys * 8, 0x00020000);
     unsigned long long best = 0ull;
-    for (int i = threadIdx.x; i < n_keys; i += 256) best = keys[i] > best ? keys[i] : best;
+    for (int base = 0; base < n_keys; base += 256 * kPerThread) {
+      unsigned long long k[kPerThread];
+#pragma unroll
+      for (int u = 0; u < kPerThread; ++u)
+        k[u] = __builtin_bit_cast(unsigned long long,
+                                  __builtin_amdgcn_raw_buffer_load_b64(rk, (base + u * 256 + threadIdx.x) * 8, 0, 0));
+#pragma unroll
+      for (int u = 0; u < kPerThread; ++u) best = k[u] > best ? k[u] : best;
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const unsigned long long other = __shfl_xor(best, o, 64);
