@@ -189,17 +189,11 @@ __global__ void __launch_bounds__(kKvWriteWaves * 64)
 // holds rotation pair l.  Query rows are rotated at pos_dev[t] into q
 // [T][q_dim], key rows rotated and value rows as they are go to slot
 // (write_pos + t) % S (the arithmetic of the RoPE kernel and of kv_row_store).
-__global__ void __launch_bounds__(kKvWriteWaves * 64)
-    rope_kv_row_kernel(KvView kv, const f16* __restrict__ qkv, int Hq, int T, const float* __restrict__ freqs,
-                       const int* __restrict__ pos_dev, f16* __restrict__ q, int write_pos) {
+__device__ __forceinline__ void rope_kv_row(const KvView& kv, int Hq, int t, int r, int lane, f16x2 v,
+                                            const float* __restrict__ freqs, const int* __restrict__ pos_dev,
+                                            f16* __restrict__ q, int write_pos) {
   constexpr int HD = 128;
-  const int lane = threadIdx.x & 63;
-  const int rows = Hq + 2 * kv.Hkv;
-  const int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
-  if (idx >= T * rows) return;
-  const int t = idx / rows, r = idx % rows;
-  const int q_dim = Hq * HD, kv_dim = kv.Hkv * HD;
-  const f16x2 v = *reinterpret_cast<const f16x2*>(qkv + (size_t)t * (q_dim + 2 * kv_dim) + (size_t)r * HD + 2 * lane);
+  const int q_dim = Hq * HD;
   kv_hvec<2> out;
   if (r < Hq + kv.Hkv) {
     const float* f = freqs + ((size_t)pos_dev[t] * (HD / 2) + lane) * 2;
@@ -216,6 +210,51 @@ __global__ void __launch_bounds__(kKvWriteWaves * 64)
   const int which = r < Hq + kv.Hkv ? 0 : 1;
   const int h = r - Hq - which * kv.Hkv;
   kv_row_store<2>(kv, which, h, (write_pos + t) % kv.S, lane, out);
+}
+
+__global__ void __launch_bounds__(kKvWriteWaves * 64)
+    rope_kv_row_kernel(KvView kv, const f16* __restrict__ qkv, int Hq, int T, const float* __restrict__ freqs,
+                       const int* __restrict__ pos_dev, f16* __restrict__ q, int write_pos) {
+  constexpr int HD = 128;
+  const int lane = threadIdx.x & 63;
+  const int rows = Hq + 2 * kv.Hkv;
+  const int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
+  if (idx >= T * rows) return;
+  const int t = idx / rows, r = idx % rows;
+  const int qkv_dim = (Hq + 2 * kv.Hkv) * HD;
+  const f16x2 v = *reinterpret_cast<const f16x2*>(qkv + (size_t)t * qkv_dim + (size_t)r * HD + 2 * lane);
+  rope_kv_row(kv, Hq, t, r, lane, v, freqs, pos_dev, q, write_pos);
+}
+
+// The same, with the row taken from the K-split partial sums of the multi-token
+// QKV GEMM (part [split][token (stride tok_stride)][part_cols] fp32): the splits
+// are summed in order and rounded with the GEMM store epilogue's arithmetic (fp16
+// of the sum, then fp16 of that plus the bias), so the row equals the one the split
+// reduce would have stored; the reduce launch is saved.
+__global__ void __launch_bounds__(kKvWriteWaves * 64)
+    reduce_rope_kv_row_kernel(KvView kv, const float* __restrict__ part, int n_splits, int tok_stride,
+                              int part_cols, const f16* __restrict__ bias, int Hq, int T,
+                              const float* __restrict__ freqs, const int* __restrict__ pos_dev, f16* __restrict__ q,
+                              int write_pos) {
+  constexpr int HD = 128;
+  const int lane = threadIdx.x & 63;
+  const int rows = Hq + 2 * kv.Hkv;
+  const int idx = blockIdx.x * kKvWriteWaves + (threadIdx.x >> 6);
+  if (idx >= T * rows) return;
+  const int t = idx / rows, r = idx % rows;
+  const int col = r * HD + 2 * lane;
+  float v0 = 0.f, v1 = 0.f;
+  for (int sp = 0; sp < n_splits; ++sp) {
+    const float2 pv = *reinterpret_cast<const float2*>(part + ((size_t)sp * tok_stride + t) * part_cols + col);
+    v0 += pv.x;
+    v1 += pv.y;
+  }
+  f16 h0 = f2h(v0), h1 = f2h(v1);
+  if (bias != nullptr) {
+    h0 = f2h(h2f(h0) + h2f(bias[col]));
+    h1 = f2h(h2f(h1) + h2f(bias[col + 1]));
+  }
+  rope_kv_row(kv, Hq, t, r, lane, f16x2{h0, h1}, freqs, pos_dev, q, write_pos);
 }
 
 // Fused bias + RoPE + KV-cache write of T tokens (rope_kv_cache_write_half_kernel,
@@ -971,6 +1010,23 @@ int launch_rope_kv_write(const KvView& kv, const f16* qkv, int Hq, int T, const 
   const int items = T * (Hq + 2 * kv.Hkv);
   hipLaunchKernelGGL(rope_kv_row_kernel, dim3((unsigned)((items + kKvWriteWaves - 1) / kKvWriteWaves)),
                      dim3(kKvWriteWaves * 64), 0, s, kv, qkv, Hq, T, freqs, pos_dev, q, write_pos);
+  return 0;
+}
+
+int launch_reduce_rope_kv_write(const KvView& kv, const float* part, int n_splits, int tok_stride, int part_cols,
+                                const f16* bias, int Hq, int T, const float* freqs, const int* pos_dev, f16* q,
+                                int write_pos, hipStream_t s) {
+  const int qkv_dim = (Hq + 2 * kv.Hkv) * kv.hd;
+  if (kv.hd != 128 || ((uintptr_t)q & 3) != 0 || n_splits < 1 || tok_stride < T || part_cols < qkv_dim ||
+      (part_cols & 1) != 0 || ((uintptr_t)part & 7) != 0) {
+    axm_set_error("reduce_rope_kv_write: head size %d (128), %d splits, token stride %d, %d partial columns",
+                  kv.hd, n_splits, tok_stride, part_cols);
+    return -2;
+  }
+  const int items = T * (Hq + 2 * kv.Hkv);
+  hipLaunchKernelGGL(reduce_rope_kv_row_kernel, dim3((unsigned)((items + kKvWriteWaves - 1) / kKvWriteWaves)),
+                     dim3(kKvWriteWaves * 64), 0, s, kv, part, n_splits, tok_stride, part_cols, bias, Hq, T, freqs,
+                     pos_dev, q, write_pos);
   return 0;
 }
 

@@ -50,6 +50,12 @@ int launch_kv_write(const KvView& kv, const f16* k_rows, const f16* v_rows, int 
 // launch; head size 128 only (-2 otherwise).
 int launch_rope_kv_write(const KvView& kv, const f16* qkv, int Hq, int T, const float* freqs, const int* pos_dev,
                          f16* q, int write_pos, hipStream_t s);
+// The same, with the qkv rows summed from the K-split partials of the multi-token
+// QKV GEMM (part [split][token, stride tok_stride][part_cols] fp32) and rounded as
+// the GEMM's store epilogue with the bias would (replaces that split reduce).
+int launch_reduce_rope_kv_write(const KvView& kv, const float* part, int n_splits, int tok_stride, int part_cols,
+                                const f16* bias, int Hq, int T, const float* freqs, const int* pos_dev, f16* q,
+                                int write_pos, hipStream_t s);
 
 // Split-KV decode attention over slots [0, active_len) of every batch entry.
 // q: [B][Hq][hd] fp16, out: [B][Hq][hd] fp16.  ws: workspace of

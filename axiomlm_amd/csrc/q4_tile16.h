@@ -55,6 +55,11 @@ struct T16Args {
   // of the next normed GEMM), fused into the split reduce when K is split.
   const f16* post_ln_w;
   f16* post_norm_out;
+  // Multi-token GEMM, store epilogue: when set (a host array of 3), a K-split launch
+  // leaves its partials in part_ws unreduced and reports {splits, token stride,
+  // part_cols} here for a consumer that reduces them itself; {0, 0, 0} when the
+  // GEMM was not split and stored its rows.
+  int* split_info;
 };
 
 // Largest K (activation length) the tile16 GEMV stages.

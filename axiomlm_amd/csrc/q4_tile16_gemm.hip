@@ -455,6 +455,15 @@ int t16_gemm_launch(T16Args a, int M, int epi, float* ws, size_t ws_bytes, hipSt
       break;
   }
   const int ts = 16 * cfg.mb;
+  if (a.split_info != nullptr) {
+    a.split_info[0] = a.split_info[1] = a.split_info[2] = 0;
+    if (splits > 1 && epi == Q4_EPI_STORE && a.post_ln_w == nullptr) {
+      a.split_info[0] = splits;
+      a.split_info[1] = ts;
+      a.split_info[2] = a.part_cols;
+      return 0;
+    }
+  }
   if (a.post_ln_w != nullptr) {
     // Residual rows then their RMSNorm: one fused launch over the partials, or
     // the norm kernel after an unsplit GEMM (and as the general fallback).

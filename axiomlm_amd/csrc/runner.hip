@@ -218,6 +218,8 @@ struct GemvCall {
   // post_norm_out, the input of the next normed GEMM.
   const f16* post_ln_w = nullptr;
   f16* post_norm_out = nullptr;
+  // Multi-token GEMM with the store epilogue: see T16Args::split_info.
+  int* split_info = nullptr;
 };
 
 template <class A>
@@ -667,6 +669,7 @@ struct axm_runner {
         a.post_ln_w = c.post_ln_w;
         a.post_norm_out = c.post_ln_w ? c.post_norm_out + (size_t)t0 * out_rows : nullptr;
         a.eps = c.eps;
+        a.split_info = T <= kTile16GemmMaxTokens ? c.split_info : nullptr;
         const int rc = t16_gemm_launch(a, mc, epi, ws, ws_bytes, s);
         if (rc) return rc;
       }
@@ -714,11 +717,19 @@ struct axm_runner {
       a.bias = (const f16*)qkv_b[i];
       a.ln_w = post && i > 0 ? nullptr : (const f16*)ln1[i];
       a.eps = d.eps;
+      // With head size 128 a K-split QKV GEMM leaves its partials to the RoPE /
+      // cache-write launch, which sums them (no separate split reduce).
+      int split_info[3] = {0, 0, 0};
+      if (d.head_dim == 128) a.split_info = split_info;
       int rc = gemv_rows(m_qkv[i], Q4_EPI_STORE, qkv_dim, a, T, s);
       if (rc) return rc;
       if (d.head_dim == 128) {
         // RoPE and the cache write in one launch.
-        rc = launch_rope_kv_write(kv, qkvbuf, d.n_head, T, d.freqs, tree_pos, q, write_pos, s);
+        if (split_info[0] > 1)
+          rc = launch_reduce_rope_kv_write(kv, ws, split_info[0], split_info[1], split_info[2], a.bias, d.n_head, T,
+                                           d.freqs, tree_pos, q, write_pos, s);
+        else
+          rc = launch_rope_kv_write(kv, qkvbuf, d.n_head, T, d.freqs, tree_pos, q, write_pos, s);
         if (rc) return rc;
       } else {
         hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, T), dim3(256), 0, s, qkvbuf, q_dim,
