@@ -1177,22 +1177,38 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 constexpr int kTreeKeys = 32;    // keys per block (the k extent of one P V MFMA)
 
-// LDS tiles of the matrix-core attention kernels, 32 keys per row.
-// vt [dim][key]: V staged transposed.  A staging write covers 16 dims spaced 8
-// apart and 4 (8 for hd 64) consecutive keys; an operand read covers 16
-// consecutive dims, 8 keys each.  Rows r and r + 8 sit on opposite halves of the
-// banks (row r ^ bit 3 of r) and the 8-key groups are XOR-swizzled by bits 1-2 and
-// 4-5 of the dim, so both spread over all banks (the former swizzle by bits 3-4
-// only put a write's 64 lanes on 8 banks).
-// pt [row][key]: P, written 4 rows x 16 keys at a time, read 8 keys per row
-// (2-way at most either way).
-__device__ __forceinline__ int vt_index(int row, int key) {
-  const int prow = row ^ ((row >> 3) & 1);
-  const int swz = ((row >> 1) ^ (row >> 4)) & 3;
-  return prow * kTreeKeys + (((key >> 3) ^ swz) << 3) + (key & 7);
-}
+// P tile of the matrix-core attention kernels, [row][key] with 32 keys per row:
+// written 4 rows x 16 keys at a time, read 8 keys per row; the 8-key groups of
+// row r are XOR-swizzled by bits 2-3 of r (2-way bank conflicts at most).
 __device__ __forceinline__ int pt_index(int row, int key) {
   return row * kTreeKeys + (((key >> 3) ^ ((row >> 2) & 3)) << 3) + (key & 7);
+}
+
+// B operand of O += P V from V rows stored key-major (row stride vrow halves;
+// seg = row 0 of a 16-dim tile): lane (l16, lq) needs dim column l16 of keys
+// 8 lq .. 8 lq + 7.  ds_read_b64_tr_b16 over a 16-lane group returns to lane i
+// column i of the 4 x 16 block whose row r is the 4 x 8 bytes the group's lanes
+// 4 r .. 4 r + 3 address, so lane i addresses key (i / 4) of the group's four,
+// dims 4 (i % 4) .. + 3; two reads give keys 8 lq .. + 3 and 8 lq + 4 .. + 7.
+typedef short tr_v4s __attribute__((vector_size(8)));
+__device__ __forceinline__ f16x8 v_operand(const f16* seg, int vrow, int l16, int lq) {
+  typedef __attribute__((address_space(3))) tr_v4s lds_v4s;
+  const f16* p0 = seg + (8 * lq + (l16 >> 2)) * vrow + 4 * (l16 & 3);
+  const tr_v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p0);
+  const tr_v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0 + 4 * vrow));
+  f16x8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = __builtin_bit_cast(f16, (short)a[e]);
+    r[4 + e] = __builtin_bit_cast(f16, (short)b[e]);
+  }
+  return r;
+}
+// Dim of output column c of a 16-dim tile whose V rows were stored in kv_half8's
+// order (int4: positions 0..7 of each 8-dim chunk hold dims 0, 2, 4, 6, 1, 3, 5, 7).
+template <int KVT>
+__device__ __forceinline__ int kv_col_dim(int c) {
+  return (c & 8) | kv_dim_of<KVT>(c & 7);
 }
 constexpr int kTreeRows = 64;    // query rows per workgroup (four waves of 16)
 
@@ -1237,13 +1253,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
   constexpr int KSTEPS = HD / 32;  // MFMA k-steps over the head dimension
   constexpr int DT = HD / 16;      // 16-wide output dimension tiles
   constexpr int kVec = kTreeKeys * HD / 8;        // 8-element V vectors per key block
-  // V block, dim-major, and per wave the P tile of its 16 rows.  Both store
-  // row r's 8-key unit u at unit u ^ swz(r), so that the transposing 2-byte
-  // writes of rows 8 (V) or 4 (P) apart fall in different banks, while a
-  // 16-byte operand read still covers whole units of one contiguous 1 KB tile.
-  __shared__ __align__(16) f16 vt[HD * kTreeKeys];
+  // The block's V rows as stored (key-major, padded rows, read transposed by
+  // v_operand) and per wave the P tile of its 16 rows.
+  constexpr int VROW = HD + 16;
+  __shared__ __align__(16) f16 vr[kTreeKeys * VROW];
   __shared__ __align__(16) f16 pt[4][16 * kTreeKeys];
-  auto vt_at = vt_index;
   auto pt_at = pt_index;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -1345,14 +1359,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
     // (otherwise the loop head copied the new ones, waiting for every load).
     __builtin_amdgcn_sched_barrier(0);
     fetch(kb0 + 2 * kTreeKeys, bc);
-    // Stage V transposed: this thread's run covers key kb0 + tid / kRunsPerKey,
-    // dims 8 kVRun (tid % kRunsPerKey) onwards.
+    // Stage V rows as converted: this thread's run covers key kb0 + tid /
+    // kRunsPerKey, dims 8 kVRun (tid % kRunsPerKey) onwards (16-byte stores; int4
+    // chunks keep kv_half8's order).
     {
       const int kk = threadIdx.x / kRunsPerKey, e0 = 8 * kVRun * (threadIdx.x % kRunsPerKey);
 #pragma unroll
-      for (int c = 0; c < kVRun; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vt[vt_at(e0 + 8 * c + kv_dim_of<KVT>(e), kk)] = vv[c][e];
+      for (int c = 0; c < kVRun; ++c) *reinterpret_cast<f16x8*>(&vr[kk * VROW + e0 + 8 * c]) = vv[c];
     }
     // S = Q K^T for the block's two 16-key halves.
     f32x4 sc[2];
@@ -1381,7 +1394,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
     const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][pt_at(l16, 8 * lq)]);
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
-      const f16x8 vb = *reinterpret_cast<const f16x8*>(&vt[vt_at(16 * d + l16, 8 * lq)]);
+      const f16x8 vb = v_operand(&vr[16 * d], VROW, l16, lq);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
     }
     __syncthreads();  // before the next block overwrites vt / pt
@@ -1406,7 +1419,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
     if (p.n_splits == 1) {
       const float inv = l[v] > 0.f ? 1.f / l[v] : 0.f;
 #pragma unroll
-      for (int d = 0; d < DT; ++d) p.out[(size_t)gr * HD + 16 * d + l16] = f2h(l[v] > 0.f ? o[d][v] * inv : 0.f);
+      for (int d = 0; d < DT; ++d)
+        p.out[(size_t)gr * HD + 16 * d + kv_col_dim<KVT>(l16)] = f2h(l[v] > 0.f ? o[d][v] * inv : 0.f);
     } else {
       float* dst = p.ws + ((size_t)gr * p.n_splits + split) * (2 + HD);
       if (l16 == 0) {
@@ -1414,7 +1428,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) t
         dst[1] = l[v];
       }
 #pragma unroll
-      for (int d = 0; d < DT; ++d) dst[2 + 16 * d + l16] = o[d][v];
+      for (int d = 0; d < DT; ++d) dst[2 + 16 * d + kv_col_dim<KVT>(l16)] = o[d][v];
     }
   }
 }
@@ -1450,10 +1464,11 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
   constexpr int KSTEPS = HD / 32;
   constexpr int DT = HD / 16;
   constexpr int kVPL = kTreeKeys * HD / 8 / 64;  // 8-element V vectors per lane and block
-  __shared__ __align__(16) f16 vt[4][HD * kTreeKeys];
+  // V rows as stored (key-major, padded rows) for the transposing LDS reads.
+  constexpr int VROW = HD + 16;
+  __shared__ __align__(16) f16 vr[4][kTreeKeys * VROW];
   __shared__ __align__(16) f16 pt[4][16 * kTreeKeys];
   __shared__ float mrg[4][16][2 + HD];
-  auto vt_at = vt_index;
   auto pt_at = pt_index;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1538,14 +1553,13 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
 #pragma unroll
       for (int c = 0; c < KSTEPS; ++c) vv[i][c] = kv_half8<KVT>(vrun[bf][i].chunk(c));
     fetch(kb0 + DEPTH * kStride, bc);
+    // V rows to LDS as converted (16-byte stores; int4 chunks keep kv_half8's order).
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
       const int j = i * 64 + lane;
       const int kk = j / 4, e0 = (HD / 4) * (j % 4);
 #pragma unroll
-      for (int c = 0; c < KSTEPS; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vt[wave][vt_at(e0 + 8 * c + kv_dim_of<KVT>(e), kk)] = vv[i][c][e];
+      for (int c = 0; c < KSTEPS; ++c) *reinterpret_cast<f16x8*>(&vr[wave][kk * VROW + e0 + 8 * c]) = vv[i][c];
     }
     f32x4 sc[2];
 #pragma unroll
@@ -1570,7 +1584,7 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
     const f16x8 pa = *reinterpret_cast<const f16x8*>(&pt[wave][pt_at(l16, 8 * lq)]);
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
-      const f16x8 vb = *reinterpret_cast<const f16x8*>(&vt[wave][vt_at(16 * d + l16, 8 * lq)]);
+      const f16x8 vb = v_operand(&vr[wave][16 * d], VROW, l16, lq);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
     }
   };
@@ -1599,8 +1613,9 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(AttnParams p) {
       mrg[wave][row][0] = m[v];
       mrg[wave][row][1] = l[v];
     }
+    // Output column l16 of tile d is dim 16 d + kv_col_dim<KVT>(l16).
 #pragma unroll
-    for (int d = 0; d < DT; ++d) mrg[wave][row][2 + 16 * d + l16] = o[d][v];
+    for (int d = 0; d < DT; ++d) mrg[wave][row][2 + 16 * d + kv_col_dim<KVT>(l16)] = o[d][v];
   }
   __syncthreads();
   for (int t = threadIdx.x; t < R * HD; t += 256) {
