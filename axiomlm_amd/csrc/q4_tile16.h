@@ -68,7 +68,8 @@ constexpr int kTile16MaxK = 16384;
 constexpr int kTile16PartsMaxK = 4096;
 constexpr int kTile16MaxParts = 8;
 
-size_t t16_smem_bytes(int M, int NT, int K);
+// LDS bytes of a GEMV workgroup of `waves` waves (before per-wave scale staging).
+size_t t16_smem_bytes(int M, int NT, int K, int waves);
 void t16_prepare_attributes();
 // Picks split / grid (a.split is overwritten); M in [1, 4].
 int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s);

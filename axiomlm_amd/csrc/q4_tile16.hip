@@ -26,8 +26,10 @@
 
 namespace {
 
+// GEMV workgroups have TH = 512 threads (8 waves) or, where a 512-thread grid
+// would leave most CUs with a single workgroup, 256 (t16_gemv_launch).
 constexpr int kT16Threads = 512;
-constexpr int kT16Waves = kT16Threads / 64;
+constexpr int kT16ThreadsSmall = 256;
 
 // Reference lane holding (r, even column c0) of an 8-row MARLIN tile
 // (inverse of quant.py:573-576).
@@ -87,29 +89,34 @@ __global__ void repack_tile16_kernel(const uint32_t* __restrict__ wm, const f16x
 // Activation staging: xs [M][K_pad] f16 (normalized if ln_w), zero block,
 // cx [M][2 KB] float2 (magic-offset-weighted sum, plain sum) per 64-group.
 //
-// Thread tid owns the 8-element vectors i = tid + r * kT16Threads of every row.
+// Thread tid owns the 8-element vectors i = tid + r * TH of every row.
 // t16_load_x issues the activation (and norm weight) loads into registers
 // before the kernel issues its weight loads: a wave's loads complete in issue
 // order, so staging that loaded x only after the weight loads would first wait
 // for every weight chunk of the wave to arrive.
 // ---------------------------------------------------------------------------
-constexpr int kT16XV = 4;  // vectors per thread and row: K <= kT16XV * kT16Threads * 8 = 16384
-constexpr int kT16MaxK = kT16XV * kT16Threads * 8;
-static_assert(kT16MaxK == kTile16MaxK, "tile16 staging bound");
-
-template <int M>
-struct T16X {
-  f16x8 x[M][kT16XV];
-  f16x8 w[kT16XV];
+constexpr int kT16MaxK = kTile16MaxK;
+// Vectors per thread and row: K <= XV * TH * 8 = kT16MaxK.
+template <int TH>
+struct T16XV {
+  static constexpr int value = kT16MaxK / (8 * TH);
 };
 
-template <int M>
-__device__ __forceinline__ void t16_load_x(const T16Args& a, T16X<M>& r) {
+template <int M, int TH>
+struct T16X {
+  static constexpr int XV = T16XV<TH>::value;
+  f16x8 x[M][XV];
+  f16x8 w[XV];
+};
+
+template <int M, int TH>
+__device__ __forceinline__ void t16_load_x(const T16Args& a, T16X<M, TH>& r) {
+  constexpr int XV = T16XV<TH>::value;
   const int tid = threadIdx.x;
   const int nv = a.K >> 3;
 #pragma unroll
-  for (int v = 0; v < kT16XV; ++v) {
-    const int i = tid + v * kT16Threads;
+  for (int v = 0; v < XV; ++v) {
+    const int i = tid + v * TH;
     const bool ok = i < nv;
 #pragma unroll
     for (int mi = 0; mi < M; ++mi) {
@@ -132,6 +139,7 @@ __device__ __forceinline__ void t16_load_x(const T16Args& a, T16X<M>& r) {
 // 8 elements 8 tid.. of x.  Every partial slot is loaded unconditionally through
 // a bounded buffer descriptor (slots past n_parts read as zero) so that the
 // number of loads in flight before the weight loads is static.
+// (512-thread workgroups only.)
 static_assert(kTile16PartsMaxK == kT16Threads * 8, "one partial vector per thread");
 struct T16Parts {
   u32x4 o[kTile16MaxParts];
@@ -156,8 +164,9 @@ __device__ __forceinline__ void t16_load_parts(const T16Args& a, T16Parts& pp) {
   }
 }
 
-template <int M>
-__device__ __forceinline__ void t16_merge_parts(const T16Args& a, const T16Parts& pp, T16X<M>& r) {
+template <int M, int TH>
+__device__ __forceinline__ void t16_merge_parts(const T16Args& a, const T16Parts& pp, T16X<M, TH>& r) {
+  static_assert(TH == kT16Threads, "partial merge with 512-thread workgroups");
   constexpr float kNoScore = -1e30f;
   // The (m, l) words are copied to scalars before the bit casts: a bit cast of an
   // ext_vector element expression reads element 0.
@@ -194,7 +203,7 @@ __device__ __forceinline__ void t16_merge_parts(const T16Args& a, const T16Parts
   for (int e = 0; e < 8; ++e) x[e] = f2h(wsum > 0.f ? acc[e] / wsum : 0.f);
   const bool ok = (int)threadIdx.x < (a.K >> 3);
 #pragma unroll
-  for (int v = 0; v < kT16XV; ++v) {
+  for (int v = 0; v < T16XV<TH>::value; ++v) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) r.x[0][v][e] = f16(0);
     r.w[v] = r.x[0][v];
@@ -202,8 +211,10 @@ __device__ __forceinline__ void t16_merge_parts(const T16Args& a, const T16Parts
   if (ok) r.x[0][0] = x;
 }
 
-template <int M>
-__device__ void t16_stage_x(const T16Args& a, const T16X<M>& r, f16* xs, f32x2* cx, float* red) {
+template <int M, int TH>
+__device__ void t16_stage_x(const T16Args& a, const T16X<M, TH>& r, f16* xs, f32x2* cx, float* red) {
+  constexpr int XV = T16XV<TH>::value;
+  constexpr int W = TH / 64;
   const int tid = threadIdx.x;
   const int K = a.K;
   const int nv = K >> 3;
@@ -216,7 +227,7 @@ __device__ void t16_stage_x(const T16Args& a, const T16X<M>& r, f16* xs, f32x2* 
     for (int mi = 0; mi < M; ++mi) {
       float s = 0.f;
 #pragma unroll
-      for (int v = 0; v < kT16XV; ++v) {
+      for (int v = 0; v < XV; ++v) {
         // Vectors past nv were loaded as zeros and add nothing.
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -225,14 +236,14 @@ __device__ void t16_stage_x(const T16Args& a, const T16X<M>& r, f16* xs, f32x2* 
         }
       }
       s = wave_sum(s);
-      if ((tid & 63) == 0) red[mi * kT16Waves + (tid >> 6)] = s;
+      if ((tid & 63) == 0) red[mi * W + (tid >> 6)] = s;
     }
     __syncthreads();
 #pragma unroll
     for (int mi = 0; mi < M; ++mi) {
       float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < kT16Waves; ++w) s += red[mi * kT16Waves + w];
+      for (int w = 0; w < W; ++w) s += red[mi * W + w];
       rinv[mi] = rms_inv_fp16(s, K, a.eps);
     }
   }
@@ -241,9 +252,9 @@ __device__ void t16_stage_x(const T16Args& a, const T16X<M>& r, f16* xs, f32x2* 
     // nv_pad is a multiple of 16 (KB*128/8) and the same for every thread, so
     // the 8-lane group reduction below always runs with full wave participation.
 #pragma unroll
-    for (int v = 0; v < kT16XV; ++v) {
-      if (v * kT16Threads >= nv_pad) break;
-      const int i = tid + v * kT16Threads;
+    for (int v = 0; v < XV; ++v) {
+      if (v * TH >= nv_pad) break;
+      const int i = tid + v * TH;
       f16x8 x = r.x[mi][v];
       if (i < nv) {
         if (a.ln_w != nullptr) {
@@ -379,8 +390,9 @@ constexpr int kT16WaveMaxChunks = 16;  // chunks per wave kT16Wave handles
 
 // G128: one (scale, bias) word per row and chunk (group-128 packs) instead of two;
 // it is applied to both 64-column halves of the chunk.
-template <int M, int NT, int EPI, int P, int MODE, bool G128>
-__global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
+template <int M, int NT, int EPI, int P, int MODE, bool G128, int TH>
+__global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
+  constexpr int W = TH / 64;  // waves per workgroup
   constexpr bool ONE = MODE != kT16Loop;
   constexpr bool SBW = MODE == kT16Wave;
   constexpr int VPC = G128 ? 4 : 8;  // 16-byte scale vectors per chunk and tile
@@ -391,13 +403,13 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
   f16* zero = xs + (size_t)M * a.KB * 128;                                   // 16 halves of zeros
   f32x2* cx = reinterpret_cast<f32x2*>(zero + 16);                           // [M][2 KB]
   float* red = reinterpret_cast<float*>(cx + (size_t)M * 2 * a.KB);          // [waves][NT][4][64]
-  u32x2* sbw = reinterpret_cast<u32x2*>(red + kT16Waves * NT * 4 * 64);      // kT16Wave: [waves][NT][per][16]
+  u32x2* sbw = reinterpret_cast<u32x2*>(red + W * NT * 4 * 64);              // kT16Wave: [waves][NT][per][16]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int S = a.split;
-  const int upw = kT16Waves / S;
+  const int upw = W / S;
   const int sub = wave % S;
   const int slot = wave / S;
   // Contiguous kb range [kb0, kb0 + my) of this wave within a unit.
@@ -440,7 +452,7 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
 
   int it = 0;
   int unit = blockIdx.x * upw + slot;
-  T16X<M> xr;
+  T16X<M, TH> xr;
   // Q4_EPI_RESID with one token may take its activations from attention split
   // partials (merged after the weight loads are issued).
   constexpr bool from_parts = EPI == kT16EpiResidParts;
@@ -448,7 +460,7 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
   if (from_parts)
     t16_load_parts(a, pp);
   else
-    t16_load_x<M>(a, xr);
+    t16_load_x<M, TH>(a, xr);
   // kT16Wave: the wave's (scale, bias) run; 16-byte vector v holds chunk v / 8,
   // rows 2 (v % 8) and 2 (v % 8) + 1 (G128: chunk v / 4, rows 4 (v % 4) ..
   // 4 (v % 4) + 3).  Issued before the weight loads so that storing it to LDS
@@ -482,8 +494,8 @@ __global__ void __launch_bounds__(kT16Threads) t16_gemv_kernel(T16Args a) {
         if (v < my * VPC) *reinterpret_cast<u32x4*>(my_sb + (size_t)t * per * 16 + 2 * v) = sbv[t][q];
       }
   }
-  if (from_parts) t16_merge_parts<M>(a, pp, xr);
-  t16_stage_x<M>(a, xr, xs, cx, red);  // ends with a workgroup barrier
+  if constexpr (from_parts) t16_merge_parts<M, TH>(a, pp, xr);
+  t16_stage_x<M, TH>(a, xr, xs, cx, red);  // ends with a workgroup barrier
 
   // LDS addresses: A operand of this lane and (corr, sum) of its D tokens.
   const f16* xa = (tokA < M) ? xs + (size_t)tokA * a.KB * 128 + 8 * kq : zero;
@@ -598,49 +610,64 @@ struct T16Depth {
   static constexpr int value = NT == 2 ? 4 : 8;
 };
 
-template <int M, int NT, int EPI, int P, int MODE>
+template <int M, int NT, int EPI, int P, int MODE, int TH>
 void t16_set_attr_mode() {
-  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE, false>,
+  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE, false, TH>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
     (void)hipGetLastError();
-  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE, true>,
+  if (hipFuncSetAttribute((const void*)t16_gemv_kernel<M, NT, EPI, P, MODE, true, TH>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
     (void)hipGetLastError();
+}
+
+template <int M, int NT, int EPI, int TH>
+void t16_set_attr_th() {
+  t16_set_attr_mode<M, NT, EPI, T16Depth<NT>::value, kT16Loop, TH>();
+  t16_set_attr_mode<M, NT, EPI, T16Depth<NT>::value, kT16OnePass, TH>();
+  t16_set_attr_mode<M, NT, EPI, kT16WaveDepth, kT16Wave, TH>();
 }
 
 template <int M, int NT, int EPI>
 void t16_set_attr() {
-  t16_set_attr_mode<M, NT, EPI, T16Depth<NT>::value, kT16Loop>();
-  t16_set_attr_mode<M, NT, EPI, T16Depth<NT>::value, kT16OnePass>();
-  t16_set_attr_mode<M, NT, EPI, kT16WaveDepth, kT16Wave>();
+  t16_set_attr_th<M, NT, EPI, kT16Threads>();
+  if constexpr (M == 1 && EPI != kT16EpiResidParts) t16_set_attr_th<M, NT, EPI, kT16ThreadsSmall>();
 }
 
-template <int M, int NT, int EPI, bool G128>
+template <int M, int NT, int EPI, bool G128, int TH>
 void t16_launch_g(const T16Args& a, int mode, int grid, size_t smem, hipStream_t s) {
-  const dim3 g(grid), b(kT16Threads);
+  const dim3 g(grid), b(TH);
   if (mode == kT16Wave)
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, kT16WaveDepth, kT16Wave, G128>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, kT16WaveDepth, kT16Wave, G128, TH>), g, b, smem, s, a);
   else if (mode == kT16OnePass)
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16OnePass, G128>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16OnePass, G128, TH>), g, b, smem, s, a);
   else
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16Loop, G128>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16Loop, G128, TH>), g, b, smem, s, a);
 }
 
 template <int M, int NT, int EPI>
-int t16_launch_one(const T16Args& a, int mode, int grid, size_t smem, hipStream_t s) {
+int t16_launch_one(const T16Args& a, int mode, int grid, size_t smem, int th, hipStream_t s) {
+  if constexpr (M == 1 && EPI != kT16EpiResidParts) {
+    if (th == kT16ThreadsSmall) {
+      if (a.g128)
+        t16_launch_g<M, NT, EPI, true, kT16ThreadsSmall>(a, mode, grid, smem, s);
+      else
+        t16_launch_g<M, NT, EPI, false, kT16ThreadsSmall>(a, mode, grid, smem, s);
+      return 0;
+    }
+  }
   if (a.g128)
-    t16_launch_g<M, NT, EPI, true>(a, mode, grid, smem, s);
+    t16_launch_g<M, NT, EPI, true, kT16Threads>(a, mode, grid, smem, s);
   else
-    t16_launch_g<M, NT, EPI, false>(a, mode, grid, smem, s);
+    t16_launch_g<M, NT, EPI, false, kT16Threads>(a, mode, grid, smem, s);
   return 0;
 }
 
 }  // namespace
 
-size_t t16_smem_bytes(int M, int NT, int K) {
+size_t t16_smem_bytes(int M, int NT, int K, int waves) {
   const int KB = (K + 127) / 128;
   return (size_t)M * KB * 128 * sizeof(f16) + 32 + (size_t)M * 2 * KB * sizeof(f32x2) +
-         (size_t)kT16Waves * NT * 4 * 64 * sizeof(float);
+         (size_t)waves * NT * 4 * 64 * sizeof(float);
 }
 
 void t16_prepare_attributes() {
@@ -663,9 +690,8 @@ void t16_prepare_attributes() {
 int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   t16_prepare_attributes();
   const int NT = (epi == Q4_EPI_SWIGLU) ? 2 : 1;
-  size_t smem = t16_smem_bytes(M, NT, a.K);
-  if (smem > 160 * 1024 || M < 1 || M > 4 || a.K > kT16MaxK) {
-    axm_set_error("tile16 gemv: M=%d K=%d unsupported (K <= %d, %zu B of LDS)", M, a.K, kT16MaxK, smem);
+  if (M < 1 || M > 4 || a.K > kT16MaxK) {
+    axm_set_error("tile16 gemv: M=%d K=%d unsupported (M in [1, 4], K <= %d)", M, a.K, kT16MaxK);
     return -2;
   }
   if (a.x_parts != nullptr &&
@@ -677,10 +703,38 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
                   kTile16PartsMaxK, kTile16MaxParts, M, a.K, a.n_parts, a.parts_hd);
     return -2;
   }
-  // Waves per unit: aim for ~8 waves per CU with >= 2 kb-loads per wave.
+  // Waves per unit: aim for ~8 waves per CU with >= 2 kb-loads per wave; the S
+  // waves of a unit belong to one workgroup.
   const int cus = axm_num_cus();
-  int S = 1;
-  while (S < kT16Waves && a.n_units * S < 8 * cus && a.KB >= 4 * S) S *= 2;
+  auto split_for = [&](int waves) {
+    int S = 1;
+    while (S < waves && a.n_units * S < 8 * cus && a.KB >= 4 * S) S *= 2;
+    return S;
+  };
+  int th = kT16Threads;
+  int S = split_for(kT16Threads / 64);
+  // Fewer than 1.5 512-thread workgroups per CU would leave some CUs with two
+  // and most with one (workgroups of one launch all resident): 256-thread
+  // workgroups spread the same waves more evenly (7B decode on one MI355X:
+  // gate|up 13.3 -> 12.3 us, down 9.0 -> 8.6 us; at 1.5-2 per CU, QKV and the
+  // lm_head, 512 threads were as fast or faster).  One token only: with more,
+  // the activation registers of 256 threads covering K <= 16384 (eight vectors
+  // per thread and token) cost more than the balance gains (two-token verify
+  // 1.33 -> 1.47 decode steps).  The split-partial source needs one thread per
+  // 8 activations of a 4096-wide row, i.e. 512 threads.
+  if (M == 1 && a.x_parts == nullptr) {
+    const int grid512 = (a.n_units + kT16Threads / 64 / S - 1) / (kT16Threads / 64 / S);
+    if (2 * grid512 < 3 * cus) {
+      th = kT16ThreadsSmall;
+      S = split_for(kT16ThreadsSmall / 64);
+    }
+  }
+  const int waves = th / 64;
+  size_t smem = t16_smem_bytes(M, NT, a.K, waves);
+  if (smem > 160 * 1024) {
+    axm_set_error("tile16 gemv: M=%d K=%d needs %zu B of LDS", M, a.K, smem);
+    return -2;
+  }
   a.split = S;
   a.w16_bytes = t16_weight_bytes(a.N_rows_alloc, a.K);
   a.sb16_bytes = t16_sb_bytes(a.N_rows_alloc, a.K, a.g128);
@@ -688,14 +742,14 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   a.unpack[1] = 0x00F000F0u;
   a.unpack[2] = 0x64006400u;
   a.unpack[3] = 0x54005400u;
-  const int upw = kT16Waves / S;
+  const int upw = waves / S;
   int grid = (a.n_units + upw - 1) / upw;
   if (S == 1 && grid > 2 * cus) grid = 2 * cus;
   // Chunks per wave; kT16Wave keeps all of them in flight (per <= depth).
   const int per = (a.KB + S - 1) / S;
   int mode = S == 1 ? kT16Loop : kT16OnePass;
   if (S > 1 && per <= kT16WaveMaxChunks) {
-    const size_t sb_lds = (size_t)kT16Waves * NT * per * 128;
+    const size_t sb_lds = (size_t)waves * NT * per * 128;
     if (smem + sb_lds <= 160 * 1024) {
       mode = kT16Wave;
       smem += sb_lds;
@@ -704,13 +758,13 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
 #define AXM_T16_CASE(MM)                                                                 \
   case MM:                                                                               \
     switch (epi) {                                                                       \
-      case Q4_EPI_STORE: return t16_launch_one<MM, 1, Q4_EPI_STORE>(a, mode, grid, smem, s);   \
-      case Q4_EPI_RESID: return t16_launch_one<MM, 1, Q4_EPI_RESID>(a, mode, grid, smem, s);   \
-      case Q4_EPI_SWIGLU: return t16_launch_one<MM, 2, Q4_EPI_SWIGLU>(a, mode, grid, smem, s); \
-      case Q4_EPI_QKV_ROPE: return t16_launch_one<MM, 1, Q4_EPI_QKV_ROPE>(a, mode, grid, smem, s); \
+      case Q4_EPI_STORE: return t16_launch_one<MM, 1, Q4_EPI_STORE>(a, mode, grid, smem, th, s);   \
+      case Q4_EPI_RESID: return t16_launch_one<MM, 1, Q4_EPI_RESID>(a, mode, grid, smem, th, s);   \
+      case Q4_EPI_SWIGLU: return t16_launch_one<MM, 2, Q4_EPI_SWIGLU>(a, mode, grid, smem, th, s); \
+      case Q4_EPI_QKV_ROPE: return t16_launch_one<MM, 1, Q4_EPI_QKV_ROPE>(a, mode, grid, smem, th, s); \
     }                                                                                    \
     break;
-  if (a.x_parts != nullptr) return t16_launch_one<1, 1, kT16EpiResidParts>(a, mode, grid, smem, s);
+  if (a.x_parts != nullptr) return t16_launch_one<1, 1, kT16EpiResidParts>(a, mode, grid, smem, th, s);
   switch (M) {
     AXM_T16_CASE(1)
     AXM_T16_CASE(2)
