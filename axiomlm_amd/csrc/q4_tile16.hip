@@ -384,8 +384,15 @@ constexpr int kT16EpiResidParts = 16;
 constexpr int kT16Loop = 0;
 constexpr int kT16OnePass = 1;
 constexpr int kT16Wave = 2;
-constexpr int kT16WaveDepth = 8;      // chunk register slots per wave in kT16Wave (a ring)
-constexpr int kT16WavePre = 4;        // chunks issued before the activation staging
+// Chunk register slots per wave in kT16Wave (a ring; 7B decode step: 6 / 8 / 12 /
+// 16 slots gave 727 / 726 / 730.5 / 729 tok/s).
+constexpr int kT16WaveDepth = 12;
+// Chunks issued before the activation staging (7B decode step on one MI355X:
+// 1 / 2 / 3 / 4 / 8 gave 698 / 721 / 725 / 713 / 529 tok/s).
+constexpr int kT16WavePre = 3;
+// Chunk jj + PRE is requested into the slot of chunk jj + PRE - P before chunk jj is
+// consumed, so PRE must stay below the ring size.
+static_assert(kT16WavePre < kT16WaveDepth, "kT16Wave ring");
 constexpr int kT16WaveMaxChunks = 16;  // chunks per wave kT16Wave handles
 
 // G128: one (scale, bias) word per row and chunk (group-128 packs) instead of two;

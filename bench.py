@@ -392,8 +392,8 @@ def main():
             "step_hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": (f"t16_gemv_kernel<1,2,2,8,2,{'true' if G == 128 else 'false'}> (fused RMSNorm + gate/up Q4 "
-                       f"G{G} GEMV on matrix cores + SwiGLU, 22016x4096)"),
+            "kernel": (f"t16_gemv_kernel<1,2,2,12,2,{'true' if G == 128 else 'false'},256> (fused RMSNorm + gate/up "
+                       f"Q4 G{G} GEMV on matrix cores + SwiGLU, 22016x4096, 256-thread workgroups)"),
             "bound": "hbm",
             "achieved": round(ach, 1),
             "peak": HBM_PEAK_GBS,
