@@ -282,9 +282,48 @@ __device__ void t16_stage_x(const T16Args& a, const T16X<M, TH>& r, f16* xs, f32
   __syncthreads();
 }
 
-// Epilogue for lane l: row = unit*16 + l%16, token = 4*(l/16) + v.
-template <int M, int NT, int EPI>
-__device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lane, const float (&v)[NT][4]) {
+// Epilogue operands of a one-token, one-pass launch, requested after the first
+// weight chunks instead of after the last: at the end of the weight stream they
+// would add a dependent round trip (two for RoPE: position, then its cos / sin)
+// to the launch's tail.  QKV: RoPE cos / sin, the bias pair and the cache slot;
+// residual epilogues: the residual value.  Lanes 0..15 hold rows unit*16 + lane.
+struct T16EpiPre {
+  float c, sn;
+  f16 b_self, b_part, resid;
+  int wp;
+};
+
+template <int EPI>
+__device__ __forceinline__ T16EpiPre t16_epi_prefetch(const T16Args& a, int unit, int lane, int pos, int wp) {
+  T16EpiPre e{1.f, 0.f, f16(0), f16(0), f16(0), wp};
+  const int row = unit * 16 + (lane & 15);
+  if (lane >= 16 || unit >= a.n_units || row >= a.N) return e;
+  if (EPI == Q4_EPI_QKV_ROPE) {
+    if (a.bias != nullptr) {
+      e.b_self = a.bias[row];
+      e.b_part = a.bias[row ^ 1];
+    }
+    const int row0 = row & ~1;
+    if (row0 < a.q_dim + a.kv_dim) {
+      const int hd = a.head_dim, half_hd = hd >> 1;
+      const int within = row0 < a.q_dim ? row0 : row0 - a.q_dim;
+      const int fi = (within % hd) >> 1;
+      const int rp = pos % a.rope_len;
+      e.c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
+      e.sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
+    }
+  } else if (EPI == Q4_EPI_RESID) {
+    e.resid = a.resid[row];
+  }
+  return e;
+}
+
+// Epilogue for lane l: row = unit*16 + l%16, token = 4*(l/16) + v.  PRE: the
+// operands come from t16_epi_prefetch (M == 1).
+template <int M, int NT, int EPI, bool PRE>
+__device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lane, const float (&v)[NT][4],
+                                             const T16EpiPre& pre) {
+  static_assert(!PRE || M == 1, "prefetched epilogue operands: one token");
   const int j = lane & 15;
   const int row = unit * 16 + j;
   if (EPI == Q4_EPI_STORE && M == 1 && a.argmax_keys != nullptr) {
@@ -311,8 +350,8 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
       f16 h_self = f2h(v[0][vi]);
       f16 h_part = f2h(partner);
       if (a.bias != nullptr) {
-        h_self = f2h(h2f(h_self) + h2f(a.bias[row]));
-        h_part = f2h(h2f(h_part) + h2f(a.bias[row ^ 1]));
+        h_self = f2h(h2f(h_self) + h2f(PRE ? pre.b_self : a.bias[row]));
+        h_part = f2h(h2f(h_part) + h2f(PRE ? pre.b_part : a.bias[row ^ 1]));
       }
       const f16 h0 = even ? h_self : h_part;
       const f16 h1 = even ? h_part : h_self;
@@ -320,13 +359,17 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
       const int hd = a.head_dim, half_hd = hd >> 1;
       f16 out = h_self;
       if (row0 < a.q_dim + a.kv_dim) {
-        const int pos = (a.rope_pos_dev ? a.rope_pos_dev[0] : a.rope_pos) + tok;
-        const int within = row0 < a.q_dim ? row0 : row0 - a.q_dim;
-        const int fi = (within % hd) >> 1;
-        const int rp = pos % a.rope_len;
-        const float c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
-        const float sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
-        out = rope_out(h0, h1, c, sn, even);
+        if (PRE) {
+          out = rope_out(h0, h1, pre.c, pre.sn, even);
+        } else {
+          const int pos = (a.rope_pos_dev ? a.rope_pos_dev[0] : a.rope_pos) + tok;
+          const int within = row0 < a.q_dim ? row0 : row0 - a.q_dim;
+          const int fi = (within % hd) >> 1;
+          const int rp = pos % a.rope_len;
+          const float c = a.freqs[((size_t)rp * half_hd + fi) * 2 + 0];
+          const float sn = a.freqs[((size_t)rp * half_hd + fi) * 2 + 1];
+          out = rope_out(h0, h1, c, sn, even);
+        }
       }
       if (row < a.q_dim) {
         a.y[(size_t)tok * a.ldy + row] = out;
@@ -334,7 +377,7 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
         const bool is_k = row < a.q_dim + a.kv_dim;
         const int within = is_k ? row - a.q_dim : row - a.q_dim - a.kv_dim;
         const int kvh = within / hd, e = within % hd;
-        const int wp = (a.write_pos_dev ? a.write_pos_dev[0] : a.write_pos) + tok;
+        const int wp = (PRE ? pre.wp : (a.write_pos_dev ? a.write_pos_dev[0] : a.write_pos)) + tok;
         f16* dst = (is_k ? a.k_out : a.v_out) + ((size_t)kvh * a.kv_stride_h + (size_t)(wp % a.max_seq) * hd + e);
         *dst = out;
       }
@@ -353,7 +396,7 @@ __device__ __forceinline__ void t16_epilogue(const T16Args& a, int unit, int lan
         a.y[(size_t)tok * a.ldy + row] = h;
       } else {
         f16* xr = a.resid + (size_t)tok * a.ldr + row;
-        *xr = f2h(h2f(*xr) + h2f(h));
+        *xr = f2h(h2f(PRE ? pre.resid : *xr) + h2f(h));
       }
     }
   }
@@ -459,6 +502,17 @@ __global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
 
   int it = 0;
   int unit = blockIdx.x * upw + slot;
+  // Prefetched epilogue operands (one token, one pass); the RoPE / cache positions
+  // are requested first (uniform, scalar loads) so that the cos / sin loads issued
+  // after the first weight chunks find them arrived.
+  constexpr int EPI_BASE = EPI == kT16EpiResidParts ? Q4_EPI_RESID : EPI;
+  constexpr bool EPI_PRE = M == 1 && ONE && (EPI_BASE == Q4_EPI_QKV_ROPE || EPI_BASE == Q4_EPI_RESID);
+  int pre_pos = 0, pre_wp = 0;
+  if constexpr (EPI_PRE && EPI_BASE == Q4_EPI_QKV_ROPE) {
+    pre_pos = a.rope_pos_dev ? a.rope_pos_dev[0] : a.rope_pos;
+    pre_wp = a.write_pos_dev ? a.write_pos_dev[0] : a.write_pos;
+  }
+  T16EpiPre epre{1.f, 0.f, f16(0), f16(0), f16(0), 0};
   T16X<M, TH> xr;
   // Q4_EPI_RESID with one token may take its activations from attention split
   // partials (merged after the weight loads are issued).
@@ -492,6 +546,9 @@ __global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
   constexpr int PRE = SBW ? kT16WavePre : P;
 #pragma unroll
   for (int j = 0; j < PRE; ++j) load(unit, j, j);
+  if constexpr (EPI_PRE) {
+    if (sub == 0) epre = t16_epi_prefetch<EPI_BASE>(a, unit, lane, pre_pos, pre_wp);
+  }
   if (SBW) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -604,8 +661,7 @@ __global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
             }
       }
     }
-    if (sub == 0 && unit < a.n_units)
-      t16_epilogue<M, NT, (EPI == kT16EpiResidParts ? Q4_EPI_RESID : EPI)>(a, unit, lane, acc);
+    if (sub == 0 && unit < a.n_units) t16_epilogue<M, NT, EPI_BASE, EPI_PRE>(a, unit, lane, acc, epre);
     if (ONE || !more) break;
     ++it;
     unit = next_unit;
