@@ -776,18 +776,19 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   };
   int th = kT16Threads;
   int S = split_for(kT16Threads / 64);
-  // Fewer than 1.5 512-thread workgroups per CU would leave some CUs with two
-  // and most with one (workgroups of one launch all resident): 256-thread
+  // Between one and 1.5 512-thread workgroups per CU, some CUs would hold two
+  // and most one (workgroups of one launch all resident): 256-thread
   // workgroups spread the same waves more evenly (7B decode on one MI355X:
-  // gate|up 13.3 -> 12.3 us, down 9.0 -> 8.6 us; at 1.5-2 per CU, QKV and the
-  // lm_head, 512 threads were as fast or faster).  One token only: with more,
+  // gate|up 13.3 -> 12.3 us).  With exactly one per CU (the down projection)
+  // and from 1.5 per CU on (QKV, lm_head) 512 threads were as fast or faster
+  // (down with 256 threads: 742 -> 731 tok/s).  One token only: with more,
   // the activation registers of 256 threads covering K <= 16384 (eight vectors
   // per thread and token) cost more than the balance gains (two-token verify
   // 1.33 -> 1.47 decode steps).  The split-partial source needs one thread per
   // 8 activations of a 4096-wide row, i.e. 512 threads.
   if (M == 1 && a.x_parts == nullptr) {
     const int grid512 = (a.n_units + kT16Threads / 64 / S - 1) / (kT16Threads / 64 / S);
-    if (2 * grid512 < 3 * cus) {
+    if (grid512 > cus && 2 * grid512 < 3 * cus) {
       th = kT16ThreadsSmall;
       S = split_for(kT16ThreadsSmall / 64);
     }
