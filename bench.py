@@ -305,8 +305,8 @@ def main():
                     help="only build the model and time the gate/up kernel (short runs under counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs the decode step on one GPU only; multi-GPU sharding is a design "
-                                   "note (DESIGN.md), so --gpus must be 1"}))
+        print(json.dumps({"error": "this build runs the decode step on one GPU only (no sharding across GPUs), "
+                                   "so --gpus must be 1"}))
         sys.exit(2)
 
     if not 1 <= args.context or args.context + args.warmup + args.steps + 1 > MAX_SEQ:
