@@ -180,10 +180,13 @@ def test_tile16_repack_roundtrip_bit_exact(dev, N_, K):
 @pytest.mark.parametrize(
     "M,N_,K,bias",
     [(1, 256, 256, False), (1, 13, 192, True), (3, 768, 256, False), (4, 1408, 704, False), (2, 96, 704, True),
-     (1, 12288, 4096, False), (1, 4096, 11008, False), (4, 22016, 4096, False), (1, 32000, 4096, False)],
+     (1, 12288, 4096, False), (1, 4096, 11008, False), (4, 22016, 4096, False), (1, 32000, 4096, False),
+     (1, 5504, 4096, True)],
 )
 def test_tile16_qmv_matches_oracle(dev, M, N_, K, bias):
-    """Matrix-core GEMV on the re-tiled copy; same bound as the reference-layout kernel."""
+    """Matrix-core GEMV on the re-tiled copy; same bound as the reference-layout kernel.
+    On a 256-CU part, 5504 rows (344 units, 344 eight-wave workgroups) take the
+    256-thread workgroups and the others the 512-thread ones."""
     from axiomlm_amd.kernels import qmv_q4_tile16, repack_q4_marlin_tile16
 
     print(f"[tile16_qmv] M={M} N={N_} K={K} bias={bias}", flush=True)
