@@ -364,6 +364,32 @@ def test_runner_verify_step_chain(dev):
     _check_logits(got, model.forward([tok], ocache)[-1], "step after verify")
 
 
+def test_runner_step_256_thread_gemvs(dev):
+    """Decode steps of a one-layer model whose widths put the QKV (4800 rows, RoPE and
+    cache-write epilogue), O (4160 rows; q_dim 4160 is past the split-partial source,
+    so a separate merge feeds it) and down (4160 rows, K 4096) GEMVs between one and
+    1.5 eight-wave workgroups per CU on a 256-CU part: their 256-thread workgroups with
+    the epilogue operands requested up front, against the oracle.  65 heads of 64,
+    GQA 13."""
+    print("[runner_256_thread_gemvs]", flush=True)
+    cfg = om.OracleConfig(n_layer=1, n_head=65, n_kv_head=5, d_model=4160, hidden=4096, vocab=1024, eps=1e-5,
+                          block_size=64)
+    W = om.make_float_weights(cfg, seed=5)
+    ow = om.pack_model_rtn(cfg, W)
+    cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, 10000.0)
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 64
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16")
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, "fp16")
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(0, cfg.vocab, 4).tolist()
+    got = run_steps(runner, cache, prompt, dev)
+    runner.check()
+    for i, tok in enumerate(prompt):
+        ref = model.forward([tok], ocache)[-1]
+        _check_logits(got[i], ref, f"step {i}")
+
+
 @pytest.mark.parametrize("kv", ["fp16", "fp8"])
 def test_runner_verify_step_split_gemms(dev, kv):
     """verify_step on a wider model (d 1024, head 128, MLP 2816) whose multi-token GEMMs
