@@ -785,8 +785,10 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   // the activation registers of 256 threads covering K <= 16384 (eight vectors
   // per thread and token) cost more than the balance gains (two-token verify
   // 1.33 -> 1.47 decode steps).  The split-partial source needs one thread per
-  // 8 activations of a 4096-wide row, i.e. 512 threads.
-  if (M == 1 && a.x_parts == nullptr) {
+  // 8 activations of a 4096-wide row, i.e. 512 threads.  Only split-K launches
+  // (S > 1, the measured one-pass forms) switch: with S == 1 the 256-thread grid
+  // would run the looping form, which was never measured against 512 threads.
+  if (M == 1 && a.x_parts == nullptr && S > 1) {
     const int grid512 = (a.n_units + kT16Threads / 64 / S - 1) / (kT16Threads / 64 / S);
     if (grid512 > cus && 2 * grid512 < 3 * cus) {
       th = kT16ThreadsSmall;

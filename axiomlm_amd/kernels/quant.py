@@ -182,15 +182,17 @@ def repack_q4_marlin_tile16(w_marlin, sb_marlin, N: int, K: int) -> tuple[torch.
     return w16, sb16
 
 
-def tile16_group_size(sb16, N_rows: int, K: int) -> int:
-    """64 or 128, from the size of a tile16 scale buffer made for N_rows x K."""
-    L = _lib.lib()
-    nbytes = sb16.numel() * sb16.element_size()
-    if nbytes == L.axm_tile16_bytes(N_rows, K, 1):
+def tile16_group_size(w16, sb16) -> int:
+    """64 or 128, from the byte ratio of a tile16 copy's codes to its scales: every
+    (16-row tile, 128-column block) holds 1024 code bytes and 128 (group 64) or 64
+    (group 128) scale bytes, whatever the number of tiles the copy was made for."""
+    wb = w16.numel() * w16.element_size()
+    sbb = sb16.numel() * sb16.element_size()
+    if wb > 0 and wb == 8 * sbb:
         return 64
-    if nbytes == L.axm_tile16_bytes(N_rows, K, 2):
+    if wb > 0 and wb == 16 * sbb:
         return 128
-    raise ValueError(f"tile16 scales of {nbytes} bytes match neither group size for {N_rows} x {K}")
+    raise ValueError(f"tile16 copy: {wb} code bytes and {sbb} scale bytes match neither group size")
 
 
 def _qmm_workspace(K: int, N: int, swiglu: bool, device):
@@ -214,7 +216,7 @@ def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
     y = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=x.device)
     b = None if bias is None else bias.to(device=x.device, dtype=torch.float16).contiguous()
     xc = x.contiguous()
-    gs = tile16_group_size(sb16, N, K)
+    gs = tile16_group_size(w16, sb16)
     if M < TILE16_GEMM_MIN_ROWS:
         _lib.check(_lib.lib().axm_qmv_q4_tile16(_lib.ptr(xc), _lib.ptr(w16), _lib.ptr(sb16), _lib.ptr(b),
                                                 _lib.ptr(y), M, K, N, gs, _lib.stream_of(x.device)),
@@ -257,7 +259,7 @@ def qmv_q4_tile16_swiglu(x, ln_w, eps: float, gu16, gusb16, H: int) -> torch.Ten
     from three rows on they are normalized first and go through the multi-token GEMM."""
     K = x.size(-1)
     M = x.numel() // K
-    gs = tile16_group_size(gusb16, 2 * int(H), K)
+    gs = tile16_group_size(gu16, gusb16)
     if M < TILE16_GEMM_MIN_ROWS:
         return _swiglu_call(_lib.lib().axm_qmv_q4_tile16_swiglu, "qmv_q4_tile16_swiglu", x, ln_w, eps, gu16, gusb16,
                             H, gs)

@@ -9,10 +9,11 @@ attribute names and argument order of the reference's pybind module
 calling a ``torch.ops.axiomlm`` custom operator (``axiomlm_amd.torch_ops``)
 or, for the runners, ``QuantizedDecodeRunner`` and the fp16 ``DecodeRunner``.
 
-Names of the reference module that belong to training (backward kernels,
-cross entropy, flash attention forward), to the fp16 ``MPSDecodeRunner`` or to
-the legacy Q4_G64 layout are not part of this path and are absent, so the
-reference's probes fall back for them as they do on any non-Metal device.
+The fp16 ``MPSDecodeRunner`` is provided by ``DecodeRunner`` (same constructor
+and methods).  Names of the reference module that belong to training (backward
+kernels, cross entropy, flash attention forward) or to the legacy Q4_G64 layout
+are not part of this path and are absent, so the reference's probes fall back
+for them as they do on any non-Metal device.
 """
 
 from __future__ import annotations

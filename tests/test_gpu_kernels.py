@@ -189,6 +189,8 @@ def test_tile16_qmv_matches_oracle(dev, M, N_, K, bias):
     256-thread workgroups and the others the 512-thread ones."""
     from axiomlm_amd.kernels import qmv_q4_tile16, repack_q4_marlin_tile16
 
+    if N_ == 5504 and torch.cuda.get_device_properties(dev).multi_processor_count != 256:
+        pytest.skip("the 5504-row case exercises the 256-thread workgroups only on a 256-CU device")
     print(f"[tile16_qmv] M={M} N={N_} K={K} bias={bias}", flush=True)
     rng = np.random.default_rng(M * 11 + N_ + K)
     w = (rng.standard_normal((N_, K)) * 0.02).astype(F16)

@@ -109,6 +109,21 @@ def test_latency_interpolation_closed_form():
     assert all(ti[n] == v for n, v in MI355X_7B_Q4_TREE_LATENCY.items()) and ti[64] > ti[32] > ti[2] > 1.0
 
 
+def test_default_profile_choice_is_pinned():
+    """The default MI355X profile with the default acceptance probabilities picks the 15-node,
+    depth-3 tree (expected 2.77 tokens, speedup 1.865), for either budget cap; a profile whose
+    t(3), t(4) sit above t(8) (the decode GEMV serving up to four rows) would not."""
+    for cap in (32, 64):
+        r = SequoiaDPOptimizer(max_budget=cap).solve_optimal_tree()
+        assert (r.optimal_N, r.max_depth) == (15, 3)
+        assert r.expected_accepted_tokens == pytest.approx(2.77, abs=5e-3)
+        assert r.speedup == pytest.approx(1.865, abs=5e-3)
+        assert r.tree_choices == [(0,), (0, 0), (0, 0, 0), (0, 0, 1), (0, 1), (0, 1, 0), (0, 2), (1,), (1, 0),
+                                  (1, 0, 0), (1, 1), (2,), (2, 0), (3,)]
+    assert all(a <= b for a, b in zip(list(MI355X_7B_Q4_TREE_LATENCY.values()),
+                                      list(MI355X_7B_Q4_TREE_LATENCY.values())[1:]))
+
+
 def test_solve_optimal_tree_picks_max_speedup():
     opt = SequoiaDPOptimizer(max_budget=32, latency_profile=M3_PRO_TREE_LATENCY)
     r = opt.solve_optimal_tree()
