@@ -51,7 +51,8 @@ FILE_FLAGS = {
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    extra = FILE_FLAGS.get(os.path.basename(src), [])
+    # AXM_HIPCC_EXTRA adds flags to every compile (diagnostic builds, e.g. -DAXM_STEP_STAMPS).
+    extra = FILE_FLAGS.get(os.path.basename(src), []) + os.environ.get("AXM_HIPCC_EXTRA", "").split()
     cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, *extra, "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

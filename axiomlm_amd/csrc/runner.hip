@@ -22,7 +22,7 @@
 
 #include "axm.h"
 #include "kernels.h"
-#include "persistent.h"
+#include "step_kernel.h"
 #include "q4_tile16.h"
 
 namespace {
@@ -312,66 +312,77 @@ struct axm_runner {
   int mode = AXM_RUNNER_MODE_GRAPH;
   hipStream_t cap_stream = nullptr;
   std::map<int, hipGraphExec_t> graphs;
-  // Persistent whole-step kernel state.
+  // Persistent whole-step kernel state (step_kernel.hip).
   bool persist_ok = false;
-  int p_grid = 0;
+  sp::Shape p_shape{};
   size_t p_smem = 0;
-  PLayer* p_layers = nullptr;              // device copy of the per-layer table
-  unsigned long long* p_bar = nullptr;     // grid barrier words
-  unsigned long long* p_head_cnt = nullptr;
+  StepLayer* p_layers = nullptr;           // device copy of the per-layer table
+  unsigned long long* p_words = nullptr;   // cross-workgroup words (sp::words_layout)
+  size_t p_words_bytes = 0;
   int64_t* p_tok_next = nullptr;
   int* p_err = nullptr;
   int* p_err_host = nullptr;               // pinned mirror, refreshed after each step
-  unsigned long long p_bar_base = 0, p_merge_base = 0;
+  unsigned p_tag = 1;                      // tag of the next launch's first phase (0 never matches)
   bool tok_next_valid = false;
 
   ~axm_runner() {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
     void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys, parts_o,
-                    qkvbuf, q8tmp, tree_pos, tree_mask, p_layers, p_bar, p_head_cnt, p_tok_next, p_err};
+                    qkvbuf, q8tmp, tree_pos, tree_mask, p_layers, p_words, p_tok_next, p_err};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     if (p_err_host) (void)hipHostFree(p_err_host);
     for (void* b : owned) (void)hipFree(b);
   }
 
-  // Set up the persistent kernel when the configuration allows it (tile16
-  // weights, fp16 KV cache, MARLIN lm_head, co-residency on every CU).  The
-  // persistent step is switched off (kPersistEnabled) while a device memory
-  // fault seen on its first launch is unexplained; set_mode(PERSISTENT) then
-  // reports it as unavailable.
-  static constexpr bool kPersistEnabled = false;
+  // Set up the persistent kernel when the configuration allows it: tile16 copies
+  // of every MARLIN Q4 matrix (group 64 or 128) and of a MARLIN lm_head, an fp16
+  // KV cache, head size 64 or 128, and co-residency of one 512-thread workgroup
+  // on every CU (step_check).
   void setup_persistent() {
-    if (!kPersistEnabled) return;
-    if (m_qkv.empty() || m_qkv[0].w16 == nullptr || d.kv_dtype != AXM_KV_FP16 || d.lm_head_format != 0 ||
-        d.group_size == 128 || d.qkv_format != 0 || d.o_format != 0 || d.gu_format != 0 || d.down_format != 0 ||
-        m_lmh.w16 == nullptr)
+    if (m_qkv.empty() || d.kv_dtype != AXM_KV_FP16 || d.lm_head_format != 0 || m_lmh.w16 == nullptr ||
+        d.qkv_format != 0 || d.o_format != 0 || d.gu_format != 0 || d.down_format != 0)
       return;
-    if (persist_check(d.d_model, d.hidden_dim, d.n_head, d.head_dim, d.vocab_size, &p_grid, &p_smem) != 0) return;
+    for (int i = 0; i < d.n_layer; ++i)
+      if (!m_qkv[i].w16 || !m_o[i].w16 || !m_gu[i].w16 || !m_dn[i].w16) return;
+    sp::Shape sh{};
+    sh.L = d.n_layer;
+    sh.D = d.d_model;
+    sh.H = d.hidden_dim;
+    sh.Hq = d.n_head;
+    sh.Hkv = d.n_kv_head;
+    sh.hd = d.head_dim;
+    sh.V = d.vocab_size;
+    sh.S = d.max_seq_len;
+    sh.g128 = d.group_size == 128 ? 1 : 0;
+    if (step_check(sh, &p_smem) != 0) return;
     const int L = d.n_layer;
-    std::vector<PLayer> host(L);
+    std::vector<StepLayer> host(L);
     for (int i = 0; i < L; ++i) {
-      PLayer& p = host[i];
-      p.qkv_w = (const u32x4*)m_qkv[i].w16;
-      p.qkv_sb = (const u32x2*)m_qkv[i].sb16;
-      p.o_w = (const u32x4*)m_o[i].w16;
-      p.o_sb = (const u32x2*)m_o[i].sb16;
-      p.gu_w = (const u32x4*)m_gu[i].w16;
-      p.gu_sb = (const u32x2*)m_gu[i].sb16;
-      p.dn_w = (const u32x4*)m_dn[i].w16;
-      p.dn_sb = (const u32x2*)m_dn[i].sb16;
+      StepLayer& p = host[i];
+      p.qkv_w = m_qkv[i].w16;
+      p.qkv_sb = m_qkv[i].sb16;
+      p.o_w = m_o[i].w16;
+      p.o_sb = m_o[i].sb16;
+      p.gu_w = m_gu[i].w16;
+      p.gu_sb = m_gu[i].sb16;
+      p.dn_w = m_dn[i].w16;
+      p.dn_sb = m_dn[i].sb16;
       p.ln1 = (const f16*)ln1[i];
       p.ln2 = (const f16*)ln2[i];
       p.qkv_bias = (const f16*)qkv_b[i];
       p.kc = (f16*)kc[i];
       p.vc = (f16*)vc[i];
     }
-    if (hipMalloc(&p_layers, sizeof(PLayer) * L) != hipSuccess ||
-        hipMemcpy(p_layers, host.data(), sizeof(PLayer) * L, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMalloc(&p_bar, kPersistBarBytes) != hipSuccess || hipMemset(p_bar, 0, kPersistBarBytes) != hipSuccess ||
-        hipMalloc(&p_head_cnt, sizeof(unsigned long long) * d.n_head) != hipSuccess ||
-        hipMemset(p_head_cnt, 0, sizeof(unsigned long long) * d.n_head) != hipSuccess ||
+    p_words_bytes = (size_t)sp::words_layout(sh).total * sizeof(unsigned long long);
+#ifdef AXM_STEP_STAMPS
+    // Diagnostic build: phase timestamps follow the words (4 per workgroup and phase).
+    p_words_bytes += (size_t)sh.G * sp::n_phases(sh) * 6 * sizeof(unsigned long long);
+#endif
+    if (hipMalloc(&p_layers, sizeof(StepLayer) * L) != hipSuccess ||
+        hipMemcpy(p_layers, host.data(), sizeof(StepLayer) * L, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMalloc(&p_words, p_words_bytes) != hipSuccess || hipMemset(p_words, 0, p_words_bytes) != hipSuccess ||
         hipMalloc(&p_tok_next, sizeof(int64_t)) != hipSuccess || hipMemset(p_tok_next, 0, sizeof(int64_t)) != hipSuccess ||
         hipMalloc(&p_err, sizeof(int)) != hipSuccess || hipMemset(p_err, 0, sizeof(int)) != hipSuccess ||
         hipHostMalloc(&p_err_host, sizeof(int), hipHostMallocDefault) != hipSuccess) {
@@ -379,37 +390,41 @@ struct axm_runner {
       return;
     }
     *p_err_host = 0;
-    persist_ok = kPersistEnabled;
+    p_shape = sh;
+    persist_ok = true;
   }
 
   int step_persistent(const int64_t* idx_dev, int64_t tok_host, int rope_pos, int write_pos, int active_len,
                       hipStream_t s) {
     if (*p_err_host != 0) {
-      axm_set_error("runner_step: an earlier persistent step timed out waiting for a grid barrier");
+      axm_set_error("runner_step: an earlier persistent step gave up waiting for another workgroup");
       return -6;
     }
-    PArgs a{};
+    const int nph = sp::n_phases(p_shape);
+    if (p_tag > 0xFFFFFFFFu - (unsigned)nph) {
+      // Tags would wrap: clear every word so that no stale tag can match, restart at 1.
+      if (hipMemsetAsync(p_words, 0, p_words_bytes, s) != hipSuccess) {
+        axm_set_error("runner_step: clearing the persistent step's words failed");
+        return -5;
+      }
+      p_tag = 1;
+    }
+    StepArgs a{};
+    a.sh = p_shape;
     a.layers = p_layers;
-    a.L = d.n_layer;
-    a.D = d.d_model;
-    a.H = d.hidden_dim;
-    a.Hq = d.n_head;
-    a.Hkv = d.n_kv_head;
-    a.hd = d.head_dim;
-    a.V = d.vocab_size;
-    a.S = d.max_seq_len;
-    a.rope_len = d.rope_len;
-    a.eps = d.eps;
-    a.scale_log2 = 1.4426950408889634f / sqrtf((float)d.head_dim);
-    a.freqs = d.freqs;
+    a.lm_w = m_lmh.w16;
+    a.lm_sb = m_lmh.sb16;
     a.lnf = (const f16*)d.lnf_w;
-    a.lm_w = (const u32x4*)m_lmh.w16;
-    a.lm_sb = (const u32x2*)m_lmh.sb16;
+    a.freqs = d.freqs;
+    a.rope_len = d.rope_len;
     a.wte_fmt = d.wte_format;
     a.wte = d.wte;
     a.wte_sb = (const f16*)d.wte_sb;
+    a.eps = d.eps;
+    a.scale_log2 = 1.4426950408889634f / sqrtf((float)d.head_dim);
     a.idx_dev = idx_dev;
     a.tok_host = tok_host;
+    a.tok_prev = p_tok_next;
     a.tok_used = reinterpret_cast<int64_t*>(reinterpret_cast<unsigned char*>(params) + kTokenOffset);
     if (idx_dev == nullptr && tok_host < 0 && !tok_next_valid) {
       // Greedy feedback after a step of another mode: reduce its argmax keys first.
@@ -420,25 +435,18 @@ struct axm_runner {
     a.rope_pos = rope_pos;
     a.write_pos = write_pos;
     a.active_len = active_len;
-    a.n_splits = persist_choose_splits(p_grid, d.n_head, d.head_dim, active_len);
-    a.bar_base = p_bar_base;
-    a.merge_base = p_merge_base;
-    a.x = x;
-    a.q = q;
-    a.attn = attn_y;
-    a.h = hbuf;
+    a.n_splits = sp::choose_splits(p_shape, active_len);
+    a.tag0 = p_tag;
+    a.spin_limit = 1 << 20;
+    a.words = p_words;
     a.logits = logits;
     a.norm_out = norm;
-    a.ws = ws;
-    a.keys = argmax_keys;
+    a.argmax_keys = argmax_keys;
     a.tok_next = p_tok_next;
-    a.bar = p_bar;
-    a.head_cnt = p_head_cnt;
     a.err = p_err;
-    const int rc = persist_launch(a, p_grid, p_smem, s);
+    const int rc = step_launch(a, p_smem, s);
     if (rc) return rc;
-    p_bar_base += (unsigned long long)persist_barriers_per_step(d.n_layer);
-    if (a.n_splits > 1) p_merge_base += (unsigned long long)d.n_layer * a.n_splits;
+    p_tag += (unsigned)nph;
     if (hipMemcpyAsync(p_err_host, p_err, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) {
       axm_set_error("runner_step: error-flag copy failed");
       return -5;
@@ -978,8 +986,8 @@ extern "C" int axm_runner_set_mode(axm_runner_t r, int mode) {
   AXM_CHECK_ARG(mode == AXM_RUNNER_MODE_GRAPH || mode == AXM_RUNNER_MODE_EAGER || mode == AXM_RUNNER_MODE_PERSISTENT,
                 -1, "runner_set_mode: unknown mode %d", mode);
   AXM_CHECK_ARG(mode != AXM_RUNNER_MODE_PERSISTENT || r->persist_ok, -1,
-                "runner_set_mode: the persistent step needs tile16 weights, an fp16 KV cache, a MARLIN lm_head and "
-                "co-residency of one workgroup per CU");
+                "runner_set_mode: the persistent step needs tile16 copies of MARLIN Q4 layer and lm_head weights, an "
+                "fp16 KV cache, head size 64 or 128 and one co-resident 512-thread workgroup per CU");
   r->mode = mode;
   return 0;
 }
@@ -995,7 +1003,7 @@ extern "C" int axm_runner_check(axm_runner_t r) {
     return -5;
   }
   if (e != 0) {
-    axm_set_error("runner_check: a persistent step timed out waiting for a grid barrier");
+    axm_set_error("runner_check: a persistent step gave up waiting for another workgroup");
     return -6;
   }
   return 0;
@@ -1081,6 +1089,13 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
 extern "C" int axm_runner_token_slot(axm_runner_t r, void** tok_out) {
   AXM_CHECK_ARG(r && tok_out, -1, "runner_token_slot: null argument");
   *tok_out = reinterpret_cast<unsigned char*>(r->params) + kTokenOffset;
+  return 0;
+}
+
+extern "C" int axm_runner_persistent_words(axm_runner_t r, void** words_out, int64_t* n_words) {
+  AXM_CHECK_ARG(r && words_out && n_words, -1, "runner_persistent_words: null argument");
+  *words_out = r->persist_ok ? (void*)r->p_words : nullptr;
+  *n_words = r->persist_ok ? (int64_t)(r->p_words_bytes / sizeof(unsigned long long)) : 0;
   return 0;
 }
 

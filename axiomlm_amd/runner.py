@@ -22,8 +22,9 @@ re-tiles every MARLIN matrix once, bit-exactly, for the matrix-core GEMV;
 The runner holds references to every tensor it was given (weights and the
 caller's KV cache views); ``step`` returns a view of a persistent logits
 buffer that is overwritten by the next call, like the reference.  ``set_mode``
-selects how a step executes: "persistent" (one cooperative launch per token,
-the default when the configuration allows it), "graph" or "eager".
+selects how a step executes: "graph" (the default: the per-op kernels replayed
+as one captured hipGraph), "eager" (the same kernels launched one by one) or
+"persistent" (one cooperative launch per token, when the configuration allows it).
 """
 
 from __future__ import annotations
@@ -195,7 +196,10 @@ class QuantizedDecodeRunner:
                 torch.cuda.synchronize(self.device)
             except Exception:
                 pass
-            _lib.lib().axm_runner_destroy(h)
+            try:
+                _lib.lib().axm_runner_destroy(h)
+            except Exception:  # interpreter shutdown: the library object may already be gone
+                pass
             self._h = None
 
     MODES = {"graph": 0, "eager": 1, "persistent": 2}
@@ -205,8 +209,8 @@ class QuantizedDecodeRunner:
         _lib.check(_lib.lib().axm_runner_set_graph(self._h, int(bool(enable))), "set_graph")
 
     def set_mode(self, mode: str) -> None:
-        """"persistent" (one cooperative launch per token, the default when available),
-        "graph" or "eager" (five kernels per layer)."""
+        """"graph" (default) or "eager" (five kernels per layer), or "persistent" (one cooperative
+        launch per token)."""
         if mode not in self.MODES:
             raise ValueError(f"mode must be one of {sorted(self.MODES)}, got {mode!r}")
         _lib.check(_lib.lib().axm_runner_set_mode(self._h, self.MODES[mode]), "set_mode")
@@ -217,7 +221,7 @@ class QuantizedDecodeRunner:
         return {v: k for k, v in self.MODES.items()}[m]
 
     def check(self) -> None:
-        """Synchronize and raise if a persistent step gave up waiting on a grid barrier."""
+        """Synchronize and raise if a persistent step gave up waiting for another workgroup."""
         _lib.check(_lib.lib().axm_runner_check(self._h), "QuantizedDecodeRunner.check")
 
     def step(self, idx, start_pos: int, write_pos: int, active_len: int) -> torch.Tensor:
@@ -303,6 +307,20 @@ class QuantizedDecodeRunner:
         p = ctypes.c_void_p()
         _lib.check(_lib.lib().axm_runner_token_slot(self._h, ctypes.byref(p)), "last_token")
         return _RawBuffer.view(p.value, 4, self.device).view(torch.int64)
+
+    def persistent_words(self) -> torch.Tensor | None:
+        """Copy of the persistent step's cross-workgroup words as int64 (payload in the low
+        32 bits, phase tag in the high 32), or None when the mode is unavailable; a
+        diagnostic view of the last layer's intermediate vectors."""
+        p = ctypes.c_void_p()
+        n = ctypes.c_int64()
+        _lib.check(_lib.lib().axm_runner_persistent_words(self._h, ctypes.byref(p), ctypes.byref(n)),
+                   "persistent_words")
+        if n.value == 0:
+            return None
+        torch.cuda.synchronize(self.device)
+        raw = _RawBuffer.view(p.value, 4 * n.value, self.device)
+        return raw.view(torch.int64).clone()
 
     def get_last_norm(self, T: int = 1) -> torch.Tensor:
         """Clone of the final normalized hidden state (mps_kernels.mm:3732-3737)."""

@@ -111,6 +111,12 @@ def build_model(c, dev, seed=0, group_size=64):
     return runner, cache, layers, lnf
 
 
+def set_mode(runner, mode: str) -> str:
+    """Select the step execution ("graph" or "persistent")."""
+    runner.set_mode(mode)
+    return runner.mode
+
+
 def time_decode(runner, cache, steps, warmup, dev, ctx0=CTX0):
     """Greedy decode: argmax of step t (device) is the token of step t+1."""
     import torch
@@ -294,6 +300,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--group", type=int, choices=(64, 128), default=HEADLINE_GROUP,
                     help="MARLIN group size of the headline decode and the gate/up roofline (default %(default)s)")
+    ap.add_argument("--mode", choices=("graph", "persistent"), default="graph",
+                    help="decode step execution: the captured per-op graph (the faster on MI355X) or the one-launch "
+                         "persistent step (default %(default)s)")
     ap.add_argument("--no-other-group", action="store_true",
                     help="skip the decode line of the other group size")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -332,6 +341,7 @@ def main():
     runner, cache, layers, lnf = build_model(c, dev, group_size=G)
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t_build
+    mode = set_mode(runner, args.mode)
     print(f"[bench] model built and packed in {t_build:.1f} s", file=sys.stderr, flush=True)
     if args.kernel_only:
         avg_us, bpl = time_gate_up_kernel(layers, c, dev, reps=20, group=G)
@@ -357,6 +367,7 @@ def main():
         del runner, cache, layers, lnf
         torch.cuda.empty_cache()
         runner, cache, layers, lnf = build_model(c, dev, group_size=other)
+        set_mode(runner, args.mode)
         if not args.no_other_group:
             ms2, _, p2 = time_decode(runner, cache, args.steps, args.warmup, dev, args.context)
             ms2 /= args.steps

@@ -326,16 +326,23 @@ int axm_runner_token_slot(axm_runner_t r, void** tok_out);
 /* Normalized final hidden state of the last call (fp16 [T][d]),
  * get_last_norm (mps_kernels.mm:3732-3737). */
 int axm_runner_last_norm(axm_runner_t r, void** norm_out);
+/* Diagnostic view of the persistent step's cross-workgroup words (uint64: 32-bit
+ * payload | 32-bit phase tag << 32) as the last persistent step left them: the
+ * residual stream, queries, new key / value rows, attention output and SwiGLU output
+ * of the last layer (layout in csrc/step_plan.h, sp::words_layout).  *n_words = 0
+ * when the persistent step is unavailable.  No counterpart in the reference. */
+int axm_runner_persistent_words(axm_runner_t r, void** words_out, int64_t* n_words);
 /* 1 = replay the per-op step as a captured hipGraph, 0 = eager launches
  * (equivalent to axm_runner_set_mode GRAPH / EAGER). */
 int axm_runner_set_graph(axm_runner_t r, int enable);
 /* Execution of a decode step:
  *   GRAPH      the per-op kernels (five per layer) replayed as a hipGraph;
  *   EAGER      the same kernels launched one by one;
- *   PERSISTENT one cooperative launch per token that runs every layer with
- *              grid barriers between phases and streams the next phase's
- *              weights while it waits (default when available: tile16
- *              weights, fp16 KV cache, MARLIN lm_head).
+ *   PERSISTENT one cooperative launch per token that runs every layer; each
+ *              phase polls the tagged words its inputs arrive in instead of
+ *              waiting at a grid barrier, and the next phase's weights stream
+ *              while it waits (available with tile16 copies of MARLIN Q4 layer
+ *              and lm_head weights, an fp16 KV cache, head size 64 or 128).
  * No counterpart in the reference, whose step is a single Metal command
  * buffer (mps_kernels.mm:3195-3263). */
 #define AXM_RUNNER_MODE_GRAPH 0
@@ -343,8 +350,8 @@ int axm_runner_set_graph(axm_runner_t r, int enable);
 #define AXM_RUNNER_MODE_PERSISTENT 2
 int axm_runner_set_mode(axm_runner_t r, int mode);
 int axm_runner_get_mode(axm_runner_t r);
-/* Synchronizes and returns -6 if a persistent step gave up waiting on a grid
- * barrier (the runner must then be recreated), 0 otherwise. */
+/* Synchronizes and returns -6 if a persistent step gave up waiting for another
+ * workgroup's output (the runner must then be recreated), 0 otherwise. */
 int axm_runner_check(axm_runner_t r);
 
 #ifdef __cplusplus

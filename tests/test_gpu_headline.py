@@ -81,22 +81,23 @@ def _fill_context(cache, ctx, seed):
     cache.layer_seq_lens[:] = [ctx] * cache.n_layer
 
 
-def test_headline_g128_7b_layer_step_greedy_and_last_norm(dev):
-    """One 7B-shape group-128 layer + 32000-row group-128 lm_head through the captured step
-    (the benchmark's kernel instantiations), 140 keys of fp16 context, one step with a given
-    token then seven device-fed greedy steps, a 4-token verify chain; logits, greedy
-    choices and get_last_norm against the oracle."""
+@pytest.mark.parametrize("mode", ["graph", "persistent"])
+def test_headline_g128_7b_layer_step_greedy_and_last_norm(dev, mode):
+    """One 7B-shape group-128 layer + 32000-row group-128 lm_head through the decode step
+    (graph: the benchmark's kernel instantiations; persistent: the one-launch step), 140
+    keys of fp16 context, one step with a given token then seven device-fed greedy steps,
+    a 4-token verify chain; logits, greedy choices and get_last_norm against the oracle."""
     from test_gpu_runner import _load_gpu_cache, build_runner
 
     cfg = om.OracleConfig(n_layer=1, n_head=32, n_kv_head=32, d_model=4096, hidden=11008, vocab=32000, eps=1e-5,
                           block_size=4096)
     S, ctx = 4096, 140
-    print(f"[headline_g128] d={cfg.d_model} heads={cfg.n_head} V={cfg.vocab} ctx={ctx}", flush=True)
+    print(f"[headline_g128] mode={mode} d={cfg.d_model} heads={cfg.n_head} V={cfg.vocab} ctx={ctx}", flush=True)
     ow = _packs(dev, cfg, 128, seed=11)
     cos, sin = om.rope_tables(cfg.head_dim, cfg.block_size, 10000.0)
     model = om.OracleModel(cfg, ow, cos, sin)
-    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16")
-    assert runner.group_size == 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16", mode=mode)
+    assert runner.group_size == 128 and runner.mode == mode
     _fill_context(cache, ctx, seed=12)
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, "fp16")
     _load_gpu_cache(ocache, cache)
@@ -143,6 +144,7 @@ def test_headline_g128_7b_layer_step_greedy_and_last_norm(dev):
         err = np.abs(g[t] - ref[t].astype(F32)).max()
         assert err <= TOL, (t, err)
     check_norm(4, ref_norm, "verify chain of 4")
+    runner.check()
 
 
 def _full_packs(dev, group=128, seed=0):

@@ -84,10 +84,8 @@ def _check_logits(got, ref, what):
     assert err <= TOL, f"{what}: max |logit diff| {err}"
 
 
-PERSIST_OFF = pytest.mark.skip(reason="persistent step switched off: its first launch faulted the GPU and the cause "
-                                      "is not yet identified")
-EXEC = [("tile16", "graph"), ("marlin", "graph"), pytest.param("tile16", "persistent", marks=PERSIST_OFF)]
-MODES = ["graph", pytest.param("persistent", marks=PERSIST_OFF)]
+EXEC = [("tile16", "graph"), ("marlin", "graph"), ("tile16", "persistent")]
+MODES = ["graph", "persistent"]
 
 
 @pytest.mark.parametrize("layout,mode", EXEC)
@@ -300,12 +298,12 @@ def test_runner_matches_reference_golden(dev, layout, mode):
     assert toks == g["greedy_tokens"].tolist()
 
 
-@PERSIST_OFF
 def test_persistent_matches_graph_wide_model(dev):
     """A wider two-layer model (d 1024, 8 heads x 128, SwiGLU 2816, vocab 4096, GQA 2 KV
     heads) where every workgroup owns several tiles per phase and attention splits:
-    the persistent step and the graph step agree to fp32-accumulation-order noise
-    (|diff| <= 2e-3 + 2e-3 |logit|) over 40 steps, and both match the oracle."""
+    the persistent step and the graph step (different summation orders: the persistent
+    kernel splits each GEMV over seven waves and merges attention splits in fp32 words)
+    agree within the parity bar over 40 steps, and the persistent step matches the oracle."""
     print("[persistent_wide]", flush=True)
     cfg = om.OracleConfig(n_layer=2, n_head=8, n_kv_head=2, d_model=1024, hidden=2816, vocab=4096, eps=1e-5,
                           block_size=512)
@@ -322,7 +320,7 @@ def test_persistent_matches_graph_wide_model(dev):
         outs[mode] = np.stack(run_steps(runner, cache, toks, dev))
         runner.check()
     d = np.abs(outs["graph"] - outs["persistent"])
-    assert np.all(d <= 2e-3 + 2e-3 * np.abs(outs["graph"])), f"max diff {d.max()}"
+    assert np.all(d <= TOL), f"max diff {d.max()}"
     model = om.OracleModel(cfg, ow, cos, sin)
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
     for i, tok in enumerate(toks):
