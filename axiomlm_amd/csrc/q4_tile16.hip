@@ -114,8 +114,11 @@ __device__ __forceinline__ void t16_load_x(const T16Args& a, T16X<M, TH>& r) {
   constexpr int XV = T16XV<TH>::value;
   const int tid = threadIdx.x;
   const int nv = a.K >> 3;
+  const int nv_pad = (a.KB * 128) >> 3;
 #pragma unroll
   for (int v = 0; v < XV; ++v) {
+    // Vectors past the padded row are never staged (workgroup-uniform bound).
+    if (v * TH >= nv_pad) break;
     const int i = tid + v * TH;
     const bool ok = i < nv;
 #pragma unroll
@@ -228,14 +231,17 @@ __device__ void t16_stage_x(const T16Args& a, const T16X<M, TH>& r, f16* xs, f32
       float s = 0.f;
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
-        // Vectors past nv were loaded as zeros and add nothing.
+        // Vectors past nv hold zeros and add nothing: the loop stops at the last
+        // vector any thread loaded (a uniform bound; K = 4096 needs one or two of
+        // the XV vectors that K = 16384 would).
+        if (v * TH >= nv) break;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float f = h2f(r.x[mi][v][e]);
           s += h2f(f2h(f * f));
         }
       }
-      s = wave_sum(s);
+      s = wave_sum_dpp(s);
       if ((tid & 63) == 0) red[mi * W + (tid >> 6)] = s;
     }
     __syncthreads();
@@ -271,8 +277,8 @@ __device__ void t16_stage_x(const T16Args& a, const T16X<M, TH>& r, f16* xs, f32
         corr += f * (((e >> 1) & 1) ? 64.f : 1024.f);
       }
       // 8 consecutive vectors form one 64-group.
-      corr = group_sum<8>(corr);
-      sum = group_sum<8>(sum);
+      corr = group8_sum_dpp(corr);
+      sum = group8_sum_dpp(sum);
       if (i < nv_pad) {
         reinterpret_cast<f16x8*>(xs + (size_t)mi * a.KB * 128)[i] = x;
         if ((tid & 7) == 0) cx[(size_t)mi * 2 * a.KB + (i >> 3)] = f32x2{corr, sum};
@@ -433,6 +439,9 @@ constexpr int kT16WaveDepth = 12;
 // Chunks issued before the activation staging (7B decode step on one MI355X:
 // 1 / 2 / 3 / 4 / 8 gave 698 / 721 / 725 / 713 / 529 tok/s).
 constexpr int kT16WavePre = 3;
+// The same PRE chunks stay requested ahead of the one being consumed after the
+// staging (keeping 5 / 7 / 9 / 11 ahead instead, topped up right after the staging
+// barrier, gave 728 / 720 / 722 / 725 against 756 tok/s).
 // Chunk jj + PRE is requested into the slot of chunk jj + PRE - P before chunk jj is
 // consumed, so PRE must stay below the ring size.
 static_assert(kT16WavePre < kT16WaveDepth, "kT16Wave ring");
@@ -769,6 +778,8 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   // Waves per unit: aim for ~8 waves per CU with >= 2 kb-loads per wave; the S
   // waves of a unit belong to one workgroup.
   const int cus = axm_num_cus();
+  // (Aiming at 16 or 32 waves per CU instead left a second round of gate|up
+  // workgroups: 764 -> 670 tok/s.)
   auto split_for = [&](int waves) {
     int S = 1;
     while (S < waves && a.n_units * S < 8 * cus && a.KB >= 4 * S) S *= 2;
