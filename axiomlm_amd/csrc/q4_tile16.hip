@@ -203,7 +203,8 @@ __device__ __forceinline__ void t16_merge_parts(const T16Args& a, const T16Parts
   }
   f16x8 x;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = f2h(wsum > 0.f ? acc[e] / wsum : 0.f);
+  // One reciprocal instead of eight divisions on the O launch's staging path.
+  for (int e = 0; e < 8; ++e) x[e] = f2h(acc[e] * (wsum > 0.f ? 1.f / wsum : 0.f));
   const bool ok = (int)threadIdx.x < (a.K >> 3);
 #pragma unroll
   for (int v = 0; v < T16XV<TH>::value; ++v) {
@@ -787,11 +788,12 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   };
   int th = kT16Threads;
   int S = split_for(kT16Threads / 64);
-  // Between one and 1.5 512-thread workgroups per CU, some CUs would hold two
-  // and most one (workgroups of one launch all resident): 256-thread
-  // workgroups spread the same waves more evenly (7B decode on one MI355X:
-  // gate|up 13.3 -> 12.3 us).  With exactly one per CU (the down projection)
-  // and from 1.5 per CU on (QKV, lm_head) 512 threads were as fast or faster
+  // Above one and up to 1.5 512-thread workgroups per CU, some CUs would hold
+  // two and the rest one (workgroups of one launch all resident): 256-thread
+  // workgroups spread the same waves evenly (7B decode on one MI355X: gate|up
+  // 13.3 -> 12.3 us; QKV, exactly 1.5 per CU, 790 -> 796 tok/s once the staging
+  // reductions moved to DPP).  With exactly one per CU (the down projection)
+  // and beyond 1.5 per CU (the lm_head) 512 threads were as fast or faster
   // (down with 256 threads: 742 -> 731 tok/s).  One token only: with more,
   // the activation registers of 256 threads covering K <= 16384 (eight vectors
   // per thread and token) cost more than the balance gains (two-token verify
@@ -801,7 +803,7 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   // would run the looping form, which was never measured against 512 threads.
   if (M == 1 && a.x_parts == nullptr && S > 1) {
     const int grid512 = (a.n_units + kT16Threads / 64 / S - 1) / (kT16Threads / 64 / S);
-    if (grid512 > cus && 2 * grid512 < 3 * cus) {
+    if (grid512 > cus && 2 * grid512 <= 3 * cus) {
       th = kT16ThreadsSmall;
       S = split_for(kT16ThreadsSmall / 64);
     }
