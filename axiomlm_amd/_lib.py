@@ -114,6 +114,7 @@ _SIGNATURES = {
     "axm_runner_last_norm": (c_int, [c_void_p, c_void_p]),
     "axm_runner_persistent_words": (c_int, [c_void_p, c_void_p, c_void_p]),
     "axm_runner_token_slot": (c_int, [c_void_p, c_void_p]),
+    "axm_runner_time_kernels": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, ctypes.POINTER(c_float)]),
     "axm_runner_set_graph": (c_int, [c_void_p, c_int]),
     "axm_runner_set_mode": (c_int, [c_void_p, c_int]),
     "axm_runner_get_mode": (c_int, [c_void_p]),

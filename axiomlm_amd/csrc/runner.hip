@@ -463,99 +463,139 @@ struct axm_runner {
 
   // Enqueue the whole single-token step on stream s (no host synchronization).
   // The decode step after set_params_kernel, which has written the token's
-  // embedding row into x.
+  // embedding row into x.  Each launch group of a layer is its own member
+  // (axm_runner_time_kernels times them one at a time).
   int enqueue_step(int n_splits, bool short_splits, hipStream_t s) {
-    const int D = d.d_model;
-    const int H = d.hidden_dim;
-
     for (int i = 0; i < d.n_layer; ++i) {
-      KvView kv = kv_view(i);
-      // 1. QKV with RMSNorm prologue and RoPE / KV-write epilogue.
-      GemvCall a{};
-      a.x = x;
-      a.ldx = D;
-      a.y = q;
-      a.ldy = q_dim;
-      a.bias = (const f16*)qkv_b[i];
-      a.ln_w = (const f16*)ln1[i];
-      a.eps = d.eps;
-      a.q_dim = q_dim;
-      a.kv_dim = kv_dim;
-      a.head_dim = d.head_dim;
-      a.freqs = d.freqs;
-      a.rope_len = d.rope_len;
-      a.rope_pos_dev = params + P_ROPE;
-      if (d.kv_dtype == AXM_KV_FP16) {
-        a.write_pos_dev = params + P_WRITE;
-        a.k_out = (f16*)kc[i];
-        a.v_out = (f16*)vc[i];
-        a.kv_stride_h = (long)d.max_seq_len * d.head_dim;
-        a.max_seq = d.max_seq_len;
-      } else {
-        // Stage fp16 k / v rows; the quantizer writes the cache slot.
-        a.k_out = kvst;
-        a.v_out = kvst + kv_dim;
-        a.kv_stride_h = d.head_dim;
-        a.max_seq = 1;
-      }
-      int rc = 0;
-      if (m_qkv[i].fmt != 0) {
-        // Q8_G64 / fp16 QKV: GEMV (+ bias) into qkvbuf, RoPE of q / k into q / kvst, then the slot write.
-        rc = dense_gemv(m_qkv[i], x, a.bias, qkvbuf, 1, qkv_dim, a.ln_w, d.eps, s);
-        if (rc) return rc;
-        hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, 1), dim3(256), 0, s, qkvbuf, q_dim,
-                           kv_dim, d.head_dim, d.freqs, params + P_ROPE, q, kvst);
-        launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
-      } else {
-        rc = run_gemv(m_qkv[i], Q4_EPI_QKV_ROPE, qkv_dim, a, 1, s);
-        if (rc) return rc;
-        if (d.kv_dtype != AXM_KV_FP16)
-          launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
-      }
-      // 2. attention over slots [0, active_len); with parts_ok the split
-      // partials are merged while the O projection stages its activations.
-      const bool merge_in_o = parts_ok && n_splits > 1;
-      if (merge_in_o)
-        rc = launch_flash_decode_parts(q, kv, d.n_head, 0, params + P_ACTIVE, n_splits, parts_o, parts_ml,
-                                       short_splits, s);
-      else
-        rc = launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
+      int rc = enqueue_qkv(i, s);
       if (rc) return rc;
-      // 3. O projection, residual add into x.
-      GemvCall o{};
-      o.x = attn_y;
-      o.ldx = q_dim;
-      o.resid = x;
-      o.ldr = D;
-      if (merge_in_o) {
-        o.x_parts = parts_o;
-        o.x_ml = parts_ml;
-        o.n_parts = n_splits;
-        o.parts_hd = d.head_dim;
-      }
-      rc = gemv(m_o[i], Q4_EPI_RESID, D, o, 1, s);
+      rc = enqueue_attention(i, n_splits, short_splits, s);
       if (rc) return rc;
-      // 4. gate/up with RMSNorm prologue and SwiGLU epilogue.
-      GemvCall g{};
-      g.x = x;
-      g.ldx = D;
-      g.y = hbuf;
-      g.ldy = H;
-      g.ln_w = (const f16*)ln2[i];
-      g.eps = d.eps;
-      g.pair_rows = H;
-      rc = gemv(m_gu[i], Q4_EPI_SWIGLU, H, g, 1, s);
+      rc = enqueue_o(i, n_splits, s);
       if (rc) return rc;
-      // 5. down projection, residual add.
-      GemvCall dn{};
-      dn.x = hbuf;
-      dn.ldx = H;
-      dn.resid = x;
-      dn.ldr = D;
-      rc = gemv(m_dn[i], Q4_EPI_RESID, D, dn, 1, s);
+      rc = enqueue_gate_up(i, s);
+      if (rc) return rc;
+      rc = enqueue_down(i, s);
       if (rc) return rc;
     }
-    // Final RMSNorm + lm_head (+ per-tile greedy argmax keys).
+    return enqueue_lm_head(s);
+  }
+
+  // The attention split count of a one-token step over active_len keys, bucketed
+  // so that one graph covers a range of lengths; splits of at most 64 keys use a
+  // smaller attention launch shape (the graph key carries both).
+  void split_shape(int active_len, int* bucket_out, bool* short_out) const {
+    const int splits = parts_ok ? attn_parts_splits(1, d.n_kv_head, active_len)
+                                : attn_choose_splits(1, d.n_kv_head, active_len);
+    int bucket = 1;
+    while (bucket < splits) bucket <<= 1;
+    if (bucket > max_splits) bucket = max_splits;
+    *bucket_out = bucket;
+    *short_out = active_len <= 64 * bucket;
+  }
+
+  // With parts_ok and more than one split, the attention leaves its split
+  // partials for the O projection to merge while staging its activations.
+  bool merge_in_o(int n_splits) const { return parts_ok && n_splits > 1; }
+
+  // 1. QKV with RMSNorm prologue and RoPE / KV-write epilogue.
+  int enqueue_qkv(int i, hipStream_t s) {
+    const int D = d.d_model;
+    KvView kv = kv_view(i);
+    GemvCall a{};
+    a.x = x;
+    a.ldx = D;
+    a.y = q;
+    a.ldy = q_dim;
+    a.bias = (const f16*)qkv_b[i];
+    a.ln_w = (const f16*)ln1[i];
+    a.eps = d.eps;
+    a.q_dim = q_dim;
+    a.kv_dim = kv_dim;
+    a.head_dim = d.head_dim;
+    a.freqs = d.freqs;
+    a.rope_len = d.rope_len;
+    a.rope_pos_dev = params + P_ROPE;
+    if (d.kv_dtype == AXM_KV_FP16) {
+      a.write_pos_dev = params + P_WRITE;
+      a.k_out = (f16*)kc[i];
+      a.v_out = (f16*)vc[i];
+      a.kv_stride_h = (long)d.max_seq_len * d.head_dim;
+      a.max_seq = d.max_seq_len;
+    } else {
+      // Stage fp16 k / v rows; the quantizer writes the cache slot.
+      a.k_out = kvst;
+      a.v_out = kvst + kv_dim;
+      a.kv_stride_h = d.head_dim;
+      a.max_seq = 1;
+    }
+    int rc = 0;
+    if (m_qkv[i].fmt != 0) {
+      // Q8_G64 / fp16 QKV: GEMV (+ bias) into qkvbuf, RoPE of q / k into q / kvst, then the slot write.
+      rc = dense_gemv(m_qkv[i], x, a.bias, qkvbuf, 1, qkv_dim, a.ln_w, d.eps, s);
+      if (rc) return rc;
+      hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, 1), dim3(256), 0, s, qkvbuf, q_dim,
+                         kv_dim, d.head_dim, d.freqs, params + P_ROPE, q, kvst);
+      launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
+    } else {
+      rc = run_gemv(m_qkv[i], Q4_EPI_QKV_ROPE, qkv_dim, a, 1, s);
+      if (rc) return rc;
+      if (d.kv_dtype != AXM_KV_FP16) launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
+    }
+    return 0;
+  }
+
+  // 2. attention over slots [0, active_len).
+  int enqueue_attention(int i, int n_splits, bool short_splits, hipStream_t s) {
+    KvView kv = kv_view(i);
+    if (merge_in_o(n_splits))
+      return launch_flash_decode_parts(q, kv, d.n_head, 0, params + P_ACTIVE, n_splits, parts_o, parts_ml,
+                                       short_splits, s);
+    return launch_flash_decode(q, kv, attn_y, d.n_head, 0, params + P_ACTIVE, n_splits, ws, s);
+  }
+
+  // 3. O projection, residual add into x.
+  int enqueue_o(int i, int n_splits, hipStream_t s) {
+    GemvCall o{};
+    o.x = attn_y;
+    o.ldx = q_dim;
+    o.resid = x;
+    o.ldr = d.d_model;
+    if (merge_in_o(n_splits)) {
+      o.x_parts = parts_o;
+      o.x_ml = parts_ml;
+      o.n_parts = n_splits;
+      o.parts_hd = d.head_dim;
+    }
+    return gemv(m_o[i], Q4_EPI_RESID, d.d_model, o, 1, s);
+  }
+
+  // 4. gate/up with RMSNorm prologue and SwiGLU epilogue.
+  int enqueue_gate_up(int i, hipStream_t s) {
+    GemvCall g{};
+    g.x = x;
+    g.ldx = d.d_model;
+    g.y = hbuf;
+    g.ldy = d.hidden_dim;
+    g.ln_w = (const f16*)ln2[i];
+    g.eps = d.eps;
+    g.pair_rows = d.hidden_dim;
+    return gemv(m_gu[i], Q4_EPI_SWIGLU, d.hidden_dim, g, 1, s);
+  }
+
+  // 5. down projection, residual add.
+  int enqueue_down(int i, hipStream_t s) {
+    GemvCall dn{};
+    dn.x = hbuf;
+    dn.ldx = d.hidden_dim;
+    dn.resid = x;
+    dn.ldr = d.d_model;
+    return gemv(m_dn[i], Q4_EPI_RESID, d.d_model, dn, 1, s);
+  }
+
+  // Final RMSNorm + lm_head (+ per-tile greedy argmax keys).
+  int enqueue_lm_head(hipStream_t s) {
+    const int D = d.d_model;
     if (d.lm_head_format == 0) {
       GemvCall l{};
       l.x = x;
@@ -566,14 +606,10 @@ struct axm_runner {
       l.eps = d.eps;
       l.x_norm_out = norm;
       l.argmax_keys = argmax_keys;
-      int rc = run_gemv(m_lmh, Q4_EPI_STORE, d.vocab_size, l, 1, s);
-      if (rc) return rc;
-    } else {
-      launch_rmsnorm(x, (const f16*)d.lnf_w, norm, 1, D, d.eps, s);
-      int rc = lm_head_dense(norm, 1, s);
-      if (rc) return rc;
+      return run_gemv(m_lmh, Q4_EPI_STORE, d.vocab_size, l, 1, s);
     }
-    return 0;
+    launch_rmsnorm(x, (const f16*)d.lnf_w, norm, 1, D, d.eps, s);
+    return lm_head_dense(norm, 1, s);
   }
 
   // Q8_G64 (format 1) or fp16 (format 2) lm_head over T normalized rows into logits.
@@ -1036,15 +1072,9 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
   const EmbedArgs emb{d.wte, (const f16*)d.wte_sb, d.wte_format, d.d_model, d.vocab_size, r->x};
   hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, r->params, (const int64_t*)idx_dev, tok_host,
                      rope_pos, write_pos, active_len, r->argmax_keys, (d.vocab_size + 7) / 8, emb);
-  // Bucket the split count so that one graph covers a range of lengths.
-  int splits = r->parts_ok ? attn_parts_splits(1, d.n_kv_head, active_len)
-                           : attn_choose_splits(1, d.n_kv_head, active_len);
   int bucket = 1;
-  while (bucket < splits) bucket <<= 1;
-  if (bucket > r->max_splits) bucket = r->max_splits;
-  // Splits of at most 64 keys use a smaller attention launch shape; the graph
-  // key carries that choice next to the split bucket.
-  const bool short_splits = active_len <= 64 * bucket;
+  bool short_splits = false;
+  r->split_shape(active_len, &bucket, &short_splits);
   const int key = 2 * bucket + (short_splits ? 1 : 0);
   if (r->mode == AXM_RUNNER_MODE_EAGER) {
     int rc = r->enqueue_step(bucket, short_splits, s);
@@ -1083,6 +1113,62 @@ extern "C" int axm_runner_step(axm_runner_t r, const void* idx_dev, int64_t tok_
   }
   AXM_LAUNCH_CHECK("runner_step");
   if (logits_out) *logits_out = r->logits;
+  return 0;
+}
+
+extern "C" int axm_runner_time_kernels(axm_runner_t r, int position, int active_len, int reps, void* stream,
+                                       float* us_out) {
+  AXM_CHECK_ARG(r && us_out, -1, "runner_time_kernels: null argument");
+  const axm_runner_desc& d = r->d;
+  AXM_CHECK_ARG(reps >= 1 && reps <= 100000, -1, "runner_time_kernels: reps %d out of [1, 100000]", reps);
+  AXM_CHECK_ARG(position >= 0 && position < d.max_seq_len, -1, "runner_time_kernels: position %d out of [0, %d)",
+                position, d.max_seq_len);
+  AXM_CHECK_ARG(active_len >= 1 && active_len <= d.max_seq_len, -1,
+                "runner_time_kernels: active_len %d out of [1, %d]", active_len, d.max_seq_len);
+  hipStream_t s = (hipStream_t)stream;
+  const EmbedArgs emb{d.wte, (const f16*)d.wte_sb, d.wte_format, d.d_model, d.vocab_size, r->x};
+  hipLaunchKernelGGL(set_params_kernel, dim3(1), dim3(256), 0, s, r->params, (const int64_t*)nullptr, (int64_t)0,
+                     position % d.rope_len, position, active_len, r->argmax_keys, (d.vocab_size + 7) / 8, emb);
+  int bucket = 1;
+  bool short_splits = false;
+  r->split_shape(active_len, &bucket, &short_splits);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    if (e0) (void)hipEventDestroy(e0);
+    axm_set_error("runner_time_kernels: event creation failed");
+    return -5;
+  }
+  int rc = 0;
+  for (int k = 0; k < 6 && rc == 0; ++k) {
+    auto one = [&](int j) -> int {
+      const int i = j % d.n_layer;
+      switch (k) {
+        case 0: return r->enqueue_qkv(i, s);
+        case 1: return r->enqueue_attention(i, bucket, short_splits, s);
+        case 2: return r->enqueue_o(i, bucket, s);
+        case 3: return r->enqueue_gate_up(i, s);
+        case 4: return r->enqueue_down(i, s);
+        default: return r->enqueue_lm_head(s);
+      }
+    };
+    for (int j = 0; j < 2 && rc == 0; ++j) rc = one(j);
+    if (rc) break;
+    (void)hipEventRecord(e0, s);
+    for (int j = 0; j < reps && rc == 0; ++j) rc = one(j);
+    (void)hipEventRecord(e1, s);
+    if (rc) break;
+    float ms = 0.f;
+    if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+      axm_set_error("runner_time_kernels: event timing failed");
+      rc = -5;
+      break;
+    }
+    us_out[k] = ms * 1000.f / (float)reps;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  AXM_LAUNCH_CHECK("runner_time_kernels");
   return 0;
 }
 

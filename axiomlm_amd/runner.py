@@ -308,6 +308,20 @@ class QuantizedDecodeRunner:
         _lib.check(_lib.lib().axm_runner_token_slot(self._h, ctypes.byref(p)), "last_token")
         return _RawBuffer.view(p.value, 4, self.device).view(torch.int64)
 
+    KERNEL_GROUPS = ("qkv", "attention", "o", "gate_up", "down", "lm_head")
+
+    def time_kernels(self, position: int, active_len: int, reps: int = 200) -> dict:
+        """Average microseconds per launch of each of the one-token step's launch groups
+        (KERNEL_GROUPS), each run `reps` times back to back over the layers in turn and
+        timed with HIP events on the runner's stream.  A measurement call with no
+        counterpart in the reference: it overwrites the runner's activations and the
+        cache slot at `position`, which the next step recomputes."""
+        out = (ctypes.c_float * 6)()
+        rc = _lib.lib().axm_runner_time_kernels(self._h, int(position), int(active_len), int(reps),
+                                                _lib.stream_of(self.device), out)
+        _lib.check(rc, "QuantizedDecodeRunner.time_kernels")
+        return {k: float(out[i]) for i, k in enumerate(self.KERNEL_GROUPS)}
+
     def persistent_words(self) -> torch.Tensor | None:
         """Copy of the persistent step's cross-workgroup words as int64 (payload in the low
         32 bits, phase tag in the high 32), or None when the mode is unavailable; a

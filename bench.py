@@ -12,7 +12,10 @@ the device).
 
 Printed JSON line: value = tokens/s; roofline = the runner's fused RMSNorm +
 gate/up GEMV + SwiGLU kernel (tile16 matrix-core layout; the largest per-launch
-weight stream, 47.6 MB at group 128) timed live with HIP events on its stream;
+weight stream, 47.6 MB at group 128) timed live with HIP events on its stream, beside
+its average inside the decode graph from the committed rocprofv3 summary;
+decode_kernels = every launch group of the step (QKV, attention, O, gate/up, down,
+lm_head) timed the same way, with its algorithmic bytes and fraction of the peak;
 cpu_baseline = the reference's CPU path restated with torch on the host cores
 (dequantize every weight on every call, then F.linear in fp16) on a bounded sample
 of the same step, extrapolated to tokens/s, plus C1 end to end and a C2 layer on the
@@ -144,55 +147,102 @@ def time_decode(runner, cache, steps, warmup, dev, ctx0=CTX0):
     return ms, wall, pos0
 
 
-def time_gate_up_kernel(layers, c, dev, reps=200, n_copies=8, group=HEADLINE_GROUP):
-    """Average duration of the runner's fused RMSNorm + gate/up + SwiGLU launch (tile16
-    matrix-core GEMV, 7B shape), timed with HIP events recorded on the stream it is
-    launched on.  Launches rotate over n_copies layers' weights (8 x 47.6 MB at group
-    128) so the stream does not sit in the 256 MB last-level cache."""
-    import torch
+KERNEL_NAMES = {
+    "qkv": "t16_gemv_kernel<1,1,3,12,2,G128,256>: RMSNorm + QKV Q4 GEMV + RoPE + fp16 KV slot write",
+    "attention": "attn_split_kernel<0,1,false,4,4>: split-KV flash decode, partials for the O projection",
+    "o": "t16_gemv_kernel<1,1,16,12,2,G128,512>: O Q4 GEMV merging the attention partials + residual",
+    "gate_up": "t16_gemv_kernel<1,2,2,12,2,G128,256>: RMSNorm + gate|up Q4 GEMV + SwiGLU",
+    "down": "t16_gemv_kernel<1,1,1,12,2,G128,512>: down Q4 GEMV + residual",
+    "lm_head": "t16_gemv_kernel<1,1,0,12,2,G128,512>: final RMSNorm + lm_head Q4 GEMV + argmax keys",
+}
 
-    from axiomlm_amd import _lib
-    from axiomlm_amd.kernels import repack_q4_marlin_tile16
 
-    d, H = c["d"], c["hidden"]
-    x = torch.randn(1, d, device=dev, dtype=torch.float16)
-    y = torch.empty(1, H, device=dev, dtype=torch.float16)
-    copies = [repack_q4_marlin_tile16(layers["gu_p"][i], layers["gu_s"][i], 2 * H, d) for i in range(n_copies)]
-    s = torch.cuda.current_stream(dev)
-    stream = _lib.stream_of(dev)
+def kernel_bytes(c, active_len: int, group: int) -> dict:
+    """Algorithmic HBM bytes of each launch group of one decode token (one layer's kernel;
+    the lm_head once): every weight byte (codes + scale + bias) once, the KV prefix once,
+    the activation vectors read and written.  The attention split partials are this
+    build's intermediate and not counted."""
+    d, H, hd = c["d"], c["hidden"], c["hd"]
+    qd, kvd = c["n_head"] * hd, c["n_kv_head"] * hd
+    return {
+        "qkv": q4_bytes(qd + 2 * kvd, d, group) + 2 * d * 2 + (qd + 2 * kvd) * 2,
+        "attention": 2 * c["n_kv_head"] * active_len * hd * 2 + qd * 2 + qd * 2,
+        "o": q4_bytes(d, qd, group) + qd * 2 + 2 * d * 2,
+        "gate_up": q4_bytes(2 * H, d, group) + 2 * d * 2 + H * 2,
+        "down": q4_bytes(d, H, group) + H * 2 + 2 * d * 2,
+        "lm_head": q4_bytes(c["vocab"], d, group) + 2 * d * 2 + c["vocab"] * 2 + d * 2,
+    }
 
-    def launch(i):
-        li = i % n_copies
-        w16, sb16 = copies[li]
-        rc = _lib.lib().axm_qmv_q4_tile16_swiglu(_lib.ptr(x), _lib.ptr(layers["ln2"][li]), 1e-5, _lib.ptr(w16),
-                                                 _lib.ptr(sb16), _lib.ptr(y), 1, d, H, group, stream)
-        _lib.check(rc, "qmv_q4_tile16_swiglu")
 
-    for i in range(10):
-        launch(i)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for i in range(reps):
-        launch(i)
-    e1.record(s)
-    torch.cuda.synchronize()
-    avg_us = e0.elapsed_time(e1) * 1000.0 / reps
-    bytes_per_launch = q4_bytes(2 * H, d, group) + d * 2 + d * 2 + H * 2  # weights + x + ln_w + y
-    del copies
-    return avg_us, bytes_per_launch
+def time_step_kernels(runner, c, position: int, active_len: int, group: int, reps: int = 200) -> dict:
+    """Each launch group of the decode step timed live with HIP events on the runner's stream
+    (QuantizedDecodeRunner.time_kernels: the runner's own launches, `reps` back to back over
+    the 32 layers' weights in turn, 3.6 GB, past the 256 MB last-level cache), with its
+    algorithmic bytes and fraction of the HBM peak."""
+    us = runner.time_kernels(position, active_len, reps)
+    nb = kernel_bytes(c, active_len, group)
+    out = {}
+    for k, t in us.items():
+        gbs = nb[k] / (t * 1e-6) / 1e9
+        out[k] = {"kernel": KERNEL_NAMES[k].replace("G128", "true" if group == 128 else "false"),
+                  "avg_launch_us": round(t, 3), "algorithmic_bytes": nb[k], "achieved_gbs": round(gbs, 1),
+                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def in_graph_profile(group=HEADLINE_GROUP):
+    """Per-kernel average durations inside the captured decode graph from the committed rocprofv3
+    kernel-trace summary (profiles/decode_7b_q4_g128_kernel_stats.json; its fields name the
+    command and the commit it was measured at).  None when absent or for group 64."""
+    path = os.path.join(ROOT, "profiles", "decode_7b_q4_g128_kernel_stats.json")
+    if group != 128 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
 
 
 def gate_up_traffic(group=HEADLINE_GROUP):
     """HBM bytes per gate/up launch measured with rocprofv3 FETCH_SIZE and WRITE_SIZE counters
     (profiles/gate_up_g128_traffic.json for group 128, gate_up_traffic.json for group 64,
-    written from two counter runs and a copy-kernel calibration; the summary beside each
-    gives the commands).  None when absent."""
+    written from two counter runs and a copy-kernel calibration; the JSON names the commands
+    and the commit).  (bytes, provenance) or (None, None) when absent."""
     path = os.path.join(ROOT, "profiles", "gate_up_g128_traffic.json" if group == 128 else "gate_up_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        j = json.load(f)
+    prov = {k: j[k] for k in ("measured_at_commit", "source", "commands") if k in j}
+    return j.get("hbm_bytes_per_launch"), prov
+
+
+TRACE_GROUPS = (("qkv", "t16_gemv_kernel<1, 1, 3,"), ("attention", "attn_split_kernel"),
+                ("o", "t16_gemv_kernel<1, 1, 16,"), ("gate_up", "t16_gemv_kernel<1, 2, 2,"),
+                ("down", "t16_gemv_kernel<1, 1, 1,"), ("lm_head", "t16_gemv_kernel<1, 1, 0,"),
+                ("set_params", "set_params_kernel"))
+
+
+def summarize_trace(csv_path: str, n_steps: int, n_layer: int = CFG_7B["n_layer"]) -> dict:
+    """In-graph per-kernel averages from a rocprofv3 --kernel-trace CSV of this benchmark: the
+    decode steps run first, so each layer kernel's first n_steps * n_layer launches (the lm_head's
+    and the parameter kernel's first n_steps) are the graph's; later launches of the same kernels
+    are time_kernels' stand-alone ones."""
+    import csv
+
+    rows = []
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    out = {}
+    for key, pat in TRACE_GROUPS:
+        durs = [(e - b) / 1000.0 for b, e, name in rows if pat in name]
+        n = n_steps * (1 if key in ("lm_head", "set_params") else n_layer)
+        if len(durs) < n:
+            continue
+        g = durs[:n]
+        out[key] = {"avg_us": round(sum(g) / n, 3), "min_us": round(min(g), 3), "max_us": round(max(g), 3),
+                    "calls": n}
+    return out
 
 
 def _cpu_model_name() -> str:
@@ -311,8 +361,15 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain device copies of 256 MiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--kernel-only", action="store_true",
-                    help="only build the model and time the gate/up kernel (short runs under counter collection)")
+                    help="only build the model and time each decode kernel 20 times (short runs under counter "
+                         "collection)")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print the in-graph per-kernel averages (JSON) of a rocprofv3 kernel trace of a run of this "
+                         "benchmark with the same --steps / --warmup, then exit (no GPU use)")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(json.dumps(summarize_trace(args.summarize_trace, 1 + args.warmup + args.steps), indent=1))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs the decode step on one GPU only (no sharding across GPUs), "
                                    "so --gpus must be 1"}))
@@ -344,8 +401,9 @@ def main():
     mode = set_mode(runner, args.mode)
     print(f"[bench] model built and packed in {t_build:.1f} s", file=sys.stderr, flush=True)
     if args.kernel_only:
-        avg_us, bpl = time_gate_up_kernel(layers, c, dev, reps=20, group=G)
-        print(json.dumps({"gate_up_avg_launch_us": round(avg_us, 3), "bytes_per_launch": bpl}), flush=True)
+        runner.step(torch.zeros(1, dtype=torch.int64, device=dev), args.context - 1, args.context - 1, args.context)
+        ks = time_step_kernels(runner, c, args.context, args.context + 1, G, reps=20)
+        print(json.dumps({k: v["avg_launch_us"] for k, v in ks.items()}), flush=True)
         return
     ms, wall, pos0 = time_decode(runner, cache, args.steps, args.warmup, dev, args.context)
     ms_per_step = ms / args.steps
@@ -355,9 +413,22 @@ def main():
     gbs = bytes_tok / (ms_per_step * 1e-3) / 1e9
     print(f"[bench] decode {ms_per_step:.3f} ms/token, {tok_s:.1f} tok/s, {gbs:.0f} GB/s step-level", file=sys.stderr,
           flush=True)
-    avg_us, bpl = time_gate_up_kernel(layers, c, dev, group=G)
-    ach = bpl / (avg_us * 1e-6) / 1e9
+    # Each decode kernel timed live after the timed region (the last step's context).
+    last = pos0 + args.steps
+    ks = time_step_kernels(runner, c, last, last + 1, G)
+    prof = in_graph_profile(G)
+    if prof is not None:
+        for k, v in ks.items():
+            pk = prof.get("kernels", {}).get(k)
+            if pk:
+                v["in_graph_avg_us"] = pk["avg_us"]
+                v["in_graph_frac"] = round(v["algorithmic_bytes"] / (pk["avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    gu = ks["gate_up"]
+    avg_us, bpl, ach = gu["avg_launch_us"], gu["algorithmic_bytes"], gu["achieved_gbs"]
+    print("[bench] kernels (us): " + ", ".join(f"{k} {v['avg_launch_us']:.2f}" for k, v in ks.items()),
+          file=sys.stderr, flush=True)
     print(f"[bench] gate/up kernel {avg_us:.2f} us, {ach:.0f} GB/s", file=sys.stderr, flush=True)
+    traffic, traffic_src = gate_up_traffic(G)
     cpu = None
     second = None
     # The CPU baseline runs on group-64 packs (the reference's CPU dequantizer's format).
@@ -410,10 +481,20 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": gate_up_traffic(G),
+            "traffic": traffic,
             "avg_launch_us": round(avg_us, 3),
             "algorithmic_bytes_per_launch": bpl,
+            "method": ("achieved / frac: algorithmic bytes / average launch duration by HIP events on the "
+                       "runner's stream, 200 launches back to back over the 32 layers' weights, after the timed "
+                       "decode; in_graph_*: the same kernel inside the captured decode graph, from the committed "
+                       "rocprofv3 kernel-trace summary"),
+            "in_graph_avg_us": gu.get("in_graph_avg_us"),
+            "in_graph_frac": gu.get("in_graph_frac"),
+            "in_graph_source": (None if prof is None else
+                                {k: prof[k] for k in ("source", "measured_at_commit", "command") if k in prof}),
+            "traffic_source": traffic_src,
         },
+        "decode_kernels": ks,
         "cpu_baseline": cpu,
         f"group{other}_decode": second,
     }

@@ -105,6 +105,25 @@ def test_runner_step_matches_oracle(dev, layout, mode):
         _check_logits(got[i], ref, f"prompt step {i}")
 
 
+def test_runner_time_kernels_then_step(dev):
+    """axm_runner_time_kernels reports a positive average for each of the six launch groups,
+    and the steps after it (the first at the position it overwrote) still match the oracle."""
+    print("[runner_time_kernels]", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    model = om.OracleModel(cfg, ow, cos, sin)
+    S = 128
+    runner, cache = build_runner(cfg, ow, cos, sin, dev, S, "fp16")
+    ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim, "fp16")
+    toks = np.random.default_rng(5).integers(0, cfg.vocab, 12).tolist()
+    got = run_steps(runner, cache, toks[:8], dev)
+    us = runner.time_kernels(8, 9, reps=5)
+    assert list(us) == list(runner.KERNEL_GROUPS)
+    assert all(v > 0.0 for v in us.values()), us
+    got += run_steps(runner, cache, toks[8:], dev)
+    for i, tok in enumerate(toks):
+        _check_logits(got[i], model.forward([tok], ocache)[-1], f"step {i}")
+
+
 def _load_gpu_cache(ocache, cache):
     k = cache.cache[:, 0, 0].cpu().numpy()
     v = cache.cache[:, 1, 0].cpu().numpy()
