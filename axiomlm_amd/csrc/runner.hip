@@ -1151,19 +1151,43 @@ extern "C" int axm_runner_time_kernels(axm_runner_t r, int position, int active_
         default: return r->enqueue_lm_head(s);
       }
     };
-    for (int j = 0; j < 2 && rc == 0; ++j) rc = one(j);
-    if (rc) break;
-    (void)hipEventRecord(e0, s);
+    // The reps launches are captured into a graph (as the step's launches are), so
+    // the host's launch rate does not bound short kernels; one untimed replay first.
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    if (hipStreamBeginCapture(r->cap_stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+      axm_set_error("runner_time_kernels: stream capture failed to start");
+      rc = -5;
+      break;
+    }
     for (int j = 0; j < reps && rc == 0; ++j) rc = one(j);
-    (void)hipEventRecord(e1, s);
+    const hipError_t ce = hipStreamEndCapture(r->cap_stream, &g);
+    if (rc == 0 && ce != hipSuccess) {
+      axm_set_error("runner_time_kernels: capture failed: %s", hipGetErrorString(ce));
+      rc = -5;
+    }
+    if (rc == 0 && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) {
+      axm_set_error("runner_time_kernels: graph instantiate failed");
+      rc = -5;
+    }
+    if (g) (void)hipGraphDestroy(g);
     if (rc) break;
+    if (hipGraphLaunch(ge, s) != hipSuccess || hipEventRecord(e0, s) != hipSuccess || hipGraphLaunch(ge, s) != hipSuccess ||
+        hipEventRecord(e1, s) != hipSuccess) {
+      axm_set_error("runner_time_kernels: graph launch failed");
+      (void)hipGraphExecDestroy(ge);
+      rc = -5;
+      break;
+    }
     float ms = 0.f;
     if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
       axm_set_error("runner_time_kernels: event timing failed");
+      (void)hipGraphExecDestroy(ge);
       rc = -5;
       break;
     }
     us_out[k] = ms * 1000.f / (float)reps;
+    (void)hipGraphExecDestroy(ge);
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);

@@ -312,8 +312,8 @@ class QuantizedDecodeRunner:
 
     def time_kernels(self, position: int, active_len: int, reps: int = 200) -> dict:
         """Average microseconds per launch of each of the one-token step's launch groups
-        (KERNEL_GROUPS), each run `reps` times back to back over the layers in turn and
-        timed with HIP events on the runner's stream.  A measurement call with no
+        (KERNEL_GROUPS), each run `reps` times back to back over the layers in turn as one
+        captured graph and timed with HIP events on the runner's stream.  A measurement call with no
         counterpart in the reference: it overwrites the runner's activations and the
         cache slot at `position`, which the next step recomputes."""
         out = (ctypes.c_float * 6)()

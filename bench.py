@@ -177,8 +177,8 @@ def kernel_bytes(c, active_len: int, group: int) -> dict:
 def time_step_kernels(runner, c, position: int, active_len: int, group: int, reps: int = 200) -> dict:
     """Each launch group of the decode step timed live with HIP events on the runner's stream
     (QuantizedDecodeRunner.time_kernels: the runner's own launches, `reps` back to back over
-    the 32 layers' weights in turn, 3.6 GB, past the 256 MB last-level cache), with its
-    algorithmic bytes and fraction of the HBM peak."""
+    the 32 layers' weights in turn, 3.6 GB, past the 256 MB last-level cache, replayed as one
+    captured graph), with its algorithmic bytes and fraction of the HBM peak."""
     us = runner.time_kernels(position, active_len, reps)
     nb = kernel_bytes(c, active_len, group)
     out = {}
@@ -485,9 +485,9 @@ def main():
             "avg_launch_us": round(avg_us, 3),
             "algorithmic_bytes_per_launch": bpl,
             "method": ("achieved / frac: algorithmic bytes / average launch duration by HIP events on the "
-                       "runner's stream, 200 launches back to back over the 32 layers' weights, after the timed "
-                       "decode; in_graph_*: the same kernel inside the captured decode graph, from the committed "
-                       "rocprofv3 kernel-trace summary"),
+                       "runner's stream around a captured graph of 200 launches back to back over the 32 layers' "
+                       "weights, after the timed decode; in_graph_*: the same kernel inside the captured decode "
+                       "graph, from the committed rocprofv3 kernel-trace summary"),
             "in_graph_avg_us": gu.get("in_graph_avg_us"),
             "in_graph_frac": gu.get("in_graph_frac"),
             "in_graph_source": (None if prof is None else

@@ -324,9 +324,9 @@ int axm_runner_speculative_decode(axm_runner_t r, const int64_t* initial_tokens,
 /* Device int64 slot holding the token id consumed by the latest step. */
 int axm_runner_token_slot(axm_runner_t r, void** tok_out);
 /* Measurement entry (no counterpart in the reference): times the launch groups of
- * the one-token step one at a time, each run reps times back to back on `stream`
- * over the layers in turn (layer j % n_layer), bracketed by HIP events after two
- * untimed launches.  us_out[6] receives the average microseconds per launch group:
+ * the one-token step one at a time, each run reps times back to back over the
+ * layers in turn (layer j % n_layer) as one captured hipGraph, replayed once untimed
+ * and once between HIP events on `stream`.  us_out[6] receives the average microseconds per launch group:
  * QKV (with its RoPE / KV-write epilogue), attention over active_len keys, O
  * projection, gate/up + SwiGLU, down projection, final norm + lm_head.  The token
  * parameters are set to id 0 at `position`; the runner's activations and the cache
