@@ -1140,15 +1140,15 @@ extern "C" int axm_runner_time_kernels(axm_runner_t r, int position, int active_
   }
   int rc = 0;
   for (int k = 0; k < 6 && rc == 0; ++k) {
-    auto one = [&](int j) -> int {
+    auto one = [&](int j, hipStream_t cs) -> int {
       const int i = j % d.n_layer;
       switch (k) {
-        case 0: return r->enqueue_qkv(i, s);
-        case 1: return r->enqueue_attention(i, bucket, short_splits, s);
-        case 2: return r->enqueue_o(i, bucket, s);
-        case 3: return r->enqueue_gate_up(i, s);
-        case 4: return r->enqueue_down(i, s);
-        default: return r->enqueue_lm_head(s);
+        case 0: return r->enqueue_qkv(i, cs);
+        case 1: return r->enqueue_attention(i, bucket, short_splits, cs);
+        case 2: return r->enqueue_o(i, bucket, cs);
+        case 3: return r->enqueue_gate_up(i, cs);
+        case 4: return r->enqueue_down(i, cs);
+        default: return r->enqueue_lm_head(cs);
       }
     };
     // The reps launches are captured into a graph (as the step's launches are), so
@@ -1160,7 +1160,7 @@ extern "C" int axm_runner_time_kernels(axm_runner_t r, int position, int active_
       rc = -5;
       break;
     }
-    for (int j = 0; j < reps && rc == 0; ++j) rc = one(j);
+    for (int j = 0; j < reps && rc == 0; ++j) rc = one(j, r->cap_stream);
     const hipError_t ce = hipStreamEndCapture(r->cap_stream, &g);
     if (rc == 0 && ce != hipSuccess) {
       axm_set_error("runner_time_kernels: capture failed: %s", hipGetErrorString(ce));

@@ -118,7 +118,9 @@ def test_runner_time_kernels_then_step(dev):
     got = run_steps(runner, cache, toks[:8], dev)
     us = runner.time_kernels(8, 9, reps=5)
     assert list(us) == list(runner.KERNEL_GROUPS)
-    assert all(v > 0.0 for v in us.values()), us
+    # Every launch takes at least the ~1.5 us a launch costs inside a graph: an empty
+    # capture would time nothing.
+    assert all(v > 1.0 for v in us.values()), us
     got += run_steps(runner, cache, toks[8:], dev)
     for i, tok in enumerate(toks):
         _check_logits(got[i], model.forward([tok], ocache)[-1], f"step {i}")
