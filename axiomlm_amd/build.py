@@ -48,7 +48,10 @@ FILE_FLAGS = {
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     # q4_tile16.hip: the same; with AGPR accumulators every GEMV chunk copied all
     # sixteen accumulator values out (7B decode step 758.7 -> 763.3 tok/s).
-    "q4_tile16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "q4_tile16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form",
+                      # The GEMV's leading scalar arguments land in SGPRs before the wave
+                      # starts: its first requests do not wait for an argument load.
+                      "-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 

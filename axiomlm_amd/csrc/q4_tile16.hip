@@ -451,7 +451,26 @@ constexpr int kT16WaveMaxChunks = 16;  // chunks per wave kT16Wave handles
 // G128: one (scale, bias) word per row and chunk (group-128 packs) instead of two;
 // it is applied to both 64-column halves of the chunk.
 template <int M, int NT, int EPI, int P, int MODE, bool G128, int TH>
-__global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
+//
+// The fields the first loads need come as leading scalar arguments, which the
+// hardware preloads into SGPRs (-mllvm -amdgpu-kernarg-preload-count): the weight,
+// scale and activation requests then issue without waiting for a scalar load of the
+// argument struct.
+__global__ void __launch_bounds__(TH)
+    t16_gemv_kernel(const f16* x_p, const f16* ln_w_p, const u32x4* w16_p, const u32x2* sb16_p, int K_p,
+                    int n_units_p, int split_p, int pair_offset_p, int w16_bytes_p, int sb16_bytes_p, T16Args a) {
+  // (At most 14 argument dwords are preloaded; KB follows from K.)
+  a.x = x_p;
+  a.ln_w = ln_w_p;
+  a.w16 = w16_p;
+  a.sb16 = sb16_p;
+  a.K = K_p;
+  a.KB = (K_p + 127) >> 7;
+  a.n_units = n_units_p;
+  a.split = split_p;
+  a.pair_offset = pair_offset_p;
+  a.w16_bytes = (size_t)w16_bytes_p;
+  a.sb16_bytes = (size_t)sb16_bytes_p;
   constexpr int W = TH / 64;  // waves per workgroup
   constexpr bool ONE = MODE != kT16Loop;
   constexpr bool SBW = MODE == kT16Wave;
@@ -478,7 +497,9 @@ __global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
   const int my = max(0, min(per, a.KB - kb0));
   const int tokA = lane & 15;  // A-operand token of this lane
   const int kq = lane >> 4;    // 8-wide k sub-block of this lane
-  const Unpack U{to_vgpr(a.unpack[0]), to_vgpr(a.unpack[1]), a.unpack[2], a.unpack[3]};
+  // The nibble masks and magic exponents as constants (no argument load ahead of the
+  // first requests); the opaque moves keep the masks in VGPRs.
+  const Unpack U{to_vgpr(0x000F000Fu), to_vgpr(0x00F000F0u), to_sgpr(0x64006400u), to_sgpr(0x54005400u)};
 
   // Raw buffer descriptors: out-of-range offsets read as zero, so every chunk
   // load is issued unconditionally and the load pipeline stays static.
@@ -494,12 +515,15 @@ __global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
   u32x2 sr[P][NT];
   // Byte offsets of (unit, ci) for this lane, OOB when outside the wave's range.
   auto load = [&](int unit, int ci, int j) {
-    const bool ok = unit < a.n_units && ci < my;
+    // Branch-free select of the offsets: the condition is wave-uniform, and as a
+    // conditional the compiler split the requests into branches whose register
+    // reuse forced a wait for every load in flight.
+    const int m = -((int)(unit < a.n_units) & (int)(ci < my));
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int base = (unit + t * a.pair_offset) * a.KB + kb0 + ci;
-      const int wo = ok ? (base * 64 + lane) * 16 : kOOB;
-      const int so = ok ? (base * 16 + (lane & 15)) * (G128 ? 4 : 8) : kOOB;
+      const int wo = (((base * 64 + lane) * 16) & m) | (kOOB & ~m);
+      const int so = (((base * 16 + (lane & 15)) * (G128 ? 4 : 8)) & m) | (kOOB & ~m);
       wr[j][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 2));
       if (!SBW && G128) {
         const uint32_t v = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0));
@@ -517,10 +541,18 @@ __global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
   // after the first weight chunks find them arrived.
   constexpr int EPI_BASE = EPI == kT16EpiResidParts ? Q4_EPI_RESID : EPI;
   constexpr bool EPI_PRE = M == 1 && ONE && (EPI_BASE == Q4_EPI_QKV_ROPE || EPI_BASE == Q4_EPI_RESID);
-  int pre_pos = 0, pre_wp = 0;
+  // The positions are vector loads left in VGPRs until the operands are requested
+  // (t16_vgpr there): a scalar copy of a loaded value made the compiler wait for it
+  // right away, before any other request of the launch was issued.  A null device
+  // pointer gives a zero-sized descriptor (the load reads 0) and the host value.
+  uint32_t pre_pos_raw = 0, pre_wp_raw = 0;
   if constexpr (EPI_PRE && EPI_BASE == Q4_EPI_QKV_ROPE) {
-    pre_pos = a.rope_pos_dev ? a.rope_pos_dev[0] : a.rope_pos;
-    pre_wp = a.write_pos_dev ? a.write_pos_dev[0] : a.write_pos;
+    const __amdgpu_buffer_rsrc_t rpp = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.rope_pos_dev, (short)0, a.rope_pos_dev ? 4 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rwp = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.write_pos_dev, (short)0, a.write_pos_dev ? 4 : 0, 0x00020000);
+    pre_pos_raw = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rpp, 0, 0, 0));
+    pre_wp_raw = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(rwp, 0, 0, 0));
   }
   T16EpiPre epre{1.f, 0.f, f16(0), f16(0), f16(0), 0};
   T16X<M, TH> xr;
@@ -557,15 +589,27 @@ __global__ void __launch_bounds__(TH) t16_gemv_kernel(T16Args a) {
 #pragma unroll
   for (int j = 0; j < PRE; ++j) load(unit, j, j);
   if constexpr (EPI_PRE) {
-    if (sub == 0) epre = t16_epi_prefetch<EPI_BASE>(a, unit, lane, pre_pos, pre_wp);
+    if (sub == 0) {
+      int pre_pos = 0, pre_wp = 0;
+      if constexpr (EPI_BASE == Q4_EPI_QKV_ROPE) {
+        pre_pos = (int)t16_vgpr(pre_pos_raw) + (a.rope_pos_dev ? 0 : a.rope_pos);
+        pre_wp = (int)t16_vgpr(pre_wp_raw) + (a.write_pos_dev ? 0 : a.write_pos);
+      }
+      epre = t16_epi_prefetch<EPI_BASE>(a, unit, lane, pre_pos, pre_wp);
+    }
   }
   if (SBW) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int q = 0; q < QS; ++q) {
+        // Every lane stores (lanes past the run into a dummy slot after the
+        // per-wave runs): with a conditional store the compiler moved the scale
+        // loads into it, behind the weight requests, and waited for all of them.
         const int v = q * 64 + lane;
-        if (v < my * VPC) *reinterpret_cast<u32x4*>(my_sb + (size_t)t * per * 16 + 2 * v) = sbv[t][q];
+        u32x4* dst = v < my * VPC ? reinterpret_cast<u32x4*>(my_sb + (size_t)t * per * 16 + 2 * v)
+                                  : reinterpret_cast<u32x4*>(sbw + (size_t)W * NT * per * 16);
+        *dst = sbv[t][q];
       }
   }
   if constexpr (from_parts) t16_merge_parts<M, TH>(a, pp, xr);
@@ -706,15 +750,19 @@ void t16_set_attr() {
   if constexpr (M == 1 && EPI != kT16EpiResidParts) t16_set_attr_th<M, NT, EPI, kT16ThreadsSmall>();
 }
 
+#define T16_HOT(a)                                                                                  \
+  (a).x, (a).ln_w, (a).w16, (a).sb16, (a).K, (a).n_units, (a).split, (a).pair_offset, (int)(a).w16_bytes, \
+      (int)(a).sb16_bytes
+
 template <int M, int NT, int EPI, bool G128, int TH>
 void t16_launch_g(const T16Args& a, int mode, int grid, size_t smem, hipStream_t s) {
   const dim3 g(grid), b(TH);
   if (mode == kT16Wave)
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, kT16WaveDepth, kT16Wave, G128, TH>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, kT16WaveDepth, kT16Wave, G128, TH>), g, b, smem, s, T16_HOT(a), a);
   else if (mode == kT16OnePass)
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16OnePass, G128, TH>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16OnePass, G128, TH>), g, b, smem, s, T16_HOT(a), a);
   else
-    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16Loop, G128, TH>), g, b, smem, s, a);
+    hipLaunchKernelGGL((t16_gemv_kernel<M, NT, EPI, T16Depth<NT>::value, kT16Loop, G128, TH>), g, b, smem, s, T16_HOT(a), a);
 }
 
 template <int M, int NT, int EPI>
@@ -828,7 +876,7 @@ int t16_gemv_launch(T16Args a, int M, int epi, hipStream_t s) {
   const int per = (a.KB + S - 1) / S;
   int mode = S == 1 ? kT16Loop : kT16OnePass;
   if (S > 1 && per <= kT16WaveMaxChunks) {
-    const size_t sb_lds = (size_t)waves * NT * per * 128;
+    const size_t sb_lds = (size_t)waves * NT * per * 128 + 16;  // + the dummy slot
     if (smem + sb_lds <= 160 * 1024) {
       mode = kT16Wave;
       smem += sb_lds;

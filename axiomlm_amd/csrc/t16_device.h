@@ -21,6 +21,21 @@ __device__ __forceinline__ uint32_t to_vgpr(uint32_t s) {
   return v;
 }
 
+// A VGPR copy the compiler cannot see through (keeps a loaded uniform value out of
+// SGPRs until here, so the wait for it lands here).
+__device__ __forceinline__ uint32_t t16_vgpr(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// A value the compiler cannot fold into a literal operand, kept in an SGPR.
+__device__ __forceinline__ uint32_t to_sgpr(uint32_t s) {
+  uint32_t v;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(v) : "s"(s));
+  return v;
+}
+
 __device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask_v, uint32_t magic_s) {
   return (w & mask_v) | magic_s;
 }
