@@ -52,6 +52,8 @@ FILE_FLAGS = {
                       # The GEMV's leading scalar arguments land in SGPRs before the wave
                       # starts: its first requests do not wait for an argument load.
                       "-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "lowbit_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "q2k_gguf.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 

@@ -111,9 +111,10 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
         p1[2 * j + 1] = hi[4 + j];
         part += h2f(lo[j]) + h2f(hi[j]) + h2f(lo[4 + j]) + h2f(hi[4 + j]);
       }
-      // Four consecutive blocks form one group (nblk is a multiple of 4).
-      part += __shfl_xor(part, 1, 64);
-      part += __shfl_xor(part, 2, 64);
+      // Four consecutive blocks form one group (nblk is a multiple of 4): a quad
+      // of lanes, summed with DPP lane moves.
+      part += dpp_move<0xB1>(part);  // quad_perm [1,0,3,2]
+      part += dpp_move<0x4E>(part);  // quad_perm [2,3,0,1]
       if (b < nblk) {
         reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[0] = p0;
         reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[1] = p1;
@@ -171,7 +172,7 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
   for (int r = 0; r < kLbRows; ++r) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const float v = wave_sum(yacc[r][m]);
+      const float v = wave_sum_dpp(yacc[r][m]);
       const int row = row0 + r;
       if (lane == 0 && row < N) {
         const float b = bias != nullptr ? h2f(bias[row]) : 0.f;

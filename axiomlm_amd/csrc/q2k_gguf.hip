@@ -26,9 +26,14 @@
 namespace {
 
 constexpr int kQ2kBlockBytes = 84;
+// Workgroup size: 512 threads for one token; 256 with several, whose registers
+// (about 160 VGPRs at four tokens and four rows) admit one 512-thread workgroup per
+// CU, so that grid ran in two rounds (C4 shapes at M = 4 with the staging rounds
+// below: 23.4 / 19.9 -> 17.4 / 17.3 us).
 constexpr int kQ2kThreads = 512;
-constexpr int kQ2kWaves = kQ2kThreads / 64;
+constexpr int kQ2kThreadsMulti = 256;
 constexpr int kQ2kMaxK = 16384;
+constexpr int kQ2kStageU = 8;  // activation vectors requested per thread and staging round
 
 __device__ __forceinline__ float q2k_src(const void* w, bool fp16, size_t i) {
   return fp16 ? h2f(reinterpret_cast<const f16*>(w)[i]) : reinterpret_cast<const float*>(w)[i];
@@ -115,8 +120,8 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 // xs: [M][K] fp16 in pair order; ss: [M][K / 16] fp32 sub-block sums.
-template <int M, int R>
-__global__ void __launch_bounds__(kQ2kThreads) q2k_gemv_kernel(const f16* __restrict__ x, int K, int N,
+template <int M, int R, int TH>
+__global__ void __launch_bounds__(TH) q2k_gemv_kernel(const f16* __restrict__ x, int K, int N,
                                                               const uint8_t* __restrict__ wq, size_t w_bytes,
                                                               const f16* __restrict__ bias, f16* __restrict__ y) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -126,7 +131,7 @@ __global__ void __launch_bounds__(kQ2kThreads) q2k_gemv_kernel(const f16* __rest
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int NB = K / 256;
-  const int row0 = (blockIdx.x * kQ2kWaves + wave) * R;
+  const int row0 = (blockIdx.x * (TH / 64) + wave) * R;
   const __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc((void*)wq, (short)0, (int)w_bytes, 0x00020000);
   constexpr int kOOB = 0x7FFFFFF0;
@@ -151,23 +156,50 @@ __global__ void __launch_bounds__(kQ2kThreads) q2k_gemv_kernel(const f16* __rest
   load(bs);
 
   // Stage x in pair order and the 16-element sums: thread -> 8 consecutive elements.
-  for (int v = tid; v < M * K / 8; v += kQ2kThreads) {
-    const int m = v / (K / 8), c = v % (K / 8);
-    const u32x4 a = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + 8 * c);
-    u32x4 p;
-    p[0] = (a[0] & 0xFFFFu) | (a[1] << 16);
-    p[1] = (a[0] >> 16) | (a[1] & 0xFFFF0000u);
-    p[2] = (a[2] & 0xFFFFu) | (a[3] << 16);
-    p[3] = (a[2] >> 16) | (a[3] & 0xFFFF0000u);
-    *reinterpret_cast<u32x4*>(xs + (size_t)m * K / 2 + 4 * c) = p;
-    float s = 0.f;
+  // Rounds of kQ2kStageU vectors per thread, all requested before any is used (a
+  // loop of one load each waited a full round trip per vector: M = 4 at K = 11008
+  // is 22 vectors per thread).
+  // Vectors past the end read zeros through a bounded descriptor (no memory traffic).
+  const int nvec = M * K / 8;
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nvec * 16, 0x00020000);
+  for (int v0 = tid; v0 < nvec; v0 += kQ2kStageU * TH) {
+    // Slices u whose first vector (thread 0's) is past the end are skipped by every
+    // thread alike (a workgroup-uniform bound).
+    const int base = v0 - tid;
+    u32x4 av[kQ2kStageU];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f16x2 hv = as_h2(a[q]);
-      s = add_rn(s, add_rn(h2f(hv.x), h2f(hv.y)));
+    for (int u = 0; u < kQ2kStageU; ++u) {
+      if (base + u * TH >= nvec) break;
+      const int v = v0 + u * TH;  // x rows are contiguous: vector v is x + 8 v
+      av[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, v < nvec ? 16 * v : kOOB, 0, 0));
     }
-    s = add_rn(s, __shfl_xor(s, 1, 64));  // elements 16(c/2) .. +15 (c and c^1 are adjacent threads)
-    if ((c & 1) == 0) ss[(size_t)m * (K / 16) + c / 2] = s;
+#pragma unroll
+    for (int u = 0; u < kQ2kStageU; ++u) {
+      if (base + u * TH >= nvec) break;
+      // Lanes past the end hold zeros and store nothing.  Vectors c and
+      // c ^ 1 of a 16-element sub-block sit in adjacent lanes, and nvec is even, so
+      // both lanes of a pair are on the same side of the end.
+      const int v = v0 + u * TH;
+      const int m = min(v, nvec - 1) / (K / 8), c = min(v, nvec - 1) % (K / 8);
+      const u32x4 a = av[u];
+      u32x4 p;
+      p[0] = (a[0] & 0xFFFFu) | (a[1] << 16);
+      p[1] = (a[0] >> 16) | (a[1] & 0xFFFF0000u);
+      p[2] = (a[2] & 0xFFFFu) | (a[3] << 16);
+      p[3] = (a[2] >> 16) | (a[3] & 0xFFFF0000u);
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f16x2 hv = as_h2(a[q]);
+        s = add_rn(s, add_rn(h2f(hv.x), h2f(hv.y)));
+      }
+      s = add_rn(s, dpp_move<0xB1>(s));  // elements 16(c/2) .. +15: the pair (c, c ^ 1)
+      if (v < nvec) {
+        *reinterpret_cast<u32x4*>(xs + (size_t)m * K / 2 + 4 * c) = p;
+        if ((c & 1) == 0) ss[(size_t)m * (K / 16) + c / 2] = s;
+      }
+    }
   }
   __syncthreads();
 
@@ -236,7 +268,7 @@ __global__ void __launch_bounds__(kQ2kThreads) q2k_gemv_kernel(const f16* __rest
 #pragma unroll
   for (int i = 0; i < R; ++i)
 #pragma unroll
-    for (int m = 0; m < M; ++m) r[i][m] = wave_sum(r[i][m]);
+    for (int m = 0; m < M; ++m) r[i][m] = wave_sum_dpp(r[i][m]);
   if (lane == 0) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -252,22 +284,22 @@ __global__ void __launch_bounds__(kQ2kThreads) q2k_gemv_kernel(const f16* __rest
   }
 }
 
-template <int M, int R>
+template <int M, int R, int TH>
 int q2k_launch_mr(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
   const size_t smem = (size_t)M * K * sizeof(f16) + (size_t)M * (K / 16) * sizeof(float);
   if (smem > 160 * 1024) {
     axm_set_error("qmv_q2_k_gguf: K=%d with %d rows needs %zu B of LDS", K, M, smem);
     return -2;
   }
-  if (smem > 64 * 1024 && hipFuncSetAttribute((const void*)q2k_gemv_kernel<M, R>,
+  if (smem > 64 * 1024 && hipFuncSetAttribute((const void*)q2k_gemv_kernel<M, R, TH>,
                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess) {
     (void)hipGetLastError();
     axm_set_error("qmv_q2_k_gguf: cannot reserve %zu B of LDS", smem);
     return -2;
   }
-  const int rows = kQ2kWaves * R;
+  const int rows = (TH / 64) * R;
   const size_t w_bytes = (size_t)N * (K / 256) * kQ2kBlockBytes;
-  hipLaunchKernelGGL((q2k_gemv_kernel<M, R>), dim3((N + rows - 1) / rows), dim3(kQ2kThreads), smem, st, x, K, N, w,
+  hipLaunchKernelGGL((q2k_gemv_kernel<M, R, TH>), dim3((N + rows - 1) / rows), dim3(TH), smem, st, x, K, N, w,
                      w_bytes, bias, y);
   return 0;
 }
@@ -278,9 +310,16 @@ int q2k_launch_mr(const f16* x, int K, int N, const uint8_t* w, const f16* bias,
 template <int M>
 int q2k_launch(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
   const int cus = axm_num_cus();
-  if (M > 1 && (N + 4 * kQ2kWaves - 1) / (4 * kQ2kWaves) >= cus) return q2k_launch_mr<M, 4>(x, K, N, w, bias, y, st);
-  if ((N + 2 * kQ2kWaves - 1) / (2 * kQ2kWaves) >= cus) return q2k_launch_mr<M, 2>(x, K, N, w, bias, y, st);
-  return q2k_launch_mr<M, 1>(x, K, N, w, bias, y, st);
+  if constexpr (M > 1) {
+    constexpr int W = kQ2kThreadsMulti / 64;
+    if ((N + 4 * W - 1) / (4 * W) >= cus) return q2k_launch_mr<M, 4, kQ2kThreadsMulti>(x, K, N, w, bias, y, st);
+    if ((N + 2 * W - 1) / (2 * W) >= cus) return q2k_launch_mr<M, 2, kQ2kThreadsMulti>(x, K, N, w, bias, y, st);
+    return q2k_launch_mr<M, 1, kQ2kThreadsMulti>(x, K, N, w, bias, y, st);
+  } else {
+    constexpr int W = kQ2kThreads / 64;
+    if ((N + 2 * W - 1) / (2 * W) >= cus) return q2k_launch_mr<M, 2, kQ2kThreads>(x, K, N, w, bias, y, st);
+    return q2k_launch_mr<M, 1, kQ2kThreads>(x, K, N, w, bias, y, st);
+  }
 }
 
 }  // namespace

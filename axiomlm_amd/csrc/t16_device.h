@@ -49,28 +49,3 @@ __device__ __forceinline__ f16x8 unpack_word(uint32_t w, const Unpack& u) {
 
 __device__ __forceinline__ float t16_silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Lane reductions of the activation staging on DPP lane moves (no LDS round trip):
-// within a 16-lane row, lane pairs (xor 1, xor 2), then the two quads of each half
-// row (row_half_mirror sends lane i to 7 - i), then the two halves (row_mirror,
-// i to 15 - i).  Every lane ends with the sum of its group; wave_sum_dpp returns
-// the wave's total (a wave-uniform value).
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float group8_sum_dpp(float v) {
-  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_move<0x141>(v);  // row_half_mirror
-  return v;
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v = group8_sum_dpp(v);
-  v += dpp_move<0x140>(v);  // row_mirror
-  // The four row sums, read out to scalars (the staging needs the total once per wave).
-  const int iv = __builtin_bit_cast(int, v);
-  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
-         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
-}
