@@ -1,6 +1,6 @@
 // Persistent decode-step kernel: one cooperative launch runs a whole batch-1
 // decode token (the work of QuantizedDecodeGraphState::step,
-// axiomlm/kernels/mps_kernels.mm:3195-3263) on one 512-thread workgroup per CU.
+// axiomlm/kernels/mps_kernels.mm:3195-3263) on one 1024-thread workgroup per CU.
 //
 // Phases (step_plan.h): per layer QKV, ATTN, O, GU, DN, then LM.  There is no
 // grid barrier.  Every value a phase hands to the next travels through 64-bit
@@ -11,14 +11,14 @@
 // so no workgroup can run two phases ahead of another, and a buffer is never
 // rewritten while a reader still expects an older tag.
 //
-// Wave 0 of each workgroup is the control wave (epilogue operands, the
-// reduction of the per-wave partial tiles, epilogues); waves 1..7 are workers
-// that stream tile16 weight chunks (1 KB each, the B operand of four
-// v_mfma_f32_16x16x32_f16) through a ring of kDepth in-flight loads.  The ring
-// runs across phases: while a worker consumes its last chunks of one GEMV, its
-// refills already request the first chunks of the next GEMV, so those loads
-// are in flight through the epilogue, the wait for the next phase's input and
-// its staging.  All eight waves stage the input vector (poll, RMSNorm, LDS).
+// Waves 0..kCtl-1 of each workgroup stage the input vector (poll, RMSNorm, LDS),
+// prepare the epilogue operands, reduce the per-wave partial tiles and run the
+// epilogues; waves kCtl..15 are workers that stream tile16 weight chunks (1 KB
+// each, the B operand of four v_mfma_f32_16x16x32_f16) through a ring of kDepth
+// in-flight loads and never poll.  The ring runs across phases: while a worker
+// consumes its last chunks of one GEMV, its refills already request the first
+// chunks of the next GEMV, so those loads are in flight through the epilogue,
+// the wait for the next phase's input and its staging.
 //
 // Every offset the kernel forms comes from step_plan.h, which a CPU check
 // (tests/cpu/step_plan_check.cpp) enumerates over whole launches.
