@@ -30,7 +30,10 @@ namespace {
 enum { P_TOKEN = 0, P_ROPE = 1, P_WRITE = 2, P_ACTIVE = 3, P_COUNT = 4 };
 // Token rows from which a multi-token step (verify / prompt chunk) runs the
 // multi-token GEMM instead of the decode GEMV per group of up to four rows.
-constexpr int kGemmMinTokens = 3;
+// Measured as verify_tree_step(N) / step on the 7B FP8 prefix-2048 model: the
+// GEMV is faster at three rows (1.49 -> 1.42 steps), the GEMM from four (GEMV
+// 1.69, GEMM 1.50).
+constexpr int kGemmMinTokens = 4;
 // Byte offset inside the parameter block of the int64 token id used by the
 // current step.
 constexpr int kTokenOffset = 72;
