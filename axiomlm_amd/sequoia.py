@@ -38,13 +38,13 @@ from .tree import MAX_TREE_NODES, compile_medusa_tree
 M3_PRO_TREE_LATENCY = {1: 1.000, 2: 1.280, 4: 1.385, 8: 1.488, 16: 2.315, 32: 3.926}
 # The same ratio for this runner on one MI355X (measure_tree_latency): 7B shape (32 layers,
 # d 4096, vocab 32000), MARLIN Q4 group 64, FP8 KV cache with a 2048-token prefix, branching
-# trees of N nodes; host wall time of whole calls.  Two nodes run the decode GEMV with two
-# token rows; from three nodes on the verify step runs the multi-token GEMM (the runner's
-# switch point), so t(N) grows monotonically with N.  With the reference's default acceptance
-# probabilities this profile makes the optimizer pick a 15-node tree of depth 3 (expected
-# 2.77 accepted tokens per step, speedup 1.86).
-MI355X_7B_Q4_TREE_LATENCY = {1: 1.0, 2: 1.28, 3: 1.37, 4: 1.37, 6: 1.38, 8: 1.39, 16: 1.43, 24: 1.59, 32: 1.64,
-                             48: 2.00, 64: 2.09}
+# trees of N nodes; host wall time of whole calls.  Two and three nodes run the decode GEMV
+# with two / three token rows; from four nodes on the verify step runs the multi-token GEMM
+# (the runner's switch point), so t(N) grows monotonically with N.  With the reference's
+# default acceptance probabilities this profile makes the optimizer pick a 15-node tree of
+# depth 3 (expected 2.77 accepted tokens per step, speedup 1.72).
+MI355X_7B_Q4_TREE_LATENCY = {1: 1.0, 2: 1.27, 3: 1.42, 4: 1.50, 6: 1.51, 8: 1.52, 16: 1.56, 24: 1.73, 32: 1.79,
+                             48: 2.17, 64: 2.27}
 
 
 @dataclass
