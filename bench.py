@@ -215,10 +215,15 @@ def gate_up_traffic(group=HEADLINE_GROUP):
     return j.get("hbm_bytes_per_launch"), prov
 
 
-TRACE_GROUPS = (("qkv", "t16_gemv_kernel<1, 1, 3,"), ("attention", "attn_split_kernel"),
-                ("o", "t16_gemv_kernel<1, 1, 16,"), ("gate_up", "t16_gemv_kernel<1, 2, 2,"),
-                ("down", "t16_gemv_kernel<1, 1, 1,"), ("lm_head", "t16_gemv_kernel<1, 1, 0,"),
-                ("set_params", "set_params_kernel"))
+# (group, name patterns): the profiler prints some kernels demangled and others (those
+# with fp16 pointer arguments) mangled, so each GEMV group carries both forms.
+TRACE_GROUPS = (("qkv", ("t16_gemv_kernel<1, 1, 3,", "t16_gemv_kernelILi1ELi1ELi3E")),
+                ("attention", ("attn_split_kernel",)),
+                ("o", ("t16_gemv_kernel<1, 1, 16,", "t16_gemv_kernelILi1ELi1ELi16E")),
+                ("gate_up", ("t16_gemv_kernel<1, 2, 2,", "t16_gemv_kernelILi1ELi2ELi2E")),
+                ("down", ("t16_gemv_kernel<1, 1, 1,", "t16_gemv_kernelILi1ELi1ELi1E")),
+                ("lm_head", ("t16_gemv_kernel<1, 1, 0,", "t16_gemv_kernelILi1ELi1ELi0E")),
+                ("set_params", ("set_params_kernel",)))
 
 
 def summarize_trace(csv_path: str, n_steps: int, n_layer: int = CFG_7B["n_layer"]) -> dict:
@@ -234,8 +239,8 @@ def summarize_trace(csv_path: str, n_steps: int, n_layer: int = CFG_7B["n_layer"
             rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
     rows.sort()
     out = {}
-    for key, pat in TRACE_GROUPS:
-        durs = [(e - b) / 1000.0 for b, e, name in rows if pat in name]
+    for key, pats in TRACE_GROUPS:
+        durs = [(e - b) / 1000.0 for b, e, name in rows if any(p in name for p in pats)]
         n = n_steps * (1 if key in ("lm_head", "set_params") else n_layer)
         if len(durs) < n:
             continue
