@@ -201,14 +201,15 @@ def _qmm_workspace(K: int, N: int, swiglu: bool, device):
 
 
 # Rows from which the tile16 entry points run the multi-token GEMM instead of the decode
-# GEMV (the runner's verify steps switch at the same count).
-TILE16_GEMM_MIN_ROWS = 3
+# GEMV, as the runner's verify steps do (a 7B layer of these calls at three rows: GEMV
+# 53.0 us, GEMM 60.7 us; at four: GEMV 62.5 us, GEMM 60.5 us).
+TILE16_GEMM_MIN_ROWS = 4
 
 
 def qmv_q4_tile16(x, w16, sb16, out_features: int, bias=None) -> torch.Tensor:
     """y = x @ W^T (+ bias) on a tile16 copy made by :func:`repack_q4_marlin_tile16`: the
-    decode GEMV for one or two rows, the multi-token GEMM (up to 64 rows per weight pass)
-    from three."""
+    decode GEMV for up to three rows, the multi-token GEMM (up to 64 rows per weight pass)
+    from four."""
     _lib.require_gpu(x, "qmv_q4_tile16")
     K = x.size(-1)
     M = x.numel() // K
@@ -256,7 +257,7 @@ def qmv_q4_marlin_swiglu(x, ln_w, eps: float, gu_w, gu_sb, H: int) -> torch.Tens
 
 def qmv_q4_tile16_swiglu(x, ln_w, eps: float, gu16, gusb16, H: int) -> torch.Tensor:
     """:func:`qmv_q4_marlin_swiglu` on the tile16 copy of the packed [W_gate; W_up] (H % 16 == 0);
-    from three rows on they are normalized first and go through the multi-token GEMM."""
+    from four rows on they are normalized first and go through the multi-token GEMM."""
     K = x.size(-1)
     M = x.numel() // K
     gs = tile16_group_size(gu16, gusb16)
