@@ -8,7 +8,13 @@
 * Tree verification must scale sub-linearly: t(N) / N < 0.6 for N = 4, 8, 16 with
   t(N) = latency(forward_tree_verify over N nodes) / latency(one node), on the
   reference's 4-layer model (tests/test_phase2_task21_verification_latency.py:133-209).
+* The runner's one-launch step (its captured graph, the reference's single command
+  buffer) must cost at most 1 / 1.2 of the host dispatch time of the same step issued
+  kernel by kernel (tests/test_phase1_task14_single_command_buffer.py:136-173: "CPU
+  dispatch overhead").  The host time of one call is measured with the device idle
+  before it; the device time of these small steps is the same in both modes.
 """
+import time
 
 import numpy as np
 import pytest
@@ -74,12 +80,12 @@ def test_tile16_gemm_bandwidth_over_marlin_layout(dev):
         assert bw_t16 > 1.25 * bw_marlin, f"M={M}: {bw_t16:.1f} GB/s vs {bw_marlin:.1f} GB/s"
 
 
-def test_tree_verify_latency_is_sublinear(dev):
+def _model4(dev):
+    """The reference's 4-layer latency model (8 heads, GQA 4:1, d 512, SwiGLU 1024, vocab
+    1024), Q4 MARLIN, with a 256-slot cache."""
     from axiomlm_amd.cache import StaticKVCache
     from axiomlm_amd.transformer import ModelConfig, Transformer
-    from axiomlm_amd.tree import build_candidate_tree
 
-    print("[perf_tree_sublinear]", flush=True)
     c = om.OracleConfig(n_layer=4, n_head=8, n_kv_head=2, d_model=512, hidden=1024, vocab=1024, eps=1e-5,
                         block_size=256)
     W = om.make_float_weights(c, seed=3)
@@ -96,6 +102,14 @@ def test_tree_verify_latency_is_sublinear(dev):
                       tie_word_embeddings=False)
     model = Transformer(cfg, sd, device=dev).quantize("q4")
     cache = StaticKVCache(1, 256, cfg.n_layer, cfg.kv_heads, cfg.head_dim, device=dev)
+    return model, cfg, cache
+
+
+def test_tree_verify_latency_is_sublinear(dev):
+    from axiomlm_amd.tree import build_candidate_tree
+
+    print("[perf_tree_sublinear]", flush=True)
+    model, cfg, cache = _model4(dev)
     g = torch.Generator(device=dev)
     g.manual_seed(1337)
     prefix = torch.randint(0, cfg.vocab_size, (1, 32), generator=g, device=dev)
@@ -120,3 +134,39 @@ def test_tree_verify_latency_is_sublinear(dev):
     for n in (4, 8, 16):
         t_n = lat[n] / lat[1]
         assert t_n / n < 0.60, f"t({n}) / {n} = {t_n / n:.3f}"
+
+
+def test_runner_graph_dispatch_faster_than_eager(dev):
+    print("[perf_dispatch]", flush=True)
+    model, cfg, cache = _model4(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(42)
+    model.forward(torch.randint(0, cfg.vocab_size, (1, 32), generator=g, device=dev), kv_caches=cache)
+    runner = model.get_decode_runner(cache)
+    idx = torch.tensor([55], dtype=torch.int64, device=dev)
+
+    def host_us(n_trials=50):
+        """Median host time of one step call, issued onto an idle device."""
+        for _ in range(5):
+            runner.step(idx, 40, 40, 41)
+        times = []
+        for _ in range(n_trials):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            runner.step(idx, 40, 40, 41)
+            times.append((time.perf_counter() - t0) * 1e6)
+        torch.cuda.synchronize()
+        return sorted(times)[n_trials // 2]
+
+    try:
+        runner.set_mode("graph")
+        logits_graph = runner.step(idx, 40, 40, 41).float().clone()
+        t_graph = host_us()
+        runner.set_mode("eager")
+        logits_eager = runner.step(idx, 40, 40, 41).float().clone()
+        t_eager = host_us()
+    finally:
+        runner.set_mode("graph")
+    print(f"[perf_dispatch] host dispatch per step: graph {t_graph:.1f} us, eager {t_eager:.1f} us", flush=True)
+    assert torch.equal(logits_graph, logits_eager)
+    assert t_eager / t_graph >= 1.20, f"{t_eager:.1f} us eager vs {t_graph:.1f} us graph"
