@@ -185,8 +185,9 @@ def test_runner_quantized_kv_matches_oracle(dev, kv):
         values produced by cancellation (RoPE rotation, the dot product itself)
         carry a larger relative error, which the log-spaced fp8 grid turns into
         several code steps.  Bar (measured 0.971 / 0.9967 for fp8): >= 95% of codes
-        identical and >= 99% within one code step.  (Op-level bit-exactness of the
-        quantizer on identical inputs is test_gpu_kernels.py::test_kv_quantize_bit_exact.)"""
+        identical and >= 99% within one code step.  (Bit-exactness on identical inputs:
+        of the quantizer op, test_gpu_kernels.py::test_kv_quantize_bit_exact; of the write
+        inside the captured step, test_runner_quantized_kv_write_layer0_bit_exact.)"""
     print(f"[runner_qkv] kv={kv}", flush=True)
     cfg, ow, cos, sin = c1_model()
     model = om.OracleModel(cfg, ow, cos, sin)
@@ -210,6 +211,38 @@ def test_runner_quantized_kv_matches_oracle(dev, kv):
             diffs.append(np.abs(_signed_codes(kv, g) - _signed_codes(kv, o)).ravel())
         _check_logits(got, ref, f"step {i}")
     _check_codes(kv, np.concatenate(diffs), "runner_qkv")
+
+
+@pytest.mark.parametrize("kv", ["fp8", "int4"])
+def test_runner_quantized_kv_write_layer0_bit_exact(dev, kv):
+    """The in-graph quantized cache write, bit for bit.  Layer 0's k / v rows depend only on
+    the token's embedding row, not on the cache, so a runner with an fp16 cache fed the same
+    tokens holds exactly the fp16 k / v (after bias and RoPE) that the quantized runner
+    writes.  Quantized by the oracle (quant.py:710-720 / 789-803) they must equal the
+    quantized runner's layer-0 codes and scales at every slot: a slot, scale or
+    rounding error of the in-graph write shows here even where the oracle-wide code
+    comparison above tolerates the neighbouring-code effect of 1-ulp k / v differences."""
+    from oracle import formats as fm
+
+    print(f"[runner_kv_write_l0] kv={kv}", flush=True)
+    cfg, ow, cos, sin = c1_model()
+    S = 128
+    r16, c16 = build_runner(cfg, ow, cos, sin, dev, S, "fp16")
+    rq, cq = build_runner(cfg, ow, cos, sin, dev, S, kv)
+    toks = np.random.default_rng(3).integers(0, cfg.vocab, 24).tolist()
+    run_steps(r16, c16, toks, dev)
+    run_steps(rq, cq, toks, dev)
+    T = len(toks)
+    quant = fm.quantize_kv_fp8_single if kv == "fp8" else fm.quantize_kv_int4_single
+    for which, name in ((0, "k"), (1, "v")):
+        x16 = c16.cache[0, which, 0, :, :T].cpu().numpy()  # [Hkv, T, hd] fp16
+        codes, scales = quant(x16)
+        got_codes = cq.cache[0, which, 0, :, :T].cpu().numpy()
+        got_scales = cq.scales[0, which, 0, :, :T].cpu().numpy()
+        assert np.array_equal(got_codes, codes), f"{name}: {np.mean(got_codes != codes):.4f} of codes differ"
+        assert np.array_equal(got_scales.view(np.uint16), scales.view(np.uint16)), f"{name}: scales differ"
+        # Slots past the written ones stay untouched (zero-initialised cache).
+        assert not cq.cache[0, which, 0, :, T:].any()
 
 
 @pytest.mark.parametrize("mode", MODES)
