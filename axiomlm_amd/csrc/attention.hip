@@ -1059,7 +1059,8 @@ int attn_flash_splits(int B, int Hq, int Hkv, int hd, int kv_dtype, int active_l
   // about two workgroups per CU for int4 / fp16 caches and one per CU for fp8
   // (whose two-block prefetch holds more registers), with every split keeping
   // >= 256 keys, two 32-key blocks per wave (1k int4 keys: 4 splits 9.4 us,
-  // 8 splits 9.9 us).
+  // 8 splits 9.9 us; half or a quarter of the chosen splits were slower at every C3
+  // length, e.g. 1k int4 keys 11.1 / 12.6 us, 32k fp8 137 / 237 against 101 us).
   const int rows = B * Hkv;
   const int target = (kv_dtype == AXM_KV_FP8 ? 1 : 2) * axm_num_cus();
   int splits = (target + rows - 1) / rows;
