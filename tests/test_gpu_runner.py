@@ -401,7 +401,7 @@ def test_runner_verify_step_chain(dev):
     ocache = om.OracleKVCache(S, cfg.n_layer, cfg.n_kv_head, cfg.head_dim)
     rng = np.random.default_rng(11)
     _prefill(runner, cache, ocache, model, rng.integers(0, cfg.vocab, 10).tolist(), dev)
-    # 2 tokens run the decode GEMV per row group, 3 and more the multi-token GEMM.
+    # 2 and 3 tokens run the decode GEMV, 4 and more the multi-token GEMM.
     for T in (2, 3, 4, 5, 17):
         seen = cache.total_seen_tokens[0]
         toks = rng.integers(0, cfg.vocab, T).tolist()
