@@ -293,7 +293,9 @@ def test_fused_gate_up_swiglu_matches_oracle(dev, layout, M, K, H, norm):
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("fmt", ["ternary", "q2"])
 @pytest.mark.parametrize("M,N_,K,bias", [(1, 11008, 4096, False), (1, 4096, 11008, False), (3, 704, 256, True),
-                                         (5, 96, 1024, False), (2, 13, 64, True), (2, 8202, 4160, True)])
+                                         (5, 96, 1024, False), (2, 13, 64, True), (2, 8202, 4160, True),
+                                         # four rows per launch, and 4 / 8 groups per lane (K up to 32768)
+                                         (4, 300, 16384, False), (1, 64, 32768, True), (2, 40, 20480, False)])
 def test_lowbit_qmv_matches_oracle(dev, fmt, M, N_, K, bias):
     """Ternary / affine 2-bit GEMV vs the reference CPU path (dequantize to fp16, then an
     fp32-accumulated fp16 linear, quant.py:298-318 / 406-426).  The packed bytes are
