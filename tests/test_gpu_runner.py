@@ -634,7 +634,10 @@ def test_sequoia_tree_loop_matches_greedy(dev):
 # Runner branches: tied Q8_G64 lm_head, fp16 embedding table, QKV bias
 # ---------------------------------------------------------------------------
 def _branch_model(variant):
-    cfg = om.OracleConfig(n_layer=2, n_head=4, n_kv_head=2, d_model=256, hidden=704, vocab=1024, eps=1e-5,
+    # big_vocab: 40000 rows make 2500 lm_head tiles, past the 2048 (8 per CU on 256 CUs)
+    # from which the tile16 GEMV runs its looping form (one wave per tile, S = 1).
+    vocab = 40000 if variant == "big_vocab" else 1024
+    cfg = om.OracleConfig(n_layer=2, n_head=4, n_kv_head=2, d_model=256, hidden=704, vocab=vocab, eps=1e-5,
                           block_size=256)
     W = om.make_float_weights(cfg, seed=7)
     if variant == "tied_q8":
@@ -652,12 +655,15 @@ def _branch_model(variant):
     return cfg, ow, cos, sin
 
 
-@pytest.mark.parametrize("variant", ["tied_q8", "fp16_wte", "qkv_bias"])
+@pytest.mark.parametrize("variant", ["tied_q8", "fp16_wte", "qkv_bias", "big_vocab"])
 def test_runner_branches_match_oracle(dev, variant):
     """The reference default head for tied embeddings (Q8_G64 lm_head shared with the
-    embedding gather, runner lm_head format 1), an fp16 embedding table (wte format 0)
-    and a QKV bias, through decode steps, a 6-token verify chain and a 9-node tree,
-    against the oracle (logits <= 1e-2)."""
+    embedding gather, runner lm_head format 1), an fp16 embedding table (wte format 0),
+    a QKV bias and a 40000-token vocabulary (the lm_head GEMV's looping form with the
+    greedy-argmax epilogue), through decode steps, a 6-token verify chain and a 9-node
+    tree, against the oracle (logits <= 1e-2); for the large vocabulary also in-graph
+    greedy steps, whose fed-back token must be the lowest-index maximum of the logits
+    the step before returned."""
     print(f"[runner_branches] {variant}", flush=True)
     cfg, ow, cos, sin = _branch_model(variant)
     model = om.OracleModel(cfg, ow, cos, sin)
@@ -689,6 +695,16 @@ def test_runner_branches_match_oracle(dev, variant):
     ref = model.forward_tree(tree, ocache, depths, masks)
     for t in range(len(tree)):
         _check_logits(g[t], ref[t], f"{variant} tree node {t}")
+    if variant == "big_vocab":
+        seen += len(tree)
+        cache.total_seen_tokens[:] = [seen] * cfg.n_layer
+        cache.layer_seq_lens[:] = [seen] * cfg.n_layer
+        expect = int(np.argmax(run_steps(runner, cache, [5], dev)[0]))
+        seen += 1
+        for i in range(8):
+            lg = runner.step_greedy(seen + i, seen + i, seen + i + 1)[0, 0].float().cpu().numpy()
+            assert int(runner.last_token().item()) == expect, f"greedy step {i}"
+            expect = int(np.argmax(lg))
 
 
 # ---------------------------------------------------------------------------
