@@ -42,7 +42,15 @@ __device__ __forceinline__ f16x2 code_pair(uint32_t w, int p) {
   return __builtin_bit_cast(f16x2, (t & 0x03000300u) | 0x44004400u);
 }
 
-// xs: [M][K] fp16, each 16-column block stored as pairs (k, k+8), k = 0..7.
+// LDS slot of activation quad q (8 staged values, 16 bytes) within its row: bits 4-6
+// of q are XORed onto bits 0-2.  Lane g reads quads 8 g .. 8 g + 7 of a row, so
+// without it the 16 lanes of one LDS cycle hit two 16-byte bank groups (8-way
+// conflicts); with it they hit 16 distinct ones.  A bijection on aligned 8-quad
+// blocks: a lane's eight quads stay its own, in another order.
+__device__ __forceinline__ int lb_lds_quad(int q) { return q ^ ((q >> 4) & 7); }
+
+// xs: [M][K] fp16, each 16-column block stored as pairs (k, k+8), k = 0..7, quad q
+// of a row at slot lb_lds_quad(q).
 // gs: [M][K/64] fp32 group sums of x.
 template <int FMT, int M, int ITERS, int kLbRows>
 __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __restrict__ x, int K, int N,
@@ -116,8 +124,9 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
       part += dpp_move<0xB1>(part);  // quad_perm [1,0,3,2]
       part += dpp_move<0x4E>(part);  // quad_perm [2,3,0,1]
       if (b < nblk) {
-        reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[0] = p0;
-        reinterpret_cast<f16x8*>(xs + (size_t)m * K + 16 * b)[1] = p1;
+        f16x8* xq = reinterpret_cast<f16x8*>(xs + (size_t)m * K);
+        xq[lb_lds_quad(2 * b)] = p0;
+        xq[lb_lds_quad(2 * b + 1)] = p1;
         if ((b & 3) == 0) gs[m * KG + b / 4] = part;
       }
     }
@@ -142,10 +151,10 @@ __global__ void __launch_bounds__(kLbThreads) lowbit_gemv_kernel(const f16* __re
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const u32x4* xp = reinterpret_cast<const u32x4*>(xs + (size_t)m * K + 64 * g);
+      const u32x4* xp = reinterpret_cast<const u32x4*>(xs + (size_t)m * K);
       u32x4 xv[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) xv[q] = xp[q];
+      for (int q = 0; q < 8; ++q) xv[q] = xp[lb_lds_quad(8 * g + q)];
       const float gsum = gs[m * KG + g];
 #pragma unroll
       for (int r = 0; r < kLbRows; ++r) {

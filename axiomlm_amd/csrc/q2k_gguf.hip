@@ -20,18 +20,16 @@
 // after a shift by 8), and OR-ing the fp16 exponent of 64.0 makes the exact halves
 // 64 + q 4^j / 16, one AND-OR per pair, consumed by one v_dot2_f32_f16.  Per
 // sub-block, sum x w = d sc (16 / 4^j) (acc - 64 S) - dmin m S with S the
-// sub-block's activation sum (staged with the activations).
+// sub-block's activation sum (staged with the activations).  That kernel runs one
+// token; two to four tokens run q2k_mfma_kernel, which dequantizes each weight once
+// and multiplies the tokens on MFMA.
 #include "kernels.h"
 
 namespace {
 
 constexpr int kQ2kBlockBytes = 84;
-// Workgroup size: 512 threads for one token; 256 with several, whose registers
-// (about 160 VGPRs at four tokens and four rows) admit one 512-thread workgroup per
-// CU, so that grid ran in two rounds (C4 shapes at M = 4 with the staging rounds
-// below: 23.4 / 19.9 -> 17.4 / 17.3 us).
+// Workgroup size of the one-token dot-product kernel.
 constexpr int kQ2kThreads = 512;
-constexpr int kQ2kThreadsMulti = 256;
 constexpr int kQ2kMaxK = 16384;
 constexpr int kQ2kStageU = 8;  // activation vectors requested per thread and staging round
 
@@ -119,50 +117,34 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
-// xs: [M][K] fp16 in pair order; ss: [M][K / 16] fp32 sub-block sums.
-template <int M, int R, int TH>
-__global__ void __launch_bounds__(TH) q2k_gemv_kernel(const f16* __restrict__ x, int K, int N,
-                                                              const uint8_t* __restrict__ wq, size_t w_bytes,
-                                                              const f16* __restrict__ bias, f16* __restrict__ y) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);            // [M][K / 2] pairs
-  float* ss = reinterpret_cast<float*>(xs + (size_t)M * K / 2);  // [M][K / 16]
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int NB = K / 256;
-  const int row0 = (blockIdx.x * (TH / 64) + wave) * R;
-  const __amdgpu_buffer_rsrc_t rw =
-      __builtin_amdgcn_make_buffer_rsrc((void*)wq, (short)0, (int)w_bytes, 0x00020000);
-  constexpr int kOOB = 0x7FFFFFF0;
-  const int t = lane & 3, bs = lane >> 2;  // sub-lane of the block, block slot
-  const int h = t >> 1, hx = t & 1;
+// LDS slot of activation quad q (8 staged values, 16 bytes) within its row: bits 4-6
+// of q are XORed onto bits 0, 2 and 3.  A GEMV read instruction has lane 4 bs + t
+// fetch quad 32 bs + 16 (t / 2) + 2 (t % 2) + c (c the same for every lane), so
+// without it the 16 lanes of one LDS cycle hit two 16-byte bank groups (8-way
+// conflicts); with it they hit 16 distinct ones.  A bijection on aligned 16-quad
+// blocks, so a row's quads stay inside the row.
+__device__ __forceinline__ int q2k_lds_quad(int q) {
+  const int s = (q >> 4) & 7;
+  return q ^ ((s & 1) | ((s & 6) << 1));
+}
 
-  // First pass's weights before the staging (loads complete in issue order).
-  u32x4 cw[R];
-  u32x2 sc[R];
-  uint32_t dd[R];
-  auto load = [&](int b) {
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const int row = row0 + i;
-      const bool ok = row < N && b < NB;
-      const int base = ok ? (row * NB + b) * kQ2kBlockBytes : kOOB;
-      cw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? base + 16 + 32 * h + 16 * hx : kOOB, 0, 0));
-      sc[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, ok ? base + 8 * h : kOOB, 0, 0));
-      dd[i] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 80 : kOOB, 0, 0);
-    }
-  };
-  load(bs);
+constexpr int kOOB = 0x7FFFFFF0;  // buffer offset past every descriptor: the load returns zeros
 
-  // Stage x in pair order and the 16-element sums: thread -> 8 consecutive elements.
-  // Rounds of kQ2kStageU vectors per thread, all requested before any is used (a
-  // loop of one load each waited a full round trip per vector: M = 4 at K = 11008
-  // is 22 vectors per thread).
-  // Vectors past the end read zeros through a bounded descriptor (no memory traffic).
+// Stage x ([M][K] fp16, rows contiguous) in LDS in pair order, 8 elements (one quad of
+// four pairs) per thread and vector, and the 16-element sums into ss [M][K / 16].
+// MODE 0 (dot-product kernel): quad c of row m at xs + m row_dw + 4 q2k_lds_quad(c),
+// sub-block s of a row at ss position s.  MODE 1 (MFMA kernel): quad c at
+// 4 c, and sub-block 16 b + 8 h + 2 j + hx of block b at 16 b + 8 h + 4 hx + j, so
+// the four sub-blocks j = 0..3 that one lane of that kernel reads are contiguous.
+// Rounds of kQ2kStageU vectors per thread, all requested before any is used (a loop
+// of one load each waited a full round trip per vector: M = 4 at K = 11008 is 22
+// vectors per thread).  Vectors past the end read zeros through a bounded descriptor
+// (no memory traffic).
+template <int TH, int MODE>
+__device__ __forceinline__ void q2k_stage_x(const f16* x, int M, int K, uint32_t* xs, int row_dw, float* ss,
+                                            int tid) {
   const int nvec = M * K / 8;
-  const __amdgpu_buffer_rsrc_t rx =
-      __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nvec * 16, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nvec * 16, 0x00020000);
   for (int v0 = tid; v0 < nvec; v0 += kQ2kStageU * TH) {
     // Slices u whose first vector (thread 0's) is past the end are skipped by every
     // thread alike (a workgroup-uniform bound).
@@ -196,11 +178,179 @@ __global__ void __launch_bounds__(TH) q2k_gemv_kernel(const f16* __restrict__ x,
       }
       s = add_rn(s, dpp_move<0xB1>(s));  // elements 16(c/2) .. +15: the pair (c, c ^ 1)
       if (v < nvec) {
-        *reinterpret_cast<u32x4*>(xs + (size_t)m * K / 2 + 4 * c) = p;
-        if ((c & 1) == 0) ss[(size_t)m * (K / 16) + c / 2] = s;
+        *reinterpret_cast<u32x4*>(xs + (size_t)m * row_dw + 4 * (MODE == 0 ? q2k_lds_quad(c) : c)) = p;
+        const int sb = c / 2;  // sub-block of the row
+        const int pos = MODE == 0 ? sb : (sb & ~15) | (sb & 8) | ((sb & 1) << 2) | ((sb >> 1) & 3);
+        if ((c & 1) == 0) ss[(size_t)m * (K / 16) + pos] = s;
       }
     }
   }
+}
+
+// Two to four tokens on MFMA: the codes of each weight are expanded once and the tokens
+// are the A rows 0..M-1 of v_mfma_f32_16x16x32_f16, so the VALU work per weight does
+// not grow with the token count (the dot-product kernel below spends two
+// v_dot2_f32_f16 per four weights and token).  A workgroup owns 16 weight rows, the B
+// columns: lane l takes row n = l & 15 and block part t = l >> 4 (half h = t / 2 and
+// the 16-byte run hx = t % 2 of the codes, as in the dot-product kernel), which is
+// also the MFMA k-group of 8 values that the lane supplies.  Its W waves take blocks
+// w, w + W, ... and add their partial products through LDS at the end.
+// The product is exact up to fp32 accumulation, as in the dot-product kernel: B holds
+// the integer sc q, made from the exact halves 64 + q 4^j / 16 of the exponent OR by
+// one fp16 fma with sc 16 / 4^j and -64 sc 16 / 4^j (both exact); the
+// MFMA chain of one block is scaled by the block's d in fp32, and the min term
+// dmin sum_s m_s S_s comes from the staged sub-block sums S.  The x rows are staged
+// with 16 bytes of padding, so the M active lanes of an A read hit distinct banks.
+template <int M, int W>
+__global__ void __launch_bounds__(W * 64) q2k_mfma_kernel(const f16* __restrict__ x, int K, int N,
+                                                          const uint8_t* __restrict__ wq, size_t w_bytes,
+                                                          const f16* __restrict__ bias, f16* __restrict__ y) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int row_dw = K / 2 + 4;
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);                 // [M][row_dw] pairs
+  float* ss = reinterpret_cast<float*>(xs + (size_t)M * row_dw);   // [M][K / 16] sums (MODE 1 order)
+  float* red = ss + (size_t)M * (K / 16);                           // [W][M][16] partial sums
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int NB = K / 256;
+  const int n = lane & 15, t = lane >> 4, h = t >> 1, hx = t & 1;
+  const int row = blockIdx.x * 16 + n;
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wq, (short)0, (int)w_bytes, 0x00020000);
+  u32x4 cw;
+  u32x2 sc;
+  uint32_t dd;
+  auto load = [&](int b) {
+    const bool ok = row < N && b < NB;
+    const int base = ok ? (row * NB + b) * kQ2kBlockBytes : 0;
+    cw = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? base + 16 + 32 * h + 16 * hx : kOOB, 0, 0));
+    sc = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, ok ? base + 8 * h : kOOB, 0, 0));
+    dd = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 80 : kOOB, 0, 0);
+  };
+  load(wave);  // the first block's codes before the staging (loads complete in issue order)
+  q2k_stage_x<W * 64, 1>(x, M, K, xs, row_dw, ss, tid);
+  __syncthreads();
+
+  const bool a_on = n < M;  // this lane's A row n is a token
+  const uint32_t* xa = xs + (size_t)(a_on ? n : 0) * row_dw;
+  f32x4 tot = {0.f, 0.f, 0.f, 0.f};  // d-scaled code products (C rows 4 t .. 4 t + 3)
+  float mins[M];                     // dmin m S of this lane's sub-blocks, token m
+#pragma unroll
+  for (int m = 0; m < M; ++m) mins[m] = 0.f;
+  for (int b = wave; b < NB; b += W) {
+    const u32x4 c0 = cw;
+    const u32x2 s0 = sc;
+    const f16x2 dm = as_h2(dd);
+    if (b + W < NB) load(b + W);
+    const int q0 = 32 * b + 16 * h + 2 * hx;  // quad of element 256 b + 128 h + 16 hx
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float mq[4];  // min codes of this lane's sub-blocks j
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // scale byte of sub-block 8 h + 2 j + hx: byte 2 j + hx of the half's eight
+      const uint32_t sbyte = (s0[j >> 1] >> (16 * (j & 1) + 8 * hx)) & 0xFFu;
+      mq[j] = (float)(sbyte >> 4);
+      // sc 16 / 4^j and -64 sc 16 / 4^j, both exact in fp16: (v - 64) sc 16 / 4^j = sc q
+      const f16 scf = (f16)((float)(sbyte & 15u) * (16.f / (float)(1 << (2 * j))));
+      const f16x2 sv = {scf, scf};
+      const f16x2 ov = -(f16x2){(f16)64.f, (f16)64.f} * sv;
+      const uint32_t mask = 0x00030003u << (2 * j);
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) {
+        // B: words 2 gp and 2 gp + 1 of the run (elements 8 gp .. 8 gp + 7 of sub-block j),
+        // in the staged pair order (e0, e2), (e1, e3), (e4, e6), (e5, e7)
+        f16x8 B;
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+          const uint32_t cword = c0[2 * gp + gg];
+          const f16x2 lo = as_h2((cword & mask) | 0x54005400u);
+          const f16x2 hi = as_h2(((cword >> 8) & mask) | 0x54005400u);
+          const f16x2 wl = __builtin_elementwise_fma(lo, sv, ov);
+          const f16x2 wh = __builtin_elementwise_fma(hi, sv, ov);
+          B[4 * gg + 0] = wl.x;
+          B[4 * gg + 1] = wl.y;
+          B[4 * gg + 2] = wh.x;
+          B[4 * gg + 3] = wh.y;
+        }
+        f16x8 A = {};
+        if (a_on) A = *reinterpret_cast<const f16x8*>(xa + 4 * (q0 + 4 * j + gp));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc, 0, 0, 0);
+      }
+    }
+    const float d = h2f(dm.x), dmin = h2f(dm.y);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tot[i] = __builtin_fmaf(d, acc[i], tot[i]);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(ss + (size_t)m * (K / 16) + 16 * b + 8 * h + 4 * hx);
+      float p = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p = __builtin_fmaf(mq[j], s4[j], p);
+      mins[m] = __builtin_fmaf(dmin, p, mins[m]);
+    }
+  }
+  // The min terms of row n sit in lanes n, n + 16, n + 32, n + 48; the code products
+  // of its tokens 0..3 in lane n (C row 4 (l / 16) + i, column l % 16 in lane l).
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    mins[m] += __shfl_xor(mins[m], 16, 64);
+    mins[m] += __shfl_xor(mins[m], 32, 64);
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[(wave * M + m) * 16 + lane] = tot[m] - mins[m];
+  }
+  __syncthreads();
+  if (tid < 16 * M) {
+    const int m = tid >> 4, nn = tid & 15;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) v = add_rn(v, red[(w * M + m) * 16 + nn]);
+    const int r = blockIdx.x * 16 + nn;
+    if (r < N) {
+      if (bias != nullptr) v = add_rn(v, h2f(bias[r]));
+      y[(size_t)m * N + r] = f2h(v);
+    }
+  }
+}
+
+// xs: [M][K] fp16 in pair order; ss: [M][K / 16] fp32 sub-block sums.
+template <int M, int R, int TH>
+__global__ void __launch_bounds__(TH) q2k_gemv_kernel(const f16* __restrict__ x, int K, int N,
+                                                              const uint8_t* __restrict__ wq, size_t w_bytes,
+                                                              const f16* __restrict__ bias, f16* __restrict__ y) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);            // [M][K / 2] pairs
+  float* ss = reinterpret_cast<float*>(xs + (size_t)M * K / 2);  // [M][K / 16]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int NB = K / 256;
+  const int row0 = (blockIdx.x * (TH / 64) + wave) * R;
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wq, (short)0, (int)w_bytes, 0x00020000);
+  const int t = lane & 3, bs = lane >> 2;  // sub-lane of the block, block slot
+  const int h = t >> 1, hx = t & 1;
+
+  // First pass's weights before the staging (loads complete in issue order).
+  u32x4 cw[R];
+  u32x2 sc[R];
+  uint32_t dd[R];
+  auto load = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int row = row0 + i;
+      const bool ok = row < N && b < NB;
+      const int base = ok ? (row * NB + b) * kQ2kBlockBytes : kOOB;
+      cw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? base + 16 + 32 * h + 16 * hx : kOOB, 0, 0));
+      sc[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, ok ? base + 8 * h : kOOB, 0, 0));
+      dd[i] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 80 : kOOB, 0, 0);
+    }
+  };
+  load(bs);
+
+  q2k_stage_x<TH, 0>(x, M, K, xs, K / 2, ss, tid);
   __syncthreads();
 
   float r[R][M];
@@ -231,9 +381,11 @@ __global__ void __launch_bounds__(TH) q2k_gemv_kernel(const f16* __restrict__ x,
         u32x4 xp[M][2];
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          const uint32_t* xr = xs + (size_t)m * K / 2 + (e0 + 32 * j) / 2;
-          xp[m][0] = *reinterpret_cast<const u32x4*>(xr);
-          xp[m][1] = *reinterpret_cast<const u32x4*>(xr + 4);
+          // quads (e0 + 32 j) / 8 (even) and the next one, which differs in bit 0 only
+          const int pq = q2k_lds_quad((e0 + 32 * j) / 8);
+          const uint32_t* xr = xs + (size_t)m * K / 2;
+          xp[m][0] = *reinterpret_cast<const u32x4*>(xr + 4 * pq);
+          xp[m][1] = *reinterpret_cast<const u32x4*>(xr + 4 * (pq ^ 1));
         }
         float sx[M];
 #pragma unroll
@@ -304,22 +456,45 @@ int q2k_launch_mr(const f16* x, int K, int N, const uint8_t* w, const f16* bias,
   return 0;
 }
 
-// Rows per wave while the grid keeps at least one workgroup per CU: two for one
-// token (measured best at the C4 shapes: 8.1 / 8.4 us against 9.9 / 8.4 with four),
-// four for several tokens, whose activation registers are shared by more rows.
-template <int M>
-int q2k_launch(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
-  const int cus = axm_num_cus();
-  if constexpr (M > 1) {
-    constexpr int W = kQ2kThreadsMulti / 64;
-    if ((N + 4 * W - 1) / (4 * W) >= cus) return q2k_launch_mr<M, 4, kQ2kThreadsMulti>(x, K, N, w, bias, y, st);
-    if ((N + 2 * W - 1) / (2 * W) >= cus) return q2k_launch_mr<M, 2, kQ2kThreadsMulti>(x, K, N, w, bias, y, st);
-    return q2k_launch_mr<M, 1, kQ2kThreadsMulti>(x, K, N, w, bias, y, st);
-  } else {
-    constexpr int W = kQ2kThreads / 64;
-    if ((N + 2 * W - 1) / (2 * W) >= cus) return q2k_launch_mr<M, 2, kQ2kThreads>(x, K, N, w, bias, y, st);
-    return q2k_launch_mr<M, 1, kQ2kThreads>(x, K, N, w, bias, y, st);
+template <int M, int W>
+int q2k_mfma_launch_w(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
+  const size_t smem = (size_t)M * (K / 2 + 4) * sizeof(uint32_t) + (size_t)M * (K / 16) * sizeof(float) +
+                      (size_t)W * M * 16 * sizeof(float);
+  if (smem > 160 * 1024) {
+    axm_set_error("qmv_q2_k_gguf: K=%d with %d rows needs %zu B of LDS", K, M, smem);
+    return -2;
   }
+  if (smem > 64 * 1024 && hipFuncSetAttribute((const void*)q2k_mfma_kernel<M, W>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess) {
+    (void)hipGetLastError();
+    axm_set_error("qmv_q2_k_gguf: cannot reserve %zu B of LDS", smem);
+    return -2;
+  }
+  const size_t w_bytes = (size_t)N * (K / 256) * kQ2kBlockBytes;
+  hipLaunchKernelGGL((q2k_mfma_kernel<M, W>), dim3((N + 15) / 16), dim3(W * 64), smem, st, x, K, N, w, w_bytes,
+                     bias, y);
+  return 0;
+}
+
+// Several tokens: the MFMA kernel with four waves per 16-row workgroup while the grid
+// holds two workgroups per CU, else sixteen (C4 shapes at four tokens: 4096 -> 11008
+// 11.3 us with four waves, 11.4 with eight, 12.2 with sixteen; 11008 -> 4096, 256
+// workgroups, 10.7 with four or eight, 10.3 with sixteen).  One token stays on the
+// dot-product kernel (the MFMA form: 8.7 / 8.0 against 8.4 / 7.8 us).
+template <int M>
+int q2k_mfma_launch(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
+  const long groups = (N + 15) / 16;
+  if (groups >= 2L * axm_num_cus()) return q2k_mfma_launch_w<M, 4>(x, K, N, w, bias, y, st);
+  return q2k_mfma_launch_w<M, 16>(x, K, N, w, bias, y, st);
+}
+
+// One token: the dot-product kernel with two rows per wave while the grid keeps at
+// least one workgroup per CU (measured best at the C4 shapes: 8.1 / 8.4 us against
+// 9.9 / 8.4 with four), else one.
+int q2k_launch1(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
+  constexpr int W = kQ2kThreads / 64;
+  if ((N + 2 * W - 1) / (2 * W) >= axm_num_cus()) return q2k_launch_mr<1, 2, kQ2kThreads>(x, K, N, w, bias, y, st);
+  return q2k_launch_mr<1, 1, kQ2kThreads>(x, K, N, w, bias, y, st);
 }
 
 }  // namespace
@@ -355,10 +530,10 @@ extern "C" int axm_qmv_q2_k_gguf(const void* x, const void* blocks, const void* 
     f16* ym = (f16*)y + (size_t)m0 * N;
     int rc;
     switch (mc) {
-      case 1: rc = q2k_launch<1>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
-      case 2: rc = q2k_launch<2>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
-      case 3: rc = q2k_launch<3>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
-      default: rc = q2k_launch<4>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
+      case 1: rc = q2k_launch1(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
+      case 2: rc = q2k_mfma_launch<2>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
+      case 3: rc = q2k_mfma_launch<3>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
+      default: rc = q2k_mfma_launch<4>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
     }
     if (rc) return rc;
   }

@@ -2,7 +2,8 @@
 packer and dequantization bit for bit, GEMV within 2e-3 relative of x times the
 oracle's fp32 dequantized weights (float64 product, one fp16 rounding) at the C4
 shapes, ragged row counts, 1-5 tokens, bias, the largest K, and on weights that
-sit exactly on the lattice."""
+sit exactly on the lattice; and the rounding of the one-token and several-token
+kernels against the float64 product."""
 
 import numpy as np
 import pytest
@@ -61,6 +62,44 @@ def _check_gemv(dev, M, N, K, bias, w=None, seed=0):
 def test_q2k_gemv_matches_oracle(dev, M, N, K, bias):
     print(f"[q2k_gemv] M={M} N={N} K={K} bias={bias}", flush=True)
     _check_gemv(dev, M, N, K, bias, seed=M * 31 + N)
+
+
+def _ulps(a, b):
+    """Distance in fp16 ulps between fp16 arrays (through zero: both distances)."""
+    ua, ub = a.view(np.uint16).astype(np.int32), b.view(np.uint16).astype(np.int32)
+    ma, mb = ua & 0x7FFF, ub & 0x7FFF  # magnitudes, ordered like the values of one sign
+    return np.where((ua >> 15) == (ub >> 15), np.abs(ma - mb), ma + mb)
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 11008, 4096), (4, 4096, 11008), (2, 300, 768), (3, 64, 16384)])
+def test_q2k_gemv_rounding(dev, M, N, K):
+    """Two to four tokens run the MFMA kernel, which multiplies the exact code products
+    sc q and applies d and the min term in fp32: at least 99 % of its outputs are the
+    fp16 rounding of the float64 product and the rest one ulp away (at the C4 shapes
+    99.8-99.9 %; a kernel that rounded each dequantized weight to fp16 gets about 58 % at
+    4096 x 2048, a plant on the CPU).  The one-token dot-product kernel is checked on
+    the same rows at its own bar: its per-sub-block sum acc - 64 S cancels a term of
+    about 64 |S| in fp32, so about 88 % of its outputs are correctly rounded and the
+    rest one ulp or up to 2e-4 (at K = 4096) away."""
+    from axiomlm_amd.kernels import qmv_q2_k_gguf
+
+    print(f"[q2k_rounding] M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(F16)
+    blocks = fm.pack_q2_k_gguf(w)
+    xn = rng.standard_normal((M, K)).astype(F16)
+    ref = xn.astype(np.float64) @ fm.dequantize_q2_k_gguf(blocks, F32).astype(np.float64).T
+    rr = ref.astype(F16)
+    bd, x = T(blocks, dev), T(xn, dev)
+    many = qmv_q2_k_gguf(x, bd).cpu().numpy()
+    one = np.concatenate([qmv_q2_k_gguf(x[m:m + 1], bd).cpu().numpy() for m in range(M)])
+    grow = np.sqrt(K / 4096.0)  # accumulation error grows like the square root of K
+    u = _ulps(many, rr)
+    assert np.all((u <= 1) | (np.abs(many - ref) <= 2e-5 * grow)), int(u.max())
+    assert np.mean(u == 0) >= 0.99, float(np.mean(u == 0))
+    u1 = _ulps(one, rr)
+    assert np.all((u1 <= 1) | (np.abs(one - ref) <= 2.5e-4 * grow)), int(u1.max())
+    assert np.mean(u1 == 0) >= 0.8, float(np.mean(u1 == 0))
 
 
 def test_q2k_gemv_on_lattice_weights(dev):
