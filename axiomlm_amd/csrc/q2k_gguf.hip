@@ -232,8 +232,8 @@ __global__ void __launch_bounds__(W * 64) q2k_mfma_kernel(const f16* __restrict_
   q2k_stage_x<W * 64, 1>(x, M, K, xs, row_dw, ss, tid);
   __syncthreads();
 
-  const bool a_on = n < M;  // this lane's A row n is a token
-  const uint32_t* xa = xs + (size_t)(a_on ? n : 0) * row_dw;
+  // A row n: token n; rows past M repeat token M - 1 and only reach C rows never stored.
+  const uint32_t* xa = xs + (size_t)min(n, M - 1) * row_dw;
   f32x4 tot = {0.f, 0.f, 0.f, 0.f};  // d-scaled code products (C rows 4 t .. 4 t + 3)
   float mins[M];                     // dmin m S of this lane's sub-blocks, token m
 #pragma unroll
@@ -273,8 +273,7 @@ __global__ void __launch_bounds__(W * 64) q2k_mfma_kernel(const f16* __restrict_
           B[4 * gg + 2] = wh.x;
           B[4 * gg + 3] = wh.y;
         }
-        f16x8 A = {};
-        if (a_on) A = *reinterpret_cast<const f16x8*>(xa + 4 * (q0 + 4 * j + gp));
+        const f16x8 A = *reinterpret_cast<const f16x8*>(xa + 4 * (q0 + 4 * j + gp));
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc, 0, 0, 0);
       }
     }

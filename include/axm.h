@@ -114,7 +114,8 @@ int axm_pack_q2_k(const void* w, int src_is_fp16, int N, int K, void* packed_u8,
 /* y = x W^T (+ bias) on the packed 2-bit rows, x fp16 [M][K], y fp16 [M][N], fp32
  * accumulation.  Replaces qmv/qmm_ternary_mps (qmv/qmm_ternary_half_kernel,
  * metal_kernels.metal:3990-4160; Python quant.py:298-336) and qmv/qmm_q2_k_mps
- * (metal_kernels.metal:4167-4334; quant.py:406-444). */
+ * (metal_kernels.metal:4167-4334; quant.py:406-444).  Exact code products: one or two
+ * tokens on v_dot2_f32_f16, three to sixteen per launch on MFMA. */
 int axm_qmv_ternary(const void* x, const void* w_packed, const void* scales, const void* bias, void* y, int M, int K,
                     int N, void* stream);
 int axm_qmv_q2_k(const void* x, const void* w_packed, const void* scales_biases, const void* bias, void* y, int M,

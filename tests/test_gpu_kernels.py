@@ -295,7 +295,11 @@ def test_fused_gate_up_swiglu_matches_oracle(dev, layout, M, K, H, norm):
 @pytest.mark.parametrize("M,N_,K,bias", [(1, 11008, 4096, False), (1, 4096, 11008, False), (3, 704, 256, True),
                                          (5, 96, 1024, False), (2, 13, 64, True), (2, 8202, 4160, True),
                                          # four rows per launch, and 4 / 8 groups per lane (K up to 32768)
-                                         (4, 300, 16384, False), (1, 64, 32768, True), (2, 40, 20480, False)])
+                                         (4, 300, 16384, False), (1, 64, 32768, True), (2, 40, 20480, False),
+                                         # several tokens per MFMA launch: 8 and 16 tokens, 6 + 1 and 6 + 2 at
+                                         # K = 11008, 16 + 1, and K = 16384 on sixteen waves
+                                         (8, 1100, 4096, False), (16, 200, 4096, True), (7, 500, 11008, False),
+                                         (8, 300, 11008, True), (17, 64, 2048, False), (3, 33, 16384, True)])
 def test_lowbit_qmv_matches_oracle(dev, fmt, M, N_, K, bias):
     """Ternary / affine 2-bit GEMV vs the reference CPU path (dequantize to fp16, then an
     fp32-accumulated fp16 linear, quant.py:298-318 / 406-426).  The packed bytes are
@@ -336,6 +340,52 @@ def test_lowbit_qmv_matches_oracle(dev, fmt, M, N_, K, bias):
         ref_exact = ref_exact + b.astype(np.float64)
     err_exact = np.abs(got - ref_exact) / (1.0 + np.abs(ref_exact))
     assert err_exact.max() <= 1e-3, f"max rel err vs unrounded weights {err_exact.max()}"
+
+
+def _ulps16(a, b):
+    """Distance in fp16 ulps between fp16 arrays (through zero: both distances)."""
+    ua, ub = a.view(np.uint16).astype(np.int32), b.view(np.uint16).astype(np.int32)
+    ma, mb = ua & 0x7FFF, ub & 0x7FFF
+    return np.where((ua >> 15) == (ub >> 15), np.abs(ma - mb), ma + mb)
+
+
+@pytest.mark.parametrize("fmt", ["ternary", "q2"])
+@pytest.mark.parametrize("M,N_,K", [(4, 11008, 4096), (4, 4096, 11008), (16, 512, 4096)])
+def test_lowbit_several_tokens_rounding(dev, fmt, M, N_, K):
+    """Three to sixteen tokens per launch run the MFMA kernel, which multiplies the exact
+    integer codes and applies each group's scale (and affine bias times the staged group
+    sum) in fp32: at least 99 % of its outputs are the fp16 rounding of the float64
+    product with the unrounded weights q s (+ b), and the rest one ulp away or within
+    2e-5 near zero.  The same rows one token at a time (the dot-product kernel) are within
+    one ulp or 2.5e-4."""
+    from axiomlm_amd.kernels import qmv_q2_k, qmv_ternary
+
+    print(f"[lowbit_rounding] fmt={fmt} M={M} N={N_} K={K}", flush=True)
+    rng = np.random.default_rng(M + N_ + K)
+    packed = rng.integers(0, 256, (N_, K // 4), dtype=np.uint8)
+    x = rng.standard_normal((M, K)).astype(F16)
+    codes = ((packed.astype(np.int64)[..., None] >> (2 * np.arange(4))) & 3).reshape(N_, K // 64, 64)
+    if fmt == "ternary":
+        s = (np.abs(rng.standard_normal((N_, K // 64))) * 0.02 + 0.001).astype(F16)
+        q = np.where(codes == 1, 1, np.where(codes == 2, -1, 0))  # lo - hi, code 3 -> 0
+        w = (q * s[..., None].astype(np.float64)).reshape(N_, K)
+        fn = lambda xx: qmv_ternary(xx, T(packed, dev), T(s, dev))
+    else:
+        s = np.stack([np.abs(rng.standard_normal((N_, K // 64))) * 0.01,
+                      rng.standard_normal((N_, K // 64)) * 0.02], axis=-1).astype(F16)
+        w = (codes * s[..., 0:1].astype(np.float64) + s[..., 1:2].astype(np.float64)).reshape(N_, K)
+        fn = lambda xx: qmv_q2_k(xx, T(packed, dev), T(s, dev))
+    ref = x.astype(np.float64) @ w.T
+    rr = ref.astype(F16)
+    xd = T(x, dev)
+    many = N(fn(xd))
+    one = np.concatenate([N(fn(xd[m:m + 1])) for m in range(M)])
+    grow = np.sqrt(K / 4096.0)
+    u = _ulps16(many, rr)
+    assert np.all((u <= 1) | (np.abs(many - ref) <= 2e-5 * grow)), int(u.max())
+    assert np.mean(u == 0) >= 0.99, float(np.mean(u == 0))
+    u1 = _ulps16(one, rr)
+    assert np.all((u1 <= 1) | (np.abs(one - ref) <= 2.5e-4 * grow)), int(u1.max())
 
 
 def test_ternary_qmv_exact_on_integers(dev):

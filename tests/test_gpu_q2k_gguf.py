@@ -58,7 +58,8 @@ def _check_gemv(dev, M, N, K, bias, w=None, seed=0):
 
 @pytest.mark.parametrize("M,N,K,bias", [(1, 11008, 4096, False), (1, 4096, 11008, False), (1, 13, 256, True),
                                         (2, 300, 768, False), (3, 129, 4096, True), (4, 4096, 4096, False),
-                                        (5, 200, 1024, False), (4, 64, 16384, False), (1, 32000, 4096, False)])
+                                        (5, 200, 1024, False), (4, 64, 16384, False), (1, 32000, 4096, False),
+                                        (2, 13, 256, True), (4, 40, 512, False)])
 def test_q2k_gemv_matches_oracle(dev, M, N, K, bias):
     print(f"[q2k_gemv] M={M} N={N} K={K} bias={bias}", flush=True)
     _check_gemv(dev, M, N, K, bias, seed=M * 31 + N)
