@@ -21,8 +21,8 @@
 // 64 + q 4^j / 16, one AND-OR per pair, consumed by one v_dot2_f32_f16.  Per
 // sub-block, sum x w = d sc (16 / 4^j) (acc - 64 S) - dmin m S with S the
 // sub-block's activation sum (staged with the activations).  That kernel runs one
-// token; two to four tokens run q2k_mfma_kernel, which dequantizes each weight once
-// and multiplies the tokens on MFMA.
+// token; two to sixteen tokens per launch run q2k_mfma_kernel, which expands each
+// weight's codes once and multiplies the tokens on MFMA.
 #include "kernels.h"
 
 namespace {
@@ -131,15 +131,12 @@ __device__ __forceinline__ int q2k_lds_quad(int q) {
 constexpr int kOOB = 0x7FFFFFF0;  // buffer offset past every descriptor: the load returns zeros
 
 // Stage x ([M][K] fp16, rows contiguous) in LDS in pair order, 8 elements (one quad of
-// four pairs) per thread and vector, and the 16-element sums into ss [M][K / 16].
-// MODE 0 (dot-product kernel): quad c of row m at xs + m row_dw + 4 q2k_lds_quad(c),
-// sub-block s of a row at ss position s.  MODE 1 (MFMA kernel): quad c at
-// 4 c, and sub-block 16 b + 8 h + 2 j + hx of block b at 16 b + 8 h + 4 hx + j, so
-// the four sub-blocks j = 0..3 that one lane of that kernel reads are contiguous.
-// Rounds of kQ2kStageU vectors per thread, all requested before any is used (a loop
-// of one load each waited a full round trip per vector: M = 4 at K = 11008 is 22
-// vectors per thread).  Vectors past the end read zeros through a bounded descriptor
-// (no memory traffic).
+// four pairs) per thread and vector.  MODE 0 (dot-product kernel): quad c of row m at
+// xs + m row_dw + 4 q2k_lds_quad(c), and the 16-element sums into ss [M][K / 16].
+// MODE 1 (MFMA kernel): quad c at 4 c, no sums.  Rounds of kQ2kStageU vectors per
+// thread, all requested before any is used (a loop of one load each waited a full
+// round trip per vector: M = 4 at K = 11008 is 22 vectors per thread).  Vectors past
+// the end read zeros through a bounded descriptor (no memory traffic).
 template <int TH, int MODE>
 __device__ __forceinline__ void q2k_stage_x(const f16* x, int M, int K, uint32_t* xs, int row_dw, float* ss,
                                             int tid) {
@@ -171,48 +168,47 @@ __device__ __forceinline__ void q2k_stage_x(const f16* x, int M, int K, uint32_t
       p[2] = (a[2] & 0xFFFFu) | (a[3] << 16);
       p[3] = (a[2] >> 16) | (a[3] & 0xFFFF0000u);
       float s = 0.f;
+      if (MODE == 0) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f16x2 hv = as_h2(a[q]);
-        s = add_rn(s, add_rn(h2f(hv.x), h2f(hv.y)));
+        for (int q = 0; q < 4; ++q) {
+          const f16x2 hv = as_h2(a[q]);
+          s = add_rn(s, add_rn(h2f(hv.x), h2f(hv.y)));
+        }
+        s = add_rn(s, dpp_move<0xB1>(s));  // elements 16(c/2) .. +15: the pair (c, c ^ 1)
       }
-      s = add_rn(s, dpp_move<0xB1>(s));  // elements 16(c/2) .. +15: the pair (c, c ^ 1)
       if (v < nvec) {
         *reinterpret_cast<u32x4*>(xs + (size_t)m * row_dw + 4 * (MODE == 0 ? q2k_lds_quad(c) : c)) = p;
-        const int sb = c / 2;  // sub-block of the row
-        const int pos = MODE == 0 ? sb : (sb & ~15) | (sb & 8) | ((sb & 1) << 2) | ((sb >> 1) & 3);
-        if ((c & 1) == 0) ss[(size_t)m * (K / 16) + pos] = s;
+        if (MODE == 0 && (c & 1) == 0) ss[(size_t)m * (K / 16) + c / 2] = s;
       }
     }
   }
 }
 
-// Two to four tokens on MFMA: the codes of each weight are expanded once and the tokens
-// are the A rows 0..M-1 of v_mfma_f32_16x16x32_f16, so the VALU work per weight does
-// not grow with the token count (the dot-product kernel below spends two
+// Two to sixteen tokens per launch on MFMA: the codes of each weight are expanded once
+// and the tokens are the A rows of v_mfma_f32_16x16x32_f16, so the VALU work per
+// weight does not grow with the token count (the dot-product kernel below spends two
 // v_dot2_f32_f16 per four weights and token).  A workgroup owns 16 weight rows, the B
 // columns: lane l takes row n = l & 15 and block part t = l >> 4 (half h = t / 2 and
 // the 16-byte run hx = t % 2 of the codes, as in the dot-product kernel), which is
 // also the MFMA k-group of 8 values that the lane supplies.  Its W waves take blocks
-// w, w + W, ... and add their partial products through LDS at the end.
+// w, w + W, ... and add their partial products through LDS at the end.  Lane l holds
+// C rows 4 (l / 16) .. + 3, the tokens of those numbers, for row n.
 // The product is exact up to fp32 accumulation, as in the dot-product kernel: B holds
 // the integer sc q, made from the exact halves 64 + q 4^j / 16 of the exponent OR by
-// one fp16 fma with sc 16 / 4^j and -64 sc 16 / 4^j (both exact); the
-// MFMA chain of one block is scaled by the block's d in fp32, and the min term
-// dmin sum_s m_s S_s comes from the staged sub-block sums S.  The x rows are staged
-// with 16 bytes of padding, so the M active lanes of an A read hit distinct banks.
-template <int M, int W>
-__global__ void __launch_bounds__(W * 64) q2k_mfma_kernel(const f16* __restrict__ x, int K, int N,
+// one fp16 fma with sc 16 / 4^j and -64 sc 16 / 4^j (both exact), and a second chain
+// multiplies the same A by the sub-block's min code m (sum_k x_k m = sum_s m_s S_s);
+// the two chains of a block are scaled by its d and dmin in fp32.  The x rows are
+// staged with 16 bytes of padding, so the A reads of 16 token rows hit distinct banks.
+template <int W>
+__global__ void __launch_bounds__(W * 64) q2k_mfma_kernel(const f16* __restrict__ x, int M, int K, int N,
                                                           const uint8_t* __restrict__ wq, size_t w_bytes,
                                                           const f16* __restrict__ bias, f16* __restrict__ y) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int row_dw = K / 2 + 4;
-  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);                 // [M][row_dw] pairs
-  float* ss = reinterpret_cast<float*>(xs + (size_t)M * row_dw);   // [M][K / 16] sums (MODE 1 order)
-  float* red = ss + (size_t)M * (K / 16);                           // [W][M][16] partial sums
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);  // [M][row_dw] pairs
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int NB = K / 256;
   const int n = lane & 15, t = lane >> 4, h = t >> 1, hx = t & 1;
   const int row = blockIdx.x * 16 + n;
@@ -229,32 +225,29 @@ __global__ void __launch_bounds__(W * 64) q2k_mfma_kernel(const f16* __restrict_
     dd = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 80 : kOOB, 0, 0);
   };
   load(wave);  // the first block's codes before the staging (loads complete in issue order)
-  q2k_stage_x<W * 64, 1>(x, M, K, xs, row_dw, ss, tid);
+  q2k_stage_x<W * 64, 1>(x, M, K, xs, row_dw, nullptr, tid);
   __syncthreads();
 
   // A row n: token n; rows past M repeat token M - 1 and only reach C rows never stored.
   const uint32_t* xa = xs + (size_t)min(n, M - 1) * row_dw;
-  f32x4 tot = {0.f, 0.f, 0.f, 0.f};  // d-scaled code products (C rows 4 t .. 4 t + 3)
-  float mins[M];                     // dmin m S of this lane's sub-blocks, token m
-#pragma unroll
-  for (int m = 0; m < M; ++m) mins[m] = 0.f;
+  f32x4 tot = {0.f, 0.f, 0.f, 0.f};
   for (int b = wave; b < NB; b += W) {
     const u32x4 c0 = cw;
     const u32x2 s0 = sc;
     const f16x2 dm = as_h2(dd);
     if (b + W < NB) load(b + W);
     const int q0 = 32 * b + 16 * h + 2 * hx;  // quad of element 256 b + 128 h + 16 hx
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float mq[4];  // min codes of this lane's sub-blocks j
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accm = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // scale byte of sub-block 8 h + 2 j + hx: byte 2 j + hx of the half's eight
       const uint32_t sbyte = (s0[j >> 1] >> (16 * (j & 1) + 8 * hx)) & 0xFFu;
-      mq[j] = (float)(sbyte >> 4);
       // sc 16 / 4^j and -64 sc 16 / 4^j, both exact in fp16: (v - 64) sc 16 / 4^j = sc q
       const f16 scf = (f16)((float)(sbyte & 15u) * (16.f / (float)(1 << (2 * j))));
       const f16x2 sv = {scf, scf};
       const f16x2 ov = -(f16x2){(f16)64.f, (f16)64.f} * sv;
+      const f16 mf = (f16)(float)(sbyte >> 4);
+      const f16x8 Bm = {mf, mf, mf, mf, mf, mf, mf, mf};
       const uint32_t mask = 0x00030003u << (2 * j);
 #pragma unroll
       for (int gp = 0; gp < 2; ++gp) {
@@ -275,37 +268,23 @@ __global__ void __launch_bounds__(W * 64) q2k_mfma_kernel(const f16* __restrict_
         }
         const f16x8 A = *reinterpret_cast<const f16x8*>(xa + 4 * (q0 + 4 * j + gp));
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc, 0, 0, 0);
+        accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bm, accm, 0, 0, 0);
       }
     }
     const float d = h2f(dm.x), dmin = h2f(dm.y);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tot[i] = __builtin_fmaf(d, acc[i], tot[i]);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const f32x4 s4 = *reinterpret_cast<const f32x4*>(ss + (size_t)m * (K / 16) + 16 * b + 8 * h + 4 * hx);
-      float p = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) p = __builtin_fmaf(mq[j], s4[j], p);
-      mins[m] = __builtin_fmaf(dmin, p, mins[m]);
-    }
+    for (int i = 0; i < 4; ++i) tot[i] = __builtin_fmaf(d, acc[i], __builtin_fmaf(-dmin, accm[i], tot[i]));
   }
-  // The min terms of row n sit in lanes n, n + 16, n + 32, n + 48; the code products
-  // of its tokens 0..3 in lane n (C row 4 (l / 16) + i, column l % 16 in lane l).
+  __syncthreads();  // every wave is done with the staged rows, which the partial sums reuse
+  float* red = reinterpret_cast<float*>(smem);  // [W][16 tokens][16 rows]
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    mins[m] += __shfl_xor(mins[m], 16, 64);
-    mins[m] += __shfl_xor(mins[m], 32, 64);
-  }
-  if (lane < 16) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) red[(wave * M + m) * 16 + lane] = tot[m] - mins[m];
-  }
+  for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * t + i) * 16 + n] = tot[i];
   __syncthreads();
   if (tid < 16 * M) {
     const int m = tid >> 4, nn = tid & 15;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) v = add_rn(v, red[(w * M + m) * 16 + nn]);
+    for (int w = 0; w < W; ++w) v = add_rn(v, red[(w * 16 + m) * 16 + nn]);
     const int r = blockIdx.x * 16 + nn;
     if (r < N) {
       if (bias != nullptr) v = add_rn(v, h2f(bias[r]));
@@ -455,23 +434,32 @@ int q2k_launch_mr(const f16* x, int K, int N, const uint8_t* w, const f16* bias,
   return 0;
 }
 
-template <int M, int W>
-int q2k_mfma_launch_w(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
-  const size_t smem = (size_t)M * (K / 2 + 4) * sizeof(uint32_t) + (size_t)M * (K / 16) * sizeof(float) +
-                      (size_t)W * M * 16 * sizeof(float);
-  if (smem > 160 * 1024) {
-    axm_set_error("qmv_q2_k_gguf: K=%d with %d rows needs %zu B of LDS", K, M, smem);
-    return -2;
-  }
-  if (smem > 64 * 1024 && hipFuncSetAttribute((const void*)q2k_mfma_kernel<M, W>,
+// LDS bytes of q2k_mfma_kernel for M tokens: padded pair rows, reused at the end for
+// the waves' partial sums.
+size_t q2k_mfma_smem(int M, int K, int W) {
+  const size_t staged = (size_t)M * (K / 2 + 4) * sizeof(uint32_t);
+  const size_t partial = (size_t)W * 16 * 16 * sizeof(float);
+  return staged > partial ? staged : partial;
+}
+
+// Tokens per q2k_mfma_kernel launch at this K: as many as LDS holds, up to 16.
+int q2k_mfma_max_tokens(int K) {
+  const int m = (int)((size_t)160 * 1024 / ((size_t)(K / 2 + 4) * sizeof(uint32_t)));
+  return m < 16 ? m : 16;
+}
+
+template <int W>
+int q2k_mfma_launch_w(const f16* x, int M, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
+  const size_t smem = q2k_mfma_smem(M, K, W);
+  if (smem > 64 * 1024 && hipFuncSetAttribute((const void*)q2k_mfma_kernel<W>,
                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess) {
     (void)hipGetLastError();
     axm_set_error("qmv_q2_k_gguf: cannot reserve %zu B of LDS", smem);
     return -2;
   }
   const size_t w_bytes = (size_t)N * (K / 256) * kQ2kBlockBytes;
-  hipLaunchKernelGGL((q2k_mfma_kernel<M, W>), dim3((N + 15) / 16), dim3(W * 64), smem, st, x, K, N, w, w_bytes,
-                     bias, y);
+  hipLaunchKernelGGL((q2k_mfma_kernel<W>), dim3((N + 15) / 16), dim3(W * 64), smem, st, x, M, K, N, w, w_bytes, bias,
+                     y);
   return 0;
 }
 
@@ -480,11 +468,10 @@ int q2k_mfma_launch_w(const f16* x, int K, int N, const uint8_t* w, const f16* b
 // 11.3 us with four waves, 11.4 with eight, 12.2 with sixteen; 11008 -> 4096, 256
 // workgroups, 10.7 with four or eight, 10.3 with sixteen).  One token stays on the
 // dot-product kernel (the MFMA form: 8.7 / 8.0 against 8.4 / 7.8 us).
-template <int M>
-int q2k_mfma_launch(const f16* x, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
+int q2k_mfma_launch(const f16* x, int M, int K, int N, const uint8_t* w, const f16* bias, f16* y, hipStream_t st) {
   const long groups = (N + 15) / 16;
-  if (groups >= 2L * axm_num_cus()) return q2k_mfma_launch_w<M, 4>(x, K, N, w, bias, y, st);
-  return q2k_mfma_launch_w<M, 16>(x, K, N, w, bias, y, st);
+  if (groups >= 2L * axm_num_cus()) return q2k_mfma_launch_w<4>(x, M, K, N, w, bias, y, st);
+  return q2k_mfma_launch_w<16>(x, M, K, N, w, bias, y, st);
 }
 
 // One token: the dot-product kernel with two rows per wave while the grid keeps at
@@ -523,18 +510,19 @@ extern "C" int axm_qmv_q2_k_gguf(const void* x, const void* blocks, const void* 
   AXM_CHECK_ARG((size_t)N * (K / 256) * kQ2kBlockBytes < (size_t)0x7FFFFFF0, -1,
                 "qmv_q2_k_gguf: weight tensor above 2 GiB");
   hipStream_t st = (hipStream_t)stream;
-  for (int m0 = 0; m0 < M; m0 += 4) {
-    const int mc = (M - m0) < 4 ? (M - m0) : 4;
+  // MFMA launches of up to q2k_mfma_max_tokens(K) tokens (16 at K <= 4096, 4 at the
+  // largest K) while at least two remain, the dot-product kernel for a single token.
+  const int mt = q2k_mfma_max_tokens(K);
+  int m0 = 0;
+  while (m0 < M) {
+    const int left = M - m0;
+    const int mc = left < 2 ? 1 : (left < mt ? left : mt);
     const f16* xm = (const f16*)x + (size_t)m0 * K;
     f16* ym = (f16*)y + (size_t)m0 * N;
-    int rc;
-    switch (mc) {
-      case 1: rc = q2k_launch1(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
-      case 2: rc = q2k_mfma_launch<2>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
-      case 3: rc = q2k_mfma_launch<3>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
-      default: rc = q2k_mfma_launch<4>(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st); break;
-    }
+    const int rc = mc == 1 ? q2k_launch1(xm, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st)
+                           : q2k_mfma_launch(xm, mc, K, N, (const uint8_t*)blocks, (const f16*)bias, ym, st);
     if (rc) return rc;
+    m0 += mc;
   }
   AXM_LAUNCH_CHECK("qmv_q2_k_gguf");
   return 0;

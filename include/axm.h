@@ -133,7 +133,7 @@ int axm_pack_q2_k_gguf(const void* w, int src_is_fp16, int N, int K, void* block
 /* blocks -> fp16 [N][K], fp32 arithmetic, one rounding. */
 int axm_dequantize_q2_k_gguf(const void* blocks, int N, int K, void* out, void* stream);
 /* y = x W^T (+ bias), x fp16 [M][K], y fp16 [M][N], fp32 accumulation; K <= 16384.  Exact code
- * products: one token on v_dot2_f32_f16, two to four per launch on MFMA. */
+ * products: one token on v_dot2_f32_f16, two to sixteen per launch on MFMA. */
 int axm_qmv_q2_k_gguf(const void* x, const void* blocks, const void* bias, void* y, int M, int K, int N,
                       void* stream);
 

@@ -59,7 +59,9 @@ def _check_gemv(dev, M, N, K, bias, w=None, seed=0):
 @pytest.mark.parametrize("M,N,K,bias", [(1, 11008, 4096, False), (1, 4096, 11008, False), (1, 13, 256, True),
                                         (2, 300, 768, False), (3, 129, 4096, True), (4, 4096, 4096, False),
                                         (5, 200, 1024, False), (4, 64, 16384, False), (1, 32000, 4096, False),
-                                        (2, 13, 256, True), (4, 40, 512, False)])
+                                        (2, 13, 256, True), (4, 40, 512, False),
+                                        # 8 and 16 tokens per launch; 7 + 2 at K = 11008 (LDS holds seven rows)
+                                        (8, 300, 4096, True), (16, 100, 2048, False), (9, 64, 11008, False)])
 def test_q2k_gemv_matches_oracle(dev, M, N, K, bias):
     print(f"[q2k_gemv] M={M} N={N} K={K} bias={bias}", flush=True)
     _check_gemv(dev, M, N, K, bias, seed=M * 31 + N)
@@ -72,16 +74,17 @@ def _ulps(a, b):
     return np.where((ua >> 15) == (ub >> 15), np.abs(ma - mb), ma + mb)
 
 
-@pytest.mark.parametrize("M,N,K", [(4, 11008, 4096), (4, 4096, 11008), (2, 300, 768), (3, 64, 16384)])
+@pytest.mark.parametrize("M,N,K", [(4, 11008, 4096), (4, 4096, 11008), (2, 300, 768), (3, 64, 16384),
+                                   (16, 512, 4096)])
 def test_q2k_gemv_rounding(dev, M, N, K):
-    """Two to four tokens run the MFMA kernel, which multiplies the exact code products
-    sc q and applies d and the min term in fp32: at least 99 % of its outputs are the
-    fp16 rounding of the float64 product and the rest one ulp away (at the C4 shapes
-    99.8-99.9 %; a kernel that rounded each dequantized weight to fp16 gets about 58 % at
-    4096 x 2048, a plant on the CPU).  The one-token dot-product kernel is checked on
-    the same rows at its own bar: its per-sub-block sum acc - 64 S cancels a term of
-    about 64 |S| in fp32, so about 88 % of its outputs are correctly rounded and the
-    rest one ulp or up to 2e-4 (at K = 4096) away."""
+    """Two to sixteen tokens per launch run the MFMA kernel, which multiplies the exact
+    code products sc q and the min codes and applies d and dmin in fp32: at least 99 %
+    of its outputs are the fp16 rounding of the float64 product and the rest one ulp
+    away (at the C4 shapes 99.8-99.9 %; a kernel that rounded each dequantized weight to
+    fp16 gets about 58 % at 4096 x 2048, a plant on the CPU).  The one-token
+    dot-product kernel is checked on the same rows at its own bar: its per-sub-block
+    sum acc - 64 S cancels a term of about 64 |S| in fp32, so about 88 % of its outputs
+    are correctly rounded and the rest one ulp or up to 2e-4 (at K = 4096) away."""
     from axiomlm_amd.kernels import qmv_q2_k_gguf
 
     print(f"[q2k_rounding] M={M} N={N} K={K}", flush=True)
