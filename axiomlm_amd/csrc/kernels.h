@@ -27,6 +27,13 @@ int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, 
                     float eps, hipStream_t s);
 int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
                    const f16* ln_w, float eps, hipStream_t s);
+// The same GEMV with the residual add fused (resid[m][n] = fp16(resid + fp16(acc)), in
+// place) or with SwiGLU over a [W_gate; W_up] matrix of N2 rows (y [M][N2 / 2]), each
+// with the rounding of the GEMV followed by launch_resid_add / launch_swiglu.
+int launch_q8_gemv_resid(const f16* x, const uint8_t* w, const f16* sb, f16* resid, int M, int K, int N,
+                         const f16* ln_w, float eps, hipStream_t s);
+int launch_q8_gemv_swiglu(const f16* x, const uint8_t* w, const f16* sb, f16* y, int M, int K, int N2,
+                          const f16* ln_w, float eps, hipStream_t s);
 
 // ---- KV cache ---------------------------------------------------------------
 #include "axm.h"  // AXM_KV_* codes

@@ -29,19 +29,52 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
-template <int M, int R>
+// Epilogues: kQ8Store y = fp16(acc) (+ bias, fp16 add); kQ8Resid: resid = fp16(resid +
+// fp16(acc)) in place (the residual stream); kQ8Swiglu: y[c] = fp16(fp16(silu(g)) * u)
+// with g, u = fp16(acc) of rows c and H + c of the [W_gate; W_up] matrix (N = 2 H).  The
+// rounding is that of the GEMV followed by resid_add_kernel / swiglu_kernel.
+enum { kQ8Store = 0, kQ8Resid = 1, kQ8Swiglu = 2 };
+// Activation vectors (8 values) per thread kept in registers across the RMSNorm
+// reduction, so that the normed prologue reads x once.
+constexpr int kQ8vRegVec = 8;
+
+template <int M, int R, int EPI>
 __global__ void __launch_bounds__(kQ8vThreads)
     q8v_kernel(const f16* __restrict__ x, int K, int N, const uint8_t* __restrict__ w, const f16* __restrict__ sb,
                const f16* __restrict__ bias, f16* __restrict__ y, const f16* __restrict__ ln_w, float eps) {
   extern __shared__ __align__(16) unsigned char smem[];
   f16* xs = reinterpret_cast<f16*>(smem);                       // [M][K]
   float* s16 = reinterpret_cast<float*>(xs + (size_t)M * K);    // [M][K / 16]
-  __shared__ float red[kQ8vWaves];
+  __shared__ float red[kQ8vWaves][M];
   __shared__ float rinv_m[M];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nvec = M * K / 8;  // 8-value vectors of x
+  const f16x8* x8 = reinterpret_cast<const f16x8*>(x);
+  const bool one_pass = nvec <= kQ8vRegVec * kQ8vThreads;
 
-  // Codes and (scale, bias) of step 0, requested before the staging.
-  const int row0 = (blockIdx.x * kQ8vWaves + wave) * R;
+  // Rows of this wave: R consecutive rows, or for SwiGLU R / 2 output columns c, each
+  // with its gate row c and up row H + c.
+  const int H = N / 2;
+  const int wrow = blockIdx.x * kQ8vWaves + wave;
+  auto row_of = [&](int i) {
+    if (EPI == kQ8Swiglu) {
+      const int c = wrow * (R / 2) + (i % (R / 2));
+      return c < H ? (i < R / 2 ? c : H + c) : N;
+    }
+    return wrow * R + i;
+  };
+
+  // The activation vectors first (loads complete in issue order: the norm then waits
+  // for them only), then the codes and (scale, bias) of step 0.
+  f16x8 xv[kQ8vRegVec];
+  if (one_pass) {
+#pragma unroll
+    for (int i = 0; i < kQ8vRegVec; ++i) {
+      const int v = tid + i * kQ8vThreads;
+      xv[i] = v < nvec ? x8[v] : f16x8{};
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, N * K, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)sb, (short)0, N * (K / 64) * 4, 0x00020000);
@@ -52,7 +85,7 @@ __global__ void __launch_bounds__(kQ8vThreads)
     const int k0 = 1024 * s + 16 * lane;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const int row = row0 + i;
+      const int row = row_of(i);
       const bool ok = row < N && k0 < K;
       cw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * K + k0 : kOOB, 0, 0));
       sv[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (row * (K / 64) + k0 / 64) * 4 : kOOB, 0, 0);
@@ -60,42 +93,97 @@ __global__ void __launch_bounds__(kQ8vThreads)
   };
   load(0);
 
-  // RMSNorm scale per token (fp16 op order of the other normed GEMVs).
-  if (ln_w != nullptr) {
-    for (int m = 0; m < M; ++m) {
-      float s = 0.f;
-      for (int k = tid; k < K; k += kQ8vThreads) {
-        const float v = h2f(x[(size_t)m * K + k]);
-        s += h2f(f2h(v * v));
-      }
-      s = wave_sum(s);
-      if (lane == 0) red[wave] = s;
-      __syncthreads();
-      if (tid == 0) {
-        float t = 0.f;
-#pragma unroll
-        for (int i = 0; i < kQ8vWaves; ++i) t += red[i];
-        rinv_m[m] = rms_inv_fp16(t, K, eps);
-      }
-      __syncthreads();
-    }
-  }
-  // Stage x (fp16) and the 16-element sums: thread -> 8 consecutive elements.
-  for (int v = tid; v < M * K / 8; v += kQ8vThreads) {
+  // Stage vector v (normalized when ln_w is set) and its share of the 16-element sums:
+  // vectors c and c ^ 1 of a row are adjacent threads (K / 8 is even).  Every lane of
+  // the wave takes part in the sum's lane swap; lanes past the last vector (both of a
+  // pair, nvec being even) store nothing.
+  auto stage = [&](int v, f16x8 h) {
+    const bool valid = v < nvec;
+    if (!valid) v = nvec - 1;
     const int m = v / (K / 8), c = v % (K / 8);
-    f16x8 h = *reinterpret_cast<const f16x8*>(x + (size_t)m * K + 8 * c);
     if (ln_w != nullptr) {
       const f16x8 lw = *reinterpret_cast<const f16x8*>(ln_w + 8 * c);
       const float ri = rinv_m[m];
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(f2h(h2f(h[e]) * ri)) * h2f(lw[e]));
     }
-    *reinterpret_cast<f16x8*>(xs + (size_t)m * K + 8 * c) = h;
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) s = add_rn(s, h2f(h[e]));
-    s = add_rn(s, __shfl_xor(s, 1, 64));  // c and c ^ 1 are adjacent lanes (K / 8 is even)
-    if ((c & 1) == 0) s16[(size_t)m * (K / 16) + c / 2] = s;
+    s = add_rn(s, __shfl_xor(s, 1, 64));
+    if (valid) {
+      *reinterpret_cast<f16x8*>(xs + (size_t)m * K + 8 * c) = h;
+      if ((c & 1) == 0) s16[(size_t)m * (K / 16) + c / 2] = s;
+    }
+  };
+
+  if (one_pass) {
+    if (ln_w != nullptr) {
+      // RMSNorm scale per token from the vectors in registers (fp16-rounded squares
+      // summed in fp32, the mean rounded to fp16 as in the other normed GEMVs).
+      float ssq[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) ssq[m] = 0.f;
+#pragma unroll
+      for (int i = 0; i < kQ8vRegVec; ++i) {
+        const int v = tid + i * kQ8vThreads;
+        if (v < nvec) {
+          float part = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float f = h2f(xv[i][e]);
+            part += h2f(f2h(f * f));
+          }
+          const int mv = v / (K / 8);
+#pragma unroll
+          for (int m = 0; m < M; ++m) ssq[m] += m == mv ? part : 0.f;
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float t = wave_sum(ssq[m]);
+        if (lane == 0) red[wave][m] = t;
+      }
+      __syncthreads();
+      if (tid < M) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < kQ8vWaves; ++i) t += red[i][tid];
+        rinv_m[tid] = rms_inv_fp16(t, K, eps);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kQ8vRegVec; ++i) {
+      const int v = tid + i * kQ8vThreads;
+      if (i * kQ8vThreads < nvec) stage(v, xv[i]);  // workgroup-uniform bound
+    }
+  } else {
+    // More activations than the registers hold: the norm scale from a strided pass over
+    // x, then a second pass that stages.
+    if (ln_w != nullptr) {
+      for (int m = 0; m < M; ++m) {
+        float sq = 0.f;
+        for (int k = tid; k < K; k += kQ8vThreads) {
+          const float v = h2f(x[(size_t)m * K + k]);
+          sq += h2f(f2h(v * v));
+        }
+        sq = wave_sum(sq);
+        if (lane == 0) red[wave][m] = sq;
+      }
+      __syncthreads();
+      if (tid < M) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < kQ8vWaves; ++i) t += red[i][tid];
+        rinv_m[tid] = rms_inv_fp16(t, K, eps);
+      }
+      __syncthreads();
+    }
+    for (int v0 = 0; v0 < nvec; v0 += kQ8vThreads) {
+      const int v = v0 + tid;
+      stage(v, v < nvec ? x8[v] : f16x8{});
+    }
   }
   __syncthreads();
 
@@ -133,9 +221,9 @@ __global__ void __launch_bounds__(kQ8vThreads)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const uint32_t cwd = c0[i][g];
-            const u32x4& xv = g < 2 ? xa[m] : xb[m];
-            acc = dot2(xv[2 * (g & 1)], q8_pair(cwd, kSelLo), acc);
-            acc = dot2(xv[2 * (g & 1) + 1], q8_pair(cwd, kSelHi), acc);
+            const u32x4& xq = g < 2 ? xa[m] : xb[m];
+            acc = dot2(xq[2 * (g & 1)], q8_pair(cwd, kSelLo), acc);
+            acc = dot2(xq[2 * (g & 1) + 1], q8_pair(cwd, kSelHi), acc);
           }
           r[i][m] += sc * (acc - 1024.f * sx[m]) + bi * sx[m];
         }
@@ -147,27 +235,45 @@ __global__ void __launch_bounds__(kQ8vThreads)
 #pragma unroll
     for (int m = 0; m < M; ++m) r[i][m] = wave_sum(r[i][m]);
   if (lane == 0) {
+    if (EPI == kQ8Swiglu) {
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const int row = row0 + i;
-      if (row >= N) continue;
+      for (int i = 0; i < R / 2; ++i) {
+        const int c = wrow * (R / 2) + i;
+        if (c >= H) continue;
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        f16 h = f2h(r[i][m]);
-        if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[row]));
-        y[(size_t)m * N + row] = h;
+        for (int m = 0; m < M; ++m) {
+          const float g = h2f(f2h(r[i][m]));
+          const f16 sg = f2h(g / (1.0f + expf(-g)));
+          y[(size_t)m * H + c] = f2h(h2f(sg) * h2f(f2h(r[R / 2 + i][m])));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int row = row_of(i);
+        if (row >= N) continue;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          f16 h = f2h(r[i][m]);
+          if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[row]));
+          f16* o = y + (size_t)m * N + row;
+          if (EPI == kQ8Resid)
+            *o = f2h(add_rn(h2f(*o), h2f(h)));
+          else
+            *o = h;
+        }
       }
     }
   }
 }
 
-template <int M, int R>
+template <int M, int R, int EPI>
 int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
                const f16* ln_w, float eps, hipStream_t s) {
   const size_t smem = (size_t)M * K * sizeof(f16) + (size_t)M * (K / 16) * sizeof(float);
   static bool attr_set = false;
   if (smem > 48 * 1024 && !attr_set) {
-    if (hipFuncSetAttribute((const void*)q8v_kernel<M, R>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void*)q8v_kernel<M, R, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             150 * 1024) != hipSuccess) {
       (void)hipGetLastError();
       axm_set_error("q8 gemv: cannot reserve %zu bytes of LDS", smem);
@@ -176,27 +282,30 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
     attr_set = true;
   }
   const int rows = kQ8vWaves * R;
-  hipLaunchKernelGGL((q8v_kernel<M, R>), dim3((N + rows - 1) / rows), dim3(kQ8vThreads), smem, s, x, K, N, w, sb,
-                     bias, y, ln_w, eps);
+  const int units = EPI == kQ8Swiglu ? N / 2 : N;   // output columns
+  const int per_wg = EPI == kQ8Swiglu ? rows / 2 : rows;
+  hipLaunchKernelGGL((q8v_kernel<M, R, EPI>), dim3((units + per_wg - 1) / per_wg), dim3(kQ8vThreads), smem, s, x, K,
+                     N, w, sb, bias, y, ln_w, eps);
   return 0;
 }
 
-// Rows per wave: four while that leaves two workgroups per CU, else two, else one.
-template <int M>
+// Rows per wave: four while that leaves two workgroups per CU, else two, else one (two
+// at least for SwiGLU, whose waves take gate / up row pairs).
+template <int M, int EPI>
 int q8v_launch_m(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
                  const f16* ln_w, float eps, hipStream_t s) {
   const int cus = axm_num_cus();
-  if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4>(x, w, sb, bias, y, K, N, ln_w, eps, s);
-  if (N >= cus * kQ8vWaves * 2) return q8v_launch<M, 2>(x, w, sb, bias, y, K, N, ln_w, eps, s);
-  return q8v_launch<M, 1>(x, w, sb, bias, y, K, N, ln_w, eps, s);
+  if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
+  if (EPI == kQ8Swiglu || N >= cus * kQ8vWaves * 2)
+    return q8v_launch<M, 2, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
+  return q8v_launch<M, (EPI == kQ8Swiglu ? 2 : 1), EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
 }
 
-}  // namespace
-
-int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
-                   const f16* ln_w, float eps, hipStream_t s) {
-  if (K % 64 != 0 || (long)N * K >= 0x7FFFFFF0L) {
-    axm_set_error("q8 gemv: K=%d must be a multiple of 64 and the codes under 2 GiB (N=%d)", K, N);
+template <int EPI>
+int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
+             const f16* ln_w, float eps, hipStream_t s) {
+  if (K % 64 != 0 || (long)N * K >= 0x7FFFFFF0L || (EPI == kQ8Swiglu && N % 2 != 0)) {
+    axm_set_error("q8 gemv: K=%d must be a multiple of 64, the codes under 2 GiB (N=%d), N even for SwiGLU", K, N);
     return -2;
   }
   // Up to four rows per launch, fewer when their LDS staging would not fit.
@@ -207,18 +316,36 @@ int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bia
     axm_set_error("q8 gemv: K=%d too large for LDS staging", K);
     return -2;
   }
+  const int ld_out = EPI == kQ8Swiglu ? N / 2 : N;
   for (int m0 = 0; m0 < M; m0 += rows_max) {
     const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
     const f16* xm = x + (size_t)m0 * K;
-    f16* ym = y + (size_t)m0 * N;
+    f16* ym = y + (size_t)m0 * ld_out;
     int rc;
     switch (mc) {
-      case 1: rc = q8v_launch_m<1>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
-      case 2: rc = q8v_launch_m<2>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
-      case 3: rc = q8v_launch_m<3>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
-      default: rc = q8v_launch_m<4>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
+      case 1: rc = q8v_launch_m<1, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
+      case 2: rc = q8v_launch_m<2, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
+      case 3: rc = q8v_launch_m<3, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
+      default: rc = q8v_launch_m<4, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
     }
     if (rc) return rc;
   }
   return 0;
+}
+
+}  // namespace
+
+int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
+                   const f16* ln_w, float eps, hipStream_t s) {
+  return q8v_rows<kQ8Store>(x, w, sb, bias, y, M, K, N, ln_w, eps, s);
+}
+
+int launch_q8_gemv_resid(const f16* x, const uint8_t* w, const f16* sb, f16* resid, int M, int K, int N,
+                         const f16* ln_w, float eps, hipStream_t s) {
+  return q8v_rows<kQ8Resid>(x, w, sb, nullptr, resid, M, K, N, ln_w, eps, s);
+}
+
+int launch_q8_gemv_swiglu(const f16* x, const uint8_t* w, const f16* sb, f16* y, int M, int K, int N2,
+                          const f16* ln_w, float eps, hipStream_t s) {
+  return q8v_rows<kQ8Swiglu>(x, w, sb, nullptr, y, M, K, N2, ln_w, eps, s);
 }

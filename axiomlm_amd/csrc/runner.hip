@@ -631,10 +631,11 @@ struct axm_runner {
     return launch_q8_gemv(x, (const uint8_t*)m.w, (const f16*)m.sb, bias, y, M, m.K, N, ln, eps, s);
   }
 
-  // A Q8_G64 or fp16 matrix: its GEMV (RMSNorm prologue, bias) followed by the
-  // epilogue as separate launches with the rounding of the fused epilogues
-  // (residual add in fp16, silu(fp16 g) * fp16 u).  Activation and output rows
-  // are contiguous ([M][K] in, [M][N] out), as every caller lays them out.
+  // A Q8_G64 or fp16 matrix: its GEMV (RMSNorm prologue, bias) with the residual /
+  // SwiGLU epilogue fused for Q8_G64 and as separate launches for fp16, with the
+  // rounding of the tile16 epilogues (residual add in fp16, silu(fp16 g) * fp16 u).
+  // Activation and output rows are contiguous ([M][K] in, [M][N] out), as every
+  // caller lays them out.
   int run_dense(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
     if (c.x_parts != nullptr || c.argmax_keys != nullptr || epi == Q4_EPI_QKV_ROPE || c.ldx != m.K) {
       axm_set_error("runner: unsupported call on a Q8_G64 / fp16 matrix (epilogue %d)", epi);
@@ -660,6 +661,9 @@ struct axm_runner {
         axm_set_error("runner: a Q8 SwiGLU needs contiguous output rows");
         return -2;
       }
+      if (m.fmt == 1)
+        return launch_q8_gemv_swiglu(xin, (const uint8_t*)m.w, (const f16*)m.sb, c.y, M, m.K, 2 * out_rows, ln,
+                                     c.eps, s);
       rc = dense_gemv(m, xin, nullptr, q8tmp, M, 2 * out_rows, ln, c.eps, s);
       if (rc) return rc;
       return launch_swiglu(q8tmp, c.y, M, out_rows, s);
@@ -669,9 +673,13 @@ struct axm_runner {
       axm_set_error("runner: a Q8 residual needs contiguous rows");
       return -2;
     }
-    rc = dense_gemv(m, xin, nullptr, q8tmp, M, out_rows, ln, c.eps, s);
+    if (m.fmt == 1) {
+      rc = launch_q8_gemv_resid(xin, (const uint8_t*)m.w, (const f16*)m.sb, c.resid, M, m.K, out_rows, ln, c.eps, s);
+    } else {
+      rc = dense_gemv(m, xin, nullptr, q8tmp, M, out_rows, ln, c.eps, s);
+      if (rc == 0) launch_resid_add(c.resid, q8tmp, (long)M * out_rows, s);
+    }
     if (rc) return rc;
-    launch_resid_add(c.resid, q8tmp, (long)M * out_rows, s);
     if (c.post_ln_w != nullptr) launch_rmsnorm(c.resid, c.post_ln_w, c.post_norm_out, M, out_rows, c.eps, s);
     return 0;
   }
