@@ -201,9 +201,14 @@ constexpr int kQ8Threads = 256;
 
 // fp16 GEMV (the dense layers of the fp16 decode runner):  y[n] = sum_k w[n][k] x[k].
 // Activations (optionally RMS-normalized with the fp16 op order of the quantized
-// paths) are staged in LDS as fp16 pairs; one wave per output row per iteration,
-// each lane streaming 16 bytes (8 weights) per step into v_dot2_f32_f16 with fp32
-// accumulation.
+// paths) are staged in LDS as fp16 pairs; one wave per output per iteration, each
+// lane streaming 16 bytes (8 weights) per step into v_dot2_f32_f16 with fp32
+// accumulation.  Epilogues (kF16Store / kF16Resid / kF16Swiglu) as those of the Q8_G64
+// GEMV: y = fp16(acc) (+ bias); resid = fp16(resid + fp16(acc)) in place; or, over a
+// [W_gate; W_up] matrix of N = 2 H rows, y[c] = fp16(fp16(silu(g)) * u) with g, u the
+// fp16 outputs of rows c and H + c, which one wave computes together.
+enum { kF16Store = 0, kF16Resid = 1, kF16Swiglu = 2 };
+template <int EPI>
 __global__ void __launch_bounds__(kQ8Threads)
     f16_gemv_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f16* __restrict__ bias,
                     f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w, float eps) {
@@ -230,36 +235,53 @@ __global__ void __launch_bounds__(kQ8Threads)
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n_waves_total = gridDim.x * (kQ8Threads / 64);
-  for (int n = blockIdx.x * (kQ8Threads / 64) + wave; n < N; n += n_waves_total) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int outs = EPI == kF16Swiglu ? N / 2 : N;
+  for (int n = blockIdx.x * (kQ8Threads / 64) + wave; n < outs; n += n_waves_total) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, accu[4] = {0.f, 0.f, 0.f, 0.f};
     const f16* wr = w + (size_t)n * K;
+    const f16* wu = w + (size_t)(n + outs) * K;  // the up row (SwiGLU)
     for (int k0 = lane * 8; k0 < K; k0 += 64 * 8) {
       const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + k0);
+      u32x4 uv = {0u, 0u, 0u, 0u};
+      if (EPI == kF16Swiglu) uv = *reinterpret_cast<const u32x4*>(wu + k0);
       for (int mi = 0; mi < M && mi < 4; ++mi) {
         const u32x4 xv = *reinterpret_cast<const u32x4*>(xh + (size_t)mi * K + k0);
         float d = acc[mi];
 #pragma unroll
         for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_fdot2(as_h2(xv[c]), as_h2(wv[c]), d, false);
         acc[mi] = d;
+        if (EPI == kF16Swiglu) {
+          float e = accu[mi];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) e = __builtin_amdgcn_fdot2(as_h2(xv[c]), as_h2(uv[c]), e, false);
+          accu[mi] = e;
+        }
       }
     }
     for (int mi = 0; mi < M && mi < 4; ++mi) {
       const float v = wave_sum(acc[mi]);
+      const float u = EPI == kF16Swiglu ? wave_sum(accu[mi]) : 0.f;
       if (lane == 0) {
-        f16 h = f2h(v);
-        if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[n]));
-        y[(size_t)mi * N + n] = h;
+        if (EPI == kF16Swiglu) {
+          const float g = h2f(f2h(v));
+          const f16 sg = f2h(g / (1.0f + expf(-g)));
+          y[(size_t)mi * outs + n] = f2h(h2f(sg) * h2f(f2h(u)));
+        } else {
+          f16 h = f2h(v);
+          if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[n]));
+          f16* o = y + (size_t)mi * N + n;
+          *o = EPI == kF16Resid ? f2h(add_rn(h2f(*o), h2f(h))) : h;
+        }
       }
     }
   }
 }
 
-}  // namespace
-
-int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
-                    float eps, hipStream_t s) {
-  if (K % 8 != 0) {
-    axm_set_error("f16 gemv: K=%d must be a multiple of 8", K);
+template <int EPI>
+int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
+                  float eps, hipStream_t s) {
+  if (K % 8 != 0 || (EPI == kF16Swiglu && N % 2 != 0)) {
+    axm_set_error("f16 gemv: K=%d must be a multiple of 8 (N=%d even for SwiGLU)", K, N);
     return -2;
   }
   int rows_max = 4;
@@ -268,13 +290,14 @@ int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, 
     axm_set_error("f16 gemv: K=%d too large for LDS staging", K);
     return -2;
   }
+  const int outs = EPI == kF16Swiglu ? N / 2 : N;
   for (int m0 = 0; m0 < M; m0 += rows_max) {
     const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
     const size_t smem = (size_t)mc * K * sizeof(f16);
     static size_t attr_bytes = 0;
     if (smem > 48 * 1024 && smem > attr_bytes) {
-      if (hipFuncSetAttribute((const void*)f16_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
-          hipSuccess) {
+      if (hipFuncSetAttribute((const void*)f16_gemv_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)smem) != hipSuccess) {
         (void)hipGetLastError();
         axm_set_error("f16 gemv: cannot reserve %zu bytes of LDS", smem);
         return -2;
@@ -282,13 +305,28 @@ int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, 
       attr_bytes = smem;
     }
     const int rows_per_block = kQ8Threads / 64;
-    int grid = (N + rows_per_block - 1) / rows_per_block;
+    int grid = (outs + rows_per_block - 1) / rows_per_block;
     const int cap = axm_num_cus() * 8;
     if (grid > cap) grid = cap;
-    hipLaunchKernelGGL(f16_gemv_kernel, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, bias,
-                       y + (size_t)m0 * N, mc, K, N, ln_w, eps);
+    hipLaunchKernelGGL(f16_gemv_kernel<EPI>, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, bias,
+                       y + (size_t)m0 * outs, mc, K, N, ln_w, eps);
   }
   return 0;
+}
+
+}  // namespace
+
+int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
+                    float eps, hipStream_t s) {
+  return f16_gemv_rows<kF16Store>(x, w, bias, y, M, K, N, ln_w, eps, s);
+}
+int launch_f16_gemv_resid(const f16* x, const f16* w, f16* resid, int M, int K, int N, const f16* ln_w, float eps,
+                          hipStream_t s) {
+  return f16_gemv_rows<kF16Resid>(x, w, nullptr, resid, M, K, N, ln_w, eps, s);
+}
+int launch_f16_gemv_swiglu(const f16* x, const f16* w, f16* y, int M, int K, int N2, const f16* ln_w, float eps,
+                           hipStream_t s) {
+  return f16_gemv_rows<kF16Swiglu>(x, w, nullptr, y, M, K, N2, ln_w, eps, s);
 }
 
 int launch_rmsnorm(const f16* x, const f16* w, f16* y, int rows, int D, float eps, hipStream_t s) {
@@ -304,18 +342,6 @@ int launch_add_rmsnorm(f16* x, const f16* r, const f16* w, f16* y, int rows, int
     hipLaunchKernelGGL(rmsnorm_vec_kernel<true>, dim3(rows), dim3(kNormThreads), 0, s, x, r, w, y, D, eps);
   else
     hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, x, r, w, y, D, eps);
-  return 0;
-}
-namespace {
-// x[i] = fp16(x[i] + y[i]): the residual add of a projection computed apart from its GEMV.
-__global__ void resid_add_kernel(f16* __restrict__ x, const f16* __restrict__ y, long n) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) x[i] = f2h(add_rn(h2f(x[i]), h2f(y[i])));
-}
-}  // namespace
-
-int launch_resid_add(f16* x, const f16* y, long n, hipStream_t s) {
-  hipLaunchKernelGGL(resid_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
   return 0;
 }
 int launch_swiglu(const f16* gu, f16* y, int rows, int H, hipStream_t s) {

@@ -32,7 +32,7 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // Epilogues: kQ8Store y = fp16(acc) (+ bias, fp16 add); kQ8Resid: resid = fp16(resid +
 // fp16(acc)) in place (the residual stream); kQ8Swiglu: y[c] = fp16(fp16(silu(g)) * u)
 // with g, u = fp16(acc) of rows c and H + c of the [W_gate; W_up] matrix (N = 2 H).  The
-// rounding is that of the GEMV followed by resid_add_kernel / swiglu_kernel.
+// rounding is that of the GEMV's fp16 output followed by an fp16 add / swiglu_kernel.
 enum { kQ8Store = 0, kQ8Resid = 1, kQ8Swiglu = 2 };
 // Activation vectors (8 values) per thread kept in registers across the RMSNorm
 // reduction, so that the normed prologue reads x once.
@@ -289,12 +289,20 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
   return 0;
 }
 
-// Rows per wave: four while that leaves two workgroups per CU, else two, else one (two
-// at least for SwiGLU, whose waves take gate / up row pairs).
+// Rows per wave: for one token eight when four would need more than one round of
+// workgroups (the one-token four-row kernel holds 81-84 VGPRs, five waves per SIMD:
+// 7B gate / up has 1376 workgroups of four-row waves for 1280 slots; the eight-row one
+// 124, four waves; mode q8 432.5 -> 440 tok/s), four while that leaves two workgroups
+// per CU, else two, else one (two at least for SwiGLU, whose waves take gate / up row
+// pairs).  A two-step prefetch ring (three register slots, the step loop unrolled by
+// three) was measured and not kept: q4_k_m 659.6 -> 663 tok/s, q8 439 -> 435.
 template <int M, int EPI>
 int q8v_launch_m(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
                  const f16* ln_w, float eps, hipStream_t s) {
   const int cus = axm_num_cus();
+  if constexpr (M == 1) {
+    if (N > 5 * cus * kQ8vWaves * 4) return q8v_launch<M, 8, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
+  }
   if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
   if (EPI == kQ8Swiglu || N >= cus * kQ8vWaves * 2)
     return q8v_launch<M, 2, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);

@@ -300,7 +300,6 @@ struct axm_runner {
   f16* logits = nullptr;
   f16* norm = nullptr;
   f16* qkvbuf = nullptr;                 // [T][qkv_dim] (multi-token paths)
-  f16* q8tmp = nullptr;                  // [T][max(D, 2H)] outputs of Q8_G64 GEMVs before their epilogue
   int* tree_pos = nullptr;               // [kMaxVerify]
   unsigned long long* tree_mask = nullptr;  // [kMaxVerify]
   float* ws = nullptr;
@@ -332,7 +331,7 @@ struct axm_runner {
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
     void* bufs[] = {params, x, q, kvst, attn_y, hbuf, logits, norm, ws, argmax_keys, parts_o,
-                    qkvbuf, q8tmp, tree_pos, tree_mask, p_layers, p_words, p_tok_next, p_err};
+                    qkvbuf, tree_pos, tree_mask, p_layers, p_words, p_tok_next, p_err};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     if (p_err_host) (void)hipHostFree(p_err_host);
@@ -632,10 +631,9 @@ struct axm_runner {
   }
 
   // A Q8_G64 or fp16 matrix: its GEMV (RMSNorm prologue, bias) with the residual /
-  // SwiGLU epilogue fused for Q8_G64 and as separate launches for fp16, with the
-  // rounding of the tile16 epilogues (residual add in fp16, silu(fp16 g) * fp16 u).
-  // Activation and output rows are contiguous ([M][K] in, [M][N] out), as every
-  // caller lays them out.
+  // SwiGLU epilogue fused, with the rounding of the tile16 epilogues (residual add in
+  // fp16, silu(fp16 g) * fp16 u).  Activation and output rows are contiguous ([M][K]
+  // in, [M][N] out), as every caller lays them out.
   int run_dense(const Mat& m, int epi, int out_rows, const GemvCall& c, int M, hipStream_t s) {
     if (c.x_parts != nullptr || c.argmax_keys != nullptr || epi == Q4_EPI_QKV_ROPE || c.ldx != m.K) {
       axm_set_error("runner: unsupported call on a Q8_G64 / fp16 matrix (epilogue %d)", epi);
@@ -664,21 +662,16 @@ struct axm_runner {
       if (m.fmt == 1)
         return launch_q8_gemv_swiglu(xin, (const uint8_t*)m.w, (const f16*)m.sb, c.y, M, m.K, 2 * out_rows, ln,
                                      c.eps, s);
-      rc = dense_gemv(m, xin, nullptr, q8tmp, M, 2 * out_rows, ln, c.eps, s);
-      if (rc) return rc;
-      return launch_swiglu(q8tmp, c.y, M, out_rows, s);
+      return launch_f16_gemv_swiglu(xin, (const f16*)m.w, c.y, M, m.K, 2 * out_rows, ln, c.eps, s);
     }
     // Q4_EPI_RESID
     if (c.ldr != out_rows) {
       axm_set_error("runner: a Q8 residual needs contiguous rows");
       return -2;
     }
-    if (m.fmt == 1) {
-      rc = launch_q8_gemv_resid(xin, (const uint8_t*)m.w, (const f16*)m.sb, c.resid, M, m.K, out_rows, ln, c.eps, s);
-    } else {
-      rc = dense_gemv(m, xin, nullptr, q8tmp, M, out_rows, ln, c.eps, s);
-      if (rc == 0) launch_resid_add(c.resid, q8tmp, (long)M * out_rows, s);
-    }
+    rc = m.fmt == 1 ? launch_q8_gemv_resid(xin, (const uint8_t*)m.w, (const f16*)m.sb, c.resid, M, m.K, out_rows, ln,
+                                           c.eps, s)
+                    : launch_f16_gemv_resid(xin, (const f16*)m.w, c.resid, M, m.K, out_rows, ln, c.eps, s);
     if (rc) return rc;
     if (c.post_ln_w != nullptr) launch_rmsnorm(c.resid, c.post_ln_w, c.post_norm_out, M, out_rows, c.eps, s);
     return 0;
@@ -991,7 +984,6 @@ extern "C" int axm_runner_create(const axm_runner_desc* desc, axm_runner_t* out)
       {(void**)&r->parts_o, attn_parts_bytes(1, d.n_head, d.head_dim)},
       {(void**)&r->argmax_keys, (size_t)((d.vocab_size + 7) / 8) * sizeof(unsigned long long)},
       {(void**)&r->qkvbuf, (size_t)T * r->qkv_dim * sizeof(f16)},
-      {(void**)&r->q8tmp, (size_t)T * (2 * d.hidden_dim > d.d_model ? 2 * d.hidden_dim : d.d_model) * sizeof(f16)},
       {(void**)&r->tree_pos, kMaxVerify * sizeof(int)},
       {(void**)&r->tree_mask, kMaxVerify * sizeof(unsigned long long)},
   };
