@@ -34,6 +34,29 @@ int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bia
 // fp16(acc)), in place) or with SwiGLU over a [W_gate; W_up] matrix of N2 rows (y
 // [M][N2 / 2]), each with the rounding of the GEMV's fp16 output followed by an fp16
 // residual add / launch_swiglu.
+// QKV epilogue of the dense GEMVs (the tile16 Q4_EPI_QKV_ROPE step for one token): the
+// fp16 outputs (+ bias) of adjacent rows (2 j, 2 j + 1) of q and k rotated at position
+// rope_pos_dev[0] (or rope_pos) + token with freqs [rope_len][hd / 2][(cos, sin)]; q rows
+// to q_out [M][q_dim], k / v rows to k_out / v_out + kvh kv_stride_h + (wp % max_seq) hd
+// + e with wp = write_pos_dev[0] (or write_pos) + token (the fp16 cache slot, or staging
+// rows with kv_stride_h = hd and max_seq = 1).
+struct QkvRope {
+  int q_dim = 0, kv_dim = 0, head_dim = 0, rope_len = 1;
+  const float* freqs = nullptr;
+  const int* rope_pos_dev = nullptr;
+  int rope_pos = 0;
+  const int* write_pos_dev = nullptr;
+  int write_pos = 0;
+  f16* q_out = nullptr;
+  f16* k_out = nullptr;
+  f16* v_out = nullptr;
+  long kv_stride_h = 0;
+  int max_seq = 1;
+};
+int launch_q8_gemv_qkv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, int M, int K, int N,
+                       const f16* ln_w, float eps, const QkvRope& r, hipStream_t s);
+int launch_f16_gemv_qkv(const f16* x, const f16* w, const f16* bias, int M, int K, int N, const f16* ln_w, float eps,
+                        const QkvRope& r, hipStream_t s);
 int launch_q8_gemv_resid(const f16* x, const uint8_t* w, const f16* sb, f16* resid, int M, int K, int N,
                          const f16* ln_w, float eps, hipStream_t s);
 int launch_q8_gemv_swiglu(const f16* x, const uint8_t* w, const f16* sb, f16* y, int M, int K, int N2,

@@ -206,12 +206,14 @@ constexpr int kQ8Threads = 256;
 // accumulation.  Epilogues (kF16Store / kF16Resid / kF16Swiglu) as those of the Q8_G64
 // GEMV: y = fp16(acc) (+ bias); resid = fp16(resid + fp16(acc)) in place; or, over a
 // [W_gate; W_up] matrix of N = 2 H rows, y[c] = fp16(fp16(silu(g)) * u) with g, u the
-// fp16 outputs of rows c and H + c, which one wave computes together.
-enum { kF16Store = 0, kF16Resid = 1, kF16Swiglu = 2 };
+// fp16 outputs of rows c and H + c, which one wave computes together; kF16Qkv: the QKV
+// RoPE / KV-slot epilogue of QkvRope on the row pairs (2 p, 2 p + 1) of one wave.
+enum { kF16Store = 0, kF16Resid = 1, kF16Swiglu = 2, kF16Qkv = 3 };
 template <int EPI>
 __global__ void __launch_bounds__(kQ8Threads)
     f16_gemv_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f16* __restrict__ bias,
-                    f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w, float eps) {
+                    f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w, float eps,
+                    QkvRope qr) {
   extern __shared__ __align__(16) f16 xh[];  // [M][K]
   __shared__ float red[4];
   for (int mi = 0; mi < M; ++mi) {
@@ -235,22 +237,24 @@ __global__ void __launch_bounds__(kQ8Threads)
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n_waves_total = gridDim.x * (kQ8Threads / 64);
-  const int outs = EPI == kF16Swiglu ? N / 2 : N;
+  constexpr bool kPair = EPI == kF16Swiglu || EPI == kF16Qkv;  // two rows per wave and output
+  const int outs = kPair ? N / 2 : N;
   for (int n = blockIdx.x * (kQ8Threads / 64) + wave; n < outs; n += n_waves_total) {
     float acc[4] = {0.f, 0.f, 0.f, 0.f}, accu[4] = {0.f, 0.f, 0.f, 0.f};
-    const f16* wr = w + (size_t)n * K;
-    const f16* wu = w + (size_t)(n + outs) * K;  // the up row (SwiGLU)
+    // rows: n (store / residual), c = n and H + c (SwiGLU), 2 n and 2 n + 1 (QKV)
+    const f16* wr = w + (size_t)(EPI == kF16Qkv ? 2 * n : n) * K;
+    const f16* wu = w + (size_t)(EPI == kF16Qkv ? 2 * n + 1 : n + outs) * K;
     for (int k0 = lane * 8; k0 < K; k0 += 64 * 8) {
       const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + k0);
       u32x4 uv = {0u, 0u, 0u, 0u};
-      if (EPI == kF16Swiglu) uv = *reinterpret_cast<const u32x4*>(wu + k0);
+      if (kPair) uv = *reinterpret_cast<const u32x4*>(wu + k0);
       for (int mi = 0; mi < M && mi < 4; ++mi) {
         const u32x4 xv = *reinterpret_cast<const u32x4*>(xh + (size_t)mi * K + k0);
         float d = acc[mi];
 #pragma unroll
         for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_fdot2(as_h2(xv[c]), as_h2(wv[c]), d, false);
         acc[mi] = d;
-        if (EPI == kF16Swiglu) {
+        if (kPair) {
           float e = accu[mi];
 #pragma unroll
           for (int c = 0; c < 4; ++c) e = __builtin_amdgcn_fdot2(as_h2(xv[c]), as_h2(uv[c]), e, false);
@@ -260,9 +264,36 @@ __global__ void __launch_bounds__(kQ8Threads)
     }
     for (int mi = 0; mi < M && mi < 4; ++mi) {
       const float v = wave_sum(acc[mi]);
-      const float u = EPI == kF16Swiglu ? wave_sum(accu[mi]) : 0.f;
+      const float u = kPair ? wave_sum(accu[mi]) : 0.f;
       if (lane == 0) {
-        if (EPI == kF16Swiglu) {
+        if (EPI == kF16Qkv) {
+          const int row0 = 2 * n, hd = qr.head_dim;
+          f16 h0 = f2h(v), h1 = f2h(u);
+          if (bias != nullptr) {
+            h0 = f2h(h2f(h0) + h2f(bias[row0]));
+            h1 = f2h(h2f(h1) + h2f(bias[row0 + 1]));
+          }
+          f16 o[2] = {h0, h1};
+          if (row0 < qr.q_dim + qr.kv_dim) {
+            const int pos = (qr.rope_pos_dev ? qr.rope_pos_dev[0] : qr.rope_pos) + mi;
+            const int within = row0 < qr.q_dim ? row0 : row0 - qr.q_dim;
+            const float* f = qr.freqs + ((size_t)(pos % qr.rope_len) * (hd / 2) + ((within % hd) >> 1)) * 2;
+            o[0] = rope_out(h0, h1, f[0], f[1], true);
+            o[1] = rope_out(h0, h1, f[0], f[1], false);
+          }
+          for (int j = 0; j < 2; ++j) {
+            const int row = row0 + j;
+            if (row < qr.q_dim) {
+              qr.q_out[(size_t)mi * qr.q_dim + row] = o[j];
+            } else {
+              const bool is_k = row < qr.q_dim + qr.kv_dim;
+              const int within = is_k ? row - qr.q_dim : row - qr.q_dim - qr.kv_dim;
+              const int wp = (qr.write_pos_dev ? qr.write_pos_dev[0] : qr.write_pos) + mi;
+              (is_k ? qr.k_out : qr.v_out)[(size_t)(within / hd) * qr.kv_stride_h +
+                                           (size_t)(wp % qr.max_seq) * hd + within % hd] = o[j];
+            }
+          }
+        } else if (EPI == kF16Swiglu) {
           const float g = h2f(f2h(v));
           const f16 sg = f2h(g / (1.0f + expf(-g)));
           y[(size_t)mi * outs + n] = f2h(h2f(sg) * h2f(f2h(u)));
@@ -279,8 +310,9 @@ __global__ void __launch_bounds__(kQ8Threads)
 
 template <int EPI>
 int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
-                  float eps, hipStream_t s) {
-  if (K % 8 != 0 || (EPI == kF16Swiglu && N % 2 != 0)) {
+                  float eps, hipStream_t s, const QkvRope& qr = QkvRope{}) {
+  constexpr bool kPair = EPI == kF16Swiglu || EPI == kF16Qkv;
+  if (K % 8 != 0 || (kPair && N % 2 != 0)) {
     axm_set_error("f16 gemv: K=%d must be a multiple of 8 (N=%d even for SwiGLU)", K, N);
     return -2;
   }
@@ -290,8 +322,17 @@ int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, in
     axm_set_error("f16 gemv: K=%d too large for LDS staging", K);
     return -2;
   }
-  const int outs = EPI == kF16Swiglu ? N / 2 : N;
+  const int outs = kPair ? N / 2 : N;
+  const int ld_out = EPI == kF16Swiglu ? N / 2 : N;
+  if (EPI == kF16Qkv && M > rows_max && (qr.rope_pos_dev || qr.write_pos_dev)) {
+    axm_set_error("f16 gemv: a QKV epilogue with device positions takes at most %d tokens", rows_max);
+    return -2;
+  }
   for (int m0 = 0; m0 < M; m0 += rows_max) {
+    QkvRope qk = qr;  // tokens m0 ..: q rows, positions and slots move with them
+    qk.q_out = qr.q_out ? qr.q_out + (size_t)m0 * qr.q_dim : nullptr;
+    qk.rope_pos += m0;
+    qk.write_pos += m0;
     const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
     const size_t smem = (size_t)mc * K * sizeof(f16);
     static size_t attr_bytes = 0;
@@ -309,7 +350,7 @@ int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, in
     const int cap = axm_num_cus() * 8;
     if (grid > cap) grid = cap;
     hipLaunchKernelGGL(f16_gemv_kernel<EPI>, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, bias,
-                       y + (size_t)m0 * outs, mc, K, N, ln_w, eps);
+                       y == nullptr ? nullptr : y + (size_t)m0 * ld_out, mc, K, N, ln_w, eps, qk);
   }
   return 0;
 }
@@ -319,6 +360,10 @@ int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, in
 int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
                     float eps, hipStream_t s) {
   return f16_gemv_rows<kF16Store>(x, w, bias, y, M, K, N, ln_w, eps, s);
+}
+int launch_f16_gemv_qkv(const f16* x, const f16* w, const f16* bias, int M, int K, int N, const f16* ln_w, float eps,
+                        const QkvRope& r, hipStream_t s) {
+  return f16_gemv_rows<kF16Qkv>(x, w, bias, nullptr, M, K, N, ln_w, eps, s, r);
 }
 int launch_f16_gemv_resid(const f16* x, const f16* w, f16* resid, int M, int K, int N, const f16* ln_w, float eps,
                           hipStream_t s) {

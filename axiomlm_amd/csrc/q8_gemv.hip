@@ -33,7 +33,9 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // fp16(acc)) in place (the residual stream); kQ8Swiglu: y[c] = fp16(fp16(silu(g)) * u)
 // with g, u = fp16(acc) of rows c and H + c of the [W_gate; W_up] matrix (N = 2 H).  The
 // rounding is that of the GEMV's fp16 output followed by an fp16 add / swiglu_kernel.
-enum { kQ8Store = 0, kQ8Resid = 1, kQ8Swiglu = 2 };
+// kQ8Qkv: the QKV RoPE / KV-slot epilogue described with QkvRope (R even: a wave's rows
+// hold whole rotation pairs).
+enum { kQ8Store = 0, kQ8Resid = 1, kQ8Swiglu = 2, kQ8Qkv = 3 };
 // Activation vectors (8 values) per thread kept in registers across the RMSNorm
 // reduction, so that the normed prologue reads x once.
 constexpr int kQ8vRegVec = 8;
@@ -41,7 +43,8 @@ constexpr int kQ8vRegVec = 8;
 template <int M, int R, int EPI>
 __global__ void __launch_bounds__(kQ8vThreads)
     q8v_kernel(const f16* __restrict__ x, int K, int N, const uint8_t* __restrict__ w, const f16* __restrict__ sb,
-               const f16* __restrict__ bias, f16* __restrict__ y, const f16* __restrict__ ln_w, float eps) {
+               const f16* __restrict__ bias, f16* __restrict__ y, const f16* __restrict__ ln_w, float eps,
+               QkvRope qr) {
   extern __shared__ __align__(16) unsigned char smem[];
   f16* xs = reinterpret_cast<f16*>(smem);                       // [M][K]
   float* s16 = reinterpret_cast<float*>(xs + (size_t)M * K);    // [M][K / 16]
@@ -235,7 +238,43 @@ __global__ void __launch_bounds__(kQ8vThreads)
 #pragma unroll
     for (int m = 0; m < M; ++m) r[i][m] = wave_sum(r[i][m]);
   if (lane == 0) {
-    if (EPI == kQ8Swiglu) {
+    if (EPI == kQ8Qkv) {
+      const int hd = qr.head_dim;
+      auto put = [&](int row, int m, f16 v) {
+        if (row < qr.q_dim) {
+          qr.q_out[(size_t)m * qr.q_dim + row] = v;
+        } else {
+          const bool is_k = row < qr.q_dim + qr.kv_dim;
+          const int within = is_k ? row - qr.q_dim : row - qr.q_dim - qr.kv_dim;
+          const int wp = (qr.write_pos_dev ? qr.write_pos_dev[0] : qr.write_pos) + m;
+          (is_k ? qr.k_out : qr.v_out)[(size_t)(within / hd) * qr.kv_stride_h + (size_t)(wp % qr.max_seq) * hd +
+                                       within % hd] = v;
+        }
+      };
+#pragma unroll
+      for (int i = 0; i < R; i += 2) {
+        const int row0 = row_of(i);
+        if (row0 >= N) continue;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          f16 h0 = f2h(r[i][m]), h1 = f2h(r[i + 1][m]);
+          if (bias != nullptr) {
+            h0 = f2h(h2f(h0) + h2f(bias[row0]));
+            h1 = f2h(h2f(h1) + h2f(bias[row0 + 1]));
+          }
+          f16 o0 = h0, o1 = h1;
+          if (row0 < qr.q_dim + qr.kv_dim) {
+            const int pos = (qr.rope_pos_dev ? qr.rope_pos_dev[0] : qr.rope_pos) + m;
+            const int within = row0 < qr.q_dim ? row0 : row0 - qr.q_dim;
+            const float* f = qr.freqs + ((size_t)(pos % qr.rope_len) * (hd / 2) + ((within % hd) >> 1)) * 2;
+            o0 = rope_out(h0, h1, f[0], f[1], true);
+            o1 = rope_out(h0, h1, f[0], f[1], false);
+          }
+          put(row0, m, o0);
+          put(row0 + 1, m, o1);
+        }
+      }
+    } else if (EPI == kQ8Swiglu) {
 #pragma unroll
       for (int i = 0; i < R / 2; ++i) {
         const int c = wrow * (R / 2) + i;
@@ -269,7 +308,7 @@ __global__ void __launch_bounds__(kQ8vThreads)
 
 template <int M, int R, int EPI>
 int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
-               const f16* ln_w, float eps, hipStream_t s) {
+               const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s) {
   const size_t smem = (size_t)M * K * sizeof(f16) + (size_t)M * (K / 16) * sizeof(float);
   static bool attr_set = false;
   if (smem > 48 * 1024 && !attr_set) {
@@ -285,7 +324,7 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
   const int units = EPI == kQ8Swiglu ? N / 2 : N;   // output columns
   const int per_wg = EPI == kQ8Swiglu ? rows / 2 : rows;
   hipLaunchKernelGGL((q8v_kernel<M, R, EPI>), dim3((units + per_wg - 1) / per_wg), dim3(kQ8vThreads), smem, s, x, K,
-                     N, w, sb, bias, y, ln_w, eps);
+                     N, w, sb, bias, y, ln_w, eps, qr);
   return 0;
 }
 
@@ -298,21 +337,22 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
 // three) was measured and not kept: q4_k_m 659.6 -> 663 tok/s, q8 439 -> 435.
 template <int M, int EPI>
 int q8v_launch_m(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
-                 const f16* ln_w, float eps, hipStream_t s) {
+                 const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s) {
+  constexpr bool kPairs = EPI == kQ8Swiglu || EPI == kQ8Qkv;  // rows come in pairs per wave
   const int cus = axm_num_cus();
   if constexpr (M == 1) {
-    if (N > 5 * cus * kQ8vWaves * 4) return q8v_launch<M, 8, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
+    if (N > 5 * cus * kQ8vWaves * 4) return q8v_launch<M, 8, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
   }
-  if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
-  if (EPI == kQ8Swiglu || N >= cus * kQ8vWaves * 2)
-    return q8v_launch<M, 2, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
-  return q8v_launch<M, (EPI == kQ8Swiglu ? 2 : 1), EPI>(x, w, sb, bias, y, K, N, ln_w, eps, s);
+  if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
+  if (kPairs || N >= cus * kQ8vWaves * 2)
+    return q8v_launch<M, 2, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
+  return q8v_launch<M, (kPairs ? 2 : 1), EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
 }
 
 template <int EPI>
 int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
-             const f16* ln_w, float eps, hipStream_t s) {
-  if (K % 64 != 0 || (long)N * K >= 0x7FFFFFF0L || (EPI == kQ8Swiglu && N % 2 != 0)) {
+             const f16* ln_w, float eps, hipStream_t s, const QkvRope& qr = QkvRope{}) {
+  if (K % 64 != 0 || (long)N * K >= 0x7FFFFFF0L || ((EPI == kQ8Swiglu || EPI == kQ8Qkv) && N % 2 != 0)) {
     axm_set_error("q8 gemv: K=%d must be a multiple of 64, the codes under 2 GiB (N=%d), N even for SwiGLU", K, N);
     return -2;
   }
@@ -329,12 +369,22 @@ int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16
     const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
     const f16* xm = x + (size_t)m0 * K;
     f16* ym = y + (size_t)m0 * ld_out;
+    QkvRope qk = qr;  // tokens m0 ..: q rows, positions and slots move with them
+    if (EPI == kQ8Qkv) {
+      qk.q_out = qr.q_out + (size_t)m0 * qr.q_dim;
+      qk.rope_pos += qr.rope_pos_dev ? 0 : m0;
+      qk.write_pos += qr.write_pos_dev ? 0 : m0;
+      if (m0 > 0 && (qr.rope_pos_dev || qr.write_pos_dev)) {
+        axm_set_error("q8 gemv: a QKV epilogue with device positions takes at most %d tokens", rows_max);
+        return -2;
+      }
+    }
     int rc;
     switch (mc) {
-      case 1: rc = q8v_launch_m<1, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
-      case 2: rc = q8v_launch_m<2, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
-      case 3: rc = q8v_launch_m<3, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
-      default: rc = q8v_launch_m<4, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, s); break;
+      case 1: rc = q8v_launch_m<1, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
+      case 2: rc = q8v_launch_m<2, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
+      case 3: rc = q8v_launch_m<3, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
+      default: rc = q8v_launch_m<4, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
     }
     if (rc) return rc;
   }
@@ -346,6 +396,11 @@ int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16
 int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
                    const f16* ln_w, float eps, hipStream_t s) {
   return q8v_rows<kQ8Store>(x, w, sb, bias, y, M, K, N, ln_w, eps, s);
+}
+
+int launch_q8_gemv_qkv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, int M, int K, int N,
+                       const f16* ln_w, float eps, const QkvRope& r, hipStream_t s) {
+  return q8v_rows<kQ8Qkv>(x, w, sb, bias, r.q_out, M, K, N, ln_w, eps, s, r);
 }
 
 int launch_q8_gemv_resid(const f16* x, const uint8_t* w, const f16* sb, f16* resid, int M, int K, int N,

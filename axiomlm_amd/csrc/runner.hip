@@ -533,12 +533,26 @@ struct axm_runner {
     }
     int rc = 0;
     if (m_qkv[i].fmt != 0) {
-      // Q8_G64 / fp16 QKV: GEMV (+ bias) into qkvbuf, RoPE of q / k into q / kvst, then the slot write.
-      rc = dense_gemv(m_qkv[i], x, a.bias, qkvbuf, 1, qkv_dim, a.ln_w, d.eps, s);
+      // Q8_G64 / fp16 QKV: the GEMV's own RoPE / KV-slot epilogue, as the tile16 one.
+      QkvRope r;
+      r.q_dim = q_dim;
+      r.kv_dim = kv_dim;
+      r.head_dim = d.head_dim;
+      r.rope_len = d.rope_len;
+      r.freqs = d.freqs;
+      r.rope_pos_dev = a.rope_pos_dev;
+      r.write_pos_dev = a.write_pos_dev;
+      r.q_out = q;
+      r.k_out = a.k_out;
+      r.v_out = a.v_out;
+      r.kv_stride_h = a.kv_stride_h;
+      r.max_seq = a.max_seq;
+      const Mat& m = m_qkv[i];
+      rc = m.fmt == 1 ? launch_q8_gemv_qkv(x, (const uint8_t*)m.w, (const f16*)m.sb, a.bias, 1, D, qkv_dim, a.ln_w,
+                                           d.eps, r, s)
+                      : launch_f16_gemv_qkv(x, (const f16*)m.w, a.bias, 1, D, qkv_dim, a.ln_w, d.eps, r, s);
       if (rc) return rc;
-      hipLaunchKernelGGL(rope_tokens_kernel, dim3((qkv_dim / 8 + 255) / 256, 1), dim3(256), 0, s, qkvbuf, q_dim,
-                         kv_dim, d.head_dim, d.freqs, params + P_ROPE, q, kvst);
-      launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
+      if (d.kv_dtype != AXM_KV_FP16) launch_kv_write(kv, kvst, kvst + kv_dim, 2 * kv_dim, 1, 0, params + P_WRITE, s);
     } else {
       rc = run_gemv(m_qkv[i], Q4_EPI_QKV_ROPE, qkv_dim, a, 1, s);
       if (rc) return rc;
