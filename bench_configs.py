@@ -167,14 +167,15 @@ def run_c4(dev):
             wb = int(N * K * per_w)
             n_copies = max(2, COLD_POOL_BYTES // wb + 1)
             packs = [tuple(t.clone() for t in packs[0]) for _ in range(n_copies)]
-            x = torch.randn(1, K, generator=g, device=dev).half()
+            for M in (1, 4):  # one token (the C4 workload), four (the several-token MFMA form)
+                x = torch.randn(M, K, generator=g, device=dev).half()
 
-            def gemv(i):
-                p, s = packs[i % n_copies]
-                return fn(x, p, s)
+                def gemv(i):
+                    p, s = packs[i % n_copies]
+                    return fn(x, p, s)
 
-            us = _graph_time_us(gemv, 2 * n_copies)
-            _line("C4", f"{fmt} {K}->{N} M=1", us, wb + (K + N) * 2, {"weight_copies": n_copies})
+                us = _graph_time_us(gemv, 2 * n_copies)
+                _line("C4", f"{fmt} {K}->{N} M={M}", us, wb + M * (K + N) * 2, {"weight_copies": n_copies})
             del packs
             torch.cuda.empty_cache()
     from axiomlm_amd.kernels import pack_linear_q2_k_gguf, qmv_q2_k_gguf
