@@ -10,7 +10,8 @@
 // (1024 + b0, 1024 + b1) (byte next to the exponent byte 0x64), consumed with the matching
 // activation pair by one v_dot2_f32_f16; sum q x = acc - 1024 * (sum x) is applied per
 // 16 codes with the group's scale and bias.  The next step's codes are requested before
-// the current ones are consumed.
+// the current ones are consumed; waves of one or two rows take two 16-code vectors per
+// lane and step.
 #include "kernels.h"
 
 namespace {
@@ -40,7 +41,7 @@ enum { kQ8Store = 0, kQ8Resid = 1, kQ8Swiglu = 2, kQ8Qkv = 3 };
 // reduction, so that the normed prologue reads x once.
 constexpr int kQ8vRegVec = 8;
 
-template <int M, int R, int EPI>
+template <int M, int R, int EPI, int V>
 __global__ void __launch_bounds__(kQ8vThreads)
     q8v_kernel(const f16* __restrict__ x, int K, int N, const uint8_t* __restrict__ w, const f16* __restrict__ sb,
                const f16* __restrict__ bias, f16* __restrict__ y, const f16* __restrict__ ln_w, float eps,
@@ -81,16 +82,21 @@ __global__ void __launch_bounds__(kQ8vThreads)
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, N * K, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)sb, (short)0, N * (K / 64) * 4, 0x00020000);
-  const int steps = (K + 1023) / 1024;
-  u32x4 cw[R];
+  // Lane l of step s takes the V * 16 codes at 1024 V s + 16 V l of each row (one
+  // 64-column group: 16 V divides 64).
+  const int steps = (K + 1024 * V - 1) / (1024 * V);
+  u32x4 cw[R][V];
   uint32_t sv[R];
   auto load = [&](int s) {
-    const int k0 = 1024 * s + 16 * lane;
+    const int k0 = 1024 * V * s + 16 * V * lane;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int row = row_of(i);
-      const bool ok = row < N && k0 < K;
-      cw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * K + k0 : kOOB, 0, 0));
+      const bool ok = row < N && k0 < K;  // K % 64 == 0: the lane's V vectors are in range together
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        cw[i][v] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * K + k0 + 16 * v : kOOB, 0, 0));
       sv[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (row * (K / 64) + k0 / 64) * 4 : kOOB, 0, 0);
     }
   };
@@ -196,39 +202,44 @@ __global__ void __launch_bounds__(kQ8vThreads)
 #pragma unroll
     for (int m = 0; m < M; ++m) r[i][m] = 0.f;
   for (int s = 0; s < steps; ++s) {
-    u32x4 c0[R];
+    u32x4 c0[R][V];
     uint32_t s0[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      c0[i] = cw[i];
+#pragma unroll
+      for (int v = 0; v < V; ++v) c0[i][v] = cw[i][v];
       s0[i] = sv[i];
     }
     if (s + 1 < steps) load(s + 1);
-    const int k0 = 1024 * s + 16 * lane;
+    const int k0 = 1024 * V * s + 16 * V * lane;
     if (k0 < K) {
-      u32x4 xa[M], xb[M];
-      float sx[M];
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        xa[m] = *reinterpret_cast<const u32x4*>(xs + (size_t)m * K + k0);
-        xb[m] = *reinterpret_cast<const u32x4*>(xs + (size_t)m * K + k0 + 8);
-        sx[m] = s16[(size_t)m * (K / 16) + k0 / 16];
-      }
-#pragma unroll
-      for (int i = 0; i < R; ++i) {
-        const f16x2 scb = as_h2(s0[i]);
-        const float sc = h2f(scb.x), bi = h2f(scb.y);
+      for (int v = 0; v < V; ++v) {
+        const int kv = k0 + 16 * v;
+        u32x4 xa[M], xb[M];
+        float sx[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          float acc = 0.f;
+          xa[m] = *reinterpret_cast<const u32x4*>(xs + (size_t)m * K + kv);
+          xb[m] = *reinterpret_cast<const u32x4*>(xs + (size_t)m * K + kv + 8);
+          sx[m] = s16[(size_t)m * (K / 16) + kv / 16];
+        }
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint32_t cwd = c0[i][g];
-            const u32x4& xq = g < 2 ? xa[m] : xb[m];
-            acc = dot2(xq[2 * (g & 1)], q8_pair(cwd, kSelLo), acc);
-            acc = dot2(xq[2 * (g & 1) + 1], q8_pair(cwd, kSelHi), acc);
+        for (int i = 0; i < R; ++i) {
+          const f16x2 scb = as_h2(s0[i]);
+          const float sc = h2f(scb.x), bi = h2f(scb.y);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            float acc = 0.f;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const uint32_t cwd = c0[i][v][g];
+              const u32x4& xq = g < 2 ? xa[m] : xb[m];
+              acc = dot2(xq[2 * (g & 1)], q8_pair(cwd, kSelLo), acc);
+              acc = dot2(xq[2 * (g & 1) + 1], q8_pair(cwd, kSelHi), acc);
+            }
+            r[i][m] += sc * (acc - 1024.f * sx[m]) + bi * sx[m];
           }
-          r[i][m] += sc * (acc - 1024.f * sx[m]) + bi * sx[m];
         }
       }
     }
@@ -306,13 +317,18 @@ __global__ void __launch_bounds__(kQ8vThreads)
   }
 }
 
+// 16-code vectors per lane and step: two for waves of one or two rows (the 4096-row O
+// and down projections, whose waves otherwise keep too few bytes in flight: mode
+// q4_k_m 653 -> 676, q8 460 -> 472 tok/s), one for more rows (two there: q8 460 ->
+// 448, the registers cost occupancy).
 template <int M, int R, int EPI>
 int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
                const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s) {
+  constexpr int V = R <= 2 ? 2 : 1;
   const size_t smem = (size_t)M * K * sizeof(f16) + (size_t)M * (K / 16) * sizeof(float);
   static bool attr_set = false;
   if (smem > 48 * 1024 && !attr_set) {
-    if (hipFuncSetAttribute((const void*)q8v_kernel<M, R, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (hipFuncSetAttribute((const void*)q8v_kernel<M, R, EPI, V>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             150 * 1024) != hipSuccess) {
       (void)hipGetLastError();
       axm_set_error("q8 gemv: cannot reserve %zu bytes of LDS", smem);
@@ -323,7 +339,7 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
   const int rows = kQ8vWaves * R;
   const int units = EPI == kQ8Swiglu ? N / 2 : N;   // output columns
   const int per_wg = EPI == kQ8Swiglu ? rows / 2 : rows;
-  hipLaunchKernelGGL((q8v_kernel<M, R, EPI>), dim3((units + per_wg - 1) / per_wg), dim3(kQ8vThreads), smem, s, x, K,
+  hipLaunchKernelGGL((q8v_kernel<M, R, EPI, V>), dim3((units + per_wg - 1) / per_wg), dim3(kQ8vThreads), smem, s, x, K,
                      N, w, sb, bias, y, ln_w, eps, qr);
   return 0;
 }
