@@ -203,86 +203,185 @@ constexpr int kQ8Threads = 256;
 // Activations (optionally RMS-normalized with the fp16 op order of the quantized
 // paths) are staged in LDS as fp16 pairs; one wave per output per iteration, each
 // lane streaming 16 bytes (8 weights) per step into v_dot2_f32_f16 with fp32
-// accumulation.  Epilogues (kF16Store / kF16Resid / kF16Swiglu) as those of the Q8_G64
+// accumulation.  A wave requests its first weights before the activation staging and
+// each next step's (the next output's, after a row's last) before the current row's
+// reduction and epilogue.  Epilogues (kF16Store / kF16Resid / kF16Swiglu) as those of the Q8_G64
 // GEMV: y = fp16(acc) (+ bias); resid = fp16(resid + fp16(acc)) in place; or, over a
 // [W_gate; W_up] matrix of N = 2 H rows, y[c] = fp16(fp16(silu(g)) * u) with g, u the
 // fp16 outputs of rows c and H + c, which one wave computes together; kF16Qkv: the QKV
 // RoPE / KV-slot epilogue of QkvRope on the row pairs (2 p, 2 p + 1) of one wave.
 enum { kF16Store = 0, kF16Resid = 1, kF16Swiglu = 2, kF16Qkv = 3 };
-// 512-element steps whose weight loads a lane issues together (fp16 runner: one 239.7,
-// four 254.3, eight 224.4 tok/s).
+// 512-element steps whose weight loads a lane issues together (fp16 runner: three 329.7,
+// four 334.5 tok/s).
 constexpr int kF16Unroll = 4;
+// Activation vectors (8 values) per thread held in registers across the RMSNorm
+// reduction when the launch's M K / 8 vectors fit (one token up to K = 12288).
+constexpr int kF16RegVec = 6;
 template <int EPI>
 __global__ void __launch_bounds__(kQ8Threads)
     f16_gemv_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f16* __restrict__ bias,
                     f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w, float eps,
                     QkvRope qr) {
   extern __shared__ __align__(16) f16 xh[];  // [M][K]
-  __shared__ float red[4];
-  for (int mi = 0; mi < M; ++mi) {
-    const f16* xr = x + (size_t)mi * K;
-    float rinv = 1.f;
-    if (ln_w != nullptr) {
-      float s = 0.f;
-      for (int k = threadIdx.x; k < K; k += kQ8Threads) {
-        const float v = h2f(xr[k]);
-        s += h2f(f2h(v * v));
-      }
-      rinv = rms_inv_fp16(block_sum_256(s, red), K, eps);
-    }
-    for (int k = threadIdx.x; k < K; k += kQ8Threads) {
-      f16 h = xr[k];
-      if (ln_w != nullptr) h = f2h(h2f(f2h(h2f(h) * rinv)) * h2f(ln_w[k]));
-      xh[(size_t)mi * K + k] = h;
-    }
-  }
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  __shared__ float red[kQ8Threads / 64][4];
+  __shared__ float rinv_m[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_waves_total = gridDim.x * (kQ8Threads / 64);
   constexpr bool kPair = EPI == kF16Swiglu || EPI == kF16Qkv;  // two rows per wave and output
   const int outs = kPair ? N / 2 : N;
-  for (int n = blockIdx.x * (kQ8Threads / 64) + wave; n < outs; n += n_waves_total) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f}, accu[4] = {0.f, 0.f, 0.f, 0.f};
-    // rows: n (store / residual), c = n and H + c (SwiGLU), 2 n and 2 n + 1 (QKV)
+  const int nvec = M * K / 8;  // 8-value vectors of x (K % 8 == 0)
+  const f16x8* x8 = reinterpret_cast<const f16x8*>(x);
+  const bool one_pass = nvec <= kF16RegVec * kQ8Threads;
+
+  // The activation vectors first (loads complete in issue order: the norm waits for
+  // them only), then the weights of the wave's first step, which stream in meanwhile.
+  f16x8 xv[kF16RegVec];
+  if (one_pass) {
+#pragma unroll
+    for (int i = 0; i < kF16RegVec; ++i) {
+      const int v = tid + i * kQ8Threads;
+      xv[i] = v < nvec ? x8[v] : f16x8{};
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // kF16Unroll 512-element steps per pass, all of their weight loads issued before
+  // any is consumed (one load per lane in flight left the stream latency-bound).
+  // Rows of output n: n (store / residual), c = n and H + c (SwiGLU), 2 n and 2 n + 1 (QKV).
+  u32x4 wv[kF16Unroll], uv[kF16Unroll];
+  auto load = [&](int n, int kb) {
     const f16* wr = w + (size_t)(EPI == kF16Qkv ? 2 * n : n) * K;
     const f16* wu = w + (size_t)(EPI == kF16Qkv ? 2 * n + 1 : n + outs) * K;
-    // kF16Unroll 512-element steps per pass, all of their weight loads issued before
-    // any is consumed (one load per lane in flight left the stream latency-bound).
-    for (int kb = 0; kb < K; kb += 64 * 8 * kF16Unroll) {
-      u32x4 wv[kF16Unroll], uv[kF16Unroll];
 #pragma unroll
-      for (int u = 0; u < kF16Unroll; ++u) {
-        const int k0 = kb + 64 * 8 * u + lane * 8;
-        const bool ok = k0 < K;
-        wv[u] = ok ? *reinterpret_cast<const u32x4*>(wr + k0) : u32x4{0u, 0u, 0u, 0u};
-        uv[u] = kPair && ok ? *reinterpret_cast<const u32x4*>(wu + k0) : u32x4{0u, 0u, 0u, 0u};
+    for (int u = 0; u < kF16Unroll; ++u) {
+      const int k0 = kb + 64 * 8 * u + lane * 8;
+      const bool ok = k0 < K;
+      wv[u] = ok ? *reinterpret_cast<const u32x4*>(wr + k0) : u32x4{0u, 0u, 0u, 0u};
+      uv[u] = kPair && ok ? *reinterpret_cast<const u32x4*>(wu + k0) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  int n = blockIdx.x * (kQ8Threads / 64) + wave;
+  if (n < outs) load(n, 0);
+
+  // Stage vector v (normalized when ln_w is set); vectors past the last store nothing.
+  auto stage = [&](int v, f16x8 h) {
+    if (v >= nvec) return;
+    const int m = v / (K / 8), c = v % (K / 8);
+    if (ln_w != nullptr) {
+      const f16x8 lw = *reinterpret_cast<const f16x8*>(ln_w + 8 * c);
+      const float ri = rinv_m[m];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(f2h(h2f(h[e]) * ri)) * h2f(lw[e]));
+    }
+    *reinterpret_cast<f16x8*>(xh + (size_t)m * K + 8 * c) = h;
+  };
+  // RMSNorm scale per token (fp16-rounded squares summed in fp32, the mean rounded to
+  // fp16 as in the other normed GEMVs) from the per-thread partial sums.
+  auto norm_scales = [&](const float (&ssq)[4]) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if (m < M) {  // launch-uniform
+        const float t = wave_sum(ssq[m]);
+        if (lane == 0) red[wave][m] = t;
       }
+    }
+    __syncthreads();
+    if (tid < M) {
+      float t = 0.f;
 #pragma unroll
-      for (int u = 0; u < kF16Unroll; ++u) {
-        const int k0 = kb + 64 * 8 * u + lane * 8;
-        if (k0 >= K) break;
-        for (int mi = 0; mi < M && mi < 4; ++mi) {
-          const u32x4 xv = *reinterpret_cast<const u32x4*>(xh + (size_t)mi * K + k0);
-          float d = acc[mi];
+      for (int i = 0; i < kQ8Threads / 64; ++i) t += red[i][tid];
+      rinv_m[tid] = rms_inv_fp16(t, K, eps);
+    }
+    __syncthreads();
+  };
+
+  if (one_pass) {
+    if (ln_w != nullptr) {
+      float ssq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_fdot2(as_h2(xv[c]), as_h2(wv[u][c]), d, false);
-          acc[mi] = d;
-          if (kPair) {
-            float e = accu[mi];
+      for (int i = 0; i < kF16RegVec; ++i) {
+        const int v = tid + i * kQ8Threads;
+        if (v < nvec) {
+          float part = 0.f;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) e = __builtin_amdgcn_fdot2(as_h2(xv[c]), as_h2(uv[u][c]), e, false);
-            accu[mi] = e;
+          for (int e = 0; e < 8; ++e) {
+            const float f = h2f(xv[i][e]);
+            part += h2f(f2h(f * f));
           }
+          const int mv = v / (K / 8);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) ssq[m] += m == mv ? part : 0.f;
+        }
+      }
+      norm_scales(ssq);
+    }
+#pragma unroll
+    for (int i = 0; i < kF16RegVec; ++i) {
+      if (i * kQ8Threads < nvec) stage(tid + i * kQ8Threads, xv[i]);  // workgroup-uniform bound
+    }
+  } else {
+    // More activations than the registers hold: the norm scale from a pass over x,
+    // then a second pass that stages.
+    if (ln_w != nullptr) {
+      float ssq[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int v = tid; v < nvec; v += kQ8Threads) {
+        const f16x8 h = x8[v];
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = h2f(h[e]);
+          part += h2f(f2h(f * f));
+        }
+        const int mv = v / (K / 8);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) ssq[m] += m == mv ? part : 0.f;
+      }
+      norm_scales(ssq);
+    }
+    for (int v = tid; v < nvec; v += kQ8Threads) stage(v, x8[v]);
+  }
+  __syncthreads();
+
+  // Steps of 512 kF16Unroll elements over the wave's outputs n, n + n_waves_total, ...:
+  // the weights of the next step (the next output's first one after a row's last) are
+  // requested before this row's reduction and epilogue.
+  float acc[4] = {0.f, 0.f, 0.f, 0.f}, accu[4] = {0.f, 0.f, 0.f, 0.f};
+  int kb = 0;
+  while (n < outs) {
+#pragma unroll
+    for (int u = 0; u < kF16Unroll; ++u) {
+      const int k0 = kb + 64 * 8 * u + lane * 8;
+      if (k0 >= K) break;
+      for (int mi = 0; mi < M && mi < 4; ++mi) {
+        const u32x4 xq = *reinterpret_cast<const u32x4*>(xh + (size_t)mi * K + k0);
+        float d = acc[mi];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_fdot2(as_h2(xq[c]), as_h2(wv[u][c]), d, false);
+        acc[mi] = d;
+        if (kPair) {
+          float e = accu[mi];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) e = __builtin_amdgcn_fdot2(as_h2(xq[c]), as_h2(uv[u][c]), e, false);
+          accu[mi] = e;
         }
       }
     }
+    const int cur = n;
+    kb += 64 * 8 * kF16Unroll;
+    if (kb < K) {
+      load(n, kb);
+      continue;
+    }
+    kb = 0;
+    n += n_waves_total;
+    if (n < outs) load(n, 0);
     for (int mi = 0; mi < M && mi < 4; ++mi) {
       const float v = wave_sum(acc[mi]);
       const float u = kPair ? wave_sum(accu[mi]) : 0.f;
+      acc[mi] = 0.f;
+      accu[mi] = 0.f;
       if (lane == 0) {
         if (EPI == kF16Qkv) {
-          const int row0 = 2 * n, hd = qr.head_dim;
+          const int row0 = 2 * cur, hd = qr.head_dim;
           f16 h0 = f2h(v), h1 = f2h(u);
           if (bias != nullptr) {
             h0 = f2h(h2f(h0) + h2f(bias[row0]));
@@ -311,11 +410,11 @@ __global__ void __launch_bounds__(kQ8Threads)
         } else if (EPI == kF16Swiglu) {
           const float g = h2f(f2h(v));
           const f16 sg = f2h(g / (1.0f + expf(-g)));
-          y[(size_t)mi * outs + n] = f2h(h2f(sg) * h2f(f2h(u)));
+          y[(size_t)mi * outs + cur] = f2h(h2f(sg) * h2f(f2h(u)));
         } else {
           f16 h = f2h(v);
-          if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[n]));
-          f16* o = y + (size_t)mi * N + n;
+          if (bias != nullptr) h = f2h(h2f(h) + h2f(bias[cur]));
+          f16* o = y + (size_t)mi * N + cur;
           *o = EPI == kF16Resid ? f2h(add_rn(h2f(*o), h2f(h))) : h;
         }
       }
@@ -329,6 +428,10 @@ int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, in
   constexpr bool kPair = EPI == kF16Swiglu || EPI == kF16Qkv;
   if (K % 8 != 0 || (kPair && N % 2 != 0)) {
     axm_set_error("f16 gemv: K=%d must be a multiple of 8 (N=%d even for SwiGLU)", K, N);
+    return -2;
+  }
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)ln_w) & 15) {
+    axm_set_error("f16 gemv: x, w and ln_w must be 16-byte aligned");
     return -2;
   }
   int rows_max = 4;
@@ -362,7 +465,16 @@ int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, in
     }
     const int rows_per_block = kQ8Threads / 64;
     int grid = (outs + rows_per_block - 1) / rows_per_block;
-    const int cap = axm_num_cus() * 8;
+    // One round of resident workgroups (the kernel's registers allow five or six per CU)
+    // that loop over the outputs: a grid of eight per CU queued the rest behind the first
+    // round (fp16 runner 334.5 -> 347.2 tok/s).
+    int per_cu = 8;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f16_gemv_kernel<EPI>, kQ8Threads, smem) != hipSuccess) {
+      (void)hipGetLastError();
+      per_cu = 8;
+    }
+    if (per_cu < 1) per_cu = 1;
+    const int cap = axm_num_cus() * per_cu;
     if (grid > cap) grid = cap;
     hipLaunchKernelGGL(f16_gemv_kernel<EPI>, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, bias,
                        y == nullptr ? nullptr : y + (size_t)m0 * ld_out, mc, K, N, ln_w, eps, qk);

@@ -852,18 +852,25 @@ def test_runner_rejects_legacy_q4_g64(dev):
 # ---------------------------------------------------------------------------
 # The fp16 runner (MPSDecodeRunner): every matrix fp16 [N][K]
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("kv,bias", [("fp16", False), ("fp16", True), ("fp8", False)])
-def test_fp16_runner_matches_oracle(dev, kv, bias):
+@pytest.mark.parametrize("kv,bias,wide", [("fp16", False, False), ("fp16", True, False), ("fp8", False, False),
+                                         ("fp16", True, True)])
+def test_fp16_runner_matches_oracle(dev, kv, bias, wide):
     """DecodeRunner with the reference MPSDecodeRunner signature (mps_kernels.mm:4328-4373) over
     fp16 weights (GQA 4 / 2 heads, optional QKV bias): 12 decode steps, verify chains of 3 and 9
     tokens and a 9-node tree against the oracle on the same fp16 weights, logits <= 1e-2
-    (quantized caches loaded into a frozen oracle cache, as for the quantized runner)."""
+    (quantized caches loaded into a frozen oracle cache, as for the quantized runner).  The wide
+    model (d 2048, SwiGLU 5632) has GEMVs whose activations exceed what the GEMV holds in
+    registers across its RMSNorm (four tokens of K = 5632), so the staging pass over x runs too."""
     from axiomlm_amd.cache import StaticKVCache
     from axiomlm_amd.runner import DecodeRunner
 
-    print(f"[fp16_runner] kv={kv} bias={bias}", flush=True)
-    cfg = om.OracleConfig(n_layer=3, n_head=4, n_kv_head=2, d_model=256, hidden=704, vocab=1024, eps=1e-5,
-                          block_size=256)
+    print(f"[fp16_runner] kv={kv} bias={bias} wide={wide}", flush=True)
+    if wide:
+        cfg = om.OracleConfig(n_layer=1, n_head=16, n_kv_head=8, d_model=2048, hidden=5632, vocab=1024, eps=1e-5,
+                              block_size=256)
+    else:
+        cfg = om.OracleConfig(n_layer=3, n_head=4, n_kv_head=2, d_model=256, hidden=704, vocab=1024, eps=1e-5,
+                              block_size=256)
     W = om.make_float_weights(cfg, seed=7)
     ow = om.fp16_model(cfg, W)
     if bias:
