@@ -347,10 +347,14 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
 // Rows per wave: for one token eight when four would need more than one round of
 // workgroups (the one-token four-row kernel holds 81-84 VGPRs, five waves per SIMD:
 // 7B gate / up has 1376 workgroups of four-row waves for 1280 slots; the eight-row one
-// 124, four waves; mode q8 432.5 -> 440 tok/s), four while that leaves two workgroups
-// per CU, else two, else one (two at least for SwiGLU, whose waves take gate / up row
-// pairs).  A two-step prefetch ring (three register slots, the step loop unrolled by
-// three) was measured and not kept: q4_k_m 659.6 -> 663 tok/s, q8 439 -> 435.
+// 124, four waves; mode q8 432.5 -> 440 tok/s), else two while the two-row waves (78
+// VGPRs, six per SIMD) fit one round (7B QKV, 12288 rows: 6144 waves of two steps in
+// place of 3072 four-row waves of four, q8 473.0 -> 481.2 tok/s), else four.  For
+// several tokens four while that leaves two workgroups per CU.  Then two, else one (two
+// at least for SwiGLU and QKV, whose waves take row pairs).  Measured and not kept: a
+// two-step prefetch ring (three register slots, the step loop unrolled by three):
+// q4_k_m 659.6 -> 663 tok/s, q8 439 -> 435; one-row waves with four vectors per lane for
+// the 4096-row O and down projections: q8 473.0 -> 468.8.
 template <int M, int EPI>
 int q8v_launch_m(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
                  const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s) {
@@ -358,8 +362,10 @@ int q8v_launch_m(const f16* x, const uint8_t* w, const f16* sb, const f16* bias,
   const int cus = axm_num_cus();
   if constexpr (M == 1) {
     if (N > 5 * cus * kQ8vWaves * 4) return q8v_launch<M, 8, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
+    if (N > 6 * cus * kQ8vWaves * 2) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
+  } else {
+    if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
   }
-  if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
   if (kPairs || N >= cus * kQ8vWaves * 2)
     return q8v_launch<M, 2, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
   return q8v_launch<M, (kPairs ? 2 : 1), EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);

@@ -432,12 +432,14 @@ def test_q8_qmv_matches_oracle(dev):
 
 
 @pytest.mark.parametrize("M,N_,K,bias", [(1, 32000, 4096, False), (1, 4096, 11008, False), (3, 12288, 4096, True),
+                                         (1, 12288, 4096, True), (1, 16384, 4096, False),
                                          (4, 4096, 11008, False), (5, 2048, 4096, True), (2, 77, 640, True),
                                          (1, 1, 64, False)])
 def test_q8_qmv_shapes_match_oracle(dev, M, N_, K, bias):
-    """The Q8_G64 GEMV at the 7B lm_head / down / QKV shapes (one, two and four rows per
-    wave), several tokens, a bias and ragged sizes, against the oracle's dequantize-then-
-    matmul (fp16 weights, as the reference CPU path rounds them), 2e-3 relative."""
+    """The Q8_G64 GEMV at the 7B lm_head / down / QKV shapes (one token: eight, two and
+    four rows per wave), several tokens, a bias and ragged sizes, against the oracle's
+    dequantize-then-matmul (fp16 weights, as the reference CPU path rounds them), 2e-3
+    relative."""
     from axiomlm_amd.kernels import qmv_q8_g64
 
     print(f"[q8_qmv] M={M} N={N_} K={K} bias={bias}", flush=True)
