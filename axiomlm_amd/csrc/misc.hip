@@ -133,12 +133,32 @@ __global__ void __launch_bounds__(256) argmax_kernel(const f16* __restrict__ log
   const f16* lr = logits + (size_t)blockIdx.x * V;
   float best = -INFINITY;
   int besti = 0x7fffffff;
-  for (int k = threadIdx.x; k < V; k += 256) {
-    const float v = h2f(lr[k]);
+  auto take = [&](float v, int k) {
     if (v > best || (v == best && k < besti)) {
       best = v;
       besti = k;
     }
+  };
+  if (V % 8 == 0 && ((uintptr_t)lr & 15) == 0) {
+    // 16-byte vectors, four requested per thread before any is compared; a thread
+    // visits its indices in increasing order, so a strict > keeps the lowest of a tie.
+    const f16x8* l8 = reinterpret_cast<const f16x8*>(lr);
+    const int nv = V / 8;
+    for (int v0 = threadIdx.x; v0 < nv; v0 += 4 * 256) {
+      f16x8 h[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) h[u] = v0 + u * 256 < nv ? l8[v0 + u * 256] : f16x8{};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * 256;
+        if (v < nv) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) take(h2f(h[u][e]), 8 * v + e);
+        }
+      }
+    }
+  } else {
+    for (int k = threadIdx.x; k < V; k += 256) take(h2f(lr[k]), k);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {

@@ -515,10 +515,22 @@ def test_swiglu_and_argmax(dev):
     got = N(swiglu_gate_up(T(gu, dev)))
     d = np.abs(got.view(np.uint16).astype(np.int32) - ref.view(np.uint16).astype(np.int32))
     assert d.max() <= 1
-    lg = rng.standard_normal((4, 32000)).astype(F16)
+    lg = rng.standard_normal((6, 32000)).astype(F16)
     lg[1, 17] = lg[1, 900] = 50.0  # tie: lowest index wins (metal_kernels.metal:437, 499)
+    # ties within one thread's vectors (indices 8 v + e, v and v + 256) and across threads
+    lg[2, 8 * 300 + 5] = lg[2, 8 * (300 + 256) + 5] = lg[2, 8 * 301 + 2] = 60.0
+    lg[3, 31999] = 70.0  # the last element
+    lg[4, :] = np.nan  # NaN compares below everything: all NaN gives index 0
+    lg[5, ::2] = np.nan
+    lg[5, 12345] = 80.0
+    want = [int(np.argmax(r)) for r in lg[:4]] + [0, 12345]
     got = N(argmax_last_token(T(lg, dev)))
-    assert got.tolist() == [int(np.argmax(r)) for r in lg] and got[1] == 17
+    assert got.tolist() == want and got[1] == 17 and got[2] == 8 * 300 + 5
+    # rows whose length is not a multiple of 8 (element loads)
+    odd = rng.standard_normal((3, 1001)).astype(F16)
+    odd[0, 1000] = 9.0
+    odd[1, 3] = odd[1, 500] = 9.0
+    assert N(argmax_last_token(T(odd, dev))).tolist() == [int(np.argmax(r)) for r in odd]
 
 
 # ---------------------------------------------------------------------------
