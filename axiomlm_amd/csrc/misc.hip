@@ -140,16 +140,18 @@ __global__ void __launch_bounds__(256) argmax_kernel(const f16* __restrict__ log
     }
   };
   if (V % 8 == 0 && ((uintptr_t)lr & 15) == 0) {
-    // 16-byte vectors, four requested per thread before any is compared; a thread
-    // visits its indices in increasing order, so a strict > keeps the lowest of a tie.
+    // 16-byte vectors, kArgVec requested per thread before any is compared (a
+    // 32000-entry row in one batch); a thread visits its indices in increasing order,
+    // so a strict > keeps the lowest of a tie.
+    constexpr int kArgVec = 16;
     const f16x8* l8 = reinterpret_cast<const f16x8*>(lr);
     const int nv = V / 8;
-    for (int v0 = threadIdx.x; v0 < nv; v0 += 4 * 256) {
-      f16x8 h[4];
+    for (int v0 = threadIdx.x; v0 < nv; v0 += kArgVec * 256) {
+      f16x8 h[kArgVec];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) h[u] = v0 + u * 256 < nv ? l8[v0 + u * 256] : f16x8{};
+      for (int u = 0; u < kArgVec; ++u) h[u] = v0 + u * 256 < nv ? l8[v0 + u * 256] : f16x8{};
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kArgVec; ++u) {
         const int v = v0 + u * 256;
         if (v < nv) {
 #pragma unroll
