@@ -1,5 +1,6 @@
 // Row-wise kernels of the decode step: RMSNorm (+ residual add), SwiGLU,
-// argmax, embedding gathers and the Q8_G64 GEMV used for tied / q8 lm_heads.
+// argmax, embedding gathers, the fp16 GEMV of the fp16 runner, and the C-ABI
+// entry points of these ops and of the Q8_G64 GEMV (q8_gemv.hip).
 //
 // Numerics follow the reference CPU path on a half-precision model: every
 // elementwise fp16 op rounds its fp32 result to fp16 (torch CPU semantics),
