@@ -22,14 +22,16 @@ int launch_embed_q8(const uint8_t* wq, const f16* sb, const int64_t* tokens, con
                     int D, int V, hipStream_t s);
 
 // ---- Q8_G64 GEMV (affine 8-bit, group 64), optional fused fp16 RMSNorm -------
+// xn_out (optional, with ln_w): the RMS-normalized rows [M][K] the GEMV staged, written
+// by its first workgroup.
 int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
-                    float eps, hipStream_t s);
+                    float eps, hipStream_t s, f16* xn_out = nullptr);
 int launch_f16_gemv_resid(const f16* x, const f16* w, f16* resid, int M, int K, int N, const f16* ln_w, float eps,
                           hipStream_t s);
 int launch_f16_gemv_swiglu(const f16* x, const f16* w, f16* y, int M, int K, int N2, const f16* ln_w, float eps,
                            hipStream_t s);
 int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
-                   const f16* ln_w, float eps, hipStream_t s);
+                   const f16* ln_w, float eps, hipStream_t s, f16* xn_out = nullptr);
 // The Q8_G64 / fp16 GEMVs with the residual add fused (resid[m][n] = fp16(resid +
 // fp16(acc)), in place) or with SwiGLU over a [W_gate; W_up] matrix of N2 rows (y
 // [M][N2 / 2]), each with the rounding of the GEMV's fp16 output followed by an fp16

@@ -244,7 +244,7 @@ template <int EPI>
 __global__ void __launch_bounds__(kQ8Threads)
     f16_gemv_kernel(const f16* __restrict__ x, const f16* __restrict__ w, const f16* __restrict__ bias,
                     f16* __restrict__ y, int M, int K, int N, const f16* __restrict__ ln_w, float eps,
-                    QkvRope qr) {
+                    QkvRope qr, f16* __restrict__ xn_out) {
   extern __shared__ __align__(16) f16 xh[];  // [M][K]
   __shared__ float red[kQ8Threads / 64][4];
   __shared__ float rinv_m[4];
@@ -296,6 +296,7 @@ __global__ void __launch_bounds__(kQ8Threads)
       for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(f2h(h2f(h[e]) * ri)) * h2f(lw[e]));
     }
     *reinterpret_cast<f16x8*>(xh + (size_t)m * K + 8 * c) = h;
+    if (xn_out != nullptr && blockIdx.x == 0) *reinterpret_cast<f16x8*>(xn_out + (size_t)m * K + 8 * c) = h;
   };
   // RMSNorm scale per token (fp16-rounded squares summed in fp32, the mean rounded to
   // fp16 as in the other normed GEMVs) from the per-thread partial sums.
@@ -447,14 +448,14 @@ __global__ void __launch_bounds__(kQ8Threads)
 
 template <int EPI>
 int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
-                  float eps, hipStream_t s, const QkvRope& qr = QkvRope{}) {
+                  float eps, hipStream_t s, const QkvRope& qr = QkvRope{}, f16* xn_out = nullptr) {
   constexpr bool kPair = EPI == kF16Swiglu || EPI == kF16Qkv;
   if (K % 8 != 0 || (kPair && N % 2 != 0)) {
     axm_set_error("f16 gemv: K=%d must be a multiple of 8 (N=%d even for SwiGLU)", K, N);
     return -2;
   }
-  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)ln_w) & 15) {
-    axm_set_error("f16 gemv: x, w and ln_w must be 16-byte aligned");
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)ln_w | (uintptr_t)xn_out) & 15) {
+    axm_set_error("f16 gemv: x, w, ln_w and xn_out must be 16-byte aligned");
     return -2;
   }
   int rows_max = 4;
@@ -500,7 +501,8 @@ int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, in
     const int cap = axm_num_cus() * per_cu;
     if (grid > cap) grid = cap;
     hipLaunchKernelGGL(f16_gemv_kernel<EPI>, dim3(grid), dim3(kQ8Threads), smem, s, x + (size_t)m0 * K, w, bias,
-                       y == nullptr ? nullptr : y + (size_t)m0 * ld_out, mc, K, N, ln_w, eps, qk);
+                       y == nullptr ? nullptr : y + (size_t)m0 * ld_out, mc, K, N, ln_w, eps, qk,
+                       xn_out == nullptr ? nullptr : xn_out + (size_t)m0 * K);
   }
   return 0;
 }
@@ -508,8 +510,8 @@ int f16_gemv_rows(const f16* x, const f16* w, const f16* bias, f16* y, int M, in
 }  // namespace
 
 int launch_f16_gemv(const f16* x, const f16* w, const f16* bias, f16* y, int M, int K, int N, const f16* ln_w,
-                    float eps, hipStream_t s) {
-  return f16_gemv_rows<kF16Store>(x, w, bias, y, M, K, N, ln_w, eps, s);
+                    float eps, hipStream_t s, f16* xn_out) {
+  return f16_gemv_rows<kF16Store>(x, w, bias, y, M, K, N, ln_w, eps, s, QkvRope{}, xn_out);
 }
 int launch_f16_gemv_qkv(const f16* x, const f16* w, const f16* bias, int M, int K, int N, const f16* ln_w, float eps,
                         const QkvRope& r, hipStream_t s) {

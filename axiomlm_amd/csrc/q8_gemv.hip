@@ -45,7 +45,7 @@ template <int M, int R, int EPI, int V>
 __global__ void __launch_bounds__(kQ8vThreads)
     q8v_kernel(const f16* __restrict__ x, int K, int N, const uint8_t* __restrict__ w, const f16* __restrict__ sb,
                const f16* __restrict__ bias, f16* __restrict__ y, const f16* __restrict__ ln_w, float eps,
-               QkvRope qr) {
+               QkvRope qr, f16* __restrict__ xn_out) {
   extern __shared__ __align__(16) unsigned char smem[];
   f16* xs = reinterpret_cast<f16*>(smem);                       // [M][K]
   float* s16 = reinterpret_cast<float*>(xs + (size_t)M * K);    // [M][K / 16]
@@ -122,6 +122,7 @@ __global__ void __launch_bounds__(kQ8vThreads)
     s = add_rn(s, __shfl_xor(s, 1, 64));
     if (valid) {
       *reinterpret_cast<f16x8*>(xs + (size_t)m * K + 8 * c) = h;
+      if (xn_out != nullptr && blockIdx.x == 0) *reinterpret_cast<f16x8*>(xn_out + (size_t)m * K + 8 * c) = h;
       if ((c & 1) == 0) s16[(size_t)m * (K / 16) + c / 2] = s;
     }
   };
@@ -323,7 +324,7 @@ __global__ void __launch_bounds__(kQ8vThreads)
 // 448, the registers cost occupancy).
 template <int M, int R, int EPI>
 int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
-               const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s) {
+               const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s, f16* xn_out) {
   constexpr int V = R <= 2 ? 2 : 1;
   const size_t smem = (size_t)M * K * sizeof(f16) + (size_t)M * (K / 16) * sizeof(float);
   static bool attr_set = false;
@@ -340,7 +341,7 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
   const int units = EPI == kQ8Swiglu ? N / 2 : N;   // output columns
   const int per_wg = EPI == kQ8Swiglu ? rows / 2 : rows;
   hipLaunchKernelGGL((q8v_kernel<M, R, EPI, V>), dim3((units + per_wg - 1) / per_wg), dim3(kQ8vThreads), smem, s, x, K,
-                     N, w, sb, bias, y, ln_w, eps, qr);
+                     N, w, sb, bias, y, ln_w, eps, qr, xn_out);
   return 0;
 }
 
@@ -357,23 +358,23 @@ int q8v_launch(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f
 // the 4096-row O and down projections: q8 473.0 -> 468.8.
 template <int M, int EPI>
 int q8v_launch_m(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int K, int N,
-                 const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s) {
+                 const f16* ln_w, float eps, const QkvRope& qr, hipStream_t s, f16* xn_out) {
   constexpr bool kPairs = EPI == kQ8Swiglu || EPI == kQ8Qkv;  // rows come in pairs per wave
   const int cus = axm_num_cus();
   if constexpr (M == 1) {
-    if (N > 5 * cus * kQ8vWaves * 4) return q8v_launch<M, 8, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
-    if (N > 6 * cus * kQ8vWaves * 2) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
+    if (N > 5 * cus * kQ8vWaves * 4) return q8v_launch<M, 8, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s, xn_out);
+    if (N > 6 * cus * kQ8vWaves * 2) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s, xn_out);
   } else {
-    if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
+    if (N >= 2 * cus * kQ8vWaves * 4) return q8v_launch<M, 4, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s, xn_out);
   }
   if (kPairs || N >= cus * kQ8vWaves * 2)
-    return q8v_launch<M, 2, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
-  return q8v_launch<M, (kPairs ? 2 : 1), EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s);
+    return q8v_launch<M, 2, EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s, xn_out);
+  return q8v_launch<M, (kPairs ? 2 : 1), EPI>(x, w, sb, bias, y, K, N, ln_w, eps, qr, s, xn_out);
 }
 
 template <int EPI>
 int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
-             const f16* ln_w, float eps, hipStream_t s, const QkvRope& qr = QkvRope{}) {
+             const f16* ln_w, float eps, hipStream_t s, const QkvRope& qr = QkvRope{}, f16* xn_out = nullptr) {
   if (K % 64 != 0 || (long)N * K >= 0x7FFFFFF0L || ((EPI == kQ8Swiglu || EPI == kQ8Qkv) && N % 2 != 0)) {
     axm_set_error("q8 gemv: K=%d must be a multiple of 64, the codes under 2 GiB (N=%d), N even for SwiGLU", K, N);
     return -2;
@@ -391,6 +392,7 @@ int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16
     const int mc = (M - m0) < rows_max ? (M - m0) : rows_max;
     const f16* xm = x + (size_t)m0 * K;
     f16* ym = y + (size_t)m0 * ld_out;
+    f16* xnm = xn_out != nullptr ? xn_out + (size_t)m0 * K : nullptr;
     QkvRope qk = qr;  // tokens m0 ..: q rows, positions and slots move with them
     if (EPI == kQ8Qkv) {
       qk.q_out = qr.q_out + (size_t)m0 * qr.q_dim;
@@ -403,10 +405,10 @@ int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16
     }
     int rc;
     switch (mc) {
-      case 1: rc = q8v_launch_m<1, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
-      case 2: rc = q8v_launch_m<2, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
-      case 3: rc = q8v_launch_m<3, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
-      default: rc = q8v_launch_m<4, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s); break;
+      case 1: rc = q8v_launch_m<1, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s, xnm); break;
+      case 2: rc = q8v_launch_m<2, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s, xnm); break;
+      case 3: rc = q8v_launch_m<3, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s, xnm); break;
+      default: rc = q8v_launch_m<4, EPI>(xm, w, sb, bias, ym, K, N, ln_w, eps, qk, s, xnm); break;
     }
     if (rc) return rc;
   }
@@ -416,8 +418,8 @@ int q8v_rows(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16
 }  // namespace
 
 int launch_q8_gemv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, f16* y, int M, int K, int N,
-                   const f16* ln_w, float eps, hipStream_t s) {
-  return q8v_rows<kQ8Store>(x, w, sb, bias, y, M, K, N, ln_w, eps, s);
+                   const f16* ln_w, float eps, hipStream_t s, f16* xn_out) {
+  return q8v_rows<kQ8Store>(x, w, sb, bias, y, M, K, N, ln_w, eps, s, QkvRope{}, xn_out);
 }
 
 int launch_q8_gemv_qkv(const f16* x, const uint8_t* w, const f16* sb, const f16* bias, int M, int K, int N,

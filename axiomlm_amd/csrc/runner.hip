@@ -624,17 +624,18 @@ struct axm_runner {
       l.argmax_keys = argmax_keys;
       return run_gemv(m_lmh, Q4_EPI_STORE, d.vocab_size, l, 1, s);
     }
-    launch_rmsnorm(x, (const f16*)d.lnf_w, norm, 1, D, d.eps, s);
-    return lm_head_dense(norm, 1, s);
+    return lm_head_dense(x, 1, (const f16*)d.lnf_w, norm, s);
   }
 
-  // Q8_G64 (format 1) or fp16 (format 2) lm_head over T normalized rows into logits.
-  int lm_head_dense(const f16* xn, int T, hipStream_t s) {
+  // Q8_G64 (format 1) or fp16 (format 2) lm_head over T rows into logits: with ln_w the
+  // GEMV applies the final RMSNorm itself and writes the normalized rows to xn_out (one
+  // launch where a separate norm took two); without, the rows are normalized already.
+  int lm_head_dense(const f16* x, int T, const f16* ln_w, f16* xn_out, hipStream_t s) {
     if (d.lm_head_format == 2)
-      return launch_f16_gemv(xn, (const f16*)d.lm_head_w, nullptr, logits, T, d.d_model, d.vocab_size, nullptr, 0.f,
-                             s);
-    return launch_q8_gemv(xn, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, T, d.d_model,
-                          d.vocab_size, nullptr, 0.f, s);
+      return launch_f16_gemv(x, (const f16*)d.lm_head_w, nullptr, logits, T, d.d_model, d.vocab_size, ln_w, d.eps,
+                             s, xn_out);
+    return launch_q8_gemv(x, (const uint8_t*)d.lm_head_w, (const f16*)d.lm_head_sb, nullptr, logits, T, d.d_model,
+                          d.vocab_size, ln_w, d.eps, s, xn_out);
   }
 
   // The GEMV of a Q8_G64 (fmt 1) or fp16 (fmt 2) matrix, [M][K] -> [M][N] rows.
@@ -855,8 +856,8 @@ struct axm_runner {
       l.x_norm_out = post ? nullptr : norm;
       return gemv_rows(m_lmh, Q4_EPI_STORE, d.vocab_size, l, T, s);
     }
-    if (!post) launch_rmsnorm(x, (const f16*)d.lnf_w, norm, T, D, d.eps, s);
-    return lm_head_dense(norm, T, s);
+    if (!post) return lm_head_dense(x, T, (const f16*)d.lnf_w, norm, s);
+    return lm_head_dense(norm, T, nullptr, nullptr, s);
   }
 
   // Re-tile one matrix for the matrix-core GEMV (runner-owned copy).

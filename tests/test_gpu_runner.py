@@ -804,6 +804,15 @@ def test_runner_verify_step_ring_wrap_gqa_head128(dev, kv):
 MODE_FORMATS = {"q4_k_m": ("q4_marlin", "q4_marlin", "q4_marlin", "q8_g64"), "q8": ("q8_g64",) * 4}
 
 
+def _check_last_norm(runner, T, ref_norm, what, tol=1e-2):
+    """get_last_norm (mps_kernels.mm:3731-3736) against the oracle's final normed rows; over a
+    Q8_G64 / fp16 lm_head the lm_head GEMV writes them from its own RMSNorm staging."""
+    got = runner.get_last_norm(T)[0].float().cpu().numpy()
+    ref = np.asarray(ref_norm, dtype=np.float32).reshape(got.shape)
+    err = np.abs(got - ref) / np.maximum(1.0, np.abs(ref))
+    assert err.max() <= tol, f"{what}: last norm {err.max():.2e}"
+
+
 @pytest.mark.parametrize("mode,kv", [("q4_k_m", "fp16"), ("q8", "fp16"), ("q4_k_m", "fp8"), ("q8", "int4")])
 def test_runner_modes_match_oracle(dev, mode, kv):
     """Modes "q4_k_m" and "q8" (transformer.py:840-847, the runner's per-matrix format
@@ -827,18 +836,21 @@ def test_runner_modes_match_oracle(dev, mode, kv):
         got = run_steps(runner, cache, [tok], dev)[0]
         if ocache.frozen:
             _load_gpu_cache(ocache, cache)
-        _check_logits(got, model.forward([tok], ocache)[-1], f"{mode} step {i}")
+        ref, ref_norm = model.forward([tok], ocache, return_norm=True)
+        _check_logits(got, ref[-1], f"{mode} step {i}")
+        _check_last_norm(runner, 1, ref_norm, f"{mode} step {i}")
     for T in (3, 9):
         seen = cache.total_seen_tokens[0]
         chain = rng.integers(0, cfg.vocab, T).tolist()
         g = runner.verify_step(torch.tensor([chain], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
         if ocache.frozen:
             _load_gpu_cache(ocache, cache)
-        ref = model.forward(chain, ocache, return_all_logits=True)
+        ref, ref_norm = model.forward(chain, ocache, return_all_logits=True, return_norm=True)
         cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
         cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
         for t in range(T):
             _check_logits(g[t], ref[t], f"{mode} verify T={T} token {t}")
+        _check_last_norm(runner, T, ref_norm, f"{mode} verify T={T}")
 
 
 def test_runner_rejects_legacy_q4_g64(dev):
@@ -896,18 +908,21 @@ def test_fp16_runner_matches_oracle(dev, kv, bias, wide):
         got = run_steps(runner, cache, [tok], dev)[0]
         if ocache.frozen:
             _load_gpu_cache(ocache, cache)
-        _check_logits(got, model.forward([tok], ocache)[-1], f"fp16 step {i}")
+        ref, ref_norm = model.forward([tok], ocache, return_norm=True)
+        _check_logits(got, ref[-1], f"fp16 step {i}")
+        _check_last_norm(runner, 1, ref_norm, f"fp16 step {i}")
     for T in (3, 9):
         seen = cache.total_seen_tokens[0]
         chain = rng.integers(0, cfg.vocab, T).tolist()
         g = runner.verify_step(torch.tensor([chain], device=dev), seen, seen, seen + T)[0].float().cpu().numpy()
         if ocache.frozen:
             _load_gpu_cache(ocache, cache)
-        ref = model.forward(chain, ocache, return_all_logits=True)
+        ref, ref_norm = model.forward(chain, ocache, return_all_logits=True, return_norm=True)
         cache.total_seen_tokens[:] = [seen + T] * cfg.n_layer
         cache.layer_seq_lens[:] = [seen + T] * cfg.n_layer
         for tt in range(T):
             _check_logits(g[tt], ref[tt], f"fp16 verify T={T} token {tt}")
+        _check_last_norm(runner, T, ref_norm, f"fp16 verify T={T}")
     if kv == "fp16":
         seen = cache.total_seen_tokens[0]
         parents = [-1, 0, 0, 1, 1, 2, 3, 5, 5]
