@@ -269,6 +269,7 @@ __global__ void __launch_bounds__(kQ8Threads)
   __builtin_amdgcn_sched_barrier(0);
   // kF16Unroll 512-element steps per pass, all of their weight loads issued before
   // any is consumed (one load per lane in flight left the stream latency-bound).
+  // Nontemporal loads: each weight is read once (fp16 runner 347.2 -> 369.4 tok/s).
   // Rows of output n: n (store / residual), c = n and H + c (SwiGLU), 2 n and 2 n + 1 (QKV).
   u32x4 wv[kF16Unroll], uv[kF16Unroll];
   auto load = [&](int n, int kb) {
@@ -278,8 +279,8 @@ __global__ void __launch_bounds__(kQ8Threads)
     for (int u = 0; u < kF16Unroll; ++u) {
       const int k0 = kb + 64 * 8 * u + lane * 8;
       const bool ok = k0 < K;
-      wv[u] = ok ? *reinterpret_cast<const u32x4*>(wr + k0) : u32x4{0u, 0u, 0u, 0u};
-      uv[u] = kPair && ok ? *reinterpret_cast<const u32x4*>(wu + k0) : u32x4{0u, 0u, 0u, 0u};
+      wv[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + k0)) : u32x4{0u, 0u, 0u, 0u};
+      uv[u] = kPair && ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wu + k0)) : u32x4{0u, 0u, 0u, 0u};
     }
   };
   int n = blockIdx.x * (kQ8Threads / 64) + wave;

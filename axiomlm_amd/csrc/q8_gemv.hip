@@ -83,7 +83,8 @@ __global__ void __launch_bounds__(kQ8vThreads)
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)sb, (short)0, N * (K / 64) * 4, 0x00020000);
   // Lane l of step s takes the V * 16 codes at 1024 V s + 16 V l of each row (one
-  // 64-column group: 16 V divides 64).
+  // 64-column group: 16 V divides 64).  Codes and scales are read once: nontemporal
+  // loads (q4_k_m 677.5 -> 682.7, q8 483.4 -> 488.0 tok/s).
   const int steps = (K + 1024 * V - 1) / (1024 * V);
   u32x4 cw[R][V];
   uint32_t sv[R];
@@ -96,8 +97,8 @@ __global__ void __launch_bounds__(kQ8vThreads)
 #pragma unroll
       for (int v = 0; v < V; ++v)
         cw[i][v] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * K + k0 + 16 * v : kOOB, 0, 0));
-      sv[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (row * (K / 64) + k0 / 64) * 4 : kOOB, 0, 0);
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * K + k0 + 16 * v : kOOB, 0, 2));
+      sv[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (row * (K / 64) + k0 / 64) * 4 : kOOB, 0, 2);
     }
   };
   load(0);
